@@ -1,0 +1,309 @@
+#!/usr/bin/env python3
+"""Benchmark of the token-mixing hot path on one MI355X.
+
+Default workload (the BASELINE metric): config 3 — paged GQA decode attention, batch 64, bf16 KV pool, lengths
+U[128, 8192], 8/2 heads x 256, block 16, sigmoid output gate fused. One step = one RocmBackend.paged_attention call
+over the whole batch (split-K kernel + merge/gate kernel), inputs already resident in HBM. Prints ONE JSON line.
+
+  value           decode-attention tokens/s = batch / step time (one attention-layer call per decode token)
+  roofline        the split-K kernel (the dominant launch): its algorithmic bytes (every visible K/V byte once, q,
+                  the block-table entries and lens it reads) / its average duration, measured with HIP events over
+                  back-to-back launches on the stream it runs on; peak = 8 TB/s HBM
+  cpu_baseline    the CPU oracle (TorchBackend.paged_attention + gate restated in torch fp32) on the same seeded
+                  inputs, timed on this host's cores
+
+Other workloads (--workload c1 | c2) print the same record for the config-1 decode (parity/latency case) and the
+config-2 DeltaNet decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache).
+Timing: W untimed warm-up steps, then K timed steps captured in one HIP graph and replayed between two events
+after a device synchronize (the eager, Python-issued rate is reported beside it).
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "metal-inference-engine_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def traffic_for(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), or None when no summary covers it."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    data = json.loads(TRAFFIC_FILE.read_text())
+    entry = data.get(kernel)
+    return entry.get("bytes_per_launch") if entry else None
+
+
+def time_region(fn, steps: int, warmup: int, stream) -> float:
+    """Average ms per call of fn over `steps` back-to-back calls on `stream` (after `warmup` calls)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def graph_time(fn, steps: int, stream) -> float:
+    """Average ms per step of `steps` calls of fn captured in one HIP graph (no host work between launches)."""
+    import torch
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            fn()
+    graph.replay()                                  # first replay uploads the graph
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def cpu_time(fn, runs: int = 3) -> float:
+    fn()                                   # warm-up
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts)
+
+
+def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
+    import torch
+    from native import kernels
+    from native.rocm_native import load
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    log(f"[bench] {workload_name}: copying inputs to {dev}")
+    sets = []
+    for i in range(args.sets):                       # distinct copies: consecutive steps never re-read a cache
+        c = case.to(dev)
+        if i:
+            c.k_pool, c.v_pool = c.k_pool.clone(), c.v_pool.clone()
+        sets.append(c)
+    torch.cuda.synchronize()
+    B, Hq, d = case.q.shape
+    it = [0]
+
+    def step():
+        c = sets[it[0] % len(sets)]
+        it[0] += 1
+        backend.paged_attention(c.q, c.k_pool, c.v_pool, c.tables, c.lens, c.block_size, c.window, gate=c.gate)
+
+    log(f"[bench] {workload_name}: timing {args.steps} steps after {args.warmup} warm-up")
+    eager_ms = time_region(step, args.steps, args.warmup, stream)
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    host_us = (time.perf_counter() - t) / args.steps * 1e6
+    torch.cuda.synchronize()
+    ms = graph_time(step, args.steps, stream)
+
+    # the split-K launch alone: back-to-back launches through the C ABI with prebuilt arguments
+    lib = load()
+    outs = [torch.empty(B, Hq, d, device=dev) for _ in sets]
+    NB, bs, Hkv, _ = case.k_pool.shape
+    max_nb = case.tables.shape[1]
+    need = lib.lib.rk_paged_decode_workspace_bytes(B, Hq, Hkv, d, bs, max_nb)
+    ws = kernels.workspace(dev, need)
+    argsets = [(0, o.data_ptr(), c.q.data_ptr(), c.k_pool.data_ptr(), c.v_pool.data_ptr(),
+                kernels.DTYPE_CODES[c.k_pool.dtype], c.tables.data_ptr(), c.lens.data_ptr(), B, Hq, Hkv, d, bs, max_nb,
+                NB, int(c.window or 0), c.gate.data_ptr(), ws.data_ptr(), ws.numel(), stream.cuda_stream)
+               for o, c in zip(outs, sets)]
+    fn = lib.lib.rk_paged_decode_phase
+    j = [0]
+
+    def split():
+        a = argsets[j[0] % len(argsets)]
+        j[0] += 1
+        if fn(*a) != 0:
+            raise RuntimeError(lib.last_error())
+
+    split_ms = time_region(split, args.steps, args.warmup, stream)
+    kv = case.kv_bytes()
+    nb = (case.lens.long() + bs - 1) // bs
+    split_bytes = kv + B * Hq * d * 4 + 4 * int(nb.sum()) + 4 * B
+    achieved = split_bytes / (split_ms * 1e-3) / 1e9
+    step_gbs = case.algorithmic_bytes() / (ms * 1e-3) / 1e9
+    log(f"[bench] {workload_name}: step {ms * 1e3:.1f} us in a graph ({step_gbs:.0f} GB/s algorithmic), "
+        f"{eager_ms * 1e3:.1f} us eager (host {host_us:.1f} us per call), split kernel {split_ms * 1e3:.1f} us "
+        f"({achieved:.0f} GB/s)")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import backend_ref
+        torch.set_num_threads(cpu_threads())
+        log(f"[bench] {workload_name}: CPU oracle on {torch.get_num_threads()} threads")
+
+        def cpu_run():
+            o = backend_ref.paged_attention(case.q, case.k_pool, case.v_pool, case.tables, case.lens,
+                                            case.block_size, case.window)
+            backend_ref.gate(o, case.gate)
+
+        t = cpu_time(cpu_run)
+        cpu = {"value": B / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"the full {workload_name} batch ({B} sequences, {int(case.lens.sum())} positions): "
+                         f"median of 3 runs after 1 warm-up, {t:.3f} s per batch"}
+    return {
+        "metric": "decode attn tokens/s @ batch 64 + achieved HBM GB/s (% of 8 TB/s), 1 GPU",
+        "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs; no model weights are involved)",
+        "config": config,
+        "hbm_gbs_step": step_gbs, "hbm_frac_step": step_gbs / HBM_PEAK_GBS,
+        "timing": "value and ms_per_step: K steps captured in one HIP graph, replayed between two events; "
+                  "eager_ms_per_step: the same K calls issued from Python",
+        "eager_ms_per_step": eager_ms, "host_us_per_call": host_us,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(f"paged_decode_split/{workload_name}"),
+                     "kernel": "paged_decode_split", "bytes_per_launch": split_bytes, "avg_ms": split_ms},
+        "cpu_baseline": cpu,
+    }
+
+
+class SlotState:
+    """A DeltaNet state holder for the CPU oracle: S [n_linear, H, dk, dv], conv_tail [n_linear, K-1, C]."""
+
+    def __init__(self, S, conv_tail):
+        self.S, self.conv_tail = S, conv_tail
+
+
+def bench_deltanet(args, backend):
+    import torch
+    import workloads as wl
+    from native import kernels
+    from oracle import backend_ref
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    B, n_linear, max_seqs = 8, 6, 64                  # 64 x 6 slots x 1 MiB per head-set = 384 MiB of state
+    case = wl.c2_deltanet_step(batch=B, max_seqs=max_seqs, n_linear=n_linear)
+    c = case.to(dev)
+    gen = torch.Generator().manual_seed(22)
+    perms = [torch.randperm(max_seqs, generator=gen)[:B].to(torch.int32).to(dev) for _ in range(8)]
+    combos = [(p, s) for p in perms for s in range(n_linear)]      # 48 distinct (slot set, layer) state blocks
+    torch.cuda.synchronize()
+    k = [0]
+
+    def step():
+        seqs, slot = combos[k[0] % len(combos)]
+        k[0] += 1
+        kernels.deltanet_decode(c.qkv, c.z, c.b, c.a, c.conv, c.S, seqs, slot, c.conv_w, c.A_log, c.dt_bias,
+                                c.norm_w, c.eps, c.dims)
+
+    # launch-bound at this size: capture the timed steps in a HIP graph and time one replay
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(args.steps):
+            step()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    nbytes = case.algorithmic_bytes()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] c2: {ms * 1e3:.2f} us per step, {gbs:.0f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu:
+        torch.set_num_threads(cpu_threads())
+        states = [SlotState(case.S[int(s)].clone(), case.conv[int(s)].clone()) for s in case.seq_index]
+
+        def cpu_run():
+            backend_ref.deltanet_decode_batch(case.qkv, case.z, case.b, case.a, states, 0, case.conv_w, case.A_log,
+                                              case.dt_bias, case.norm_w, case.eps, case.dims)
+        t = cpu_time(cpu_run, runs=5)
+        cpu = {"value": B / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"one batch-{B} step, median of 5 after 1 warm-up, {t * 1e3:.2f} ms"}
+    return {
+        "metric": "DeltaNet decode step tokens/s @ batch 8 + achieved HBM GB/s (% of 8 TB/s), 1 GPU",
+        "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded)", "config": {"workload": "config 2: DeltaNet decode step, batch 8, 16 heads x "
+                                                             "128 x 128 fp32 state, conv 4 over 6144 channels"},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": traffic_for("deltanet_step/c2"), "kernel": "deltanet_step_kernel",
+                     "bytes_per_launch": nbytes, "avg_ms": ms},
+        "cpu_baseline": cpu,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3"])
+    ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the sequences of a batch shard across GPUs with no exchange, so N GPUs run N independent copies "
+              "of this benchmark.", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    import workloads as wl
+    from backend.rocm import RocmBackend
+    backend = RocmBackend("cuda:0")
+    if args.workload == "c3":
+        case = wl.c3_paged_decode()
+        lens = case.lens
+        config = {"workload": "config 3: paged GQA decode, batch 64, bf16 KV, fp32 accumulate, 8/2 heads x 256, "
+                              "block 16, lengths U[128, 8192], pool 1.25 x positions, sigmoid gate",
+                  "batch": 64, "total_positions": int(lens.sum()), "num_blocks": int(case.k_pool.shape[0]),
+                  "kv_bytes": case.kv_bytes()}
+        rec = bench_paged_decode(case, args, backend, "c3", config)
+    elif args.workload == "c1":
+        case = wl.c1_paged_decode()
+        args.sets = max(args.sets, 64)                 # 64 x 8 MiB pools > the 256 MB Infinity Cache
+        rec = bench_paged_decode(case, args, backend, "c1",
+                                 {"workload": "config 1: paged GQA decode, batch 1, fp32 KV, 512 positions"})
+        rec["metric"] = "decode attn tokens/s @ batch 1 (config 1 latency case), 1 GPU"
+        rec["dtype"] = "f32"
+    else:
+        rec = bench_deltanet(args, backend)
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

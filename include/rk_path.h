@@ -1,0 +1,95 @@
+/* rk_path.h — C ABI of the MI355X (gfx950) token-mixing kernels.
+ *
+ * Every entry point takes raw device pointers, plain integer shapes and the caller's stream (a hipStream_t passed
+ * as void*; NULL means the null stream). Nothing here allocates device memory, copies a pool or synchronises:
+ * outputs, workspaces and state buffers belong to the caller (PyTorch tensors in the Python host code), and every
+ * launch is enqueued on the given stream. Return value: RK_OK (0) or an RK_ERR_* code, with a message available from
+ * rk_last_error() (thread-local). No entry point aborts the process.
+ *
+ * Reference interfaces each entry point replaces are cited as path:line in MeKaustubh07/metal-inference-engine.
+ */
+#ifndef RK_PATH_H
+#define RK_PATH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RK_ABI_VERSION 1
+
+/* status codes */
+#define RK_OK 0
+#define RK_ERR_ARG 1         /* null pointer, bad shape or size */
+#define RK_ERR_UNSUPPORTED 2 /* dtype or shape with no kernel instance */
+#define RK_ERR_WORKSPACE 3   /* caller workspace smaller than the *_workspace_bytes() figure */
+#define RK_ERR_HIP 4         /* HIP runtime error (launch, device query) */
+
+/* element types of caller buffers */
+#define RK_F32 0
+#define RK_BF16 1
+
+/* ---- library / errors (replaces the mr_* status + error-buffer convention of src/native/metal_runtime.mm:20-43) */
+const char* rk_last_error(void);
+void rk_clear_error(void);
+int rk_abi_version(void);
+/* compute units and gcnArchName ("gfx950:...") of the current device */
+int rk_device_info(int* compute_units, char* arch, int arch_len);
+
+/* ---- P1: paged GQA decode attention (+ optional fused sigmoid output gate)
+ * Replaces MetalBackend.paged_attention + paged_attention_decode<T> (src/backend/metal.py:212-223,
+ * src/kernels/attention.metal:87-159); semantics of TorchBackend.paged_attention (src/backend/torch_ref.py:75-88)
+ * and the gate of src/models/qwen3_5.py:271.
+ *   out    [B, Hq, D] fp32              q [B, Hq, D] fp32
+ *   k_pool, v_pool: one layer of the pool, [num_blocks, block_size, Hkv, D], kv_dtype RK_F32 or RK_BF16
+ *   tables [B, max_nb] int32 (rows 0-padded), lens [B] int32 (positions 0..lens[i]-1 are read)
+ *   window 0 = none, else each sequence reads only positions lens[i]-window .. lens[i]-1
+ *   gate   NULL or [B, Hq*D] fp32: out *= sigmoid(gate)
+ *   workspace: rk_paged_decode_workspace_bytes(...) bytes of device memory (split-K partials); no zeroing needed.
+ * D in {64, 128, 256}; Hq / Hkv <= 8; B <= 1024. */
+size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_size, int max_nb);
+int rk_paged_decode(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                    const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
+                    int max_nb, int num_blocks, int window, const float* gate, void* workspace,
+                    size_t workspace_bytes, void* stream);
+/* The two launches of rk_paged_decode, separately (phase 0: split-K partials into the workspace; phase 1: merge,
+ * gate, write out). Used to time the dominant phase on its own; rk_paged_decode == phase 0 then phase 1. */
+int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
+                          int kv_dtype, const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D,
+                          int block_size, int max_nb, int num_blocks, int window, const float* gate,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- paged KV cache write (scatter) and read (gather)
+ * rk_kv_write replaces PagedKVPool.write_batch / PagedSequence.write (src/state.py:131-134, 163-170):
+ *   pool[slot[i] / block_size, slot[i] % block_size, :, :] = src[i]  for i < n, both K and V,
+ *   slot = block * block_size + offset (int64), src [n, Hkv, D] in src_dtype, converted to pool_dtype
+ *   (fp32 -> bf16 rounds to nearest even, as torch's .to(torch.bfloat16)).
+ * rk_kv_gather replaces PagedSequence.read and the gather of TorchBackend.paged_attention
+ * (src/state.py:172-180; src/backend/torch_ref.py:82-86): out[t - lo] = pool row of position t for lo <= t < end,
+ * through one sequence's block table `table` (int32, entry j = physical block of logical block j). Bit-exact copy. */
+int rk_kv_write(void* k_pool, void* v_pool, int pool_dtype, const int64_t* slots, const void* k_src,
+                const void* v_src, int src_dtype, int n, int Hkv, int D, int block_size, int num_blocks,
+                void* stream);
+int rk_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool, int dtype, const int32_t* table,
+                 int table_len, int lo, int end, int Hkv, int D, int block_size, int num_blocks, void* stream);
+
+/* ---- P2: fused Gated DeltaNet decode step for B sequences (conv + SiLU, l2norm, beta/decay, delta rule, gated
+ * RMSNorm). Replaces MetalBackend.deltanet_decode_batch + conv_step + gdn_decode (src/backend/metal.py:232-256;
+ * src/kernels/deltanet.metal:9-92) with the semantics of TorchBackend.deltanet_decode(_batch)
+ * (src/backend/torch_ref.py:61-73, 90-93).
+ *   out [B, H*dv] fp32; qkv [B, C] fp32 (C = 2*H*dk + H*dv, pre-conv); z [B, H*dv]; b, a [B, H]
+ *   conv_state [seqs, n_linear, K-1, C] fp32 and S [seqs, n_linear, H, dk, dv] fp32, both updated in place at
+ *   [seq_index[i], slot]; conv_w [C, K]; A_log, dt_bias [H]; norm_w [dv]; seq_index [B] int32.
+ * dk = dv = 128, K = 4. */
+int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float* b, const float* a,
+                       float* conv_state, float* S, const float* conv_w, const float* A_log, const float* dt_bias,
+                       const float* norm_w, const int32_t* seq_index, int B, int H, int dk, int dv, int conv_k,
+                       int n_linear, int slot, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RK_PATH_H */

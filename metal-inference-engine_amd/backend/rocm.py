@@ -1,0 +1,88 @@
+"""RocmBackend: the engine's token-mixing operations on hand-written HIP kernels for MI355X (gfx950).
+
+The `rocm` counterpart of MetalBackend (src/backend/metal.py:28): the same method names, signatures and fp32 return
+tensors as the Backend protocol (src/backend/base.py:11-67) for the decode/prefill token-mixing path. Every method
+runs through librk_path.so; there is no CPU path and no second implementation to fall back to: without a ROCm GPU or
+without the built library, construction raises.
+
+Method -> kernel:
+  paged_attention        rk_paged_decode   (P1; + optional fused sigmoid gate)
+  attention, T == 1      rk_paged_decode on the contiguous cache viewed as one block (the reference's
+                         attention_decode, src/backend/metal.py:197-210)
+  deltanet_decode[_batch] rk_deltanet_decode (P2; states of one HybridPool in one launch, a standalone state as a
+                         pool of one, src/backend/metal.py:232-256)
+"""
+import torch
+
+from native import kernels
+from native.rocm_native import load
+
+KV_DTYPES = kernels.KV_DTYPES
+
+
+class RocmBackend:
+    """Token-mixing backend on one ROCm device. Not thread-safe (one engine thread owns the device, as in the
+    reference's scheduler); every launch goes on torch's current stream of that device, without host syncs."""
+
+    def __init__(self, device: str | torch.device = "cuda"):
+        if not torch.cuda.is_available():
+            raise RuntimeError("RocmBackend needs a ROCm GPU (torch.cuda.is_available() is False)")
+        dev = torch.device(device)
+        self.device = torch.device("cuda", dev.index if dev.index is not None else torch.cuda.current_device())
+        self.lib = load()
+        arch = torch.cuda.get_device_properties(self.device).gcnArchName
+        if not arch.startswith("gfx950"):
+            raise RuntimeError(f"librk_path.so is built for gfx950 only; device {self.device} is {arch}")
+        self.name = "rocm"
+        self._seq0 = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+    # ---- P1: decode attention
+    def paged_attention(self, q, k_pool, v_pool, tables, lens, block_size, window=None, gate=None):
+        """q [B, Hq, d]; k_pool / v_pool one layer [blocks, bs, Hkv, d] (fp32 or bf16, read in place); tables
+        [B, max_nb] int32; lens [B] int32 -> [B, Hq, d] fp32. gate [B, Hq * d] (optional): the sigmoid output gate of
+        src/models/qwen3_5.py:271 applied in the same launch sequence."""
+        if k_pool.dtype != v_pool.dtype or k_pool.dtype not in KV_DTYPES:
+            raise TypeError(f"paged_attention: keys and values must both be float32 or bfloat16, not "
+                            f"{k_pool.dtype} / {v_pool.dtype}")
+        return kernels.paged_decode(q, k_pool, v_pool, tables, lens, block_size, window, gate)
+
+    def attention(self, q, k, v, causal=True, window=None):
+        """q [T, Hq, d], k/v [S, Hkv, d] -> [T, Hq, d] fp32. T == 1 (decode on a contiguous cache) runs the paged
+        decode kernel on the cache viewed as a single block."""
+        T, Hq, d = q.shape
+        if T != 1:
+            raise NotImplementedError("RocmBackend.attention: multi-query prefill attention goes through "
+                                      "paged_prefill_attention")
+        if window is not None and window < 1:
+            raise ValueError(f"window must be at least 1, not {window}")
+        if window and k.shape[0] > window:
+            k, v = k[-window:], v[-window:]
+        if k.dtype != v.dtype or k.dtype not in KV_DTYPES:
+            k, v = k.float(), v.float()
+        S, Hkv, _ = k.shape
+        kp = k.contiguous().view(1, S, Hkv, d)
+        vp = v.contiguous().view(1, S, Hkv, d)
+        tables = self._seq0.view(1, 1)
+        lens = torch.full((1,), S, dtype=torch.int32, device=self.device)
+        return kernels.paged_decode(q, kp, vp, tables, lens, S)
+
+    # ---- P2: DeltaNet decode step
+    def deltanet_decode(self, qkv, z, b, a, state, slot, conv_w, A_log, dt_bias, norm_w, eps, dims):
+        return self.deltanet_decode_batch(qkv, z, b, a, [state], slot, conv_w, A_log, dt_bias, norm_w, eps, dims)
+
+    def deltanet_decode_batch(self, qkv, z, b, a, states, slot, conv_w, A_log, dt_bias, norm_w, eps, dims):
+        """B sequences, one token each; row i belongs to states[i]. One launch when the states share a HybridPool
+        (or for a lone standalone state); otherwise one launch per state, each a pool of one."""
+        pool = getattr(states[0], "pool", None)
+        if pool is not None and all(getattr(st, "pool", None) is pool for st in states):
+            S, conv, seqs = pool.S, pool.conv, pool.seq_index(states)
+        elif len(states) == 1:
+            S, conv, seqs = states[0].S.unsqueeze(0), states[0].conv_tail.unsqueeze(0), self._seq0
+        else:
+            return torch.cat([self.deltanet_decode_batch(qkv[i:i + 1], z[i:i + 1], b[i:i + 1], a[i:i + 1], [st], slot,
+                                                         conv_w, A_log, dt_bias, norm_w, eps, dims)
+                              for i, st in enumerate(states)])
+        return kernels.deltanet_decode(qkv, z, b, a, conv, S, seqs, slot, conv_w, A_log, dt_bias, norm_w, eps, dims)
+
+    def sync(self) -> None:
+        torch.cuda.synchronize(self.device)

@@ -1,0 +1,56 @@
+"""Build librk_path.so: every HIP source in this directory, compiled ahead of time for gfx950 only.
+
+The counterpart of the reference's scripts/build_native.sh (clang++ -framework Metal ... -shared), which builds its
+one native file into build/. Here hipcc compiles each translation unit to an object and links one shared library
+next to the sources, so the library travels with the tree. Usage: python native/build.py [-v]
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "librk_path.so"
+OBJ_DIR = HERE / "_obj"
+SOURCES = ["rk_abi.cpp", "paged_decode.hip", "kv_cache.hip", "deltanet_step.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# packed-fp32 VALU forms are switched off for all device code (see the header of rk_device.h)
+FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _compile(src: str, verbose: bool) -> Path:
+    obj = OBJ_DIR / (Path(src).stem + ".o")
+    cmd = [HIPCC, "-x", "hip", "-c", str(HERE / src), "-o", str(obj)] + FLAGS
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # the host pass does not know the packed-fp32 target feature and says so: not an error
+    noise = [ln for ln in (r.stderr or "").splitlines() if "not a recognized feature" not in ln]
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n" + "\n".join(noise))
+    if verbose and noise:
+        print("\n".join(noise))
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link librk_path.so (always rebuilds). Returns the library path."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-shared", "-o", str(tmp)] + [str(o) for o in objs] + [f"--offload-arch={ARCH}", "-fPIC"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n" + r.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

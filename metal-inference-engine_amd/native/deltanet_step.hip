@@ -1,0 +1,184 @@
+// P2: fused Gated DeltaNet decode step (one new token per sequence), gfx950.
+//
+// Semantics: TorchBackend.deltanet_decode (src/backend/torch_ref.py:61-73) = ops.causal_conv1d (src/ops.py:127-139)
+// -> split q|k|v -> ops.l2norm (q also * 1/sqrt(dk)) -> beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias)
+// (threshold 20) -> ops.gated_delta_recurrent with T = 1 (src/ops.py:142-157) -> ops.rms_norm_gated
+// (src/ops.py:120-124). The conv tail and S are updated in place at [seq_index[i], slot] (src/state.py:428-429;
+// the Metal pair conv_step + gdn_decode, src/kernels/deltanet.metal:9-92, indexes them the same way).
+//
+// One workgroup of 512 threads per (sequence, head). The head's 128 x 128 fp32 state is loaded once into registers
+// (thread = 8 rows x 4 columns, a row of 32 threads reads 512 contiguous bytes), decayed, rank-1 updated and written
+// back once: 2 x 64 KiB of HBM traffic per head, the algorithmic minimum. The S loads are issued first, so the
+// convolution of the head's 384 channels, the l2 norms and the gate parameters are computed while they are in
+// flight. Elementwise steps keep the reference's operation order (products rounded before sums, no contraction into
+// FMA) wherever the reference rounds them separately; only the lengths-128 sums are reordered (tree instead of
+// sequential), which moves results by a few ulp.
+#include "rk_device.h"
+#include "rk_internal.h"
+
+namespace rk {
+namespace {
+
+constexpr int kDK = 128, kDV = 128, kTaps = 4, kThreads = 512;
+
+struct StepArgs {
+    float* out;
+    const float* qkv;
+    const float* z;
+    const float* b;
+    const float* a;
+    float* conv;
+    float* S;
+    const float* conv_w;
+    const float* A_log;
+    const float* dt_bias;
+    const float* norm_w;
+    const int32_t* seq;
+    int B, H, C, n_linear, slot;
+    float eps;
+};
+
+__global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
+    __shared__ float us[3 * kDK];        // conv + SiLU output of this head: q | k | v
+    __shared__ float qn[kDK], kn[kDK], dl[kDV];
+    __shared__ float red[16][kDV];       // partial sums over row groups
+    __shared__ float wsum[16];
+
+    const int t = threadIdx.x;
+    const int bi = blockIdx.x / p.H, h = blockIdx.x % p.H;
+    const int H = p.H, C = p.C;
+    const long long seq = p.seq[bi];
+    float* Sh = p.S + (((seq * p.n_linear + p.slot) * H + h) * kDK) * kDV;
+    float* tail = p.conv + (seq * p.n_linear + p.slot) * (long long)(kTaps - 1) * C;
+
+    // ---- 1. state tile of this thread, loaded first
+    const int cg = t & 31, rg = t >> 5;       // columns 4*cg .. 4*cg+3, rows 8*rg .. 8*rg+7
+    float4 s[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) s[r] = *reinterpret_cast<const float4*>(Sh + (8 * rg + r) * kDV + 4 * cg);
+
+    // ---- 2. causal conv (taps 0..2 = tail, tap 3 = current token) + SiLU for the head's 384 channels
+    if (t < 3 * kDK) {
+        const int part = t / kDK, j = t % kDK;
+        const int c = part == 0 ? h * kDK + j : (part == 1 ? H * kDK + h * kDK + j : 2 * H * kDK + h * kDV + j);
+        const float x = p.qkv[(long long)bi * C + c];
+        const float h0 = tail[c], h1 = tail[C + c], h2 = tail[2 * C + c];
+        const float4 w = *reinterpret_cast<const float4*>(p.conv_w + (long long)c * kTaps);
+        float y = __fmul_rn(h0, w.x);
+        y = __fadd_rn(y, __fmul_rn(h1, w.y));
+        y = __fadd_rn(y, __fmul_rn(h2, w.z));
+        y = __fadd_rn(y, __fmul_rn(x, w.w));
+        us[t] = y / (1.0f + expf(-y));
+        tail[c] = h1;
+        tail[C + c] = h2;
+        tail[2 * C + c] = x;
+    }
+    __syncthreads();
+
+    // ---- 3. l2 norms of q and k (sum of squares + 1e-6), q scale 1/sqrt(dk); gate parameters
+    if (t < 2 * kDK) {
+        const float x = us[t];
+        const float sq = wave_sum(__fmul_rn(x, x));
+        if ((t & 63) == 0) wsum[t >> 6] = sq;
+    }
+    __syncthreads();
+    if (t < kDK) {
+        const float inv_q = 1.0f / sqrtf(wsum[0] + wsum[1] + 1e-6f);
+        const float inv_k = 1.0f / sqrtf(wsum[2] + wsum[3] + 1e-6f);
+        qn[t] = __fmul_rn(__fmul_rn(us[t], inv_q), 1.0f / sqrtf((float)kDK));
+        kn[t] = __fmul_rn(us[kDK + t], inv_k);
+    }
+    const float beta = 1.0f / (1.0f + expf(-p.b[(long long)bi * H + h]));
+    const float ab = p.a[(long long)bi * H + h] + p.dt_bias[h];
+    const float sp = ab > 20.0f ? ab : log1pf(expf(ab));
+    const float g = -expf(p.A_log[h]) * sp;
+    const float decay = expf(g);
+    __syncthreads();
+
+    // ---- 4. decay, kv = k^T S (decayed), delta = beta * (v - kv)
+    float kvp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const float kr = kn[8 * rg + r];
+        s[r].x = __fmul_rn(s[r].x, decay);
+        s[r].y = __fmul_rn(s[r].y, decay);
+        s[r].z = __fmul_rn(s[r].z, decay);
+        s[r].w = __fmul_rn(s[r].w, decay);
+        kvp[0] = fmaf(s[r].x, kr, kvp[0]);
+        kvp[1] = fmaf(s[r].y, kr, kvp[1]);
+        kvp[2] = fmaf(s[r].z, kr, kvp[2]);
+        kvp[3] = fmaf(s[r].w, kr, kvp[3]);
+    }
+    *reinterpret_cast<float4*>(&red[rg][4 * cg]) = make_float4(kvp[0], kvp[1], kvp[2], kvp[3]);
+    __syncthreads();
+    if (t < kDV) {
+        float kv = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) kv += red[r][t];
+        dl[t] = __fmul_rn(us[2 * kDK + t] - kv, beta);
+    }
+    __syncthreads();
+
+    // ---- 5. S += k delta^T (written back), o = q^T S (updated state)
+    const float4 d4 = *reinterpret_cast<const float4*>(&dl[4 * cg]);
+    float op[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const float kr = kn[8 * rg + r], qr = qn[8 * rg + r];
+        s[r].x = __fadd_rn(s[r].x, __fmul_rn(kr, d4.x));
+        s[r].y = __fadd_rn(s[r].y, __fmul_rn(kr, d4.y));
+        s[r].z = __fadd_rn(s[r].z, __fmul_rn(kr, d4.z));
+        s[r].w = __fadd_rn(s[r].w, __fmul_rn(kr, d4.w));
+        *reinterpret_cast<float4*>(Sh + (8 * rg + r) * kDV + 4 * cg) = s[r];
+        op[0] = fmaf(s[r].x, qr, op[0]);
+        op[1] = fmaf(s[r].y, qr, op[1]);
+        op[2] = fmaf(s[r].z, qr, op[2]);
+        op[3] = fmaf(s[r].w, qr, op[3]);
+    }
+    *reinterpret_cast<float4*>(&red[rg][4 * cg]) = make_float4(op[0], op[1], op[2], op[3]);
+    __syncthreads();
+
+    // ---- 6. gated RMSNorm over dv: o * rsqrt(mean(o^2) + eps) * w * silu(z)
+    float o = 0.0f;
+    if (t < kDV) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o += red[r][t];
+        const float sq = wave_sum(__fmul_rn(o, o));
+        if ((t & 63) == 0) wsum[4 + (t >> 6)] = sq;
+    }
+    __syncthreads();
+    if (t < kDV) {
+        const float rstd = 1.0f / sqrtf((wsum[4] + wsum[5]) / (float)kDV + p.eps);
+        const float zj = p.z[(long long)bi * H * kDV + h * kDV + t];
+        const float silu = zj / (1.0f + expf(-zj));
+        p.out[(long long)bi * H * kDV + h * kDV + t] = __fmul_rn(__fmul_rn(__fmul_rn(o, rstd), p.norm_w[t]), silu);
+    }
+}
+
+}  // namespace
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" {
+
+int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float* b, const float* a,
+                       float* conv_state, float* S, const float* conv_w, const float* A_log, const float* dt_bias,
+                       const float* norm_w, const int32_t* seq_index, int B, int H, int dk, int dv, int conv_k,
+                       int n_linear, int slot, float eps, void* stream) {
+    if (!out || !qkv || !z || !b || !a || !conv_state || !S || !conv_w || !A_log || !dt_bias || !norm_w || !seq_index)
+        return fail(RK_ERR_ARG, "rk_deltanet_decode: null pointer");
+    if (B < 1 || H < 1 || n_linear < 1 || slot < 0 || slot >= n_linear)
+        return fail(RK_ERR_ARG, "rk_deltanet_decode: B %d H %d n_linear %d slot %d", B, H, n_linear, slot);
+    if (dk != kDK || dv != kDV || conv_k != kTaps)
+        return fail(RK_ERR_UNSUPPORTED, "rk_deltanet_decode: dk %d dv %d conv kernel %d (built for 128/128/4)", dk, dv,
+                    conv_k);
+    StepArgs p;
+    p.out = out; p.qkv = qkv; p.z = z; p.b = b; p.a = a; p.conv = conv_state; p.S = S; p.conv_w = conv_w;
+    p.A_log = A_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.seq = seq_index;
+    p.B = B; p.H = H; p.C = 2 * H * dk + H * dv; p.n_linear = n_linear; p.slot = slot; p.eps = eps;
+    hipLaunchKernelGGL(deltanet_step_kernel, dim3(B * H), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
+    return check_launch("deltanet_step");
+}
+
+}  // extern "C"

@@ -1,0 +1,161 @@
+"""Tensor-level wrappers of the C ABI: argument checks, dtype codes, output / workspace allocation, current stream.
+
+PyTorch is used here only for device memory and the stream: every computation is a HIP kernel of librk_path.so.
+Checks mirror the reference's host-side refusals (MetalBackend._kv_kernel raises TypeError for a KV dtype it has no
+kernel for, src/backend/metal.py:189-195) and turn shape mistakes into ValueError before anything is launched.
+"""
+import torch
+
+from native.rocm_native import RK_BF16, RK_F32, load
+
+DTYPE_CODES = {torch.float32: RK_F32, torch.bfloat16: RK_BF16}
+KV_DTYPES = (torch.float32, torch.bfloat16)
+
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _need_cuda(name: str, *ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    for t in ts:
+        if t.device.type != "cuda":
+            raise ValueError(f"{name}: tensors must be on a ROCm device, got {t.device}")
+        if t.device != dev:
+            raise ValueError(f"{name}: tensors on different devices ({dev}, {t.device})")
+    return dev
+
+
+def _contig(name: str, t: torch.Tensor, arg: str) -> torch.Tensor:
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: {arg} must be contiguous")
+    return t
+
+
+def workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """A device scratch buffer of at least nbytes, reused across calls on the device (calls are stream-ordered)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _workspaces.get(idx)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _workspaces[idx] = buf
+    return buf
+
+
+def paged_decode(q, k_pool, v_pool, tables, lens, block_size: int, window: int | None = None, gate=None,
+                 out=None, phase: int | None = None) -> torch.Tensor:
+    """Batched decode attention over one layer of a paged pool (rk_paged_decode). q [B, Hq, d] -> [B, Hq, d] fp32.
+    k_pool / v_pool [num_blocks, block_size, Hkv, d] fp32 or bf16; tables [B, max_nb] int32; lens [B] int32;
+    gate None or [B, Hq * d] (out *= sigmoid(gate)). phase 0 / 1 runs one of the two launches (for timing)."""
+    name = "paged_attention"
+    if k_pool.dtype != v_pool.dtype or k_pool.dtype not in KV_DTYPES:
+        raise TypeError(f"{name}: keys and values must both be float32 or bfloat16, not {k_pool.dtype} / {v_pool.dtype}")
+    if q.dim() != 3 or k_pool.dim() != 4 or k_pool.shape != v_pool.shape:
+        raise ValueError(f"{name}: q {tuple(q.shape)}, pools {tuple(k_pool.shape)} / {tuple(v_pool.shape)}")
+    B, Hq, d = q.shape
+    NB, bs, Hkv, dp = k_pool.shape
+    if dp != d or bs != block_size:
+        raise ValueError(f"{name}: pool [{NB}, {bs}, {Hkv}, {dp}] vs head_dim {d}, block_size {block_size}")
+    if tables.dim() != 2 or tables.shape[0] != B or lens.shape != (B,):
+        raise ValueError(f"{name}: tables {tuple(tables.shape)} / lens {tuple(lens.shape)} for batch {B}")
+    if tables.dtype != torch.int32 or lens.dtype != torch.int32:
+        raise TypeError(f"{name}: tables and lens must be int32, not {tables.dtype} / {lens.dtype}")
+    dev = _need_cuda(name, q, k_pool, v_pool, tables, lens)
+    _contig(name, k_pool, "k_pool"); _contig(name, v_pool, "v_pool")
+    _contig(name, tables, "tables"); _contig(name, lens, "lens")
+    q = q.to(torch.float32).contiguous()
+    if gate is not None:
+        gate = gate.to(torch.float32).contiguous()
+        if gate.numel() != B * Hq * d:
+            raise ValueError(f"{name}: gate has {gate.numel()} elements, expected {B * Hq * d}")
+        _need_cuda(name, q, gate)
+    if out is None:
+        out = torch.empty(B, Hq, d, dtype=torch.float32, device=dev)
+    lib = load()
+    max_nb = tables.shape[1]
+    need = lib.lib.rk_paged_decode_workspace_bytes(B, Hq, Hkv, d, bs, max_nb)
+    ws = workspace(dev, need)
+    args = (out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype],
+            tables.data_ptr(), lens.data_ptr(), B, Hq, Hkv, d, bs, max_nb, NB, int(window or 0),
+            gate.data_ptr() if gate is not None else None, ws.data_ptr(), ws.numel(), _stream(dev))
+    if phase is None:
+        lib.call("rk_paged_decode", *args)
+    else:
+        lib.call("rk_paged_decode_phase", int(phase), *args)
+    return out
+
+
+def kv_write(k_pool, v_pool, slots, k, v) -> None:
+    """pool[slots // bs, slots % bs] = k / v for a [num_blocks, bs, Hkv, d] pool layer (rk_kv_write). slots int64."""
+    name = "kv_write"
+    n = slots.numel()
+    if n == 0:
+        return
+    if k_pool.dtype not in KV_DTYPES or v_pool.dtype != k_pool.dtype:
+        raise TypeError(f"{name}: pool dtype {k_pool.dtype} / {v_pool.dtype}")
+    NB, bs, Hkv, d = k_pool.shape
+    k = k.reshape(n, Hkv, d)
+    v = v.reshape(n, Hkv, d)
+    if k.dtype not in KV_DTYPES:
+        k = k.float()
+    if v.dtype != k.dtype:
+        v = v.to(k.dtype)
+    k, v = k.contiguous(), v.contiguous()
+    slots = slots.to(device=k_pool.device, dtype=torch.int64).contiguous()
+    dev = _need_cuda(name, k_pool, v_pool, slots, k, v)
+    _contig(name, k_pool, "k_pool"); _contig(name, v_pool, "v_pool")
+    load().call("rk_kv_write", k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype], slots.data_ptr(),
+                k.data_ptr(), v.data_ptr(), DTYPE_CODES[k.dtype], n, Hkv, d, bs, NB, _stream(dev))
+
+
+def kv_gather(k_pool, v_pool, table, lo: int, end: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Positions lo .. end-1 of one sequence, gathered through its block table (int32 device tensor)."""
+    name = "kv_gather"
+    NB, bs, Hkv, d = k_pool.shape
+    dev = _need_cuda(name, k_pool, v_pool, table)
+    table = table.to(torch.int32).contiguous()
+    ko = torch.empty(end - lo, Hkv, d, dtype=k_pool.dtype, device=dev)
+    vo = torch.empty(end - lo, Hkv, d, dtype=v_pool.dtype, device=dev)
+    if end > lo:
+        load().call("rk_kv_gather", ko.data_ptr(), vo.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                    DTYPE_CODES[k_pool.dtype], table.data_ptr(), table.numel(), lo, end, Hkv, d, bs, NB,
+                    _stream(dev))
+    return ko, vo
+
+
+def deltanet_decode(qkv, z, b, a, conv_state, S, seq_index, slot: int, conv_w, A_log, dt_bias, norm_w,
+                    eps: float, dims) -> torch.Tensor:
+    """One fused Gated DeltaNet decode step for B sequences (rk_deltanet_decode) -> [B, H * dv] fp32.
+    conv_state [seqs, n_linear, K-1, C] and S [seqs, n_linear, H, dk, dv] (fp32, contiguous) are updated in place at
+    [seq_index[i], slot]."""
+    name = "deltanet_decode"
+    H, dk, dv, key_dim = dims
+    if key_dim != H * dk:
+        raise ValueError(f"{name}: key_dim {key_dim} != H * dk = {H * dk}")
+    B, C = qkv.shape
+    if C != 2 * key_dim + H * dv:
+        raise ValueError(f"{name}: qkv has {C} channels, expected {2 * key_dim + H * dv}")
+    if S.dtype != torch.float32 or conv_state.dtype != torch.float32:
+        raise TypeError(f"{name}: state must be float32, not {S.dtype} / {conv_state.dtype}")
+    if S.dim() != 5 or S.shape[2:] != (H, dk, dv) or conv_state.dim() != 4 or conv_state.shape[3] != C:
+        raise ValueError(f"{name}: S {tuple(S.shape)}, conv {tuple(conv_state.shape)}")
+    n_linear = S.shape[1]
+    K = conv_w.shape[1]
+    if conv_state.shape[1] != n_linear or conv_state.shape[2] != K - 1:
+        raise ValueError(f"{name}: conv state {tuple(conv_state.shape)} vs {n_linear} layers, kernel {K}")
+    if not 0 <= slot < n_linear:
+        raise ValueError(f"{name}: slot {slot} outside [0, {n_linear})")
+    dev = _need_cuda(name, qkv, S, conv_state)
+    _contig(name, S, "S"); _contig(name, conv_state, "conv_state")
+    f = lambda t: t.to(device=dev, dtype=torch.float32).contiguous()
+    qkv, z, b, a = f(qkv), f(z), f(b), f(a)
+    conv_w, A_log, dt_bias, norm_w = f(conv_w), f(A_log), f(dt_bias), f(norm_w)
+    seq_index = seq_index.to(device=dev, dtype=torch.int32).contiguous()
+    out = torch.empty(B, H * dv, dtype=torch.float32, device=dev)
+    load().call("rk_deltanet_decode", out.data_ptr(), qkv.data_ptr(), z.data_ptr(), b.data_ptr(), a.data_ptr(),
+                conv_state.data_ptr(), S.data_ptr(), conv_w.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(),
+                norm_w.data_ptr(), seq_index.data_ptr(), B, H, dk, dv, K, n_linear, int(slot), float(eps),
+                _stream(dev))
+    return out

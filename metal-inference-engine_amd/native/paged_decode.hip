@@ -1,0 +1,622 @@
+// P1: paged GQA decode attention over a block-table KV pool, gfx950.
+//
+// Semantics (reference): TorchBackend.paged_attention gathers each sequence's positions through its block table and
+// runs ops.attention with one query (src/backend/torch_ref.py:75-88, src/ops.py:65-104); the Metal kernel it
+// replaces is paged_attention_decode<T> (src/kernels/attention.metal:87-159). Pool row of position s of sequence i:
+// ((tables[i][s / bs] * bs + s % bs) * Hkv + kvh) * D (attention.metal:115).
+//
+// Design (one wavefront per workgroup, "stream-K" split):
+//   * Work unit = one 16-position tile of one (sequence, kv-head) pair. Units are numbered pair-major, and the NW
+//     waves of the grid take equal contiguous unit ranges, so every wave streams the same number of KV bytes no
+//     matter how unequal the sequence lengths are. A wave whose range crosses pairs writes one partial per pair.
+//   * Each wave serves all G = Hq/Hkv query heads of its kv-head, so every K/V byte is read from HBM once.
+//   * QK^T on MFMA (v_mfma_f32_16x16x32_bf16): A = the G query rows split exactly into three bf16 parts
+//     (q = hi + mid + lo), B = 16 keys x 32 dims. bf16 keys are exact MFMA operands; fp32 keys are split the same
+//     way (three MFMA passes), so both pool types get fp32-accurate scores, and a bf16 pool gives bit-for-bit the
+//     result of the fp32 pool holding the widened values (the extra passes only add exact zeros).
+//   * Online softmax in base 2 (scores pre-scaled by log2(e)/sqrt(D)); row max by DPP inside 16-lane rows.
+//   * PV on the VALU in fp32: each lane owns 8 consecutive dims of one position row (coalesced 16/32-byte loads);
+//     probabilities are broadcast through LDS.
+//   * Merge kernel: one workgroup per pair combines its partials (m, l, acc) in wave order, divides, applies the
+//     optional sigmoid gate and writes [B, Hq, D].
+// Bounds: lens are clamped to max_nb * bs and table entries to [0, num_blocks), so a malformed table cannot make a
+// load leave the pool. Positions outside [s0, len) are never used: their scores are replaced (not added) by -inf and
+// their V values by 0 before the FMA, so a NaN-poisoned block outside the window cannot leak in.
+#include "rk_device.h"
+#include "rk_internal.h"
+
+namespace rk {
+namespace {
+
+constexpr int kMaxBatch = 1024;
+constexpr int kTile = 16;
+
+struct DecodeArgs {
+    float* part;
+    float* out;
+    const float* q;
+    const void* kp;
+    const void* vp;
+    const int32_t* tables;
+    const int32_t* lens;
+    const float* gate;
+    int B, Hq, Hkv, G, bs, max_nb, num_blocks, window, NW;
+    float qscale;   // log2(e) / sqrt(D)
+};
+
+struct SeqRange {
+    int L, s0, t0, units;   // clamped length, first visible position, first tile, tile count
+};
+
+__device__ __forceinline__ SeqRange seq_range(const DecodeArgs& a, int b) {
+    SeqRange r;
+    int L = a.lens[b];
+    int cap = a.max_nb * a.bs;
+    L = L < cap ? L : cap;
+    if (L <= 0) {
+        r.L = 0; r.s0 = 0; r.t0 = 0; r.units = 0;
+        return r;
+    }
+    r.L = L;
+    r.s0 = (a.window > 0 && L > a.window) ? L - a.window : 0;
+    r.t0 = r.s0 / kTile;
+    r.units = (L + kTile - 1) / kTile - r.t0;
+    return r;
+}
+
+// Element offset of position s (already clamped to a visible position) of one sequence / kv-head.
+__device__ __forceinline__ long long kv_row(const int32_t* table, int s, int bs, int Hkv, int kvh, int D,
+                                            int num_blocks) {
+    int blk = table[s / bs];
+    blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);
+    return ((long long)(blk * (long long)bs + s % bs) * Hkv + kvh) * D;
+}
+
+// Exclusive prefix of per-sequence unit counts into cum[0..B], computed by one wave. Returns the total.
+__device__ int unit_prefix(const DecodeArgs& a, int* cum) {
+    const int lane = threadIdx.x & 63;
+    int carry = 0;
+    for (int b0 = 0; b0 < a.B; b0 += 64) {
+        int b = b0 + lane;
+        int x = b < a.B ? seq_range(a, b).units : 0;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            int y = __shfl_up(x, off);
+            if (lane >= off) x += y;
+        }
+        if (b < a.B) cum[b + 1] = carry + x;
+        carry += __shfl(x, 63);
+    }
+    if (lane == 0) cum[0] = 0;
+    return carry;
+}
+
+// wave that owns unit u: max w with floor(U * w / NW) <= u
+__device__ __forceinline__ int wave_of(long long u, long long U, int NW) {
+    return (int)(((u + 1) * (long long)NW - 1) / U);
+}
+
+template <typename T>
+struct KVLoad;
+
+// bf16 pool: 8 elements = one 16-byte load.
+template <>
+struct KVLoad<uint16_t> {
+    static constexpr int KS = 1;   // key splits
+    struct Vec { u32x4 w; };
+    __device__ static Vec load(const void* base, long long off) {
+        Vec v;
+        v.w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
+        return v;
+    }
+    __device__ static void key_operands(const Vec& v, u32x4* ops) { ops[0] = v.w; }
+    __device__ static void widen(const Vec& v, float* f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[2 * j] = bf16_lo(v.w[j]);
+            f[2 * j + 1] = bf16_hi(v.w[j]);
+        }
+    }
+};
+
+// fp32 pool: 8 elements = two 16-byte loads; keys are split into three exact bf16 parts.
+template <>
+struct KVLoad<float> {
+    static constexpr int KS = 3;
+    struct Vec { u32x4 w0, w1; };
+    __device__ static Vec load(const void* base, long long off) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(base) + off);
+        Vec v;
+        v.w0 = p[0];
+        v.w1 = p[1];
+        return v;
+    }
+    __device__ static void key_operands(const Vec& v, u32x4* ops) {
+        Split3 s[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s[j] = split3(__uint_as_float(v.w0[j]));
+            s[4 + j] = split3(__uint_as_float(v.w1[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ops[0][j] = pack_hi2(s[2 * j].hi, s[2 * j + 1].hi);
+            ops[1][j] = pack_hi2(s[2 * j].mid, s[2 * j + 1].mid);
+            ops[2][j] = pack_hi2(s[2 * j].lo, s[2 * j + 1].lo);
+        }
+    }
+    __device__ static void widen(const Vec& v, float* f) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f[j] = __uint_as_float(v.w0[j]);
+            f[4 + j] = __uint_as_float(v.w1[j]);
+        }
+    }
+};
+
+template <typename T, int D, int GP>
+__global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
+    using LD = KVLoad<T>;
+    constexpr int NIT = D / 32;              // MFMA k-steps per tile
+    constexpr int NT = (3 * GP + 15) / 16;   // A tiles: 3 query splits x GP heads, 16 rows each
+    constexpr int LPT = D / 8;               // lanes per position row in the V layout
+    constexpr int TPI = 64 / LPT;            // positions per V step
+    constexpr int NVI = kTile / TPI;         // V steps per tile
+    constexpr int KS = LD::KS;
+    constexpr int HB = GP / 4;               // head blocks of 4 in the score layout
+
+    __shared__ int cum[kMaxBatch + 1];
+    __shared__ __attribute__((aligned(16))) float p_lds[kTile * GP];
+    __shared__ __attribute__((aligned(16))) float alpha_lds[GP];
+
+    const int lane = threadIdx.x;
+    const int w = blockIdx.x;
+    const int row = lane & 15;     // MFMA row / column owned by this lane
+    const int grp = lane >> 4;     // k-slot group (operands) / row block (accumulator)
+
+    const int total = unit_prefix(a, cum);
+    __syncthreads();
+    const long long U = (long long)a.Hkv * total;
+    if (U == 0) return;
+    long long u = U * w / a.NW;
+    const long long u_end = U * (w + 1) / a.NW;
+    if (u >= u_end) return;
+
+    // locate the sequence owning unit u: largest b with Hkv * cum[b] <= u
+    int lo_b = 0, hi_b = a.B - 1;
+    while (lo_b < hi_b) {
+        int mid = (lo_b + hi_b + 1) >> 1;
+        if ((long long)a.Hkv * cum[mid] <= u) lo_b = mid; else hi_b = mid - 1;
+    }
+    int b = lo_b;
+    SeqRange sr = seq_range(a, b);
+    long long rel = u - (long long)a.Hkv * cum[b];
+    int kvh = (int)(rel / sr.units);
+    int off = (int)(rel % sr.units);
+
+    while (u < u_end) {
+        const int pair = b * a.Hkv + kvh;
+        const long long left = u_end - u;
+        const int n_here = (long long)(sr.units - off) < left ? sr.units - off : (int)left;
+        const int32_t* table = a.tables + (long long)b * a.max_nb;
+
+        // ---- query operands: rows r of A tile tt hold split (m / GP) of head (m % GP), m = 16 * tt + r
+        u32x4 qa[NT][NIT];
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            const int m = 16 * tt + row;
+            const int s = m / GP, h = m % GP;
+            const bool valid = s < 3 && h < a.G;
+            const float* qh = a.q + ((long long)b * a.Hq + kvh * a.G + (valid ? h : 0)) * D;
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int d = 32 * it + 8 * grp;
+                uint32_t bits[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    Split3 sp = split3(valid ? qh[d + e] * a.qscale : 0.0f);
+                    bits[e] = s == 0 ? sp.hi : (s == 1 ? sp.mid : sp.lo);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) qa[tt][it][j] = pack_hi2(bits[2 * j], bits[2 * j + 1]);
+            }
+        }
+
+        float m_run[4], l_run[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.0f; }
+        float acc[GP][8];
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+
+        for (int ti = 0; ti < n_here; ++ti) {
+            const int tbase = (sr.t0 + off + ti) * kTile;
+            const bool partial = tbase < sr.s0 || tbase + kTile > sr.L;
+
+            // ---- issue K and V loads for this tile
+            const int tk = tbase + row;
+            const bool kvalid = tk >= sr.s0 && tk < sr.L;
+            const int tkc = tk < sr.s0 ? sr.s0 : (tk >= sr.L ? sr.L - 1 : tk);
+            const long long krow = kv_row(table, tkc, a.bs, a.Hkv, kvh, D, a.num_blocks);
+            typename LD::Vec kv[NIT];
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, krow + 32 * it + 8 * grp);
+
+            typename LD::Vec vv[NVI];
+            bool vvalid[NVI];
+#pragma unroll
+            for (int vi = 0; vi < NVI; ++vi) {
+                const int tv = tbase + vi * TPI + lane / LPT;
+                vvalid[vi] = tv >= sr.s0 && tv < sr.L;
+                const int tvc = tv < sr.s0 ? sr.s0 : (tv >= sr.L ? sr.L - 1 : tv);
+                vv[vi] = LD::load(a.vp, kv_row(table, tvc, a.bs, a.Hkv, kvh, D, a.num_blocks) + (lane % LPT) * 8);
+            }
+
+            // ---- scores: D[m][n] = sum_d A[m][d] * K[n][d]
+            f32x4 sacc[NT];
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) sacc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                u32x4 kb[KS];
+                LD::key_operands(kv[it], kb);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int tt = 0; tt < NT; ++tt) sacc[tt] = mfma16x16x32(qa[tt][it], kb[ks], sacc[tt]);
+            }
+            // sum the three query splits: afterwards lane (grp, row) holds heads 4*(grp % HB) + i of position row
+            float sc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float x = sacc[0][i];
+#pragma unroll
+                for (int tt = 1; tt < NT; ++tt) x += sacc[tt][i];
+                if (GP == 4) x += __shfl_xor(x, 16);
+                x += __shfl_xor(x, 32);
+                sc[i] = kvalid ? x : -INFINITY;
+            }
+
+            // ---- online softmax (base 2) per head, over the 16 positions of this row
+            float pr[4], al[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float mt = row16_max(sc[i]);
+                const float mn = fmaxf(m_run[i], mt);
+                al[i] = fast_exp2(m_run[i] - mn);
+                pr[i] = fast_exp2(sc[i] - mn);
+                l_run[i] = l_run[i] * al[i] + pr[i];
+                m_run[i] = mn;
+            }
+            if (grp < HB) {
+                *reinterpret_cast<float4*>(&p_lds[row * GP + 4 * grp]) = make_float4(pr[0], pr[1], pr[2], pr[3]);
+                if (row == 0)
+                    *reinterpret_cast<float4*>(&alpha_lds[4 * grp]) = make_float4(al[0], al[1], al[2], al[3]);
+            }
+            __syncthreads();
+
+            // ---- acc = acc * alpha + P V
+            float alh[GP];
+#pragma unroll
+            for (int h4 = 0; h4 < GP / 4; ++h4) {
+                float4 t = *reinterpret_cast<const float4*>(&alpha_lds[4 * h4]);
+                alh[4 * h4] = t.x; alh[4 * h4 + 1] = t.y; alh[4 * h4 + 2] = t.z; alh[4 * h4 + 3] = t.w;
+            }
+#pragma unroll
+            for (int h = 0; h < GP; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] *= alh[h];
+#pragma unroll
+            for (int vi = 0; vi < NVI; ++vi) {
+                float vf[8];
+                LD::widen(vv[vi], vf);
+                if (partial && !vvalid[vi]) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) vf[e] = 0.0f;
+                }
+                const int pos = vi * TPI + lane / LPT;
+                float ph[GP];
+#pragma unroll
+                for (int h4 = 0; h4 < GP / 4; ++h4) {
+                    float4 t = *reinterpret_cast<const float4*>(&p_lds[pos * GP + 4 * h4]);
+                    ph[4 * h4] = t.x; ph[4 * h4 + 1] = t.y; ph[4 * h4 + 2] = t.z; ph[4 * h4 + 3] = t.w;
+                }
+#pragma unroll
+                for (int h = 0; h < GP; ++h)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(ph[h], vf[e], acc[h][e]);
+            }
+            __syncthreads();   // p_lds / alpha_lds are rewritten by the next tile
+        }
+
+        // ---- flush the partial of (wave w, pair): acc [GP][D], then m [GP], l [GP]
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float x = acc[h][e];
+                if (TPI >= 8) x += dpp_f32<0x128>(x);   // lanes l and l ^ 8 share dims when a row is 8 lanes
+                if (TPI >= 4) x += __shfl_xor(x, 16);
+                x += __shfl_xor(x, 32);
+                acc[h][e] = x;
+            }
+        float* slot = a.part + (long long)(w + pair) * (GP * (D + 2));
+        if (lane < LPT) {
+#pragma unroll
+            for (int h = 0; h < GP; ++h) {
+                float4* dst = reinterpret_cast<float4*>(slot + h * D + lane * 8);
+                dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+                dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+            }
+        }
+        float lsum[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lsum[i] = row16_sum(l_run[i]);
+        if (grp < HB && row == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                slot[GP * D + 4 * grp + i] = m_run[i];
+                slot[GP * D + GP + 4 * grp + i] = lsum[i];
+            }
+        }
+
+        // ---- next pair
+        u += n_here;
+        off = 0;
+        if (++kvh == a.Hkv) {
+            kvh = 0;
+            do {
+                ++b;
+            } while (b < a.B && seq_range(a, b).units == 0);
+            if (b >= a.B) break;
+            sr = seq_range(a, b);
+        }
+    }
+}
+
+// One workgroup per (sequence, kv-head) pair. The pair's units were covered by the contiguous wave ranges
+// [wa, wb]; waves whose range is empty (more waves than units) wrote nothing and are skipped. Partials are combined
+// in wave order: M = max_w m_w, scale_w = 2^(m_w - M), out = sum_w scale_w acc_w / sum_w scale_w l_w.
+template <int D, int GP>
+__global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
+    constexpr int kT = 256;
+    constexpr int NO = (GP * D + kT - 1) / kT;      // outputs per thread (upper bound)
+    __shared__ int ired[2][kT];
+    __shared__ float fred[kT][GP];
+    __shared__ float scale[kT][GP];
+    __shared__ int live[kT];
+    __shared__ float Mh[GP], Dh[GP];
+    const int tid = threadIdx.x;
+    const int pair = blockIdx.x;
+    const int b = pair / a.Hkv, kvh = pair % a.Hkv;
+
+    // units before sequence b and in total
+    int below = 0, all = 0;
+    for (int j = tid; j < a.B; j += kT) {
+        const int n = seq_range(a, j).units;
+        all += n;
+        if (j < b) below += n;
+    }
+    ired[0][tid] = below;
+    ired[1][tid] = all;
+    __syncthreads();
+    for (int s = kT / 2; s > 0; s >>= 1) {
+        if (tid < s) {
+            ired[0][tid] += ired[0][tid + s];
+            ired[1][tid] += ired[1][tid + s];
+        }
+        __syncthreads();
+    }
+    below = ired[0][0];
+    all = ired[1][0];
+    const SeqRange sr = seq_range(a, b);
+    float* out = a.out + ((long long)b * a.Hq + kvh * a.G) * D;
+    if (sr.units == 0) {
+        for (int i = tid; i < a.G * D; i += kT) out[i] = 0.0f;
+        return;
+    }
+    const long long U = (long long)a.Hkv * all;
+    const long long u0 = (long long)a.Hkv * below + (long long)kvh * sr.units;
+    const int wa = wave_of(u0, U, a.NW), wb = wave_of(u0 + sr.units - 1, U, a.NW);
+    const long long stride = GP * (D + 2);
+    auto nonempty = [&](int w) { return U * w / a.NW < U * (w + 1) / a.NW; };
+
+    // pass 1: per-head max of the partial maxima
+    float mx[GP];
+#pragma unroll
+    for (int h = 0; h < GP; ++h) mx[h] = -INFINITY;
+    for (int w = wa + tid; w <= wb; w += kT) {
+        if (!nonempty(w)) continue;
+        const float* m = a.part + (w + pair) * stride + GP * D;
+#pragma unroll
+        for (int h = 0; h < GP; ++h) mx[h] = fmaxf(mx[h], m[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < GP; ++h) fred[tid][h] = mx[h];
+    __syncthreads();
+    for (int s = kT / 2; s > 0; s >>= 1) {
+        if (tid < s)
+#pragma unroll
+            for (int h = 0; h < GP; ++h) fred[tid][h] = fmaxf(fred[tid][h], fred[tid + s][h]);
+        __syncthreads();
+    }
+    if (tid < GP) Mh[tid] = fred[0][tid];
+    __syncthreads();
+
+    // pass 2: scales per chunk of 256 waves, numerators per output, denominators per head
+    float num[NO], den[GP];
+#pragma unroll
+    for (int k = 0; k < NO; ++k) num[k] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < GP; ++h) den[h] = 0.0f;
+    for (int c0 = wa; c0 <= wb; c0 += kT) {
+        const int w = c0 + tid;
+        const bool ok = w <= wb && nonempty(w);
+        live[tid] = ok;
+        if (ok) {
+            const float* m = a.part + (w + pair) * stride + GP * D;
+#pragma unroll
+            for (int h = 0; h < GP; ++h) {
+                const float sc = fast_exp2(m[h] - Mh[h]);
+                scale[tid][h] = sc;
+                den[h] = fmaf(sc, m[GP + h], den[h]);
+            }
+        }
+        __syncthreads();
+        const int n_in = min(kT, wb - c0 + 1);
+#pragma unroll
+        for (int k = 0; k < NO; ++k) {
+            const int i = tid + k * kT;
+            if (i >= a.G * D) break;
+            const int h = i / D, d = i % D;
+            for (int s = 0; s < n_in; ++s)
+                if (live[s]) num[k] = fmaf(scale[s][h], a.part[(c0 + s + pair) * stride + h * D + d], num[k]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int h = 0; h < GP; ++h) fred[tid][h] = den[h];
+    __syncthreads();
+    for (int s = kT / 2; s > 0; s >>= 1) {
+        if (tid < s)
+#pragma unroll
+            for (int h = 0; h < GP; ++h) fred[tid][h] += fred[tid + s][h];
+        __syncthreads();
+    }
+    if (tid < GP) Dh[tid] = fred[0][tid];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NO; ++k) {
+        const int i = tid + k * kT;
+        if (i >= a.G * D) break;
+        const int h = i / D, d = i % D;
+        float o = num[k] / Dh[h];
+        if (a.gate) {
+            const float gv = a.gate[(long long)b * a.Hq * D + (long long)(kvh * a.G + h) * D + d];
+            o = o * (1.0f / (1.0f + expf(-gv)));
+        }
+        out[i] = o;
+    }
+}
+
+typedef void (*SplitFn)(DecodeArgs);
+typedef void (*MergeFn)(DecodeArgs);
+
+template <typename T>
+SplitFn pick_split(int D, int GP) {
+    if (GP == 4) {
+        if (D == 64) return paged_decode_split<T, 64, 4>;
+        if (D == 128) return paged_decode_split<T, 128, 4>;
+        if (D == 256) return paged_decode_split<T, 256, 4>;
+    } else {
+        if (D == 64) return paged_decode_split<T, 64, 8>;
+        if (D == 128) return paged_decode_split<T, 128, 8>;
+        if (D == 256) return paged_decode_split<T, 256, 8>;
+    }
+    return nullptr;
+}
+
+MergeFn pick_merge(int D, int GP) {
+    if (GP == 4) {
+        if (D == 64) return paged_decode_merge<64, 4>;
+        if (D == 128) return paged_decode_merge<128, 4>;
+        if (D == 256) return paged_decode_merge<256, 4>;
+    } else {
+        if (D == 64) return paged_decode_merge<64, 8>;
+        if (D == 128) return paged_decode_merge<128, 8>;
+        if (D == 256) return paged_decode_merge<256, 8>;
+    }
+    return nullptr;
+}
+
+// Number of waves for the split phase: the unit count's upper bound, capped at 8 waves per compute unit.
+int split_waves(int B, int Hkv, int block_size, int max_nb) {
+    const long long upper = (long long)B * Hkv * (((long long)max_nb * block_size + kTile - 1) / kTile);
+    int cus = device_cus();
+    if (cus <= 0) cus = 256;
+    const long long cap = (long long)cus * 8;
+    long long nw = upper < cap ? upper : cap;
+    return (int)(nw < 1 ? 1 : nw);
+}
+
+size_t workspace_bytes(int B, int Hkv, int D, int GP, int NW) {
+    return (size_t)(NW + (size_t)B * Hkv) * GP * (D + 2) * sizeof(float);
+}
+
+int validate(const float* out, const float* q, const void* kp, const void* vp, int kv_dtype, const int32_t* tables,
+             const int32_t* lens, int B, int Hq, int Hkv, int D, int bs, int max_nb, int num_blocks, int window) {
+    if (!out || !q || !kp || !vp || !tables || !lens) return fail(RK_ERR_ARG, "rk_paged_decode: null pointer");
+    if (B < 1 || B > kMaxBatch) return fail(RK_ERR_ARG, "rk_paged_decode: batch %d outside [1, %d]", B, kMaxBatch);
+    if (Hkv < 1 || Hq < Hkv || Hq % Hkv) return fail(RK_ERR_ARG, "rk_paged_decode: %d query heads over %d kv heads", Hq, Hkv);
+    if (Hq / Hkv > 8) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: group size %d > 8", Hq / Hkv);
+    if (D != 64 && D != 128 && D != 256) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: head_dim %d not in {64,128,256}", D);
+    if (bs < 1 || max_nb < 1 || num_blocks < 1) return fail(RK_ERR_ARG, "rk_paged_decode: block_size %d, max_nb %d, num_blocks %d", bs, max_nb, num_blocks);
+    if (window < 0) return fail(RK_ERR_ARG, "rk_paged_decode: window %d < 0", window);
+    if (kv_dtype != RK_F32 && kv_dtype != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: kv dtype %d", kv_dtype);
+    return RK_OK;
+}
+
+}  // namespace
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" {
+
+size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_size, int max_nb) {
+    if (B < 1 || Hkv < 1 || Hq < Hkv || block_size < 1 || max_nb < 1) return 0;
+    const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
+    return workspace_bytes(B, Hkv, D, GP, split_waves(B, Hkv, block_size, max_nb));
+}
+
+int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
+                          int kv_dtype, const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D,
+                          int block_size, int max_nb, int num_blocks, int window, const float* gate,
+                          void* workspace, size_t workspace_bytes_, void* stream) {
+    int rc = validate(out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                      num_blocks, window);
+    if (rc) return rc;
+    if (phase != 0 && phase != 1) return fail(RK_ERR_ARG, "rk_paged_decode_phase: phase %d", phase);
+    const int G = Hq / Hkv;
+    const int GP = G <= 4 ? 4 : 8;
+    const int NW = split_waves(B, Hkv, block_size, max_nb);
+    const size_t need = workspace_bytes(B, Hkv, D, GP, NW);
+    if (!workspace || workspace_bytes_ < need)
+        return fail(RK_ERR_WORKSPACE, "rk_paged_decode: workspace %zu bytes < %zu needed", workspace_bytes_, need);
+
+    DecodeArgs a;
+    a.part = static_cast<float*>(workspace);
+    a.out = out;
+    a.q = q;
+    a.kp = k_pool;
+    a.vp = v_pool;
+    a.tables = tables;
+    a.lens = lens;
+    a.gate = gate;
+    a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = G; a.bs = block_size; a.max_nb = max_nb;
+    a.num_blocks = num_blocks; a.window = window; a.NW = NW;
+    a.qscale = kLog2e / sqrtf((float)D);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (phase == 0) {
+        SplitFn fn = kv_dtype == RK_BF16 ? pick_split<uint16_t>(D, GP) : pick_split<float>(D, GP);
+        hipLaunchKernelGGL(fn, dim3(NW), dim3(64), 0, s, a);
+        return check_launch("paged_decode_split");
+    }
+    hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(256), 0, s, a);
+    return check_launch("paged_decode_merge");
+}
+
+int rk_paged_decode(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                    const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
+                    int max_nb, int num_blocks, int window, const float* gate, void* workspace,
+                    size_t workspace_bytes_, void* stream) {
+    int rc = rk_paged_decode_phase(0, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size,
+                                   max_nb, num_blocks, window, gate, workspace, workspace_bytes_, stream);
+    if (rc) return rc;
+    return rk_paged_decode_phase(1, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size,
+                                 max_nb, num_blocks, window, gate, workspace, workspace_bytes_, stream);
+}
+
+}  // extern "C"

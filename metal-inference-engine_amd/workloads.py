@@ -1,0 +1,162 @@
+"""Seeded synthetic inputs for the five benchmark configurations of the token-mixing path.
+
+Every tensor is drawn on the CPU from a torch.Generator seeded per configuration, so the HIP kernels (after a copy
+to the GPU) and the CPU reference see identical bits. Model shapes are Qwen3.5-0.8B/2B's: attention 8 query / 2 kv
+heads x 256, DeltaNet 16 heads x 128 x 128, conv kernel 4 over 6144 channels, KV blocks of 16 positions.
+"""
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+HQ, HKV, HEAD_DIM, BLOCK = 8, 2, 256, 16
+DN_HEADS, DN_DK, DN_DV, CONV_K = 16, 128, 128, 4
+KEY_DIM = DN_HEADS * DN_DK
+CONV_DIM = 2 * KEY_DIM + DN_HEADS * DN_DV
+
+
+@dataclass
+class PagedDecodeCase:
+    """One layer of a paged pool plus a decode batch: q [B, Hq, d] fp32, gate [B, Hq*d] fp32,
+    k_pool / v_pool [NB, bs, Hkv, d], tables [B, max_nb] int32 (0-padded), lens [B] int32."""
+    q: torch.Tensor
+    gate: torch.Tensor
+    k_pool: torch.Tensor
+    v_pool: torch.Tensor
+    tables: torch.Tensor
+    lens: torch.Tensor
+    block_size: int
+    window: int | None = None
+    meta: dict = field(default_factory=dict)
+
+    def to(self, device) -> "PagedDecodeCase":
+        f = lambda t: t.to(device)
+        return PagedDecodeCase(f(self.q), f(self.gate), f(self.k_pool), f(self.v_pool), f(self.tables),
+                               f(self.lens), self.block_size, self.window, dict(self.meta))
+
+    def kv_bytes(self) -> int:
+        """Bytes of K and V one decode call must read: every visible position of every sequence, both pools."""
+        Hkv, d = self.k_pool.shape[2], self.k_pool.shape[3]
+        L = self.lens.long()
+        if self.window:
+            L = L.clamp(max=self.window)
+        return int(L.sum()) * Hkv * d * self.k_pool.element_size() * 2
+
+    def algorithmic_bytes(self) -> int:
+        """KV read once + q, gate, out (fp32) + the table entries and lens actually read."""
+        B, Hq, d = self.q.shape
+        nb = (self.lens.long() + self.block_size - 1) // self.block_size
+        return self.kv_bytes() + B * Hq * d * 4 * 3 + 4 * int(nb.sum()) + 4 * B
+
+
+def _tables_from_perm(perm: list[int], nbs: list[int]) -> torch.Tensor:
+    width = max(nbs)
+    rows, at = [], 0
+    for n in nbs:
+        rows.append(perm[at:at + n] + [0] * (width - n))
+        at += n
+    return torch.tensor(rows, dtype=torch.int32)
+
+
+def paged_decode_case(lens: list[int], num_blocks: int, Hq: int = HQ, Hkv: int = HKV, d: int = HEAD_DIM,
+                      block_size: int = BLOCK, kv_dtype=torch.float32, seed: int = 0, q_scale: float = 1.0,
+                      window: int | None = None) -> PagedDecodeCase:
+    """Sequences of the given lengths whose blocks are a seeded random, non-contiguous choice of the pool's."""
+    gen = torch.Generator().manual_seed(seed)
+    nbs = [math.ceil(n / block_size) for n in lens]
+    if sum(nbs) > num_blocks:
+        raise ValueError(f"{sum(nbs)} blocks needed, pool has {num_blocks}")
+    perm = torch.randperm(num_blocks, generator=gen).tolist()
+    tables = _tables_from_perm(perm, nbs)
+    B = len(lens)
+    q = torch.randn(B, Hq, d, generator=gen) * q_scale
+    gate = torch.randn(B, Hq * d, generator=gen)
+    k_pool = torch.randn(num_blocks, block_size, Hkv, d, generator=gen).to(kv_dtype)
+    v_pool = torch.randn(num_blocks, block_size, Hkv, d, generator=gen).to(kv_dtype)
+    return PagedDecodeCase(q, gate, k_pool, v_pool, tables, torch.tensor(lens, dtype=torch.int32), block_size,
+                           window, {"lens": list(lens), "num_blocks": num_blocks})
+
+
+def c1_paged_decode(seed: int = 1) -> PagedDecodeCase:
+    """Config 1: batch 1, fp32 pool of 256 blocks, context 512 (32 blocks, a seeded permutation), gate ~ N(0,1)."""
+    gen = torch.Generator().manual_seed(seed)
+    table = torch.randperm(256, generator=gen)[:32].to(torch.int32).view(1, 32)
+    q = torch.randn(1, HQ, HEAD_DIM, generator=gen)
+    gate = torch.randn(1, HQ * HEAD_DIM, generator=gen)
+    k_pool = torch.randn(256, BLOCK, HKV, HEAD_DIM, generator=gen)
+    v_pool = torch.randn(256, BLOCK, HKV, HEAD_DIM, generator=gen)
+    return PagedDecodeCase(q, gate, k_pool, v_pool, table, torch.tensor([512], dtype=torch.int32), BLOCK, None,
+                           {"config": "c1"})
+
+
+def c3_lens(seed: int = 3, batch: int = 64) -> list[int]:
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randint(128, 8193, (batch,), generator=gen).tolist()
+
+
+def c3_paged_decode(seed: int = 3, batch: int = 64) -> PagedDecodeCase:
+    """Config 3: batch 64, lengths U[128, 8192], bf16 pool sized to 1.25 x total positions (in blocks), each
+    sequence's blocks a slice of a seeded permutation of the pool; q, gate fp32 ~ N(0,1)."""
+    lens = c3_lens(seed, batch)
+    num_blocks = math.ceil(1.25 * sum(lens) / BLOCK)
+    case = paged_decode_case(lens, num_blocks, kv_dtype=torch.bfloat16, seed=seed + 1000)
+    case.meta["config"] = "c3"
+    return case
+
+
+@dataclass
+class DeltaNetStepCase:
+    """Inputs of one batched DeltaNet decode step. S / conv are full pool tensors
+    [max_seqs, n_linear, ...]; seq_index picks the batch's slots; slot is the layer."""
+    qkv: torch.Tensor
+    z: torch.Tensor
+    b: torch.Tensor
+    a: torch.Tensor
+    conv: torch.Tensor
+    S: torch.Tensor
+    seq_index: torch.Tensor
+    slot: int
+    conv_w: torch.Tensor
+    A_log: torch.Tensor
+    dt_bias: torch.Tensor
+    norm_w: torch.Tensor
+    eps: float
+    dims: tuple
+
+    def to(self, device) -> "DeltaNetStepCase":
+        f = lambda t: t.to(device)
+        return DeltaNetStepCase(f(self.qkv), f(self.z), f(self.b), f(self.a), f(self.conv), f(self.S),
+                                f(self.seq_index), self.slot, f(self.conv_w), f(self.A_log), f(self.dt_bias),
+                                f(self.norm_w), self.eps, self.dims)
+
+    def algorithmic_bytes(self) -> int:
+        B = self.qkv.shape[0]
+        H, dk, dv, _ = self.dims
+        C = self.qkv.shape[1]
+        K = self.conv_w.shape[1]
+        state = 2 * B * H * dk * dv * 4
+        tail = 2 * B * (K - 1) * C * 4
+        io = B * C * 4 + self.conv_w.numel() * 4 + 2 * B * H * dv * 4
+        small = (2 * B * H + 2 * H + dv + B) * 4
+        return state + tail + io + small
+
+
+def c2_deltanet_step(seed: int = 2, batch: int = 8, max_seqs: int | None = None, n_linear: int = 1,
+                     slot: int = 0, A_log_zero: bool = True) -> DeltaNetStepCase:
+    """Config 2: batch 8, 16 heads, 128 x 128 fp32 state S ~ N(0, 0.02^2), conv tail ~ N(0,1), conv_w = 0.5 N,
+    z, b, a ~ N(0,1), A_log = dt_bias = 0 (so beta = sigmoid(N), log-decay = -softplus(N)), norm_w = 1 + 0.1 N,
+    eps 1e-6. max_seqs > batch gives a larger pool whose slots the batch occupies at seeded positions."""
+    gen = torch.Generator().manual_seed(seed)
+    max_seqs = max_seqs or batch
+    r = lambda *s, scale=1.0: torch.randn(*s, generator=gen) * scale
+    S = r(max_seqs, n_linear, DN_HEADS, DN_DK, DN_DV, scale=0.02)
+    conv = r(max_seqs, n_linear, CONV_K - 1, CONV_DIM)
+    seq_index = torch.randperm(max_seqs, generator=gen)[:batch].to(torch.int32)
+    qkv, z = r(batch, CONV_DIM), r(batch, DN_HEADS * DN_DV)
+    b, a = r(batch, DN_HEADS), r(batch, DN_HEADS)
+    conv_w = r(CONV_DIM, CONV_K, scale=0.5)
+    A_log = torch.zeros(DN_HEADS) if A_log_zero else r(DN_HEADS)
+    dt_bias = torch.zeros(DN_HEADS) if A_log_zero else r(DN_HEADS)
+    norm_w = 1.0 + r(DN_DV, scale=0.1)
+    return DeltaNetStepCase(qkv, z, b, a, conv, S, seq_index, slot, conv_w, A_log, dt_bias, norm_w, 1e-6,
+                            (DN_HEADS, DN_DK, DN_DV, KEY_DIM))

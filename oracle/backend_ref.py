@@ -1,0 +1,61 @@
+"""fp32 CPU restatement of TorchBackend's token-mixing methods (src/backend/torch_ref.py). TEST INFRASTRUCTURE ONLY.
+
+States are duck-typed: anything with `S` [n_linear, H, dk, dv] and `conv_tail` [n_linear, K-1, C] tensors (a
+HybridState view of a pool slot, or a plain holder), updated in place at [slot] as the reference does.
+"""
+import torch
+
+from oracle import ops_ref
+
+
+def gated_delta(q, k, v, beta, g, S):
+    """Recurrent form for one token, chunked form otherwise (torch_ref.py:52-56)."""
+    if q.shape[0] == 1:
+        return ops_ref.gated_delta_recurrent(q, k, v, beta, g, S)
+    return ops_ref.gated_delta_chunked(q, k, v, beta, g, S)
+
+
+def deltanet_decode(qkv, z, b, a, state, slot, conv_w, A_log, dt_bias, norm_w, eps, dims):
+    """One token of one DeltaNet layer, torch_ref.py:61-73. Returns [1, H * dv]; updates state.conv_tail[slot] and
+    state.S[slot] in place."""
+    H, dk, dv, key_dim = dims
+    u, state.conv_tail[slot] = ops_ref.causal_conv1d(qkv.float(), state.conv_tail[slot], conv_w)
+    q = ops_ref.l2norm(u[:, :key_dim].reshape(1, H, dk).float()) * (1.0 / dk ** 0.5)
+    k = ops_ref.l2norm(u[:, key_dim:2 * key_dim].reshape(1, H, dk).float())
+    v = u[:, 2 * key_dim:].reshape(1, H, dv).float()
+    beta = torch.sigmoid(b.float())
+    ab = a.float() + dt_bias
+    g = -torch.exp(A_log) * torch.where(ab > 20, ab, torch.log1p(torch.exp(ab)))
+    o, state.S[slot] = gated_delta(q, k, v, beta, g, state.S[slot])
+    return ops_ref.rms_norm_gated(o.reshape(H, dv), z.reshape(H, dv), norm_w, eps).reshape(1, H * dv)
+
+
+def deltanet_decode_batch(qkv, z, b, a, states, slot, conv_w, A_log, dt_bias, norm_w, eps, dims):
+    """One sequence at a time (torch_ref.py:90-93) -> [B, H * dv]."""
+    return torch.cat([deltanet_decode(qkv[i:i + 1], z[i:i + 1], b[i:i + 1], a[i:i + 1], st, slot, conv_w, A_log,
+                                      dt_bias, norm_w, eps, dims) for i, st in enumerate(states)])
+
+
+def paged_gather(k_pool, v_pool, table_row, n: int, block_size: int, window: int | None = None):
+    """The positions a decode query reads, gathered through one block-table row (torch_ref.py:81-86)."""
+    nb = -(-n // block_size)
+    s0 = max(0, n - window) if window else 0
+    b0 = s0 // block_size
+    rows = slice(s0 - b0 * block_size, n - b0 * block_size)
+    idx = table_row[b0:nb].long()
+    return k_pool[idx].flatten(0, 1)[rows], v_pool[idx].flatten(0, 1)[rows]
+
+
+def paged_attention(q, k_pool, v_pool, tables, lens, block_size, window=None):
+    """Gather each sequence, then ordinary attention with its one query (torch_ref.py:75-88) -> [B, Hq, d]."""
+    outs = []
+    for i in range(q.shape[0]):
+        K, V = paged_gather(k_pool, v_pool, tables[i], int(lens[i]), block_size, window)
+        outs.append(ops_ref.attention(q[i:i + 1], K, V, causal=True, window=window))
+    return torch.cat(outs)
+
+
+def gate(o: torch.Tensor, gate_logits: torch.Tensor) -> torch.Tensor:
+    """The attention output gate before o_proj: o.reshape(N, Hq*d) * sigmoid(gate) (src/models/qwen3_5.py:271)."""
+    N = o.shape[0]
+    return (o.reshape(N, -1) * torch.sigmoid(gate_logits.float())).reshape(o.shape)

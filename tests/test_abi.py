@@ -1,0 +1,106 @@
+"""The C ABI (include/rk_path.h) without a GPU: the library loads, exports every declared function, the ctypes
+signatures agree with the header's parameter lists, and argument errors come back as status codes with a message
+(validation happens before any HIP call, so these run on any machine)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from native import rocm_native
+from native.rocm_native import SIGNATURES, NativeRocm
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "rk_path.h"
+
+
+def declarations() -> dict[str, list[str]]:
+    """name -> list of parameter declarations, for every function prototype in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^[\w\s\*]*?\b(rk_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        params = [p.strip() for p in m.group(2).replace("\n", " ").split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = params
+    return out
+
+
+def kind(param: str) -> str:
+    if "*" in param:
+        return "char*" if param.startswith("char") else "ptr"
+    t = param.rsplit(" ", 1)[0]
+    return {"int": "int", "size_t": "size_t", "float": "float"}[t]
+
+
+CTYPE_KIND = {ctypes.c_void_p: "ptr", ctypes.c_char_p: "char*", ctypes.c_int: "int", ctypes.c_size_t: "size_t",
+              ctypes.c_float: "float"}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not rocm_native.LIB_PATH.exists():
+        pytest.fail(f"{rocm_native.LIB_PATH} is not built (run __graft_entry__.build())")
+    return NativeRocm()
+
+
+def test_header_and_binding_declare_the_same_functions():
+    assert set(declarations()) == set(SIGNATURES)
+
+
+@pytest.mark.parametrize("name", sorted(SIGNATURES))
+def test_signature_matches_header(name):
+    params = declarations()[name]
+    _, argtypes = SIGNATURES[name]
+    assert [kind(p) for p in params] == [CTYPE_KIND[a] for a in argtypes], name
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declarations():
+        assert hasattr(lib.lib, name), name
+    assert lib.lib.rk_abi_version() == rocm_native.ABI_VERSION
+
+
+def test_null_pointer_is_an_argument_error(lib):
+    rc = lib.lib.rk_paged_decode(None, None, None, None, 1, None, None, 1, 8, 2, 256, 16, 1, 1, 0, None, None, 0,
+                                 None)
+    assert rc == 1 and "null pointer" in lib.last_error()
+
+
+def test_unsupported_shapes_are_refused(lib):
+    fake = 4096                            # never dereferenced: validation fails first
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 8, 2, 96, 16, 1, 1, 0, None, fake, 1 << 20,
+                                 None)
+    assert rc == 2 and "head_dim 96" in lib.last_error()
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 7, fake, fake, 1, 8, 2, 256, 16, 1, 1, 0, None, fake, 1 << 20,
+                                 None)
+    assert rc == 2 and "dtype" in lib.last_error()
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 9, 2, 256, 16, 1, 1, 0, None, fake, 1 << 20,
+                                 None)
+    assert rc == 1
+    args = [fake] * 12 + [8, 16, 64, 64, 4, 1, 0, ctypes.c_float(1e-6), None]
+    assert lib.lib.rk_deltanet_decode(*args) == 2 and "dk 64" in lib.last_error()
+    args = [fake] * 12 + [8, 16, 128, 128, 4, 2, 2, ctypes.c_float(1e-6), None]
+    assert lib.lib.rk_deltanet_decode(*args) == 1 and "slot 2" in lib.last_error()
+
+
+def test_too_small_workspace_is_refused(lib):
+    fake = 4096
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 64, 8, 2, 256, 16, 512, 20000, 0, None, fake,
+                                 16, None)
+    assert rc == 3 and "workspace" in lib.last_error()
+
+
+def test_gather_table_bounds_checked_on_host(lib):
+    fake = 4096
+    rc = lib.lib.rk_kv_gather(fake, fake, fake, fake, 1, fake, 2, 0, 40, 2, 64, 16, 8, None)
+    assert rc == 1 and "table" in lib.last_error()
+
+
+def test_empty_work_is_a_no_op(lib):
+    assert lib.lib.rk_kv_write(None, None, 1, None, None, None, 0, 0, 2, 64, 16, 8, None) == 0
+    assert lib.lib.rk_kv_gather(None, None, None, None, 1, None, 0, 5, 5, 2, 64, 16, 8, None) == 0
+
+
+def test_workspace_size_formula(lib):
+    """(waves + B * Hkv) partial records of GP * (D + 2) floats; waves = min(units upper bound, 8 per CU)."""
+    n = lib.lib.rk_paged_decode_workspace_bytes(64, 8, 2, 256, 16, 512)
+    assert n > 0 and n % (4 * (256 + 2) * 4) == 0
+    assert lib.lib.rk_paged_decode_workspace_bytes(0, 8, 2, 256, 16, 512) == 0

@@ -1,0 +1,179 @@
+"""Pins of the CPU oracle (oracle/) — against float64 brute force, the committed golden fixtures (tests/golden/,
+written by make_golden.py from float64 definitions and from transformers' Qwen3.5 routines), library routines, and
+the invariants the reference's own tests hold. Each check is chosen so that a plausible slip (mask offset, GQA head
+mapping, missing decay, transposed operand, wrong substitution order) fails it."""
+import os
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import SlotState, rel_err
+from oracle import backend_ref, brute, ops_ref
+
+GOLD = Path(__file__).resolve().parent / "golden"
+os.environ.setdefault("HF_HUB_OFFLINE", "1")
+
+
+def t(a, dtype=torch.float32):
+    return torch.tensor(np.asarray(a), dtype=dtype)
+
+
+# ---------------------------------------------------------------- attention (ops.attention, src/ops.py:65-104)
+
+@pytest.mark.parametrize("T,S,Hq,Hkv,d,window", [(1, 1, 8, 2, 32, None), (1, 300, 8, 2, 64, None),
+                                                  (5, 5, 4, 2, 16, None), (6, 15, 4, 2, 16, None),
+                                                  (7, 40, 14, 2, 16, 9), (1, 50, 16, 4, 32, 16),
+                                                  (3, 3, 4, 1, 8, 1)])
+def test_attention_matches_float64_brute_force(T, S, Hq, Hkv, d, window):
+    g = torch.Generator().manual_seed(T * 1000 + S)
+    q, k, v = torch.randn(T, Hq, d, generator=g), torch.randn(S, Hkv, d, generator=g), torch.randn(S, Hkv, d, generator=g)
+    got = ops_ref.attention(q, k, v, causal=True, window=window)
+    want = brute.attention(q.numpy(), k.numpy(), v.numpy(), True, window)
+    assert rel_err(got, want) < 2e-6
+
+
+def test_attention_fixture():
+    f = np.load(GOLD / "prefill_attention.npz")
+    assert rel_err(ops_ref.attention(t(f["q"]), t(f["k"]), t(f["v"])), f["out_full"]) < 2e-6
+    assert rel_err(ops_ref.attention(t(f["q"]), t(f["k"]), t(f["v"]), window=4), f["out_w4"]) < 2e-6
+
+
+def test_one_key_returns_its_value():
+    q, k, v = torch.randn(1, 8, 16), torch.randn(1, 2, 16), torch.randn(1, 2, 16)
+    assert torch.equal(ops_ref.attention(q, k, v), v.repeat_interleave(4, dim=1))
+
+
+def test_large_scores_stay_finite():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 8, 64, generator=g) * 30
+    k, v = torch.randn(300, 2, 64, generator=g), torch.randn(300, 2, 64, generator=g)
+    got = ops_ref.attention(q, k, v)
+    assert torch.isfinite(got).all()
+    assert rel_err(got, brute.attention(q.numpy(), k.numpy(), v.numpy())) < 1e-5
+
+
+# ---------------------------------------------------------------- paged decode (torch_ref.py:75-88)
+
+def test_paged_decode_fixture():
+    f = np.load(GOLD / "paged_decode.npz")
+    args = (t(f["q"]), t(f["k_pool"]), t(f["v_pool"]), t(f["tables"], torch.int32), t(f["lens"], torch.int32),
+            int(f["block_size"]))
+    assert rel_err(backend_ref.paged_attention(*args), f["out_full"]) < 2e-6
+    assert rel_err(backend_ref.paged_attention(*args, window=12), f["out_w12"]) < 2e-6
+    gated = backend_ref.gate(backend_ref.paged_attention(*args), t(f["gate"]))
+    assert rel_err(gated, f["out_gated"]) < 2e-6
+
+
+@pytest.mark.parametrize("bs", [1, 4, 16])
+def test_paged_gather_is_the_address_map(bs):
+    g = torch.Generator().manual_seed(bs)
+    pool = torch.randn(40, bs, 2, 8, generator=g)
+    table = torch.randperm(40, generator=g)[:30].to(torch.int32)
+    for n, W in ((1, None), (bs * 3 + 1, None), (bs * 7, 5), (29 * bs, bs + 2)):
+        K, _ = backend_ref.paged_gather(pool, pool, table, n, bs, W)
+        s0 = max(0, n - W) if W else 0
+        want = brute.gather_positions(pool.numpy(), table.numpy(), s0, n, bs)
+        assert np.array_equal(K.numpy(), want)
+
+
+def test_paged_equals_contiguous_exactly():
+    g = torch.Generator().manual_seed(7)
+    lens, bs = [1, 7, 16, 33, 300], 16
+    nbs = [-(-n // bs) for n in lens]
+    perm = torch.randperm(32, generator=g).tolist()
+    rows, at = [], 0
+    for n in nbs:
+        rows.append(perm[at:at + n] + [0] * (max(nbs) - n))
+        at += n
+    tables = torch.tensor(rows, dtype=torch.int32)
+    kp, vp = torch.randn(32, bs, 2, 64, generator=g), torch.randn(32, bs, 2, 64, generator=g)
+    q = torch.randn(5, 8, 64, generator=g)
+    got = backend_ref.paged_attention(q, kp, vp, tables, torch.tensor(lens, dtype=torch.int32), bs)
+    for i, n in enumerate(lens):
+        K = kp[tables[i, :nbs[i]].long()].flatten(0, 1)[:n]
+        V = vp[tables[i, :nbs[i]].long()].flatten(0, 1)[:n]
+        assert torch.equal(got[i:i + 1], ops_ref.attention(q[i:i + 1], K, V))
+
+
+# ---------------------------------------------------------------- DeltaNet pieces (ops.py:115-193)
+
+def test_conv_fixture_and_library_conv1d():
+    f = np.load(GOLD / "conv.npz")
+    out, tail = ops_ref.causal_conv1d(t(f["x"]), t(f["tail"]), t(f["w"]))
+    assert rel_err(out, f["out"]) < 1e-6
+    assert np.array_equal(tail.numpy(), f["tail_new"].astype(np.float32))
+    b_out, b_tail = brute.conv_silu(f["x"], f["tail"], f["w"])
+    assert rel_err(out, b_out) < 1e-6
+
+
+def test_l2norm_is_transformers_l2norm():
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as hf
+    x = torch.randn(5, 16, 128)
+    assert torch.equal(ops_ref.l2norm(x), hf.l2norm(x, dim=-1, eps=1e-6))
+
+
+def test_rms_norm_gated_closed_form():
+    x, z, w = torch.randn(6, 128, dtype=torch.float64), torch.randn(6, 128, dtype=torch.float64), torch.randn(128)
+    want = x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6) * w.double() * z * torch.sigmoid(z)
+    assert rel_err(ops_ref.rms_norm_gated(x.float(), z.float(), w, 1e-6), want) < 1e-6
+
+
+def delta_inputs():
+    f = np.load(GOLD / "delta_rule.npz")
+    return f, [t(f[k]) for k in ("q", "k", "v", "beta", "g", "S0")]
+
+
+def test_recurrent_matches_brute_and_transformers():
+    f, (q, k, v, beta, g, S0) = delta_inputs()
+    o, S = ops_ref.gated_delta_recurrent(q, k, v, beta, g, S0)
+    assert rel_err(o, f["out_brute"]) < 1e-5 and rel_err(S, f["S_brute"]) < 1e-5
+    assert rel_err(o, f["out_hf_recurrent"]) < 1e-5 and rel_err(S, f["S_hf_recurrent"]) < 1e-5
+
+
+def test_chunked_matches_brute_and_transformers():
+    f, (q, k, v, beta, g, S0) = delta_inputs()
+    o, S = ops_ref.gated_delta_chunked(q, k, v, beta, g, S0)
+    assert rel_err(o, f["out_brute"]) < 1e-5 and rel_err(S, f["S_brute"]) < 1e-5
+    assert rel_err(o, f["out_hf_chunked"]) < 1e-5 and rel_err(S, f["S_hf_chunked"]) < 1e-5
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 130])
+def test_chunked_equals_recurrent(T):
+    g_ = torch.Generator().manual_seed(T)
+    H, dk, dv = 3, 16, 12
+    q = ops_ref.l2norm(torch.randn(T, H, dk, generator=g_)) / dk ** 0.5
+    k = ops_ref.l2norm(torch.randn(T, H, dk, generator=g_))
+    v = torch.randn(T, H, dv, generator=g_)
+    beta = torch.sigmoid(torch.randn(T, H, generator=g_))
+    g = -torch.nn.functional.softplus(torch.randn(T, H, generator=g_))
+    S0 = torch.randn(H, dk, dv, generator=g_) * 0.1
+    o_r, S_r = ops_ref.gated_delta_recurrent(q, k, v, beta, g, S0)
+    o_c, S_c = ops_ref.gated_delta_chunked(q, k, v, beta, g, S0)
+    assert rel_err(o_c, o_r) < 1e-5 and rel_err(S_c, S_r) < 1e-5
+
+
+def test_zero_beta_and_decay_leave_state_unchanged():
+    T, H, dk, dv = 70, 2, 8, 8
+    S0 = torch.randn(H, dk, dv)
+    o, S = ops_ref.gated_delta_chunked(torch.randn(T, H, dk), torch.randn(T, H, dk), torch.randn(T, H, dv),
+                                       torch.zeros(T, H), torch.zeros(T, H), S0)
+    assert torch.allclose(S, S0, rtol=0, atol=1e-6)
+
+
+def test_deltanet_step_fixture():
+    f = np.load(GOLD / "deltanet_step.npz")
+    H, dk, dv, key_dim = (int(x) for x in f["dims"])
+    st = SlotState(t(f["S"])[None].clone(), t(f["tail"])[None].clone())
+    out = backend_ref.deltanet_decode(t(f["qkv"]), t(f["z"]), t(f["b"]), t(f["a"]), st, 0, t(f["conv_w"]),
+                                      t(f["A_log"]), t(f["dt_bias"]), t(f["norm_w"]), 1e-6, (H, dk, dv, key_dim))
+    assert rel_err(out, f["out"]) < 1e-5
+    assert rel_err(st.S[0], f["S_new"]) < 1e-5
+    assert np.array_equal(st.conv_tail[0].numpy(), f["tail_new"].astype(np.float32))
+
+
+def test_softplus_threshold_is_torch_softplus():
+    ab = torch.tensor([-30.0, -1.0, 0.0, 5.0, 19.99, 20.0, 20.01, 50.0])
+    mine = torch.where(ab > 20, ab, torch.log1p(torch.exp(ab)))
+    assert torch.allclose(mine, torch.nn.functional.softplus(ab), rtol=1e-6, atol=0)
