@@ -5,30 +5,38 @@
 // replaces is paged_attention_decode<T> (src/kernels/attention.metal:87-159). Pool row of position s of sequence i:
 // ((tables[i][s / bs] * bs + s % bs) * Hkv + kvh) * D (attention.metal:115).
 //
-// Design (one wavefront per workgroup, "stream-K" split):
-//   * Work unit = one 16-position tile of one (sequence, kv-head) pair. Units are numbered pair-major, and the NW
-//     waves of the grid take equal contiguous unit ranges, so every wave streams the same number of KV bytes no
-//     matter how unequal the sequence lengths are. A wave whose range crosses pairs writes one partial per pair.
-//   * Each wave serves all G = Hq/Hkv query heads of its kv-head, so every K/V byte is read from HBM once.
+// Design ("stream-K" split over positions, then a merge):
+//   * Work unit = one 16-position tile of one sequence. Units are numbered sequence-major and the NW split
+//     workgroups take equal contiguous unit ranges, so every workgroup streams the same number of KV bytes however
+//     unequal the lengths are. A workgroup whose range crosses sequences writes one partial per sequence.
+//   * A split workgroup has one wave per kv-head; the waves walk the same tiles, so the interleaved halves of every
+//     pool row ([bs][Hkv][D]) are fetched together. Each wave serves all G = Hq/Hkv query heads of its kv-head, so
+//     every K/V byte is read from HBM once.
 //   * QK^T on MFMA (v_mfma_f32_16x16x32_bf16): A = the G query rows split exactly into three bf16 parts
-//     (q = hi + mid + lo), B = 16 keys x 32 dims. bf16 keys are exact MFMA operands; fp32 keys are split the same
-//     way (three MFMA passes), so both pool types get fp32-accurate scores, and a bf16 pool gives bit-for-bit the
-//     result of the fp32 pool holding the widened values (the extra passes only add exact zeros).
+//     (q = hi + mid + lo, kept in LDS), B = 16 keys x 32 dims. bf16 keys are exact MFMA operands; fp32 keys are split
+//     the same way (three MFMA passes), so both pool types get fp32-accurate scores, and a bf16 pool gives bit for
+//     bit the result of the fp32 pool holding the widened values (the extra passes only add exact zeros).
+//   * Loads are software-pipelined: the next tile's keys are issued after this tile's MFMAs and its values after
+//     this tile's PV, so every wave always has a tile's K or V in flight. When tiles align with blocks
+//     (block_size % 16 == 0) one vector load fetches the block numbers of 64 tiles.
 //   * Online softmax in base 2 (scores pre-scaled by log2(e)/sqrt(D)); row max by DPP inside 16-lane rows.
 //   * PV on the VALU in fp32: each lane owns 8 consecutive dims of one position row (coalesced 16/32-byte loads);
 //     probabilities are broadcast through LDS.
-//   * Merge kernel: one workgroup per pair combines its partials (m, l, acc) in wave order, divides, applies the
-//     optional sigmoid gate and writes [B, Hq, D].
+//   * Merge kernel: one workgroup per (sequence, kv-head) combines its partials (m, l, acc) in workgroup order,
+//     divides, applies the optional sigmoid gate and writes [B, Hq, D].
 // Bounds: lens are clamped to max_nb * bs and table entries to [0, num_blocks), so a malformed table cannot make a
 // load leave the pool. Positions outside [s0, len) are never used: their scores are replaced (not added) by -inf and
 // their V values by 0 before the FMA, so a NaN-poisoned block outside the window cannot leak in.
 #include "rk_device.h"
 #include "rk_internal.h"
 
+#include <stdlib.h>
+
 namespace rk {
 namespace {
 
 constexpr int kMaxBatch = 1024;
+constexpr int kMaxKvHeads = 4;     // one wave per kv head in a split workgroup of at most 256 threads
 constexpr int kTile = 16;
 
 struct DecodeArgs {
@@ -110,6 +118,10 @@ struct KVLoad<uint16_t> {
         return v;
     }
     __device__ static void key_operands(const Vec& v, u32x4* ops) { ops[0] = v.w; }
+    __device__ static void keep_if(Vec& v, bool keep) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        v.w = keep ? v.w : z;
+    }
     __device__ static void widen(const Vec& v, float* f) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -130,6 +142,11 @@ struct KVLoad<float> {
         v.w0 = p[0];
         v.w1 = p[1];
         return v;
+    }
+    __device__ static void keep_if(Vec& v, bool keep) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        v.w0 = keep ? v.w0 : z;
+        v.w1 = keep ? v.w1 : z;
     }
     __device__ static void key_operands(const Vec& v, u32x4* ops) {
         Split3 s[8];
@@ -154,8 +171,74 @@ struct KVLoad<float> {
     }
 };
 
-template <typename T, int D, int GP>
-__global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
+// LDS bytes one wave of the split kernel uses: the query A operands (NT x NIT x 64 lanes x 16 B), the 16 x GP
+// probabilities of the current tile and the GP rescale factors.
+template <int D, int GP>
+constexpr int wave_lds_bytes() {
+    return ((3 * GP + 15) / 16) * (D / 32) * 64 * 16 + kTile * GP * 4 + GP * 4;
+}
+
+// Element offsets of the pool rows this lane reads for one tile, and which of them are visible positions. With
+// block-aligned tiles (ALIGNED: block_size % 16 == 0) the 16 positions lie in one block, so the V rows are one base
+// plus a uniform stride; otherwise every row is looked up through the table (positions clamped to visible ones).
+template <int NVI, int TPI, int LPT, bool ALIGNED>
+struct TileRows;
+
+template <int NVI, int TPI, int LPT>
+struct TileRows<NVI, TPI, LPT, true> {
+    long long krow, vbase, vstride;
+    uint32_t vmask;            // bit vi: V position of step vi is visible
+    bool kvalid, partial;
+    __device__ long long vrow(int vi) const { return vbase + vi * vstride; }
+    __device__ bool vvalid(int vi) const { return (vmask >> vi) & 1u; }
+};
+
+template <int NVI, int TPI, int LPT>
+struct TileRows<NVI, TPI, LPT, false> {
+    long long krow, vr[NVI];
+    uint32_t vmask;
+    bool kvalid, partial;
+    __device__ long long vrow(int vi) const { return vr[vi]; }
+    __device__ bool vvalid(int vi) const { return (vmask >> vi) & 1u; }
+};
+
+template <int NVI, int TPI, int LPT, bool ALIGNED>
+__device__ __forceinline__ TileRows<NVI, TPI, LPT, ALIGNED> tile_rows(const DecodeArgs& a, const int32_t* table,
+                                                                        const SeqRange& sr, int tbase, int blk,
+                                                                        int kvh, int D, int lane) {
+    TileRows<NVI, TPI, LPT, ALIGNED> r;
+    r.partial = tbase < sr.s0 || tbase + kTile > sr.L;
+    const int tk = tbase + (lane & 15);
+    r.kvalid = tk >= sr.s0 && tk < sr.L;
+    r.vmask = 0;
+#pragma unroll
+    for (int vi = 0; vi < NVI; ++vi) {
+        const int tv = tbase + vi * TPI + lane / LPT;
+        r.vmask |= (uint32_t)(tv >= sr.s0 && tv < sr.L) << vi;
+    }
+    if constexpr (ALIGNED) {
+        // rows past the length are still rows of the allocated block: no clamping needed for addressing
+        const long long row0 = (long long)blk * a.bs + tbase % a.bs;
+        r.krow = ((row0 + (lane & 15)) * a.Hkv + kvh) * D;
+        r.vbase = ((row0 + lane / LPT) * a.Hkv + kvh) * D + (lane % LPT) * 8;
+        r.vstride = (long long)TPI * a.Hkv * D;
+    } else {
+        const int tkc = tk < sr.s0 ? sr.s0 : (tk >= sr.L ? sr.L - 1 : tk);
+        r.krow = kv_row(table, tkc, a.bs, a.Hkv, kvh, D, a.num_blocks);
+#pragma unroll
+        for (int vi = 0; vi < NVI; ++vi) {
+            const int tv = tbase + vi * TPI + lane / LPT;
+            const int tvc = tv < sr.s0 ? sr.s0 : (tv >= sr.L ? sr.L - 1 : tv);
+            r.vr[vi] = kv_row(table, tvc, a.bs, a.Hkv, kvh, D, a.num_blocks) + (lane % LPT) * 8;
+        }
+    }
+    return r;
+}
+
+// One workgroup = Hkv waves, wave k serving kv-head k: the waves of a workgroup walk the same tiles, so both halves
+// of every interleaved pool row ([bs][Hkv][D]) are fetched together.
+template <typename T, int D, int GP, bool ALIGNED>
+__global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
     using LD = KVLoad<T>;
     constexpr int NIT = D / 32;              // MFMA k-steps per tile
     constexpr int NT = (3 * GP + 15) / 16;   // A tiles: 3 query splits x GP heads, 16 rows each
@@ -165,43 +248,43 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
     constexpr int KS = LD::KS;
     constexpr int HB = GP / 4;               // head blocks of 4 in the score layout
 
-    __shared__ int cum[kMaxBatch + 1];
-    __shared__ __attribute__((aligned(16))) float p_lds[kTile * GP];
-    __shared__ __attribute__((aligned(16))) float alpha_lds[GP];
-
-    const int lane = threadIdx.x;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int lane = threadIdx.x & 63;
+    const int kvh = threadIdx.x >> 6;
     const int w = blockIdx.x;
     const int row = lane & 15;     // MFMA row / column owned by this lane
     const int grp = lane >> 4;     // k-slot group (operands) / row block (accumulator)
 
-    const int total = unit_prefix(a, cum);
+    int* cum = reinterpret_cast<int*>(smem);
+    char* wl = smem + (((a.B + 1) * 4 + 15) & ~15) + kvh * wave_lds_bytes<D, GP>();
+    u32x4* qop = reinterpret_cast<u32x4*>(wl);
+    float* p_lds = reinterpret_cast<float*>(wl + NT * NIT * 64 * 16);
+    float* alpha_lds = p_lds + kTile * GP;
+
+    if (kvh == 0) unit_prefix(a, cum);
     __syncthreads();
-    const long long U = (long long)a.Hkv * total;
+    const long long U = cum[a.B];
     if (U == 0) return;
     long long u = U * w / a.NW;
     const long long u_end = U * (w + 1) / a.NW;
     if (u >= u_end) return;
 
-    // locate the sequence owning unit u: largest b with Hkv * cum[b] <= u
-    int lo_b = 0, hi_b = a.B - 1;
+    int lo_b = 0, hi_b = a.B - 1;       // largest b with cum[b] <= u
     while (lo_b < hi_b) {
-        int mid = (lo_b + hi_b + 1) >> 1;
-        if ((long long)a.Hkv * cum[mid] <= u) lo_b = mid; else hi_b = mid - 1;
+        const int mid = (lo_b + hi_b + 1) >> 1;
+        if (cum[mid] <= u) lo_b = mid; else hi_b = mid - 1;
     }
     int b = lo_b;
     SeqRange sr = seq_range(a, b);
-    long long rel = u - (long long)a.Hkv * cum[b];
-    int kvh = (int)(rel / sr.units);
-    int off = (int)(rel % sr.units);
+    int off = (int)(u - cum[b]);
 
     while (u < u_end) {
-        const int pair = b * a.Hkv + kvh;
         const long long left = u_end - u;
         const int n_here = (long long)(sr.units - off) < left ? sr.units - off : (int)left;
         const int32_t* table = a.tables + (long long)b * a.max_nb;
+        const int tile0 = sr.t0 + off;
 
-        // ---- query operands: rows r of A tile tt hold split (m / GP) of head (m % GP), m = 16 * tt + r
-        u32x4 qa[NT][NIT];
+        // ---- query operands of (b, kvh): row r of A tile tt holds split (m / GP) of head (m % GP), m = 16 tt + r
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
             const int m = 16 * tt + row;
@@ -211,14 +294,19 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const int d = 32 * it + 8 * grp;
+                const float4 x0 = *reinterpret_cast<const float4*>(qh + d);
+                const float4 x1 = *reinterpret_cast<const float4*>(qh + d + 4);
+                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                 uint32_t bits[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    Split3 sp = split3(valid ? qh[d + e] * a.qscale : 0.0f);
+                    const Split3 sp = split3(valid ? xs[e] * a.qscale : 0.0f);
                     bits[e] = s == 0 ? sp.hi : (s == 1 ? sp.mid : sp.lo);
                 }
+                u32x4 op;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) qa[tt][it][j] = pack_hi2(bits[2 * j], bits[2 * j + 1]);
+                for (int j = 0; j < 4; ++j) op[j] = pack_hi2(bits[2 * j], bits[2 * j + 1]);
+                qop[(tt * NIT + it) * 64 + lane] = op;
             }
         }
 
@@ -231,30 +319,30 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 
+        // block of each tile (ALIGNED): lane j holds the table entry of tile ti0 + j, read once per 64 tiles
+        int blk_lane = 0;
+        auto refill = [&](int ti0) {
+            if (!ALIGNED) return;
+            const int t = (tile0 + ti0 + lane) * kTile;
+            const int j = ti0 + lane < n_here ? t / a.bs : 0;
+            int blk = table[j < a.max_nb ? j : 0];
+            blk_lane = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+        };
+        auto rows_of = [&](int ti) {
+            const int blk = ALIGNED ? __builtin_amdgcn_readlane(blk_lane, ti & 63) : 0;
+            return tile_rows<NVI, TPI, LPT, ALIGNED>(a, table, sr, (tile0 + ti) * kTile, blk, kvh, D, lane);
+        };
+
+        refill(0);
+        TileRows<NVI, TPI, LPT, ALIGNED> cur = rows_of(0);
+        typename LD::Vec kv[NIT], vv[NVI];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
+#pragma unroll
+        for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
+
         for (int ti = 0; ti < n_here; ++ti) {
-            const int tbase = (sr.t0 + off + ti) * kTile;
-            const bool partial = tbase < sr.s0 || tbase + kTile > sr.L;
-
-            // ---- issue K and V loads for this tile
-            const int tk = tbase + row;
-            const bool kvalid = tk >= sr.s0 && tk < sr.L;
-            const int tkc = tk < sr.s0 ? sr.s0 : (tk >= sr.L ? sr.L - 1 : tk);
-            const long long krow = kv_row(table, tkc, a.bs, a.Hkv, kvh, D, a.num_blocks);
-            typename LD::Vec kv[NIT];
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, krow + 32 * it + 8 * grp);
-
-            typename LD::Vec vv[NVI];
-            bool vvalid[NVI];
-#pragma unroll
-            for (int vi = 0; vi < NVI; ++vi) {
-                const int tv = tbase + vi * TPI + lane / LPT;
-                vvalid[vi] = tv >= sr.s0 && tv < sr.L;
-                const int tvc = tv < sr.s0 ? sr.s0 : (tv >= sr.L ? sr.L - 1 : tv);
-                vv[vi] = LD::load(a.vp, kv_row(table, tvc, a.bs, a.Hkv, kvh, D, a.num_blocks) + (lane % LPT) * 8);
-            }
-
-            // ---- scores: D[m][n] = sum_d A[m][d] * K[n][d]
+            // ---- scores: S[m][n] = sum_d A[m][d] * K[n][d]
             f32x4 sacc[NT];
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) sacc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -265,9 +353,20 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                    for (int tt = 0; tt < NT; ++tt) sacc[tt] = mfma16x16x32(qa[tt][it], kb[ks], sacc[tt]);
+                    for (int tt = 0; tt < NT; ++tt)
+                        sacc[tt] = mfma16x16x32(qop[(tt * NIT + it) * 64 + lane], kb[ks], sacc[tt]);
             }
-            // sum the three query splits: afterwards lane (grp, row) holds heads 4*(grp % HB) + i of position row
+
+            // ---- keys of the next tile go in flight now
+            TileRows<NVI, TPI, LPT, ALIGNED> nxt = cur;
+            if (ti + 1 < n_here) {
+                if (ALIGNED && ((ti + 1) & 63) == 0) refill(ti + 1);
+                nxt = rows_of(ti + 1);
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, nxt.krow + 32 * it + 8 * grp);
+            }
+
+            // sum the three query splits: lane (grp, row) then holds heads 4 * (grp % HB) + i of position row
             float sc[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -276,10 +375,10 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
                 for (int tt = 1; tt < NT; ++tt) x += sacc[tt][i];
                 if (GP == 4) x += __shfl_xor(x, 16);
                 x += __shfl_xor(x, 32);
-                sc[i] = kvalid ? x : -INFINITY;
+                sc[i] = cur.kvalid ? x : -INFINITY;
             }
 
-            // ---- online softmax (base 2) per head, over the 16 positions of this row
+            // ---- online softmax (base 2) per head over the 16 positions of this row
             float pr[4], al[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -301,26 +400,26 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
             float alh[GP];
 #pragma unroll
             for (int h4 = 0; h4 < GP / 4; ++h4) {
-                float4 t = *reinterpret_cast<const float4*>(&alpha_lds[4 * h4]);
+                const float4 t = *reinterpret_cast<const float4*>(&alpha_lds[4 * h4]);
                 alh[4 * h4] = t.x; alh[4 * h4 + 1] = t.y; alh[4 * h4 + 2] = t.z; alh[4 * h4 + 3] = t.w;
             }
 #pragma unroll
             for (int h = 0; h < GP; ++h)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[h][e] *= alh[h];
+            if (cur.partial) {                 // first / last tile: values of hidden positions become 0
+#pragma unroll
+                for (int vi = 0; vi < NVI; ++vi) LD::keep_if(vv[vi], cur.vvalid(vi));
+            }
 #pragma unroll
             for (int vi = 0; vi < NVI; ++vi) {
                 float vf[8];
                 LD::widen(vv[vi], vf);
-                if (partial && !vvalid[vi]) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) vf[e] = 0.0f;
-                }
                 const int pos = vi * TPI + lane / LPT;
                 float ph[GP];
 #pragma unroll
                 for (int h4 = 0; h4 < GP / 4; ++h4) {
-                    float4 t = *reinterpret_cast<const float4*>(&p_lds[pos * GP + 4 * h4]);
+                    const float4 t = *reinterpret_cast<const float4*>(&p_lds[pos * GP + 4 * h4]);
                     ph[4 * h4] = t.x; ph[4 * h4 + 1] = t.y; ph[4 * h4 + 2] = t.z; ph[4 * h4 + 3] = t.w;
                 }
 #pragma unroll
@@ -328,10 +427,17 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(ph[h], vf[e], acc[h][e]);
             }
+
+            // ---- values of the next tile go in flight now
+            if (ti + 1 < n_here) {
+#pragma unroll
+                for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, nxt.vrow(vi));
+            }
+            cur = nxt;
             __syncthreads();   // p_lds / alpha_lds are rewritten by the next tile
         }
 
-        // ---- flush the partial of (wave w, pair): acc [GP][D], then m [GP], l [GP]
+        // ---- flush the partial of (workgroup w, sequence b, kv-head): acc [GP][D], then m [GP], l [GP]
 #pragma unroll
         for (int h = 0; h < GP; ++h)
 #pragma unroll
@@ -342,7 +448,7 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
                 x += __shfl_xor(x, 32);
                 acc[h][e] = x;
             }
-        float* slot = a.part + (long long)(w + pair) * (GP * (D + 2));
+        float* slot = a.part + ((long long)(w + b) * a.Hkv + kvh) * (GP * (D + 2));
         if (lane < LPT) {
 #pragma unroll
             for (int h = 0; h < GP; ++h) {
@@ -362,22 +468,19 @@ __global__ __launch_bounds__(64) void paged_decode_split(DecodeArgs a) {
             }
         }
 
-        // ---- next pair
+        // ---- next sequence
         u += n_here;
         off = 0;
-        if (++kvh == a.Hkv) {
-            kvh = 0;
-            do {
-                ++b;
-            } while (b < a.B && seq_range(a, b).units == 0);
-            if (b >= a.B) break;
-            sr = seq_range(a, b);
-        }
+        do {
+            ++b;
+        } while (b < a.B && seq_range(a, b).units == 0);
+        if (b >= a.B) break;
+        sr = seq_range(a, b);
     }
 }
 
-// One workgroup per (sequence, kv-head) pair. The pair's units were covered by the contiguous wave ranges
-// [wa, wb]; waves whose range is empty (more waves than units) wrote nothing and are skipped. Partials are combined
+// One workgroup per (sequence, kv-head) pair. The sequence's tiles were covered by the contiguous ranges of split
+// workgroups [wa, wb]; a workgroup whose range is empty (more workgroups than tiles) wrote nothing and is skipped. Partials are combined
 // in wave order: M = max_w m_w, scale_w = 2^(m_w - M), out = sum_w scale_w acc_w / sum_w scale_w l_w.
 template <int D, int GP>
 __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
@@ -417,11 +520,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
         for (int i = tid; i < a.G * D; i += kT) out[i] = 0.0f;
         return;
     }
-    const long long U = (long long)a.Hkv * all;
-    const long long u0 = (long long)a.Hkv * below + (long long)kvh * sr.units;
+    const long long U = all;
+    const long long u0 = below;
     const int wa = wave_of(u0, U, a.NW), wb = wave_of(u0 + sr.units - 1, U, a.NW);
     const long long stride = GP * (D + 2);
     auto nonempty = [&](int w) { return U * w / a.NW < U * (w + 1) / a.NW; };
+    auto slot_of = [&](int w) { return (long long)(w + b) * a.Hkv + kvh; };
 
     // pass 1: per-head max of the partial maxima
     float mx[GP];
@@ -429,7 +533,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
     for (int h = 0; h < GP; ++h) mx[h] = -INFINITY;
     for (int w = wa + tid; w <= wb; w += kT) {
         if (!nonempty(w)) continue;
-        const float* m = a.part + (w + pair) * stride + GP * D;
+        const float* m = a.part + slot_of(w) * stride + GP * D;
 #pragma unroll
         for (int h = 0; h < GP; ++h) mx[h] = fmaxf(mx[h], m[h]);
     }
@@ -447,8 +551,15 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
 
     // pass 2: scales per chunk of 256 waves, numerators per output, denominators per head
     float num[NO], den[GP];
+    int off[NO], hk[NO];                 // this thread's outputs i = tid + k * 256: offset h * D + d, head h
 #pragma unroll
-    for (int k = 0; k < NO; ++k) num[k] = 0.0f;
+    for (int k = 0; k < NO; ++k) {
+        const int i = tid + k * kT;
+        const int ic = i < a.G * D ? i : 0;
+        num[k] = 0.0f;
+        hk[k] = ic / D;
+        off[k] = (ic / D) * D + ic % D;
+    }
 #pragma unroll
     for (int h = 0; h < GP; ++h) den[h] = 0.0f;
     for (int c0 = wa; c0 <= wb; c0 += kT) {
@@ -456,7 +567,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
         const bool ok = w <= wb && nonempty(w);
         live[tid] = ok;
         if (ok) {
-            const float* m = a.part + (w + pair) * stride + GP * D;
+            const float* m = a.part + slot_of(w) * stride + GP * D;
 #pragma unroll
             for (int h = 0; h < GP; ++h) {
                 const float sc = fast_exp2(m[h] - Mh[h]);
@@ -466,13 +577,25 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
         }
         __syncthreads();
         const int n_in = min(kT, wb - c0 + 1);
+        // batches of 8 slots: all loads of a batch are issued before any is used (addresses are inside the
+        // workspace even for skipped slots; their values are discarded by a select, never multiplied)
+        for (int s0 = 0; s0 < n_in; s0 += 8) {
+            float v[8][NO];
 #pragma unroll
-        for (int k = 0; k < NO; ++k) {
-            const int i = tid + k * kT;
-            if (i >= a.G * D) break;
-            const int h = i / D, d = i % D;
-            for (int s = 0; s < n_in; ++s)
-                if (live[s]) num[k] = fmaf(scale[s][h], a.part[(c0 + s + pair) * stride + h * D + d], num[k]);
+            for (int j = 0; j < 8; ++j) {
+                const long long slot = slot_of(c0 + min(s0 + j, n_in - 1)) * stride;
+#pragma unroll
+                for (int k = 0; k < NO; ++k) v[j][k] = a.part[slot + off[k]];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool use = s0 + j < n_in && live[s0 + j];
+#pragma unroll
+                for (int k = 0; k < NO; ++k) {
+                    const float t = fmaf(scale[min(s0 + j, n_in - 1)][hk[k]], v[j][k], num[k]);
+                    num[k] = use ? t : num[k];
+                }
+            }
         }
         __syncthreads();
     }
@@ -504,18 +627,30 @@ __global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
 typedef void (*SplitFn)(DecodeArgs);
 typedef void (*MergeFn)(DecodeArgs);
 
-template <typename T>
+template <typename T, bool ALIGNED>
 SplitFn pick_split(int D, int GP) {
     if (GP == 4) {
-        if (D == 64) return paged_decode_split<T, 64, 4>;
-        if (D == 128) return paged_decode_split<T, 128, 4>;
-        if (D == 256) return paged_decode_split<T, 256, 4>;
+        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED>;
+        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED>;
+        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED>;
     } else {
-        if (D == 64) return paged_decode_split<T, 64, 8>;
-        if (D == 128) return paged_decode_split<T, 128, 8>;
-        if (D == 256) return paged_decode_split<T, 256, 8>;
+        if (D == 64) return paged_decode_split<T, 64, 8, ALIGNED>;
+        if (D == 128) return paged_decode_split<T, 128, 8, ALIGNED>;
+        if (D == 256) return paged_decode_split<T, 256, 8, ALIGNED>;
     }
     return nullptr;
+}
+
+SplitFn pick_split(int kv_dtype, bool aligned, int D, int GP) {
+    if (kv_dtype == RK_BF16) return aligned ? pick_split<uint16_t, true>(D, GP) : pick_split<uint16_t, false>(D, GP);
+    return aligned ? pick_split<float, true>(D, GP) : pick_split<float, false>(D, GP);
+}
+
+int split_lds_bytes(int B, int Hkv, int D, int GP) {
+    int per_wave = 0;
+    if (GP == 4) per_wave = D == 64 ? wave_lds_bytes<64, 4>() : D == 128 ? wave_lds_bytes<128, 4>() : wave_lds_bytes<256, 4>();
+    else per_wave = D == 64 ? wave_lds_bytes<64, 8>() : D == 128 ? wave_lds_bytes<128, 8>() : wave_lds_bytes<256, 8>();
+    return (((B + 1) * 4 + 15) & ~15) + Hkv * per_wave;
 }
 
 MergeFn pick_merge(int D, int GP) {
@@ -531,18 +666,26 @@ MergeFn pick_merge(int D, int GP) {
     return nullptr;
 }
 
-// Number of waves for the split phase: the unit count's upper bound, capped at 8 waves per compute unit.
-int split_waves(int B, int Hkv, int block_size, int max_nb) {
-    const long long upper = (long long)B * Hkv * (((long long)max_nb * block_size + kTile - 1) / kTile);
+// Workgroups of the split phase (Hkv waves each): the tile count's upper bound, capped so that about
+// kWavesPerCU waves per compute unit are resident. RK_PAGED_DECODE_WAVES_PER_CU overrides the cap (tuning).
+constexpr int kWavesPerCU = 8;
+
+int split_groups(int B, int Hkv, int block_size, int max_nb) {
+    static int per_cu = [] {
+        const char* e = getenv("RK_PAGED_DECODE_WAVES_PER_CU");
+        const int v = e ? atoi(e) : 0;
+        return v > 0 ? v : kWavesPerCU;
+    }();
+    const long long upper = (long long)B * (((long long)max_nb * block_size + kTile - 1) / kTile);
     int cus = device_cus();
     if (cus <= 0) cus = 256;
-    const long long cap = (long long)cus * 8;
+    const long long cap = (long long)cus * per_cu / Hkv;
     long long nw = upper < cap ? upper : cap;
     return (int)(nw < 1 ? 1 : nw);
 }
 
 size_t workspace_bytes(int B, int Hkv, int D, int GP, int NW) {
-    return (size_t)(NW + (size_t)B * Hkv) * GP * (D + 2) * sizeof(float);
+    return (size_t)(NW + (size_t)B) * Hkv * GP * (D + 2) * sizeof(float);
 }
 
 int validate(const float* out, const float* q, const void* kp, const void* vp, int kv_dtype, const int32_t* tables,
@@ -551,6 +694,7 @@ int validate(const float* out, const float* q, const void* kp, const void* vp, i
     if (B < 1 || B > kMaxBatch) return fail(RK_ERR_ARG, "rk_paged_decode: batch %d outside [1, %d]", B, kMaxBatch);
     if (Hkv < 1 || Hq < Hkv || Hq % Hkv) return fail(RK_ERR_ARG, "rk_paged_decode: %d query heads over %d kv heads", Hq, Hkv);
     if (Hq / Hkv > 8) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: group size %d > 8", Hq / Hkv);
+    if (Hkv > kMaxKvHeads) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: %d kv heads > %d", Hkv, kMaxKvHeads);
     if (D != 64 && D != 128 && D != 256) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: head_dim %d not in {64,128,256}", D);
     if (bs < 1 || max_nb < 1 || num_blocks < 1) return fail(RK_ERR_ARG, "rk_paged_decode: block_size %d, max_nb %d, num_blocks %d", bs, max_nb, num_blocks);
     if (window < 0) return fail(RK_ERR_ARG, "rk_paged_decode: window %d < 0", window);
@@ -568,7 +712,7 @@ extern "C" {
 size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_size, int max_nb) {
     if (B < 1 || Hkv < 1 || Hq < Hkv || block_size < 1 || max_nb < 1) return 0;
     const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
-    return workspace_bytes(B, Hkv, D, GP, split_waves(B, Hkv, block_size, max_nb));
+    return workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb));
 }
 
 int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
@@ -581,7 +725,7 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     if (phase != 0 && phase != 1) return fail(RK_ERR_ARG, "rk_paged_decode_phase: phase %d", phase);
     const int G = Hq / Hkv;
     const int GP = G <= 4 ? 4 : 8;
-    const int NW = split_waves(B, Hkv, block_size, max_nb);
+    const int NW = split_groups(B, Hkv, block_size, max_nb);
     const size_t need = workspace_bytes(B, Hkv, D, GP, NW);
     if (!workspace || workspace_bytes_ < need)
         return fail(RK_ERR_WORKSPACE, "rk_paged_decode: workspace %zu bytes < %zu needed", workspace_bytes_, need);
@@ -600,8 +744,8 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     a.qscale = kLog2e / sqrtf((float)D);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (phase == 0) {
-        SplitFn fn = kv_dtype == RK_BF16 ? pick_split<uint16_t>(D, GP) : pick_split<float>(D, GP);
-        hipLaunchKernelGGL(fn, dim3(NW), dim3(64), 0, s, a);
+        SplitFn fn = pick_split(kv_dtype, block_size % kTile == 0, D, GP);
+        hipLaunchKernelGGL(fn, dim3(NW), dim3(64 * Hkv), split_lds_bytes(B, Hkv, D, GP), s, a);
         return check_launch("paged_decode_split");
     }
     hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(256), 0, s, a);
