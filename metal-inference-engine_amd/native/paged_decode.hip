@@ -5,10 +5,11 @@
 // replaces is paged_attention_decode<T> (src/kernels/attention.metal:87-159). Pool row of position s of sequence i:
 // ((tables[i][s / bs] * bs + s % bs) * Hkv + kvh) * D (attention.metal:115).
 //
-// Design ("stream-K" split over positions, then a merge):
-//   * Work unit = one 16-position tile of one sequence. Units are numbered sequence-major and the NW split
-//     workgroups take equal contiguous unit ranges, so every workgroup streams the same number of KV bytes however
-//     unequal the lengths are. A workgroup whose range crosses sequences writes one partial per sequence.
+// Design (split over positions, then a merge):
+//   * Work unit = one 16-position tile of one sequence. Sequence b gets n(b) = max(1, round(units(b) NW / U))
+//     split workgroups (U = all tiles, NW = the target workgroup count) that take equal contiguous parts of its
+//     tiles, so every workgroup streams about U / NW tiles however unequal the lengths are, never crosses a
+//     sequence, and writes exactly one partial (m, l, acc) per kv-head.
 //   * A split workgroup has one wave per kv-head; the waves walk the same tiles, so the interleaved halves of every
 //     pool row ([bs][Hkv][D]) are fetched together. Each wave serves all G = Hq/Hkv query heads of its kv-head, so
 //     every K/V byte is read from HBM once.
@@ -80,28 +81,47 @@ __device__ __forceinline__ long long kv_row(const int32_t* table, int s, int bs,
     return ((long long)(blk * (long long)bs + s % bs) * Hkv + kvh) * D;
 }
 
-// Exclusive prefix of per-sequence unit counts into cum[0..B], computed by one wave. Returns the total.
-__device__ int unit_prefix(const DecodeArgs& a, int* cum) {
+// Workgroup plan, computed by one wave: wg0[b] = first split workgroup of sequence b (exclusive prefix of
+// n(b) = units ? max(1, round(units * NW / U)) : 0), wg0[B] = workgroups in use. Returns U (all tiles).
+__device__ long long plan_workgroups(const DecodeArgs& a, int* wg0) {
     const int lane = threadIdx.x & 63;
-    int carry = 0;
+    long long U = 0;
     for (int b0 = 0; b0 < a.B; b0 += 64) {
-        int b = b0 + lane;
+        const int b = b0 + lane;
         int x = b < a.B ? seq_range(a, b).units : 0;
 #pragma unroll
+        for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+        U += x;
+    }
+    int carry = 0;
+    for (int b0 = 0; b0 < a.B; b0 += 64) {
+        const int b = b0 + lane;
+        const int units = b < a.B ? seq_range(a, b).units : 0;
+        int x = 0;
+        if (units > 0) {
+            const long long r = ((long long)units * a.NW + U / 2) / U;
+            x = r < 1 ? 1 : (int)r;
+        }
+#pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            int y = __shfl_up(x, off);
+            const int y = __shfl_up(x, off);
             if (lane >= off) x += y;
         }
-        if (b < a.B) cum[b + 1] = carry + x;
+        if (b < a.B) wg0[b + 1] = carry + x;
         carry += __shfl(x, 63);
     }
-    if (lane == 0) cum[0] = 0;
-    return carry;
+    if (lane == 0) wg0[0] = 0;
+    return U;
 }
 
-// wave that owns unit u: max w with floor(U * w / NW) <= u
-__device__ __forceinline__ int wave_of(long long u, long long U, int NW) {
-    return (int)(((u + 1) * (long long)NW - 1) / U);
+// largest b with wg0[b] <= w (wg0 non-decreasing, wg0[0] = 0)
+__device__ __forceinline__ int seq_of_workgroup(const int* wg0, int B, int w) {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (wg0[mid] <= w) lo = mid; else hi = mid - 1;
+    }
+    return lo;
 }
 
 template <typename T>
@@ -119,8 +139,8 @@ struct KVLoad<uint16_t> {
     }
     __device__ static void key_operands(const Vec& v, u32x4* ops) { ops[0] = v.w; }
     __device__ static void keep_if(Vec& v, bool keep) {
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        v.w = keep ? v.w : z;
+        const uint32_t m = keep ? 0xffffffffu : 0u;
+        v.w &= u32x4{m, m, m, m};
     }
     __device__ static void widen(const Vec& v, float* f) {
 #pragma unroll
@@ -144,9 +164,9 @@ struct KVLoad<float> {
         return v;
     }
     __device__ static void keep_if(Vec& v, bool keep) {
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        v.w0 = keep ? v.w0 : z;
-        v.w1 = keep ? v.w1 : z;
+        const uint32_t m = keep ? 0xffffffffu : 0u;
+        v.w0 &= u32x4{m, m, m, m};
+        v.w1 &= u32x4{m, m, m, m};
     }
     __device__ static void key_operands(const Vec& v, u32x4* ops) {
         Split3 s[8];
@@ -255,93 +275,104 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
     const int row = lane & 15;     // MFMA row / column owned by this lane
     const int grp = lane >> 4;     // k-slot group (operands) / row block (accumulator)
 
-    int* cum = reinterpret_cast<int*>(smem);
+    int* wg0 = reinterpret_cast<int*>(smem);
     char* wl = smem + (((a.B + 1) * 4 + 15) & ~15) + kvh * wave_lds_bytes<D, GP>();
     u32x4* qop = reinterpret_cast<u32x4*>(wl);
     float* p_lds = reinterpret_cast<float*>(wl + NT * NIT * 64 * 16);
     float* alpha_lds = p_lds + kTile * GP;
 
-    if (kvh == 0) unit_prefix(a, cum);
+    if (kvh == 0) plan_workgroups(a, wg0);
     __syncthreads();
-    const long long U = cum[a.B];
-    if (U == 0) return;
-    long long u = U * w / a.NW;
-    const long long u_end = U * (w + 1) / a.NW;
-    if (u >= u_end) return;
+    if (w >= wg0[a.B]) return;
+    const int b = seq_of_workgroup(wg0, a.B, w);
+    const int r = w - wg0[b], nwg = wg0[b + 1] - wg0[b];
+    const SeqRange sr = seq_range(a, b);
+    const int ta = (int)((long long)sr.units * r / nwg), tb = (int)((long long)sr.units * (r + 1) / nwg);
+    const int n_here = tb - ta;
+    const int32_t* table = a.tables + (long long)b * a.max_nb;
+    const int tile0 = sr.t0 + ta;
 
-    int lo_b = 0, hi_b = a.B - 1;       // largest b with cum[b] <= u
-    while (lo_b < hi_b) {
-        const int mid = (lo_b + hi_b + 1) >> 1;
-        if (cum[mid] <= u) lo_b = mid; else hi_b = mid - 1;
+    // ---- query rows of (b, kvh) requested first; split into MFMA operands once the first tile's loads are out
+    float4 qx[NT][NIT][2];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+        const int m = 16 * tt + row;
+        const int h = m % GP;
+        const bool valid = m / GP < 3 && h < a.G;
+        const float* qh = a.q + ((long long)b * a.Hq + kvh * a.G + (valid ? h : 0)) * D;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int d = 32 * it + 8 * grp;
+            qx[tt][it][0] = *reinterpret_cast<const float4*>(qh + d);
+            qx[tt][it][1] = *reinterpret_cast<const float4*>(qh + d + 4);
+        }
     }
-    int b = lo_b;
-    SeqRange sr = seq_range(a, b);
-    int off = (int)(u - cum[b]);
 
-    while (u < u_end) {
-        const long long left = u_end - u;
-        const int n_here = (long long)(sr.units - off) < left ? sr.units - off : (int)left;
-        const int32_t* table = a.tables + (long long)b * a.max_nb;
-        const int tile0 = sr.t0 + off;
+    float m_run[4], l_run[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.0f; }
+    float acc[GP][8];
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 
-        // ---- query operands of (b, kvh): row r of A tile tt holds split (m / GP) of head (m % GP), m = 16 tt + r
+    // block of each tile (ALIGNED): lane j holds the table entry of tile seg + j; tiles are walked in segments of 64
+    // so the inner loop never reloads it
+    int blk_lane = 0;
+    auto refill = [&](int seg) {
+        if (!ALIGNED) return;
+        const int t = (tile0 + seg + lane) * kTile;
+        const int j = seg + lane < n_here ? t / a.bs : 0;
+        const int blk = table[j < a.max_nb ? j : 0];
+        blk_lane = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+    };
+    auto rows_of = [&](int seg, int ti) {
+        const int blk = ALIGNED ? __builtin_amdgcn_readlane(blk_lane, ti) : 0;
+        return tile_rows<NVI, TPI, LPT, ALIGNED>(a, table, sr, (tile0 + seg + ti) * kTile, blk, kvh, D, lane);
+    };
+
+    for (int seg = 0; seg < n_here; seg += 64) {
+        const int nseg = n_here - seg < 64 ? n_here - seg : 64;
+        refill(seg);
+        TileRows<NVI, TPI, LPT, ALIGNED> cur = rows_of(seg, 0);
+        typename LD::Vec kv[NIT], vv[NVI];
+        // issue order K then V, here and in the loop, so that waiting for a tile's keys never waits for its values
+        // (the scheduling barriers keep the compiler from reordering the two groups of loads)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            const int m = 16 * tt + row;
-            const int s = m / GP, h = m % GP;
-            const bool valid = s < 3 && h < a.G;
-            const float* qh = a.q + ((long long)b * a.Hq + kvh * a.G + (valid ? h : 0)) * D;
+        for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int it = 0; it < NIT; ++it) {
-                const int d = 32 * it + 8 * grp;
-                const float4 x0 = *reinterpret_cast<const float4*>(qh + d);
-                const float4 x1 = *reinterpret_cast<const float4*>(qh + d + 4);
-                const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                uint32_t bits[8];
+        for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
+        __builtin_amdgcn_sched_barrier(0);
+
+        if (seg == 0) {
+            // operands: row r of A tile tt holds split (m / GP) of head (m % GP), m = 16 tt + r, scaled by
+            // log2(e)/sqrt(D); each lane reads back only its own operands, so no barrier is needed
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const Split3 sp = split3(valid ? xs[e] * a.qscale : 0.0f);
-                    bits[e] = s == 0 ? sp.hi : (s == 1 ? sp.mid : sp.lo);
+            for (int tt = 0; tt < NT; ++tt) {
+                const int s = (16 * tt + row) / GP;
+                const bool valid = s < 3 && (16 * tt + row) % GP < a.G;
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    const float xs[8] = {qx[tt][it][0].x, qx[tt][it][0].y, qx[tt][it][0].z, qx[tt][it][0].w,
+                                         qx[tt][it][1].x, qx[tt][it][1].y, qx[tt][it][1].z, qx[tt][it][1].w};
+                    uint32_t bits[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const Split3 sp = split3(valid ? xs[e] * a.qscale : 0.0f);
+                        bits[e] = s == 0 ? sp.hi : (s == 1 ? sp.mid : sp.lo);
+                    }
+                    u32x4 op;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) op[j] = pack_hi2(bits[2 * j], bits[2 * j + 1]);
+                    qop[(tt * NIT + it) * 64 + lane] = op;
                 }
-                u32x4 op;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) op[j] = pack_hi2(bits[2 * j], bits[2 * j + 1]);
-                qop[(tt * NIT + it) * 64 + lane] = op;
             }
         }
 
-        float m_run[4], l_run[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.0f; }
-        float acc[GP][8];
-#pragma unroll
-        for (int h = 0; h < GP; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
-
-        // block of each tile (ALIGNED): lane j holds the table entry of tile ti0 + j, read once per 64 tiles
-        int blk_lane = 0;
-        auto refill = [&](int ti0) {
-            if (!ALIGNED) return;
-            const int t = (tile0 + ti0 + lane) * kTile;
-            const int j = ti0 + lane < n_here ? t / a.bs : 0;
-            int blk = table[j < a.max_nb ? j : 0];
-            blk_lane = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
-        };
-        auto rows_of = [&](int ti) {
-            const int blk = ALIGNED ? __builtin_amdgcn_readlane(blk_lane, ti & 63) : 0;
-            return tile_rows<NVI, TPI, LPT, ALIGNED>(a, table, sr, (tile0 + ti) * kTile, blk, kvh, D, lane);
-        };
-
-        refill(0);
-        TileRows<NVI, TPI, LPT, ALIGNED> cur = rows_of(0);
-        typename LD::Vec kv[NIT], vv[NVI];
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
-#pragma unroll
-        for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
-
-        for (int ti = 0; ti < n_here; ++ti) {
+        for (int ti = 0; ti < nseg; ++ti) {
             // ---- scores: S[m][n] = sum_d A[m][d] * K[n][d]
             f32x4 sacc[NT];
 #pragma unroll
@@ -357,14 +388,14 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
                         sacc[tt] = mfma16x16x32(qop[(tt * NIT + it) * 64 + lane], kb[ks], sacc[tt]);
             }
 
-            // ---- keys of the next tile go in flight now
-            TileRows<NVI, TPI, LPT, ALIGNED> nxt = cur;
-            if (ti + 1 < n_here) {
-                if (ALIGNED && ((ti + 1) & 63) == 0) refill(ti + 1);
-                nxt = rows_of(ti + 1);
+            // ---- keys of the next tile go in flight now. Issued unconditionally (the last tile of a segment
+            // re-requests its own rows, which hit in L2): a conditional issue would make every later wait for this
+            // tile's values a wait for all outstanding loads.
+            const TileRows<NVI, TPI, LPT, ALIGNED> nxt = rows_of(seg, ti + 1 < nseg ? ti + 1 : ti);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, nxt.krow + 32 * it + 8 * grp);
-            }
+            for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, nxt.krow + 32 * it + 8 * grp);
+            __builtin_amdgcn_sched_barrier(0);
 
             // sum the three query splits: lane (grp, row) then holds heads 4 * (grp % HB) + i of position row
             float sc[4];
@@ -394,7 +425,7 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
                 if (row == 0)
                     *reinterpret_cast<float4*>(&alpha_lds[4 * grp]) = make_float4(al[0], al[1], al[2], al[3]);
             }
-            __syncthreads();
+            wave_lds_sync();
 
             // ---- acc = acc * alpha + P V
             float alh[GP];
@@ -407,10 +438,10 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
             for (int h = 0; h < GP; ++h)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[h][e] *= alh[h];
-            if (cur.partial) {                 // first / last tile: values of hidden positions become 0
+            // values of hidden positions become 0 (branch-free: a branch here would make the compiler wait for
+            // every outstanding load, including the next tile's keys)
 #pragma unroll
-                for (int vi = 0; vi < NVI; ++vi) LD::keep_if(vv[vi], cur.vvalid(vi));
-            }
+            for (int vi = 0; vi < NVI; ++vi) LD::keep_if(vv[vi], cur.vvalid(vi));
 #pragma unroll
             for (int vi = 0; vi < NVI; ++vi) {
                 float vf[8];
@@ -429,195 +460,128 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
             }
 
             // ---- values of the next tile go in flight now
-            if (ti + 1 < n_here) {
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, nxt.vrow(vi));
-            }
+            for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, nxt.vrow(vi));
+            __builtin_amdgcn_sched_barrier(0);
             cur = nxt;
-            __syncthreads();   // p_lds / alpha_lds are rewritten by the next tile
+            wave_lds_sync();   // p_lds / alpha_lds are rewritten by the next tile
         }
+    }
 
-        // ---- flush the partial of (workgroup w, sequence b, kv-head): acc [GP][D], then m [GP], l [GP]
+    // ---- the partial of (workgroup w, kv-head): acc [GP][D], then m [GP], l [GP]
 #pragma unroll
-        for (int h = 0; h < GP; ++h)
+    for (int h = 0; h < GP; ++h)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float x = acc[h][e];
-                if (TPI >= 8) x += dpp_f32<0x128>(x);   // lanes l and l ^ 8 share dims when a row is 8 lanes
-                if (TPI >= 4) x += __shfl_xor(x, 16);
-                x += __shfl_xor(x, 32);
-                acc[h][e] = x;
-            }
-        float* slot = a.part + ((long long)(w + b) * a.Hkv + kvh) * (GP * (D + 2));
-        if (lane < LPT) {
-#pragma unroll
-            for (int h = 0; h < GP; ++h) {
-                float4* dst = reinterpret_cast<float4*>(slot + h * D + lane * 8);
-                dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-                dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-            }
+        for (int e = 0; e < 8; ++e) {
+            float x = acc[h][e];
+            if (TPI >= 8) x += dpp_f32<0x128>(x);   // lanes l and l ^ 8 share dims when a row is 8 lanes
+            if (TPI >= 4) x += __shfl_xor(x, 16);
+            x += __shfl_xor(x, 32);
+            acc[h][e] = x;
         }
-        float lsum[4];
+    float* slot = a.part + ((long long)w * a.Hkv + kvh) * (GP * (D + 2));
+    if (lane < LPT) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lsum[i] = row16_sum(l_run[i]);
-        if (grp < HB && row == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                slot[GP * D + 4 * grp + i] = m_run[i];
-                slot[GP * D + GP + 4 * grp + i] = lsum[i];
-            }
+        for (int h = 0; h < GP; ++h) {
+            float4* dst = reinterpret_cast<float4*>(slot + h * D + lane * 8);
+            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
         }
-
-        // ---- next sequence
-        u += n_here;
-        off = 0;
-        do {
-            ++b;
-        } while (b < a.B && seq_range(a, b).units == 0);
-        if (b >= a.B) break;
-        sr = seq_range(a, b);
+    }
+    float lsum[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lsum[i] = row16_sum(l_run[i]);
+    if (grp < HB && row == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            slot[GP * D + 4 * grp + i] = m_run[i];
+            slot[GP * D + GP + 4 * grp + i] = lsum[i];
+        }
     }
 }
 
-// One workgroup per (sequence, kv-head) pair. The sequence's tiles were covered by the contiguous ranges of split
-// workgroups [wa, wb]; a workgroup whose range is empty (more workgroups than tiles) wrote nothing and is skipped. Partials are combined
-// in wave order: M = max_w m_w, scale_w = 2^(m_w - M), out = sum_w scale_w acc_w / sum_w scale_w l_w.
+// One workgroup per (sequence, kv-head) pair: combines the partials of the sequence's split workgroups
+// [wg0[b], wg0[b + 1]) in workgroup order with a running maximum. For each chunk of up to 32 partials the
+// accumulators, maxima and sums are all requested before any is used (one memory round trip per chunk), then
+// M' = max(M, m_w), num = num * 2^(M - M') + sum_w 2^(m_w - M') acc_w, den likewise with l_w; out = num / den.
+constexpr int kMergeThreads = 512;
+
 template <int D, int GP>
-__global__ __launch_bounds__(256) void paged_decode_merge(DecodeArgs a) {
-    constexpr int kT = 256;
+__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a) {
+    constexpr int kT = kMergeThreads;
     constexpr int NO = (GP * D + kT - 1) / kT;      // outputs per thread (upper bound)
-    __shared__ int ired[2][kT];
-    __shared__ float fred[kT][GP];
-    __shared__ float scale[kT][GP];
-    __shared__ int live[kT];
-    __shared__ float Mh[GP], Dh[GP];
+    constexpr int kCh = NO <= 2 ? 32 : 16;           // partials per memory round trip
+    __shared__ int wg0[kMaxBatch + 1];
+    __shared__ float ml[kCh][2][GP];
     const int tid = threadIdx.x;
     const int pair = blockIdx.x;
     const int b = pair / a.Hkv, kvh = pair % a.Hkv;
-
-    // units before sequence b and in total
-    int below = 0, all = 0;
-    for (int j = tid; j < a.B; j += kT) {
-        const int n = seq_range(a, j).units;
-        all += n;
-        if (j < b) below += n;
-    }
-    ired[0][tid] = below;
-    ired[1][tid] = all;
+    if (tid < 64) plan_workgroups(a, wg0);
     __syncthreads();
-    for (int s = kT / 2; s > 0; s >>= 1) {
-        if (tid < s) {
-            ired[0][tid] += ired[0][tid + s];
-            ired[1][tid] += ired[1][tid + s];
-        }
-        __syncthreads();
-    }
-    below = ired[0][0];
-    all = ired[1][0];
-    const SeqRange sr = seq_range(a, b);
+    const int w0 = wg0[b], nwg = wg0[b + 1] - wg0[b];
     float* out = a.out + ((long long)b * a.Hq + kvh * a.G) * D;
-    if (sr.units == 0) {
+    if (nwg == 0) {                                  // empty sequence (length 0)
         for (int i = tid; i < a.G * D; i += kT) out[i] = 0.0f;
         return;
     }
-    const long long U = all;
-    const long long u0 = below;
-    const int wa = wave_of(u0, U, a.NW), wb = wave_of(u0 + sr.units - 1, U, a.NW);
     const long long stride = GP * (D + 2);
-    auto nonempty = [&](int w) { return U * w / a.NW < U * (w + 1) / a.NW; };
-    auto slot_of = [&](int w) { return (long long)(w + b) * a.Hkv + kvh; };
+    auto slot_of = [&](int w) { return ((long long)w * a.Hkv + kvh) * stride; };
 
-    // pass 1: per-head max of the partial maxima
-    float mx[GP];
-#pragma unroll
-    for (int h = 0; h < GP; ++h) mx[h] = -INFINITY;
-    for (int w = wa + tid; w <= wb; w += kT) {
-        if (!nonempty(w)) continue;
-        const float* m = a.part + slot_of(w) * stride + GP * D;
-#pragma unroll
-        for (int h = 0; h < GP; ++h) mx[h] = fmaxf(mx[h], m[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < GP; ++h) fred[tid][h] = mx[h];
-    __syncthreads();
-    for (int s = kT / 2; s > 0; s >>= 1) {
-        if (tid < s)
-#pragma unroll
-            for (int h = 0; h < GP; ++h) fred[tid][h] = fmaxf(fred[tid][h], fred[tid + s][h]);
-        __syncthreads();
-    }
-    if (tid < GP) Mh[tid] = fred[0][tid];
-    __syncthreads();
-
-    // pass 2: scales per chunk of 256 waves, numerators per output, denominators per head
-    float num[NO], den[GP];
-    int off[NO], hk[NO];                 // this thread's outputs i = tid + k * 256: offset h * D + d, head h
+    int off[NO], hk[NO];                 // this thread's outputs i = tid + k * kT: offset h * D + d, head h
+    float M[NO], num[NO], den[NO];
 #pragma unroll
     for (int k = 0; k < NO; ++k) {
         const int i = tid + k * kT;
         const int ic = i < a.G * D ? i : 0;
-        num[k] = 0.0f;
         hk[k] = ic / D;
-        off[k] = (ic / D) * D + ic % D;
+        off[k] = ic;
+        M[k] = -INFINITY;
+        num[k] = 0.0f;
+        den[k] = 0.0f;
     }
+    for (int c0 = 0; c0 < nwg; c0 += kCh) {
+        const int n_in = min(kCh, nwg - c0);
+        // all loads of the chunk first (indices clamped to the chunk's last partial)
+        float v[kCh][NO];
 #pragma unroll
-    for (int h = 0; h < GP; ++h) den[h] = 0.0f;
-    for (int c0 = wa; c0 <= wb; c0 += kT) {
-        const int w = c0 + tid;
-        const bool ok = w <= wb && nonempty(w);
-        live[tid] = ok;
-        if (ok) {
-            const float* m = a.part + slot_of(w) * stride + GP * D;
+        for (int j = 0; j < kCh; ++j) {
+            const long long base = slot_of(w0 + c0 + min(j, n_in - 1));
 #pragma unroll
-            for (int h = 0; h < GP; ++h) {
-                const float sc = fast_exp2(m[h] - Mh[h]);
-                scale[tid][h] = sc;
-                den[h] = fmaf(sc, m[GP + h], den[h]);
-            }
+            for (int k = 0; k < NO; ++k) v[j][k] = a.part[base + off[k]];
+        }
+        for (int t = tid; t < kCh * 2 * GP; t += kT) {
+            const int j = t / (2 * GP), rr = t % (2 * GP);
+            ml[j][rr / GP][rr % GP] = a.part[slot_of(w0 + c0 + min(j, n_in - 1)) + GP * D + rr];
         }
         __syncthreads();
-        const int n_in = min(kT, wb - c0 + 1);
-        // batches of 8 slots: all loads of a batch are issued before any is used (addresses are inside the
-        // workspace even for skipped slots; their values are discarded by a select, never multiplied)
-        for (int s0 = 0; s0 < n_in; s0 += 8) {
-            float v[8][NO];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const long long slot = slot_of(c0 + min(s0 + j, n_in - 1)) * stride;
+        for (int k = 0; k < NO; ++k) {
+            float mx = M[k];
 #pragma unroll
-                for (int k = 0; k < NO; ++k) v[j][k] = a.part[slot + off[k]];
+            for (int j = 0; j < kCh; ++j) mx = j < n_in ? fmaxf(mx, ml[j][0][hk[k]]) : mx;
+            const float rs = fast_exp2(M[k] - mx);      // 0 on the first chunk (M = -inf, mx finite)
+            float nk = num[k] * rs, dk = den[k] * rs;
+#pragma unroll
+            for (int j = 0; j < kCh; ++j) {
+                const float sc = fast_exp2(ml[j][0][hk[k]] - mx);
+                const float tn = fmaf(sc, v[j][k], nk), td = fmaf(sc, ml[j][1][hk[k]], dk);
+                nk = j < n_in ? tn : nk;                 // a select: clamped duplicates never enter
+                dk = j < n_in ? td : dk;
             }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const bool use = s0 + j < n_in && live[s0 + j];
-#pragma unroll
-                for (int k = 0; k < NO; ++k) {
-                    const float t = fmaf(scale[min(s0 + j, n_in - 1)][hk[k]], v[j][k], num[k]);
-                    num[k] = use ? t : num[k];
-                }
-            }
+            num[k] = nk;
+            den[k] = dk;
+            M[k] = mx;
         }
         __syncthreads();
     }
-#pragma unroll
-    for (int h = 0; h < GP; ++h) fred[tid][h] = den[h];
-    __syncthreads();
-    for (int s = kT / 2; s > 0; s >>= 1) {
-        if (tid < s)
-#pragma unroll
-            for (int h = 0; h < GP; ++h) fred[tid][h] += fred[tid + s][h];
-        __syncthreads();
-    }
-    if (tid < GP) Dh[tid] = fred[0][tid];
-    __syncthreads();
 #pragma unroll
     for (int k = 0; k < NO; ++k) {
         const int i = tid + k * kT;
         if (i >= a.G * D) break;
-        const int h = i / D, d = i % D;
-        float o = num[k] / Dh[h];
+        float o = num[k] / den[k];
         if (a.gate) {
-            const float gv = a.gate[(long long)b * a.Hq * D + (long long)(kvh * a.G + h) * D + d];
+            const float gv = a.gate[(long long)b * a.Hq * D + (long long)kvh * a.G * D + i];
             o = o * (1.0f / (1.0f + expf(-gv)));
         }
         out[i] = o;
@@ -668,7 +632,7 @@ MergeFn pick_merge(int D, int GP) {
 
 // Workgroups of the split phase (Hkv waves each): the tile count's upper bound, capped so that about
 // kWavesPerCU waves per compute unit are resident. RK_PAGED_DECODE_WAVES_PER_CU overrides the cap (tuning).
-constexpr int kWavesPerCU = 8;
+constexpr int kWavesPerCU = 6;
 
 int split_groups(int B, int Hkv, int block_size, int max_nb) {
     static int per_cu = [] {
@@ -684,6 +648,7 @@ int split_groups(int B, int Hkv, int block_size, int max_nb) {
     return (int)(nw < 1 ? 1 : nw);
 }
 
+// n(b) <= units(b) NW / U + 1, so at most NW + B split workgroups are ever used: the grid and the partials.
 size_t workspace_bytes(int B, int Hkv, int D, int GP, int NW) {
     return (size_t)(NW + (size_t)B) * Hkv * GP * (D + 2) * sizeof(float);
 }
@@ -745,10 +710,10 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (phase == 0) {
         SplitFn fn = pick_split(kv_dtype, block_size % kTile == 0, D, GP);
-        hipLaunchKernelGGL(fn, dim3(NW), dim3(64 * Hkv), split_lds_bytes(B, Hkv, D, GP), s, a);
+        hipLaunchKernelGGL(fn, dim3(NW + B), dim3(64 * Hkv), split_lds_bytes(B, Hkv, D, GP), s, a);
         return check_launch("paged_decode_split");
     }
-    hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
     return check_launch("paged_decode_merge");
 }
 

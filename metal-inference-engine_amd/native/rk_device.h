@@ -89,4 +89,13 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Ordering point for LDS data exchanged between the lanes of ONE wave (a wave-private LDS region). The LDS unit
+// executes a wave's instructions in order, so only the compiler has to be kept from moving accesses across it;
+// unlike __syncthreads() it does not wait for the wave's outstanding global loads.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace rk
