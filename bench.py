@@ -263,12 +263,61 @@ def bench_deltanet(args, backend):
     }
 
 
+def bench_prefill(args, backend):
+    import torch
+    import workloads as wl
+    from native import kernels
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    case = wl.c5_prefill()
+    c = case.to(dev)
+    torch.cuda.synchronize()
+
+    def step():
+        kernels.paged_prefill(c.q, c.k_new, c.v_new, c.k_pool, c.v_pool, c.tables, c.cu_seqlens, c.starts,
+                              c.block_size, gate=c.gate)
+
+    ms = time_region(step, args.steps, args.warmup, stream)
+    flops = case.flops()
+    tflops = flops / (ms * 1e-3) / 1e12
+    N = case.q.shape[0]
+    log(f"[bench] c5: {ms * 1e3:.1f} us per packed prefill, {tflops:.1f} TFLOP/s")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import prefill_ref
+        torch.set_num_threads(cpu_threads())
+        # sample: the shortest segment, scaled to the whole batch by flops
+        s = min(range(len(case.starts)), key=lambda i: case.lengths()[i] * (case.starts[i] + case.lengths()[i]))
+        lo, hi = case.cu_seqlens[s], case.cu_seqlens[s + 1]
+        one = wl.PrefillCase(case.q[lo:hi], case.k_new[lo:hi], case.v_new[lo:hi], case.gate[lo:hi], case.k_pool,
+                             case.v_pool, case.tables[s:s + 1], [0, hi - lo], [case.starts[s]], case.block_size)
+        t = cpu_time(lambda: prefill_ref.packed_prefill(one.q, one.k_new, one.v_new, one.k_pool.clone(),
+                                                        one.v_pool.clone(), one.tables, one.cu_seqlens, one.starts,
+                                                        one.block_size, one.gate), runs=1)
+        t_full = t * flops / one.flops()
+        cpu = {"value": N / t_full, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"segment {s} alone ({hi - lo} new tokens on a {case.starts[s]}-token prefix), "
+                         f"{t:.2f} s, scaled to the whole pack by flops"}
+    return {
+        "metric": "packed prefill attention tokens/s (config 5) + TFLOP/s (% of bf16 MFMA peak), 1 GPU",
+        "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded)",
+        "config": {"workload": "config 5: 8 packed segments, new U[64, 2048] on prefixes U[0, 16384], 8/2 heads x 256, "
+                               "block 16, causal, gate, KV write-back", "new_tokens": N, "flops": flops},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s", "frac": tflops / 2500.0,
+                     "traffic": traffic_for("prefill_attention/c5"), "kernel": "prefill_attention (+ prefill_kv_write)",
+                     "avg_ms": ms},
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c5"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -299,6 +348,8 @@ def main() -> int:
                                  {"workload": "config 1: paged GQA decode, batch 1, fp32 KV, 512 positions"})
         rec["metric"] = "decode attn tokens/s @ batch 1 (config 1 latency case), 1 GPU"
         rec["dtype"] = "f32"
+    elif args.workload == "c5":
+        rec = bench_prefill(args, backend)
     else:
         rec = bench_deltanet(args, backend)
     print(json.dumps(rec), flush=True)

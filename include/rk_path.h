@@ -88,6 +88,23 @@ int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float
                        const float* norm_w, const int32_t* seq_index, int B, int H, int dk, int dv, int conv_k,
                        int n_linear, int slot, float eps, void* stream);
 
+/* ---- P4: packed (varlen) prefill attention over the paged pool, with the KV write-back of the new tokens.
+ * Replaces, per packed segment, the model's kv.write -> kv.read -> attention(causal) -> * sigmoid(gate) sequence
+ * (src/models/qwen3_5.py:112-120; PagedSequence.write / read, src/state.py:163-180; ops.attention, src/ops.py:65-104;
+ * the packing of src/models/packing.py:21-31, cu_seqlens = segment row offsets).
+ *   out [N, Hq, D] fp32; q [N, Hq, D] (q_dtype); k_new, v_new [N, Hkv, D] (new_dtype): rows cu[s] .. cu[s+1]-1 are
+ *   segment s, whose first new token is at absolute position start[s] of the sequence with block-table row s of
+ *   tables [S, max_nb] (blocks for positions < start[s] + n[s] must be allocated).
+ *   The new rows are written into k_pool / v_pool (pool_dtype; fp32 -> bf16 rounds to nearest even) before any
+ *   attention reads, then query i of segment s attends causally to positions 0 .. start[s] + i.
+ *   work [n_work] int32: (segment << 16) | query block (blocks of 32 queries), in the order to schedule them
+ *   (longest key range first balances the grid); every block of every segment must appear once.
+ *   gate NULL or [N, Hq*D] fp32. Group size Hq / Hkv = 4, D in {128, 256}. bf16 MFMA operands, fp32 accumulation. */
+int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, const void* v_new, int new_dtype,
+                     void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
+                     const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
+                     int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const float* gate, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,8 @@ Method -> kernel:
                          attention_decode, src/backend/metal.py:197-210)
   deltanet_decode[_batch] rk_deltanet_decode (P2; states of one HybridPool in one launch, a standalone state as a
                          pool of one, src/backend/metal.py:232-256)
+  paged_prefill_attention rk_paged_prefill (P4; the packed prefill of full_attention, src/models/qwen3_5.py:112-120:
+                         KV write-back, causal attention over prefix + new tokens, fused gate)
 """
 import torch
 
@@ -65,6 +67,17 @@ class RocmBackend:
         tables = self._seq0.view(1, 1)
         lens = torch.full((1,), S, dtype=torch.int32, device=self.device)
         return kernels.paged_decode(q, kp, vp, tables, lens, S)
+
+    # ---- P4: packed prefill attention
+    def paged_prefill_attention(self, q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
+                                gate=None):
+        """Packed prefill of one attention layer for S segments: writes k_new / v_new [N, Hkv, d] into the pool
+        layer at positions start_pos[s] + i of segment s (rows cu_seqlens[s] .. cu_seqlens[s+1]-1, block-table row
+        s of tables [S, max_nb]), then causal attention of q [N, Hq, d] over each segment's prefix and new keys
+        -> [N, Hq, d] fp32, times sigmoid(gate [N, Hq*d]) when given. The reference runs this per segment as
+        kv.write -> kv.read -> attention(causal) -> gate (src/models/qwen3_5.py:112-120)."""
+        return kernels.paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
+                                     gate)
 
     # ---- P2: DeltaNet decode step
     def deltanet_decode(self, qkv, z, b, a, state, slot, conv_w, A_log, dt_bias, norm_w, eps, dims):

@@ -159,3 +159,67 @@ def deltanet_decode(qkv, z, b, a, conv_state, S, seq_index, slot: int, conv_w, A
                 norm_w.data_ptr(), seq_index.data_ptr(), B, H, dk, dv, K, n_linear, int(slot), float(eps),
                 _stream(dev))
     return out
+
+
+PREFILL_BLOCK = 32          # queries per work item of rk_paged_prefill
+
+
+def prefill_work(lengths: list[int], starts: list[int]) -> list[int]:
+    """The work list of rk_paged_prefill: one item (segment << 16 | query block) per block of 32 new queries,
+    longest key range first so the longest items start first."""
+    items = []
+    for s, (n, p) in enumerate(zip(lengths, starts)):
+        for qb in range(-(-n // PREFILL_BLOCK)):
+            items.append((p + min(n, (qb + 1) * PREFILL_BLOCK), (s << 16) | qb))
+    items.sort(key=lambda x: -x[0])
+    return [w for _, w in items]
+
+
+def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size: int, gate=None,
+                  out=None) -> torch.Tensor:
+    """Packed prefill attention (rk_paged_prefill): writes the new K/V rows into one pool layer, then causal GQA
+    attention of every segment's new queries over its prefix + new keys -> [N, Hq, d] fp32 (* sigmoid(gate)).
+    cu_seqlens (S + 1 row offsets) and start_pos (S absolute positions) are host-side lists / CPU tensors, as the
+    packing step produces them; tables [S, max_nb] int32 on the device."""
+    name = "paged_prefill"
+    cu = [int(x) for x in cu_seqlens]
+    st = [int(x) for x in start_pos]
+    S = len(st)
+    if len(cu) != S + 1 or cu[0] != 0 or any(b < a for a, b in zip(cu, cu[1:])):
+        raise ValueError(f"{name}: cu_seqlens {cu[:8]}... must be S + 1 non-decreasing offsets from 0")
+    N, Hq, d = q.shape
+    if cu[-1] != N or k_new.shape[0] != N or v_new.shape != k_new.shape:
+        raise ValueError(f"{name}: q {tuple(q.shape)}, k_new {tuple(k_new.shape)}, cu_seqlens end {cu[-1]}")
+    if k_pool.dtype != v_pool.dtype or k_pool.dtype not in KV_DTYPES:
+        raise TypeError(f"{name}: pools must both be float32 or bfloat16, not {k_pool.dtype} / {v_pool.dtype}")
+    NB, bs, Hkv, dp = k_pool.shape
+    if dp != d or bs != block_size or k_new.shape[1:] != (Hkv, d):
+        raise ValueError(f"{name}: pool {tuple(k_pool.shape)} vs q {tuple(q.shape)}, k_new {tuple(k_new.shape)}")
+    if tables.dim() != 2 or tables.shape[0] != S or tables.dtype != torch.int32:
+        raise ValueError(f"{name}: tables {tuple(tables.shape)} {tables.dtype} for {S} segments")
+    for s in range(S):
+        if st[s] < 0 or -(-(st[s] + cu[s + 1] - cu[s]) // bs) > tables.shape[1]:
+            raise ValueError(f"{name}: segment {s} reaches position {st[s] + cu[s + 1] - cu[s]}, table covers "
+                             f"{tables.shape[1] * bs}")
+    dev = _need_cuda(name, q, k_new, v_new, k_pool, v_pool, tables)
+    _contig(name, k_pool, "k_pool"); _contig(name, v_pool, "v_pool"); _contig(name, tables, "tables")
+    as_kv = lambda t: t if t.dtype in KV_DTYPES else t.float()
+    q, k_new, v_new = as_kv(q).contiguous(), as_kv(k_new).contiguous(), as_kv(v_new).to(as_kv(k_new).dtype).contiguous()
+    if gate is not None:
+        gate = gate.to(torch.float32).contiguous()
+        if gate.numel() != N * Hq * d:
+            raise ValueError(f"{name}: gate has {gate.numel()} elements, expected {N * Hq * d}")
+    if out is None:
+        out = torch.empty(N, Hq, d, dtype=torch.float32, device=dev)
+    if N == 0:
+        return out
+    from state import to_device
+    meta = to_device(torch.tensor(cu + st + prefill_work([b - a for a, b in zip(cu, cu[1:])], st),
+                                  dtype=torch.int32), dev)
+    n_work = meta.numel() - (2 * S + 1)
+    load().call("rk_paged_prefill", out.data_ptr(), q.data_ptr(), DTYPE_CODES[q.dtype], k_new.data_ptr(),
+                v_new.data_ptr(), DTYPE_CODES[k_new.dtype], k_pool.data_ptr(), v_pool.data_ptr(),
+                DTYPE_CODES[k_pool.dtype], tables.data_ptr(), tables.shape[1], meta.data_ptr(),
+                meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq, Hkv, d, bs, NB,
+                gate.data_ptr() if gate is not None else None, _stream(dev))
+    return out

@@ -1,0 +1,354 @@
+// P4: packed (varlen) prefill attention over a paged KV pool, gfx950.
+//
+// Semantics: for every packed segment s (new rows cu[s] .. cu[s+1]-1 of one sequence whose first new token sits at
+// absolute position p[s]) the reference writes the new keys / values into the sequence's blocks, gathers positions
+// 0 .. p[s]+n[s]-1 back through the block table and runs causal GQA attention, query i at position p[s]+i; the
+// output is then multiplied by sigmoid(gate) (src/models/qwen3_5.py:112-120, src/state.py:163-180,
+// src/ops.py:65-104, src/models/packing.py:21-31). Here:
+//   1. prefill_kv_write: the new K/V rows go into the pool first (rounded to the pool's type), so attention reads
+//      exactly what the reference's gather reads back.
+//   2. prefill_attention: one workgroup per (segment, block of 32 queries, kv-head), one wave per query head of the
+//      group. Key tiles of 64 positions are staged in LDS (K as rows, V transposed to [dim][key]) and shared by the
+//      G waves. Per wave the scores are computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16_bf16 (A = 32 keys
+//      x 16 dims from LDS, B = 16 dims x 32 queries from registers), so each lane owns one query column: the online
+//      softmax needs one cross-lane exchange, and the probabilities, rounded to bf16, are already in the B-operand
+//      layout of the second product O^T += V^T P^T (A = 32 dims x 16 keys from LDS). fp32 accumulation throughout;
+//      operands are bf16 (q, k, v as stored; p rounded), so results carry bf16-level error.
+//   3. The output is divided by the softmax sum, gated and written as fp32 [N, Hq, D].
+// Bounds: key positions past a segment's length are clamped for addressing (and masked), table entries clamped to
+// the pool, query rows past the segment clamped for loading (and not stored).
+#include "rk_device.h"
+#include "rk_internal.h"
+
+namespace rk {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBQ = 32;    // queries per wave
+constexpr int kBK = 64;    // keys per tile
+constexpr int kKPad = 8;   // bf16 padding of a K row in LDS (16 bytes)
+constexpr int kVPad = 8;   // bf16 padding of a V^T row in LDS
+
+struct PrefillArgs {
+    float* out;                 // [N, Hq, D]
+    const void* q;              // [N, Hq, D] q_dtype
+    const void* k_new;          // [N, Hkv, D] new_dtype
+    const void* v_new;
+    void* kp;                   // pool layer [NB, bs, Hkv, D] pool_dtype
+    void* vp;
+    const int32_t* tables;      // [S, max_nb]
+    const int32_t* cu;          // [S + 1] new-row offsets
+    const int32_t* start;       // [S] absolute position of each segment's first new token
+    const int32_t* work;        // [n_work] (segment << 16) | query block, longest first
+    const float* gate;          // [N, Hq * D] or null
+    int q_dtype, new_dtype, pool_dtype;
+    int S, n_work, N, Hq, Hkv, G, bs, max_nb, num_blocks;
+    float qscale;               // log2(e) / sqrt(D)
+};
+
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ long long pool_row(const PrefillArgs& a, const int32_t* table, int pos, int kvh, int D) {
+    int blk = table[pos / a.bs];
+    blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+    return (((long long)blk * a.bs + pos % a.bs) * a.Hkv + kvh) * D;
+}
+
+// 8 consecutive elements at element offset off as bf16 bits (fp32 sources rounded to nearest even)
+__device__ __forceinline__ u32x4 load8_bf16(const void* base, long long off, int dtype) {
+    if (dtype == RK_BF16) return *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+    const float4 x = p[0], y = p[1];
+    u32x4 r;
+    r[0] = (uint32_t)f32_to_bf16_rne(x.x) | ((uint32_t)f32_to_bf16_rne(x.y) << 16);
+    r[1] = (uint32_t)f32_to_bf16_rne(x.z) | ((uint32_t)f32_to_bf16_rne(x.w) << 16);
+    r[2] = (uint32_t)f32_to_bf16_rne(y.x) | ((uint32_t)f32_to_bf16_rne(y.y) << 16);
+    r[3] = (uint32_t)f32_to_bf16_rne(y.z) | ((uint32_t)f32_to_bf16_rne(y.w) << 16);
+    return r;
+}
+
+__device__ __forceinline__ int segment_of(const int32_t* cu, int S, int row) {
+    int lo = 0, hi = S - 1;                 // largest s with cu[s] <= row
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (cu[mid] <= row) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// ---- 1. new K/V rows into the pool: one thread moves 8 elements of one row (K and V)
+__global__ __launch_bounds__(256) void prefill_kv_write(PrefillArgs a, int D) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int row = a.Hkv * D, per = row / 8;
+    if (i >= (long long)a.N * per) return;
+    const int n = (int)(i / per), c = (int)(i % per) * 8;
+    const int s = segment_of(a.cu, a.S, n);
+    const int pos = a.start[s] + (n - a.cu[s]);
+    const int32_t* table = a.tables + (long long)s * a.max_nb;
+    const int j = pos / a.bs;
+    if (j >= a.max_nb) return;
+    const int blk = table[j];
+    if (blk < 0 || blk >= a.num_blocks) return;
+    const long long dst = ((long long)blk * a.bs + pos % a.bs) * row + c;
+    const long long src = (long long)n * row + c;
+    if (a.pool_dtype == RK_BF16) {
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.kp) + dst) = load8_bf16(a.k_new, src, a.new_dtype);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.vp) + dst) = load8_bf16(a.v_new, src, a.new_dtype);
+    } else {
+        const void* srcs[2] = {a.k_new, a.v_new};
+        void* dsts[2] = {a.kp, a.vp};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float f[8];
+            if (a.new_dtype == RK_BF16) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(srcs[t]) + src);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { f[2 * e] = bf16_lo(w[e]); f[2 * e + 1] = bf16_hi(w[e]); }
+            } else {
+                const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(srcs[t]) + src);
+                const float4 x = p[0], y = p[1];
+                f[0] = x.x; f[1] = x.y; f[2] = x.z; f[3] = x.w; f[4] = y.x; f[5] = y.y; f[6] = y.z; f[7] = y.w;
+            }
+            float4* d4 = reinterpret_cast<float4*>(reinterpret_cast<float*>(dsts[t]) + dst);
+            d4[0] = make_float4(f[0], f[1], f[2], f[3]);
+            d4[1] = make_float4(f[4], f[5], f[6], f[7]);
+        }
+    }
+}
+
+// ---- 2. attention. blockDim = G * 64 = 256 (one wave per query head of kv-head blockIdx.y), work item blockIdx.x.
+// One wave per SIMD: 512 registers per lane hold the O^T accumulators, the Q^T operands and the prefetched tile.
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_attention(PrefillArgs a) {
+    constexpr int NKS = D / 16;          // k-steps of S^T (dims)
+    constexpr int NDT = D / 32;          // 32-row tiles of O^T (dims)
+    constexpr int KROW = D + kKPad;      // LDS K row stride (bf16)
+    constexpr int VROW = kBK + kVPad;    // LDS V^T row stride (bf16)
+    constexpr int KBUF = kBK * KROW, VBUF = D * VROW;
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];   // [2][K tile] then [2][V^T tile]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = blockDim.x;
+    const int kvh = blockIdx.y;
+    const int item = a.work[blockIdx.x];
+    const int seg = item >> 16, qblk = item & 0xffff;
+    const int row0 = a.cu[seg] + qblk * kBQ;
+    const int nq = min(kBQ, a.cu[seg + 1] - row0);
+    const int p0 = a.start[seg] + qblk * kBQ;       // position of the block's first query
+    const int n_keys = p0 + nq;                      // keys 0 .. p0 + nq - 1
+    const int32_t* table = a.tables + (long long)seg * a.max_nb;
+    const int head = kvh * a.G + wave;
+    const int col = lane & 31, kg = lane >> 5;      // query column, k-slot group
+    const int qpos = p0 + (col < nq ? col : nq - 1);
+
+    // ---- Q^T operands (B of S^T): lane holds q[query col][d = 16 ks + 8 kg .. + 8]
+    u32x4 qop[NKS];
+    {
+        const long long base = ((long long)(row0 + (col < nq ? col : nq - 1)) * a.Hq + head) * D;
+#pragma unroll
+        for (int t = 0; t < NKS; ++t) qop[t] = load8_bf16(a.q, base + 16 * t + 8 * kg, a.q_dtype);
+    }
+
+    f32x16 o[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) o[t] = f32x16{};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // staging: a thread moves jobs of 8 keys x 8 dims (K as 8 row pieces, V transposed in registers)
+    constexpr int kJobs = (kBK / 8) * (D / 8);
+    constexpr int kMaxJobs = (kJobs + 255) / 256;    // per thread (the workgroup has 4 waves)
+    u32x4 kr[kMaxJobs][8], vr[kMaxJobs][8];
+    auto fetch = [&](int tile) {
+        const int k0 = tile * kBK;
+#pragma unroll
+        for (int jb = 0; jb < kMaxJobs; ++jb) {
+            const int job = tid + jb * nthr;
+            if (job >= kJobs) break;
+            const int kgp = job / (D / 8), dc = job % (D / 8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                int pos = k0 + 8 * kgp + j;
+                pos = pos < n_keys ? pos : n_keys - 1;
+                const long long off = pool_row(a, table, pos, kvh, D) + 8 * dc;
+                kr[jb][j] = load8_bf16(a.kp, off, a.pool_dtype);
+                vr[jb][j] = load8_bf16(a.vp, off, a.pool_dtype);
+            }
+        }
+    };
+    auto stash = [&](int buf) {
+        uint16_t* ks = lds + buf * KBUF;
+        uint16_t* vt = lds + 2 * KBUF + buf * VBUF;
+#pragma unroll
+        for (int jb = 0; jb < kMaxJobs; ++jb) {
+            const int job = tid + jb * nthr;
+            if (job >= kJobs) break;
+            const int kgp = job / (D / 8), dc = job % (D / 8);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(&ks[(8 * kgp + j) * KROW + 8 * dc]) = kr[jb][j];
+            // transpose: output e (dim 8 dc + e) gathers element e of the 8 key rows
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                u32x4 t;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const uint32_t lo = e & 1 ? vr[jb][2 * jj][e / 2] >> 16 : vr[jb][2 * jj][e / 2] & 0xffffu;
+                    const uint32_t hi = e & 1 ? vr[jb][2 * jj + 1][e / 2] >> 16 : vr[jb][2 * jj + 1][e / 2] & 0xffffu;
+                    t[jj] = lo | (hi << 16);
+                }
+                *reinterpret_cast<u32x4*>(&vt[(8 * dc + e) * VROW + 8 * kgp]) = t;
+            }
+        }
+    };
+
+    const int n_tiles = (n_keys + kBK - 1) / kBK;
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int tile = 0; tile < n_tiles; ++tile) {
+        const int k0 = tile * kBK;
+        const uint16_t* ks = lds + (tile & 1) * KBUF;
+        const uint16_t* vt = lds + 2 * KBUF + (tile & 1) * VBUF;
+        if (tile + 1 < n_tiles) fetch(tile + 1);   // in flight during this tile's products
+
+        // ---- S^T = K Q^T for the 64 keys (two 32-key tiles)
+        f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int t = 0; t < NKS; ++t) {
+                const u32x4 ka = *reinterpret_cast<const u32x4*>(&ks[(32 * mt + col) * KROW + 16 * t + 8 * kg]);
+                s[mt] = mfma32(ka, qop[t], s[mt]);
+            }
+
+        // ---- mask, scale (base 2), online softmax over this lane's query column
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 32 * mt + 8 * (r / 4) + 4 * kg + (r % 4);
+                const float v = key <= qpos ? s[mt][r] * a.qscale : -INFINITY;
+                s[mt][r] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run, tmax);     // finite: key 0 <= qpos is in the first tile
+        const float alpha = fast_exp2(m_run - m_new);
+        float psum = 0.0f;
+        u32x4 pop[4];                                // B operands of the 4 key k-steps
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                float pv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    pv[e] = fast_exp2(s[mt][8 * half + e] - m_new);
+                    psum += pv[e];
+                }
+                u32x4 w;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    w[j] = (uint32_t)f32_to_bf16_rne(pv[2 * j]) | ((uint32_t)f32_to_bf16_rne(pv[2 * j + 1]) << 16);
+                pop[2 * mt + half] = w;
+            }
+        psum += __shfl_xor(psum, 32);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < NDT; ++t) o[t] *= alpha;
+        }
+
+        // ---- O^T += V^T P^T: k-step (mt, half) covers keys 32 mt + 16 half + 8 (e / 4) + 4 kg + e % 4
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const uint16_t* vrow = &vt[(32 * dt + col) * VROW];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int kb = 32 * (u >> 1) + 16 * (u & 1) + 4 * kg;
+                const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + kb);
+                const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + kb + 8);
+                const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
+                o[dt] = mfma32(va, pop[u], o[dt]);
+            }
+        }
+        if (tile + 1 < n_tiles) stash((tile + 1) & 1);   // the other buffer: last read two tiles ago
+        __syncthreads();
+    }
+
+    // ---- out[row0 + col][head][d] = O^T[d][col] / l (* sigmoid(gate)); lanes of both k-slot groups hold rows
+    if (col < nq) {
+        const float inv = 1.0f / l_run;
+        const long long orow = (long long)(row0 + col) * a.Hq + head;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = 32 * dt + 8 * r4 + 4 * kg;
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = o[dt][4 * r4 + i] * inv;
+                    if (a.gate) {
+                        const float g = a.gate[orow * D + d + i];
+                        v[i] = v[i] * (1.0f / (1.0f + expf(-g)));
+                    }
+                }
+                *reinterpret_cast<float4*>(a.out + orow * D + d) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+    }
+}
+
+}  // namespace
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" {
+
+int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, const void* v_new, int new_dtype,
+                     void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
+                     const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
+                     int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const float* gate, void* stream) {
+    if (N == 0) return RK_OK;
+    if (!out || !q || !k_new || !v_new || !k_pool || !v_pool || !tables || !cu_seqlens || !start_pos || !work)
+        return fail(RK_ERR_ARG, "rk_paged_prefill: null pointer");
+    if (S < 1 || N < 1 || n_work < 1 || n_work > 65535 * 8 || max_nb < 1 || block_size < 1 || num_blocks < 1)
+        return fail(RK_ERR_ARG, "rk_paged_prefill: S %d N %d n_work %d max_nb %d block_size %d", S, N, n_work, max_nb,
+                    block_size);
+    if (Hkv < 1 || Hq % Hkv || Hq / Hkv != 4)
+        return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d query heads over %d kv heads (built for groups of 4)",
+                    Hq, Hkv);
+    if (D != 128 && D != 256) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: head_dim %d not in {128, 256}", D);
+    for (int dt : {q_dtype, new_dtype, pool_dtype})
+        if (dt != RK_F32 && dt != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: dtype %d", dt);
+    PrefillArgs a;
+    a.out = out; a.q = q; a.k_new = k_new; a.v_new = v_new; a.kp = k_pool; a.vp = v_pool; a.tables = tables;
+    a.cu = cu_seqlens; a.start = start_pos; a.work = work; a.gate = gate;
+    a.q_dtype = q_dtype; a.new_dtype = new_dtype; a.pool_dtype = pool_dtype;
+    a.S = S; a.n_work = n_work; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.bs = block_size;
+    a.max_nb = max_nb; a.num_blocks = num_blocks;
+    a.qscale = kLog2e / sqrtf((float)D);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const long long threads = (long long)N * (Hkv * D / 8);
+    hipLaunchKernelGGL(prefill_kv_write, dim3((unsigned)ceil_div((size_t)threads, 256)), dim3(256), 0, s, a, D);
+    int rc = check_launch("prefill_kv_write");
+    if (rc) return rc;
+    const size_t lds = 2 * (size_t)(kBK * (D + kKPad) + D * (kBK + kVPad)) * sizeof(uint16_t);
+    if (D == 256) {
+        static bool attr256 = false;
+        if (!attr256) {
+            hipFuncSetAttribute((const void*)prefill_attention<256>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            attr256 = true;
+        }
+        hipLaunchKernelGGL(prefill_attention<256>, dim3(n_work, Hkv), dim3(64 * a.G), lds, s, a);
+    } else {
+        hipLaunchKernelGGL(prefill_attention<128>, dim3(n_work, Hkv), dim3(64 * a.G), lds, s, a);
+    }
+    return check_launch("prefill_attention");
+}
+
+}  // extern "C"

@@ -29,6 +29,7 @@ SIGNATURES = {
     "rk_kv_write": (c_int, [P, P, c_int, P, P, P, c_int] + [c_int] * 5 + [P]),
     "rk_kv_gather": (c_int, [P, P, P, P, c_int, P] + [c_int] * 7 + [P]),
     "rk_deltanet_decode": (c_int, [P] * 12 + [c_int] * 7 + [c_float, P]),
+    "rk_paged_prefill": (c_int, [P, P, c_int, P, P, c_int, P, P, c_int, P, c_int, P, P, P] + [c_int] * 8 + [P, P]),
 }
 
 

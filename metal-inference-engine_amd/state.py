@@ -132,6 +132,17 @@ class PagedKVPool:
         lens = torch.tensor([p + 1 for p in starts], dtype=torch.int32)
         return tuple(to_device(t, dev) for t in (blocks, offsets, tables, lens))
 
+    def prefill_layout(self, seqs: list["PagedSequence"], starts: list[int], lengths: list[int]):
+        """Packed prefill of len(seqs) segments, segment s adding lengths[s] tokens at positions starts[s] .. of
+        seqs[s] (blocks already reserved): (tables [S, max_nb] int32 on the pool's device, cu_seqlens, starts) with
+        cu_seqlens the S + 1 row offsets of the packed batch (the layout src/models/packing.py:21-31 packs)."""
+        width = max(1, max(len(s.block_table) for s in seqs))
+        tables = torch.tensor([s.block_table + [0] * (width - len(s.block_table)) for s in seqs], dtype=torch.int32)
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + n)
+        return to_device(tables, self.k.device), cu, list(starts)
+
     def write_rows(self, layer: int, slots: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         """k, v [n, Hkv, d] into flat row indices slots = block * block_size + offset of one layer."""
         if self.k.is_cuda:

@@ -160,3 +160,72 @@ def c2_deltanet_step(seed: int = 2, batch: int = 8, max_seqs: int | None = None,
     norm_w = 1.0 + r(DN_DV, scale=0.1)
     return DeltaNetStepCase(qkv, z, b, a, conv, S, seq_index, slot, conv_w, A_log, dt_bias, norm_w, 1e-6,
                             (DN_HEADS, DN_DK, DN_DV, KEY_DIM))
+
+
+@dataclass
+class PrefillCase:
+    """Packed prefill of one attention layer: segment s adds lengths[s] tokens after a prefix of starts[s] positions
+    already in the pool. q [N, Hq, d], k_new / v_new [N, Hkv, d], gate [N, Hq*d]; pool [NB, bs, Hkv, d];
+    tables [S, max_nb] int32 (each segment's blocks, non-contiguous, covering prefix + new tokens)."""
+    q: torch.Tensor
+    k_new: torch.Tensor
+    v_new: torch.Tensor
+    gate: torch.Tensor
+    k_pool: torch.Tensor
+    v_pool: torch.Tensor
+    tables: torch.Tensor
+    cu_seqlens: list
+    starts: list
+    block_size: int
+
+    def to(self, device) -> "PrefillCase":
+        f = lambda t: t.to(device)
+        return PrefillCase(f(self.q), f(self.k_new), f(self.v_new), f(self.gate), f(self.k_pool), f(self.v_pool),
+                           f(self.tables), list(self.cu_seqlens), list(self.starts), self.block_size)
+
+    def clone(self) -> "PrefillCase":
+        return PrefillCase(self.q, self.k_new, self.v_new, self.gate, self.k_pool.clone(), self.v_pool.clone(),
+                           self.tables, list(self.cu_seqlens), list(self.starts), self.block_size)
+
+    def lengths(self) -> list[int]:
+        return [b - a for a, b in zip(self.cu_seqlens, self.cu_seqlens[1:])]
+
+    def flops(self) -> int:
+        """QK^T and PV over the causal key range: sum over segments of 4 Hq d (n p + n (n + 1) / 2)."""
+        Hq, d = self.q.shape[1], self.q.shape[2]
+        return sum(4 * Hq * d * (n * p + n * (n + 1) // 2) for n, p in zip(self.lengths(), self.starts))
+
+    def hbm_bytes(self) -> int:
+        """Each segment's prefix + new K/V read once, the new rows written once, q / gate read and out written."""
+        Hkv, d = self.k_pool.shape[2], self.k_pool.shape[3]
+        e = self.k_pool.element_size()
+        row = 2 * Hkv * d * e
+        N, Hq = self.q.shape[0], self.q.shape[1]
+        return sum((n + p) * row + n * row for n, p in zip(self.lengths(), self.starts)) + \
+            N * Hq * d * (self.q.element_size() + self.gate.element_size() + 4)
+
+
+def prefill_case(lengths: list[int], starts: list[int], Hq: int = HQ, Hkv: int = HKV, d: int = HEAD_DIM,
+                 block_size: int = BLOCK, dtype=torch.bfloat16, seed: int = 0, slack: float = 1.25) -> PrefillCase:
+    gen = torch.Generator().manual_seed(seed)
+    nbs = [math.ceil((n + p) / block_size) for n, p in zip(lengths, starts)]
+    num_blocks = max(1, math.ceil(slack * sum(nbs)))
+    perm = torch.randperm(num_blocks, generator=gen).tolist()
+    tables = _tables_from_perm(perm, nbs)
+    N = sum(lengths)
+    r = lambda *s: torch.randn(*s, generator=gen).to(dtype)
+    q, k_new, v_new, gate = r(N, Hq, d), r(N, Hkv, d), r(N, Hkv, d), r(N, Hq * d)
+    k_pool, v_pool = r(num_blocks, block_size, Hkv, d), r(num_blocks, block_size, Hkv, d)
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    return PrefillCase(q, k_new, v_new, gate, k_pool, v_pool, tables, cu, list(starts), block_size)
+
+
+def c5_prefill(seed: int = 5) -> PrefillCase:
+    """Config 5: 8 segments, new lengths U[64, 2048], prefixes U[0, 16384], bf16 everything, 8/2 heads x 256,
+    block 16, sigmoid gate; the prefix K/V are the random pool contents under each segment's table."""
+    gen = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(64, 2049, (8,), generator=gen).tolist()
+    starts = torch.randint(0, 16385, (8,), generator=gen).tolist()
+    return prefill_case(lengths, starts, seed=seed + 1000)
