@@ -12,8 +12,9 @@ over the whole batch (split-K kernel + merge/gate kernel), inputs already reside
   cpu_baseline    the CPU oracle (TorchBackend.paged_attention + gate restated in torch fp32) on the same seeded
                   inputs, timed on this host's cores
 
-Other workloads (--workload c1 | c2) print the same record for the config-1 decode (parity/latency case) and the
-config-2 DeltaNet decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache).
+Other workloads print the same record for: c1, the config-1 decode (parity/latency case); c2, the config-2 DeltaNet
+decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache); c4, the config-4
+chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention.
 Timing: W untimed warm-up steps, then K timed steps captured in one HIP graph and replayed between two events
 after a device synchronize (the eager, Python-issued rate is reported beside it).
 """
@@ -312,12 +313,75 @@ def bench_prefill(args, backend):
     }
 
 
+def bench_chunked_delta(args, backend):
+    """Config 4: one packed call over 4 sequences x 4096 tokens (both kernels), captured in a HIP graph."""
+    import torch
+    import workloads as wl
+    from native import kernels
+    from native.rocm_native import load
+    from state import to_device
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    case = wl.c4_chunked_delta()
+    c = case.to(dev)
+    N, H, dk = case.q.shape
+    dv = case.v.shape[2]
+    cu = case.cu_seqlens
+    cuc = [0]
+    for a, b in zip(cu, cu[1:]):
+        cuc.append(cuc[-1] + -(-(b - a) // kernels.DELTA_CHUNK))
+    meta = to_device(torch.tensor(cu + cuc, dtype=torch.int32), dev)
+    lib = load()
+    ws = torch.empty(lib.lib.rk_gated_delta_workspace_bytes(cuc[-1], H), dtype=torch.uint8, device=dev)
+    out = torch.empty(N, H, dv, dtype=torch.float32, device=dev)
+    S = c.S.clone()
+    n = len(cu) - 1
+    torch.cuda.synchronize()
+
+    def step():      # the state is carried from step to step; its values do not change the work
+        lib.call("rk_gated_delta_chunked", out.data_ptr(), S.data_ptr(), S.stride(0), c.q.data_ptr(), c.k.data_ptr(),
+                 c.v.data_ptr(), 1, c.beta.data_ptr(), c.g.data_ptr(), meta.data_ptr(), meta.data_ptr() + 4 * (n + 1),
+                 None, n, cuc[-1], H, dk, dv, ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+
+    eager = time_region(step, args.steps, args.warmup, stream)
+    ms = graph_time(step, args.steps, stream)
+    flops = case.flops()
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = case.hbm_bytes() / (ms * 1e-3) / 1e9
+    log(f"[bench] c4: {ms * 1e3:.1f} us per packed call (eager {eager * 1e3:.1f} us), {tflops:.1f} TFLOP/s "
+        f"({tflops / 25:.1f}% of bf16 MFMA peak), {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import ops_ref
+        torch.set_num_threads(cpu_threads())
+        lo, hi = cu[0], cu[1]
+        f = lambda x: x[lo:hi].float()
+        t = cpu_time(lambda: ops_ref.gated_delta_chunked(f(case.q), f(case.k), f(case.v), f(case.beta), f(case.g),
+                                                         case.S[0].clone()), runs=1)
+        t_full = t * n
+        cpu = {"value": N / t_full, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"sequence 0 alone ({hi - lo} tokens, {H} heads), {t:.2f} s, times {n} sequences"}
+    return {
+        "metric": "chunked gated delta prefill tokens/s (config 4) + TFLOP/s (% of bf16 MFMA peak), 1 GPU",
+        "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded)",
+        "config": {"workload": "config 4: chunked gated delta rule, 4 x 4096 tokens packed, 16 heads, dk = dv = 128, "
+                               "chunk 64, bf16 inputs, fp32 state from zero", "tokens": N, "flops": flops,
+                   "hbm_bytes": case.hbm_bytes()},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s", "frac": tflops / 2500.0,
+                     "traffic": traffic_for("chunked_delta/c4"), "kernel": "delta_chunk_prep + delta_chunk_scan",
+                     "avg_ms": ms, "hbm_frac": gbs / HBM_PEAK_GBS},
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c5"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -350,6 +414,8 @@ def main() -> int:
         rec["dtype"] = "f32"
     elif args.workload == "c5":
         rec = bench_prefill(args, backend)
+    elif args.workload == "c4":
+        rec = bench_chunked_delta(args, backend)
     else:
         rec = bench_deltanet(args, backend)
     print(json.dumps(rec), flush=True)

@@ -105,6 +105,23 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
                      int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const float* gate, void* stream);
 
+/* ---- P3: chunked gated delta rule (64-token chunks, WY / UT form) for packed prefill of the linear-attention
+ * layers. Replaces Backend.gated_delta with T > 1 (TorchBackend.gated_delta -> ops.gated_delta_chunked,
+ * src/backend/torch_ref.py:52-56, src/ops.py:160-193; called per segment from src/models/qwen3_5.py:157), for any
+ * number of packed sequences in one call.
+ *   out [N, H, dv] fp32; q, k [N, H, dk], v [N, H, dv] in in_dtype (RK_F32 or RK_BF16; q already scaled);
+ *   beta, g [N, H] fp32; rows cu_seqlens[i] .. cu_seqlens[i+1]-1 are sequence i (device int32 [n_seqs + 1]);
+ *   cu_chunks (device int32 [n_seqs + 1]) = prefix sums of ceil(len_i / 64), total_chunks = cu_chunks[n_seqs].
+ *   State of sequence i: S + idx * s_stride (elements), [H, dk, dv] fp32, read as the initial state and
+ *   overwritten with the final state; idx = seq_index[i] (device int32 [n_seqs]) or i when seq_index is NULL.
+ *   workspace: rk_gated_delta_workspace_bytes(total_chunks, H) bytes (per-chunk coefficients and T); no zeroing.
+ * dk = dv = 128. fp32-level results: fp32 operands enter the bf16 MFMA as exact three-piece splits. */
+size_t rk_gated_delta_workspace_bytes(int total_chunks, int H);
+int rk_gated_delta_chunked(float* out, float* S, long long s_stride, const void* q, const void* k, const void* v,
+                           int in_dtype, const float* beta, const float* g, const int32_t* cu_seqlens,
+                           const int32_t* cu_chunks, const int32_t* seq_index, int n_seqs, int total_chunks, int H,
+                           int dk, int dv, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,6 +13,8 @@ Method -> kernel:
                          pool of one, src/backend/metal.py:232-256)
   paged_prefill_attention rk_paged_prefill (P4; the packed prefill of full_attention, src/models/qwen3_5.py:112-120:
                          KV write-back, causal attention over prefix + new tokens, fused gate)
+  gated_delta[_packed]   rk_gated_delta_chunked (P3; the chunked delta rule of the linear-attention prefill,
+                         src/models/qwen3_5.py:157, for one sequence or many packed sequences per launch pair)
 """
 import torch
 
@@ -78,6 +80,22 @@ class RocmBackend:
         kv.write -> kv.read -> attention(causal) -> gate (src/models/qwen3_5.py:112-120)."""
         return kernels.paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
                                      gate)
+
+    # ---- P3: chunked gated delta rule
+    def gated_delta(self, q, k, v, beta, g, S):
+        """Backend.gated_delta (src/backend/base.py:47-48): q, k [T, H, dk] (q already scaled), v [T, H, dv],
+        beta, g [T, H], S [H, dk, dv] -> (o [T, H, dv] fp32, new S fp32); the input state is left as it was. The
+        reference runs the chunked form for T > 1 and the recurrent form for T == 1 (src/backend/torch_ref.py:52-56);
+        both compute the same rule, and here both run the chunked kernel (one token is one partial chunk)."""
+        S_new = S.to(torch.float32).contiguous().clone().unsqueeze(0)
+        o = kernels.gated_delta_chunked(q, k, v, beta, g, S_new, [0, q.shape[0]])
+        return o, S_new[0]
+
+    def gated_delta_packed(self, q, k, v, beta, g, cu_seqlens, S, seq_index=None):
+        """gated_delta for several packed sequences in one launch pair (the model's packed prefill calls it once
+        per segment, src/models/qwen3_5.py:136-162): rows cu_seqlens[i] .. cu_seqlens[i+1]-1 are sequence i, whose
+        state S[seq_index[i]] (or S[i]) of the fp32 [n, H, dk, dv] states is updated in place -> o [N, H, dv]."""
+        return kernels.gated_delta_chunked(q, k, v, beta, g, S, cu_seqlens, seq_index)
 
     # ---- P2: DeltaNet decode step
     def deltanet_decode(self, qkv, z, b, a, state, slot, conv_w, A_log, dt_bias, norm_w, eps, dims):

@@ -223,3 +223,59 @@ def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos
                 meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq, Hkv, d, bs, NB,
                 gate.data_ptr() if gate is not None else None, _stream(dev))
     return out
+
+
+DELTA_CHUNK = 64            # tokens per chunk of rk_gated_delta_chunked
+
+
+def gated_delta_chunked(q, k, v, beta, g, S, cu_seqlens, seq_index=None, out=None) -> torch.Tensor:
+    """Chunked gated delta rule over packed sequences (rk_gated_delta_chunked) -> o [N, H, dv] fp32.
+    q, k [N, H, dk], v [N, H, dv] (bf16 all three, or anything else, taken as fp32; q already scaled);
+    beta, g [N, H]; cu_seqlens: host list / CPU tensor of n_seqs + 1 row offsets (as the packing step produces).
+    S: fp32 states, updated in place, indexed along dim 0 (each S[i] a contiguous [H, dk, dv]); sequence i uses
+    S[seq_index[i]] (seq_index: device int32 [n_seqs]) or S[i]."""
+    name = "gated_delta"
+    cu = [int(x) for x in cu_seqlens]
+    n_seqs = len(cu) - 1
+    if n_seqs < 1 or cu[0] != 0 or any(b < a for a, b in zip(cu, cu[1:])):
+        raise ValueError(f"{name}: cu_seqlens {cu[:8]}... must be n_seqs + 1 non-decreasing offsets from 0")
+    if q.dim() != 3 or k.shape != q.shape or v.dim() != 3 or v.shape[:2] != q.shape[:2]:
+        raise ValueError(f"{name}: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    N, H, dk = q.shape
+    dv = v.shape[2]
+    if cu[-1] != N or beta.shape != (N, H) or g.shape != (N, H):
+        raise ValueError(f"{name}: {N} rows, cu_seqlens end {cu[-1]}, beta {tuple(beta.shape)}, g {tuple(g.shape)}")
+    if S.dtype != torch.float32 or S.dim() != 4 or S.shape[1:] != (H, dk, dv) or \
+            S.stride()[1:] != (dk * dv, dv, 1):
+        raise ValueError(f"{name}: states {tuple(S.shape)} {S.dtype} must be fp32 [n, {H}, {dk}, {dv}] with "
+                         "contiguous inner dims")
+    if seq_index is None and S.shape[0] < n_seqs:
+        raise ValueError(f"{name}: {n_seqs} sequences but {S.shape[0]} states")
+    dev = _need_cuda(name, q, k, v, beta, g, S)
+    if seq_index is not None:
+        _need_cuda(name, seq_index)
+        if seq_index.dtype != torch.int32 or seq_index.numel() != n_seqs:
+            raise ValueError(f"{name}: seq_index must be int32 [{n_seqs}]")
+    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        q, k, v = q.float(), k.float(), v.float()
+    # rows are read as 16-byte vectors: a contiguous view at an odd offset is copied to a fresh (aligned) buffer
+    q, k, v = (x.contiguous() if x.is_contiguous() and x.data_ptr() % 16 == 0 else x.clone(
+        memory_format=torch.contiguous_format) for x in (q, k, v))
+    beta, g = beta.to(torch.float32).contiguous(), g.to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty(N, H, dv, dtype=torch.float32, device=dev)
+    if N == 0:
+        return out
+    cuc = [0]
+    for a, b in zip(cu, cu[1:]):
+        cuc.append(cuc[-1] + -(-(b - a) // DELTA_CHUNK))
+    from state import to_device
+    meta = to_device(torch.tensor(cu + cuc, dtype=torch.int32), dev)
+    lib = load()
+    nbytes = lib.lib.rk_gated_delta_workspace_bytes(cuc[-1], H)
+    ws = workspace(dev, nbytes)
+    lib.call("rk_gated_delta_chunked", out.data_ptr(), S.data_ptr(), S.stride(0), q.data_ptr(), k.data_ptr(),
+             v.data_ptr(), DTYPE_CODES[q.dtype], beta.data_ptr(), g.data_ptr(), meta.data_ptr(),
+             meta.data_ptr() + 4 * (n_seqs + 1), seq_index.data_ptr() if seq_index is not None else None, n_seqs,
+             cuc[-1], H, dk, dv, ws.data_ptr(), ws.numel(), _stream(dev))
+    return out

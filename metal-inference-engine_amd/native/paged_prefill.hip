@@ -339,11 +339,7 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     if (rc) return rc;
     const size_t lds = 2 * (size_t)(kBK * (D + kKPad) + D * (kBK + kVPad)) * sizeof(uint16_t);
     if (D == 256) {
-        static bool attr256 = false;
-        if (!attr256) {
-            hipFuncSetAttribute((const void*)prefill_attention<256>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            attr256 = true;
-        }
+        if (int rc2 = allow_dynamic_lds((const void*)prefill_attention<256>, lds)) return rc2;
         hipLaunchKernelGGL(prefill_attention<256>, dim3(n_work, Hkv), dim3(64 * a.G), lds, s, a);
     } else {
         hipLaunchKernelGGL(prefill_attention<128>, dim3(n_work, Hkv), dim3(64 * a.G), lds, s, a);

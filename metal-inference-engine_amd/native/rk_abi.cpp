@@ -4,6 +4,8 @@
 #include <string.h>
 
 #include <mutex>
+#include <set>
+#include <tuple>
 #include <unordered_map>
 
 #include "rk_internal.h"
@@ -12,6 +14,8 @@ namespace {
 thread_local char g_err[1024] = "";
 std::mutex g_cu_mutex;
 std::unordered_map<int, int> g_cus;
+std::mutex g_lds_mutex;
+std::set<std::tuple<int, const void*, size_t>> g_lds_set;
 }  // namespace
 
 namespace rk {
@@ -40,6 +44,21 @@ int device_cus() {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
     g_cus[dev] = n;
     return n;
+}
+
+int allow_dynamic_lds(const void* func, size_t bytes) {
+    if (bytes <= 65536) return RK_OK;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(RK_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_lds_mutex);
+    const auto key = std::make_tuple(dev, func, bytes);
+    if (g_lds_set.count(key)) return RK_OK;
+    e = hipFuncSetAttribute(func, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess)
+        return fail(RK_ERR_HIP, "hipFuncSetAttribute(max dynamic LDS %zu): %s", bytes, hipGetErrorString(e));
+    g_lds_set.insert(key);
+    return RK_OK;
 }
 
 }  // namespace rk

@@ -18,6 +18,9 @@ int check_launch(const char* what);
 // Compute units of the current device (cached per device id).
 int device_cus();
 
+// Raise the dynamic LDS limit of kernel `func` to `bytes` on the current device (once per device, kernel and size).
+int allow_dynamic_lds(const void* func, size_t bytes);
+
 inline size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
 
 }  // namespace rk

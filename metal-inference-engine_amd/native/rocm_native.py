@@ -5,7 +5,7 @@ status per call and an error string). Here the library holds no device, queue or
 raw device pointers of PyTorch tensors and the current HIP stream, and launches on it.
 """
 import ctypes
-from ctypes import c_char_p, c_float, c_int, c_size_t, c_void_p
+from ctypes import c_char_p, c_float, c_int, c_longlong, c_size_t, c_void_p
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
@@ -30,6 +30,9 @@ SIGNATURES = {
     "rk_kv_gather": (c_int, [P, P, P, P, c_int, P] + [c_int] * 7 + [P]),
     "rk_deltanet_decode": (c_int, [P] * 12 + [c_int] * 7 + [c_float, P]),
     "rk_paged_prefill": (c_int, [P, P, c_int, P, P, c_int, P, P, c_int, P, c_int, P, P, P] + [c_int] * 8 + [P, P]),
+    "rk_gated_delta_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "rk_gated_delta_chunked": (c_int, [P, P, c_longlong, P, P, P, c_int, P, P, P, P, P] + [c_int] * 5
+                               + [P, c_size_t, P]),
 }
 
 

@@ -229,3 +229,67 @@ def c5_prefill(seed: int = 5) -> PrefillCase:
     lengths = torch.randint(64, 2049, (8,), generator=gen).tolist()
     starts = torch.randint(0, 16385, (8,), generator=gen).tolist()
     return prefill_case(lengths, starts, seed=seed + 1000)
+
+
+@dataclass
+class ChunkedDeltaCase:
+    """Packed prefill of one linear-attention layer's delta rule: sequence i is rows cu_seqlens[i] ..
+    cu_seqlens[i+1]-1 of q, k [N, H, dk] (l2-normalised, q also * 1/sqrt(dk)), v [N, H, dv], beta, g [N, H] (fp32),
+    starting from state S [n_seqs, H, dk, dv] fp32."""
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    beta: torch.Tensor
+    g: torch.Tensor
+    S: torch.Tensor
+    cu_seqlens: list
+
+    def to(self, device) -> "ChunkedDeltaCase":
+        f = lambda t: t.to(device)
+        return ChunkedDeltaCase(f(self.q), f(self.k), f(self.v), f(self.beta), f(self.g), f(self.S),
+                                list(self.cu_seqlens))
+
+    def lengths(self) -> list[int]:
+        return [b - a for a, b in zip(self.cu_seqlens, self.cu_seqlens[1:])]
+
+    def chunks(self) -> int:
+        return sum(-(-n // 64) for n in self.lengths())
+
+    def flops(self) -> int:
+        """Algorithmic flops of the reference's chunked form per (chunk, head): five 64 x 64 x dk products (K K^T,
+        Q K^T, A V, A K, P vn), three 64 x dk x dv products (W S, Q S, K^T vn) and the 64^3 / 3 substitution."""
+        H, dk, dv = self.q.shape[1], self.q.shape[2], self.v.shape[2]
+        per = 5 * 2 * 64 * 64 * dk + 3 * 2 * 64 * dk * dv + 64 ** 3 // 3
+        return self.chunks() * H * per
+
+    def hbm_bytes(self) -> int:
+        """q, k, v and beta, g read once, o written once (fp32), the states read and written once."""
+        N, H, dk = self.q.shape
+        dv = self.v.shape[2]
+        return N * H * (2 * dk * self.q.element_size() + dv * self.v.element_size() + 2 * 4 + dv * 4) + \
+            2 * self.S.numel() * 4
+
+
+def chunked_delta_case(lengths: list[int], H: int = DN_HEADS, dtype=torch.bfloat16, seed: int = 0,
+                       state_scale: float = 0.0) -> ChunkedDeltaCase:
+    """q, k ~ N(0,1) l2-normalised (q then * 1/sqrt(dk)), v ~ N(0,1), all stored in dtype; beta = sigmoid(N);
+    g = -softplus(N); S0 = state_scale * N (0: zero state)."""
+    gen = torch.Generator().manual_seed(seed)
+    N = sum(lengths)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    l2 = lambda x: x * torch.rsqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    q = (l2(r(N, H, DN_DK)) * (1.0 / math.sqrt(DN_DK))).to(dtype)
+    k = l2(r(N, H, DN_DK)).to(dtype)
+    v = r(N, H, DN_DV).to(dtype)
+    beta = torch.sigmoid(r(N, H))
+    g = -torch.nn.functional.softplus(r(N, H))
+    S = r(len(lengths), H, DN_DK, DN_DV) * state_scale
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    return ChunkedDeltaCase(q, k, v, beta, g, S, cu)
+
+
+def c4_chunked_delta(seed: int = 4) -> ChunkedDeltaCase:
+    """Config 4: batch 4 x 4096 tokens, 16 heads, dk = dv = 128, bf16 inputs, fp32 state starting at zero."""
+    return chunked_delta_case([4096] * 4, seed=seed)

@@ -89,6 +89,28 @@ def delta_rule():
              S_hf_chunked=S_c[0].numpy())
 
 
+def delta_rule_128():
+    """The kernel's shape: T = 70 (one full chunk + 6 tokens), 1 head, dk = dv = 128, nonzero S0. Inputs are
+    bf16-representable (stored as bf16 bit patterns, uint16), so the same values feed the bf16 and fp32 kernel paths;
+    expected values from the float64 brute force, rounded to fp32."""
+    rng = np.random.default_rng(106)
+    T, H, dk, dv = 70, 1, 128, 128
+    to_bf16 = lambda a: (torch.tensor(a, dtype=torch.float32).to(torch.bfloat16).view(torch.int16).numpy()
+                         .view(np.uint16))
+    from_bf16 = lambda b: (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    l2 = lambda x: x / np.sqrt((x ** 2).sum(-1, keepdims=True) + 1e-6)
+    q = to_bf16(l2(rng.standard_normal((T, H, dk))) / np.sqrt(dk))
+    k = to_bf16(l2(rng.standard_normal((T, H, dk))))
+    v = to_bf16(rng.standard_normal((T, H, dv)))
+    S0 = to_bf16(rng.standard_normal((H, dk, dv)) * 0.1)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((T, H))))).astype(np.float32)
+    g = (-np.log1p(np.exp(rng.standard_normal((T, H))))).astype(np.float32)
+    o, S = brute.delta_rule(from_bf16(q), from_bf16(k), from_bf16(v), beta.astype(np.float64), g.astype(np.float64),
+                            from_bf16(S0))
+    np.savez(OUT / "delta_rule_128.npz", q_bf16=q, k_bf16=k, v_bf16=v, S0_bf16=S0, beta=beta, g=g,
+             out=o.astype(np.float32), S=S.astype(np.float32))
+
+
 def deltanet_step():
     """One decode step of a small DeltaNet layer (H 2, dk = dv = 8, conv 4 over 2*16 + 16 = 48 channels)."""
     rng = np.random.default_rng(104)
@@ -119,6 +141,6 @@ def conv():
 
 
 if __name__ == "__main__":
-    for f in (paged_decode, prefill_attention, delta_rule, deltanet_step, conv):
+    for f in (paged_decode, prefill_attention, delta_rule, delta_rule_128, deltanet_step, conv):
         f()
         print("wrote", f.__name__)

@@ -27,11 +27,11 @@ def kind(param: str) -> str:
     if "*" in param:
         return "char*" if param.startswith("char") else "ptr"
     t = param.rsplit(" ", 1)[0]
-    return {"int": "int", "size_t": "size_t", "float": "float"}[t]
+    return {"int": "int", "size_t": "size_t", "float": "float", "long long": "long long"}[t]
 
 
 CTYPE_KIND = {ctypes.c_void_p: "ptr", ctypes.c_char_p: "char*", ctypes.c_int: "int", ctypes.c_size_t: "size_t",
-              ctypes.c_float: "float"}
+              ctypes.c_float: "float", ctypes.c_longlong: "long long"}
 
 
 @pytest.fixture(scope="module")
@@ -104,3 +104,21 @@ def test_workspace_size_formula(lib):
     n = lib.lib.rk_paged_decode_workspace_bytes(64, 8, 2, 256, 16, 512)
     assert n > 0 and n % (4 * (256 + 2) * 4) == 0
     assert lib.lib.rk_paged_decode_workspace_bytes(0, 8, 2, 256, 16, 512) == 0
+
+
+def test_gated_delta_arguments_checked_on_host(lib):
+    fake = 4096
+    ws = lib.lib.rk_gated_delta_workspace_bytes(256, 16)
+    assert ws == 256 * 16 * (10 * 256 + 4 * 64) * 4 and lib.lib.rk_gated_delta_workspace_bytes(-1, 16) == 0
+
+    def call(**kw):
+        a = dict(out=fake, S=fake, stride=16 * 128 * 128, q=fake, k=fake, v=fake, dt=1, beta=fake, g=fake, cu=fake,
+                 cuc=fake, idx=None, n=4, chunks=256, H=16, dk=128, dv=128, ws=fake, wsb=ws)
+        a.update(kw)
+        return lib.lib.rk_gated_delta_chunked(*a.values(), None)
+
+    assert call(q=None) == 1 and "null pointer" in lib.last_error()
+    assert call(dk=64) == 2 and "dk 64" in lib.last_error()
+    assert call(dt=7) == 2 and "dtype" in lib.last_error()
+    assert call(stride=128) == 1 and "stride" in lib.last_error()
+    assert call(wsb=ws - 1) == 3 and "workspace" in lib.last_error()

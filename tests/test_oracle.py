@@ -139,6 +139,15 @@ def test_chunked_matches_brute_and_transformers():
     assert rel_err(o, f["out_hf_chunked"]) < 1e-5 and rel_err(S, f["S_hf_chunked"]) < 1e-5
 
 
+def test_chunked_matches_brute_at_kernel_shape():
+    """dk = dv = 128 with bf16-representable inputs (the fixture the GPU kernel is also checked against)."""
+    f = np.load(GOLD / "delta_rule_128.npz")
+    wide = lambda b: torch.from_numpy((b.astype(np.uint32) << 16).view(np.float32))
+    o, S = ops_ref.gated_delta_chunked(wide(f["q_bf16"]), wide(f["k_bf16"]), wide(f["v_bf16"]), t(f["beta"]),
+                                       t(f["g"]), wide(f["S0_bf16"]))
+    assert rel_err(o, f["out"]) < 1e-5 and rel_err(S, f["S"]) < 1e-5
+
+
 @pytest.mark.parametrize("T", [1, 63, 64, 65, 130])
 def test_chunked_equals_recurrent(T):
     g_ = torch.Generator().manual_seed(T)
