@@ -13,18 +13,25 @@
 //
 // Two kernels:
 //   delta_chunk_prep  one workgroup per (chunk, head), all chunks in parallel: beta, G (summed in fp64 and rounded
-//                     once, as torch's CPU cumsum of fp32 accumulates in double), exp(G), exp(G_last - G); the Gram
-//                     matrix K K^T on MFMA; T by blocked inversion of the unit lower triangular matrix (16 x 16
-//                     diagonal blocks by substitution, off-diagonal blocks by fp32 MFMA products in three levels).
-//                     Writes T's ten lower 16 x 16 tiles and the coefficient rows to the workspace.
-//   delta_chunk_scan  one workgroup per (sequence, head, 16-column slice of S): the columns of S evolve
-//                     independently, so the serial pass over a sequence's chunks runs 8 workgroups wide per head.
-//                     Wave w owns token rows 16w..16w+15 of the chunk and state rows 32w..32w+31; the three
-//                     exchanges per chunk (state pieces, Y, vn) go through LDS behind LDS-only barriers, so the next
-//                     chunk's global loads stay in flight across them.
+//                     once, as torch's CPU cumsum of fp32 accumulates in double), exp(G), exp(G_last - G); K K^T and
+//                     Q K^T on MFMA from K rows staged in LDS; P = Q K^T * D; T by blocked inversion of the unit lower
+//                     triangular matrix (16 x 16 diagonal blocks by substitution, off-diagonal blocks by fp32 MFMA
+//                     products in three levels). T and P go to the workspace already split into bf16 pieces, in the
+//                     operand order the scan loads, so the 8 scan workgroups of a head share them instead of each
+//                     recomputing them.
+//   delta_chunk_scan  one workgroup per (sequence, head, 32-column slice of S): the columns of S evolve
+//                     independently, so the serial pass over a sequence's chunks runs 4 workgroups wide per head.
+//                     Wave w owns token rows 16w..16w+15 of the chunk and state rows 32w..32w+31 (two 16-column
+//                     tiles sharing every A operand: the K / Q / T / P bytes a CU pulls from L2 per chunk, which
+//                     bound this kernel, are spread over 32 columns); the three
+//                     exchanges per chunk (state pieces, Y, vn) go through LDS behind LDS-only barriers. Everything
+//                     chunk c+1 reads from global memory (K, Q, V rows, coefficients, T and P pieces) is requested at
+//                     the start of chunk c, so memory latency hides behind a whole chunk of work.
 // Precision: every product with an fp32 operand (S, Y, vn, T, P, fp32 inputs) runs on bf16 MFMA with that operand
 // split exactly into three bf16 pieces (truncation) and the piece products of order >= 2^-16 kept; bf16 inputs are
 // exact operands. Products are therefore exact to ~2^-20 relative and accumulate in fp32: fp32-level results.
+#include <type_traits>
+
 #include "rk_device.h"
 #include "rk_internal.h"
 
@@ -33,12 +40,16 @@ namespace {
 
 constexpr int kC = 64;                       // tokens per chunk
 constexpr int kDk = 128, kDv = 128;
-constexpr int kCols = 16;                    // state columns per scan workgroup
-constexpr int kSlices = kDv / kCols;         // 8
-constexpr int kNS = 3;                       // bf16 pieces of an fp32 operand
-constexpr int kTiles = 10;                   // lower 16 x 16 tiles of a 64 x 64 matrix
+constexpr int kCT = 2;                       // 16-column tiles of the state per scan wave
+constexpr int kCols = 16 * kCT;              // state columns per scan workgroup
+constexpr int kSlices = kDv / kCols;         // 4
+constexpr int kNS = 3;                       // bf16 pieces of an fp32 operand that changes with the state
+// bf16 pieces of the stored T and P entries: 3 = exact (truncation); 2 = round to nearest (2^-17), which saves a
+// third of the workspace traffic (6% of the call at config 4) but raises the output error ~10x, to ~5e-6
+constexpr int kTP = 3;
 constexpr int kCoefRows = 4;                 // beta, G, exp(G), exp(G_last - G)
-constexpr int kChunkFloats = kTiles * 256 + kCoefRows * kC;
+// per (chunk, head): T and P as kTP bf16 pieces of 3072 elements each, then the coefficient rows
+constexpr int kChunkFloats = 2 * kTP * 3072 / 2 + kCoefRows * kC;
 constexpr int kPieceRow = kC + 8;            // bf16 row stride of the [piece][column][token] exchange arrays
 constexpr int kStateRow = kDk + 8;           // bf16 row stride of the [piece][column][dk] state pieces
 
@@ -53,7 +64,7 @@ struct DeltaArgs {
     const int32_t* cu;          // [n_seqs + 1] token offsets
     const int32_t* cu_chunks;   // [n_seqs + 1] chunk offsets (ceil(len / 64) per sequence)
     const int32_t* seq_index;   // [n_seqs] state index of each sequence, or null for 0 .. n_seqs-1
-    float* ws;                  // [total_chunks, H, kChunkFloats]
+    float* ws;                  // [total_chunks, H] records of kChunkFloats floats
     long long s_stride;
     int n_seqs, H, n_pairs;
 };
@@ -61,9 +72,8 @@ struct DeltaArgs {
 // ---- operands: 8 consecutive elements of one row per lane, as bf16 pieces
 __device__ __forceinline__ uint32_t mask_if(bool keep) { return keep ? 0xffffffffu : 0u; }
 __device__ __forceinline__ float to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+__device__ __forceinline__ float to_f32(uint32_t x) { return __uint_as_float(x << 16); }   // bf16 bits, zero-extended
 __device__ __forceinline__ float to_f32(float x) { return x; }
-// Index of lower tile (a, b), b <= a, of a 64 x 64 matrix stored as its ten 16 x 16 lower tiles.
-__host__ __device__ constexpr int tile_of(int a, int b) { return a * (a + 1) / 2 + b; }
 
 template <typename In> struct Row8;
 template <> struct Row8<uint16_t> {            // bf16 input: one exact piece
@@ -99,6 +109,20 @@ __device__ __forceinline__ void split8(const float (&x)[8], u32x4 (&o)[kNS]) {
         o[0][j] = pack_hi2(s0.hi, s1.hi);
         o[1][j] = pack_hi2(s0.mid, s1.mid);
         o[2][j] = pack_hi2(s0.lo, s1.lo);
+    }
+}
+// Two-piece split of 4 fp32 values, rounding to nearest at both steps: x = hi + lo + e with |e| <= 2^-17 |x|.
+__device__ __forceinline__ void split4_rn(const float (&x)[4], u32x2 (&o)[kTP]) {
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        hi[e] = f32_to_bf16_rne(x[e]);
+        lo[e] = f32_to_bf16_rne(x[e] - __uint_as_float(hi[e] << 16));
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        o[0][j] = hi[2 * j] | (hi[2 * j + 1] << 16);
+        o[1][j] = lo[2 * j] | (lo[2 * j + 1] << 16);
     }
 }
 // Split of 4 fp32 values: kNS pieces of 4 bf16 each (2 dwords).
@@ -151,14 +175,41 @@ __device__ __forceinline__ int seq_of_chunk(const DeltaArgs& p, int gc) {
     return lo;
 }
 
+// Per-chunk workspace record (floats): T and P as kNS bf16 pieces each, in the operand order the scan reads, then the
+// coefficient rows. Row tile a (rows 16a .. 16a+15) keeps columns 0 .. rt_width(a)-1, the 32-token k-steps that reach
+// its diagonal: 32, 32, 64, 64 columns (3072 elements per piece).
+__host__ __device__ constexpr int rt_width(int a) { return a < 2 ? 32 : 64; }
+__host__ __device__ constexpr int rt_base(int a) { return a == 0 ? 0 : (a == 1 ? 512 : (a == 2 ? 1024 : 2048)); }
+constexpr int kPieceElems = 3072;                                  // bf16 elements of one piece of T or P
+constexpr int kTOff = 0;                                           // T pieces   (uint16 offset)
+constexpr int kPOff = kTP * kPieceElems;                           // P pieces   (uint16 offset)
+constexpr int kCoefOff = kTP * kPieceElems;                        // coefficients (float offset: after 2 x kTP pieces)
+
 // =====================================================================================================================
-// Phase 1: per-chunk coefficients and T
+// Phase 1: per-chunk coefficients, T and P
 // =====================================================================================================================
 template <typename In>
+struct PrepStage {
+    static constexpr int kRow = kDk + (sizeof(In) == 2 ? 8 : 4);
+};
+
+// split 4 fp32 values and store them as kTP pieces of 4 bf16 at dst + piece * kPieceElems
+__device__ __forceinline__ void store_pieces4(uint16_t* dst, const float (&x)[4]) {
+    u32x2 pc[kTP];
+    if constexpr (kTP == kNS) split4(x, pc); else split4_rn(x, pc);
+#pragma unroll
+    for (int pi = 0; pi < kTP; ++pi) *reinterpret_cast<u32x2*>(dst + pi * kPieceElems) = pc[pi];
+}
+
+template <typename In>
 __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
-    __shared__ float sA[kC][kC + 1];       // -beta_i (K K^T)_ij D_ij, strictly lower (read only below the diagonal)
-    __shared__ float sT[kC][kC + 1];       // T, lower triangle
-    __shared__ float sTmp[4][16][17];      // per-wave 16 x 16 scratch
+    using St = PrepStage<In>;
+    __shared__ float sA[kC][kC + 1];                       // A0 = -beta_i (K K^T)_ij D_ij below the diagonal
+    __shared__ __align__(16) char sKT[kC * St::kRow * sizeof(In) > kC * (kC + 1) * 4
+                                          ? kC * St::kRow * sizeof(In) : kC * (kC + 1) * 4];
+    __shared__ float sTmp[4][16][17];                      // per-wave 16 x 16 scratch
+    In* sK = reinterpret_cast<In*>(sKT);                   // K rows of the chunk, until the Gram products are done
+    float (*sT)[kC + 1] = reinterpret_cast<float (*)[kC + 1]>(sKT);   // then T
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, r = lane & 15;
     const int gc = blockIdx.x, h = blockIdx.y, H = p.H;
@@ -167,60 +218,86 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     const int nt = min(kC, p.cu[s + 1] - t0);
     if (nt <= 0) return;                  // offsets inconsistent with cu_chunks: nothing of this chunk is read
     const In* K = static_cast<const In*>(p.k);
+    const In* Q = static_cast<const In*>(p.q);
 
-    // K rows of row tile w (A operand); issued first
-    Row8<In> ka[4];
+    // K and Q rows of row tile w, zero past the sequence's end; all loads issued up front
+    Row8<In> ka[4], qa[4];
     {
         const int t = 16 * w + r;
         const long long off = ((long long)(t0 + min(t, nt - 1)) * H + h) * kDk + 8 * q;
+        const uint32_t m = mask_if(t < nt);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             ka[k].load(K + off + 32 * k);
-            ka[k].keep(mask_if(t < nt));
+            qa[k].load(Q + off + 32 * k);
+            ka[k].keep(m);
+            qa[k].keep(m);
         }
     }
-
-    // beta and the cumulative log-decay of the chunk, one token per lane (every wave keeps its own copy)
     const bool live = lane < nt;
     const long long ti = (long long)(t0 + min(lane, nt - 1)) * H + h;
     const float bl = live ? p.beta[ti] : 0.f;
-    double acc = live ? (double)p.g[ti] : 0.0;
+    const float gl = live ? p.g[ti] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        In* dst = sK + (16 * w + r) * St::kRow + 32 * k + 8 * q;
+        if constexpr (sizeof(In) == 2) {
+            *reinterpret_cast<u32x4*>(dst) = ka[k].v;
+        } else {
+            *reinterpret_cast<f32x4*>(dst) = ka[k].a;
+            *reinterpret_cast<f32x4*>(dst + 4) = ka[k].b;
+        }
+    }
+    // cumulative log-decay of the chunk, one token per lane (every wave keeps its own copy)
+    double acc = gl;
 #pragma unroll
     for (int off = 1; off < kC; off <<= 1) {
         const double y = __shfl_up(acc, off);
         if (lane >= off) acc += y;
     }
     const float G = (float)acc;
-
-    // A0 tiles (w, b), b <= w: -beta_i * (K K^T)_ij * exp(G_i - G_j) for j < i
-    float Gi[4], bi[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        Gi[i] = __shfl(G, 16 * w + 4 * q + i);
-        bi[i] = __shfl(bl, 16 * w + 4 * q + i);
-    }
-    for (int b = 0; b <= w; ++b) {
-        const int t = 16 * b + r;
-        const long long off = ((long long)(t0 + min(t, nt - 1)) * H + h) * kDk + 8 * q;
-        f32x4 kk = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            Row8<In> kb;
-            kb.load(K + off + 32 * k);
-            kb.keep(mask_if(t < nt));
-            u32x4 pa[Row8<In>::KP], pb[Row8<In>::KP];
-            ka[k].pieces(pa);
-            kb.pieces(pb);
-            kk = mma(pa, pb, kk);
-        }
-        const float Gj = __shfl(G, t);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 16 * w + 4 * q + i;
-            sA[row][t] = t < row ? -(bi[i] * kk[i]) * expf(Gi[i] - Gj) : 0.f;
-        }
-    }
     lds_barrier();
+
+    // Tiles (b, w) of K K^T and of P^T = K Q^T (A = K rows of tile b from LDS, B = this wave's K / Q rows): lane (q, r)
+    // holds entries (t', t) = (16b + 4q + i, 16w + r), i.e. row t of A0 and P at columns t'.
+    uint16_t* ws16 = reinterpret_cast<uint16_t*>(p.ws + ((size_t)gc * H + h) * kChunkFloats);
+    const float Gt = __shfl(G, 16 * w + r), bt = __shfl(bl, 16 * w + r);
+    const int t = 16 * w + r;
+    for (int b = 0; b < 2 * ((w >> 1) + 1); ++b) {
+        float pv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (b <= w) {
+            f32x4 kk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                Row8<In> kb;
+                const In* src = sK + (16 * b + r) * St::kRow + 32 * k + 8 * q;
+                if constexpr (sizeof(In) == 2) {
+                    kb.v = *reinterpret_cast<const u32x4*>(src);
+                } else {
+                    kb.a = *reinterpret_cast<const f32x4*>(src);
+                    kb.b = *reinterpret_cast<const f32x4*>(src + 4);
+                }
+                u32x4 pa[Row8<In>::KP], pb[Row8<In>::KP];
+                kb.pieces(pa);
+                ka[k].pieces(pb);
+                kk = mma(pa, pb, kk);
+                qa[k].pieces(pb);
+                pq = mma(pa, pb, pq);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tp = 16 * b + 4 * q + i;
+                const float Gp = __shfl(G, tp);
+                // masked before exp; exp(x) as 2^(x log2 e) on v_exp_f32: within ~1e-6 relative for the
+                // |x| < 20 that carry weight (the rounding of x log2 e is |x| 2^-24)
+                const float d = tp <= t ? fast_exp2((Gt - Gp) * kLog2e) : 0.f;
+                sA[t][tp] = tp < t ? -(bt * kk[i]) * d : 0.f;
+                pv[i] = pq[i] * d;
+            }
+        }
+        store_pieces4(ws16 + kPOff + rt_base(w) + r * rt_width(w) + 16 * b + 4 * q, pv);
+    }
+    lds_barrier();                         // sK is dead from here: its space holds T
 
     // diagonal block w of T = (I - A0)^-1: lane r keeps column r, rows by forward substitution
     {
@@ -238,17 +315,17 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     }
     lds_barrier();
 
-    // off-diagonal blocks, one level of distance d = w - j at a time: T_wj = T_ww * sum_{k=j}^{w-1} A0_wk T_kj
+    // off-diagonal blocks, one distance d = w - j at a time: T_wj = T_ww * sum_{k=j}^{w-1} A0_wk T_kj
     for (int d = 1; d < 4; ++d) {
         if (w >= d) {
             const int j = w - d;
-            f32x4 t = {0.f, 0.f, 0.f, 0.f};
+            f32x4 tt = {0.f, 0.f, 0.f, 0.f};
             for (int kb = j; kb < w; ++kb)
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
-                    t = mfma_f32(sA[16 * w + r][16 * kb + 4 * ks + q], sT[16 * kb + 4 * ks + q][16 * j + r], t);
+                    tt = mfma_f32(sA[16 * w + r][16 * kb + 4 * ks + q], sT[16 * kb + 4 * ks + q][16 * j + r], tt);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sTmp[w][4 * q + i][r] = t[i];
+            for (int i = 0; i < 4; ++i) sTmp[w][4 * q + i][r] = tt[i];
             wave_lds_sync();
             f32x4 u = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -260,17 +337,21 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
         lds_barrier();
     }
 
-    float* wsc = p.ws + ((size_t)gc * H + h) * kChunkFloats;
+    // T pieces, row-tile blocks as for P; entries above the diagonal are zero
 #pragma unroll
-    for (int tile = 0; tile < kTiles; ++tile) {
-        const int a = tile < 1 ? 0 : (tile < 3 ? 1 : (tile < 6 ? 2 : 3));
-        const int b = tile - tile_of(a, 0);
-        const int e = threadIdx.x;
-        wsc[tile * 256 + e] = sT[16 * a + (e >> 4)][16 * b + (e & 15)];
+    for (int it = 0; it < kPieceElems / 4 / 256; ++it) {
+        const int off = 4 * (threadIdx.x + 256 * it);
+        const int a = off < 512 ? 0 : (off < 1024 ? 1 : (off < 2048 ? 2 : 3));
+        const int rel = off - rt_base(a);
+        const int row = 16 * a + rel / rt_width(a), col = rel % rt_width(a);
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = col + e <= row ? sT[row][col + e] : 0.f;
+        store_pieces4(ws16 + kTOff + off, x);
     }
     if (w == 0) {
         const float Glast = __shfl(G, kC - 1);
-        float* cf = wsc + kTiles * 256;
+        float* cf = p.ws + ((size_t)gc * H + h) * kChunkFloats + kCoefOff;
         cf[lane] = bl;
         cf[kC + lane] = G;
         cf[2 * kC + lane] = expf(G);
@@ -283,14 +364,12 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
 // =====================================================================================================================
 template <typename In>
 struct ScanLayout {
-    static constexpr int kKr = kDk + (sizeof(In) == 2 ? 8 : 4);   // row stride of staged K rows [token][dk]
     static constexpr int kKt = kC + (sizeof(In) == 2 ? 8 : 4);    // row stride of staged K^T [dk][token]
     static constexpr size_t sp = 0;                                               // state pieces
     static constexpr size_t yp = sp + (size_t)kNS * kCols * kStateRow * 2;        // Y pieces
     static constexpr size_t vp = yp + (size_t)kNS * kCols * kPieceRow * 2;        // vn pieces
     static constexpr size_t vq = vp + (size_t)kNS * kCols * kPieceRow * 2;        // exp(G_last - G) vn pieces
-    static constexpr size_t kr = vq + (size_t)kNS * kCols * kPieceRow * 2;        // K rows
-    static constexpr size_t kt = kr + (size_t)kC * kKr * sizeof(In);              // K^T
+    static constexpr size_t kt = vq + (size_t)kNS * kCols * kPieceRow * 2;        // K^T
     static constexpr size_t bytes = kt + (size_t)kDk * kKt * sizeof(In);
 };
 
@@ -298,7 +377,7 @@ template <typename In, int W>
 __device__ __forceinline__ void scan_wave(const DeltaArgs& p, char* lds, int s, int h, int slice) {
     using L = ScanLayout<In>;
     constexpr int KP = Row8<In>::KP;
-    constexpr int KS = (W >> 1) + 1;      // 32-token k-steps of T and P below the diagonal for row tile W
+    constexpr int KS = (W >> 1) + 1;      // 32-token k-steps of T and P that reach row tile W's diagonal
     const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
     const int H = p.H;
     const int T0 = p.cu[s], Tn = p.cu[s + 1] - T0;
@@ -316,254 +395,271 @@ __device__ __forceinline__ void scan_wave(const DeltaArgs& p, char* lds, int s, 
     uint16_t* yp = reinterpret_cast<uint16_t*>(lds + L::yp);
     uint16_t* vp = reinterpret_cast<uint16_t*>(lds + L::vp);
     uint16_t* vq = reinterpret_cast<uint16_t*>(lds + L::vq);
-    In* kr = reinterpret_cast<In*>(lds + L::kr);
     In* kt = reinterpret_cast<In*>(lds + L::kt);
+    // [piece][column][row] exchange arrays: element (row, column 16 ct + r) of piece pi
+    auto xrow = [&](uint16_t* base, int stride, int pi, int ct) { return base + (pi * kCols + 16 * ct + r) * stride; };
 
-    // state rows 32W + 16u + 4q + i, column col0 + r (MFMA accumulator layout of the update)
-    f32x4 st[2];
+    // state rows 32W + 16u + 4q + i, columns col0 + 16ct + r (MFMA accumulator layout of the update)
+    f32x4 st[2][kCT];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st[u][i] = Sg[(32 * W + 16 * u + 4 * q + i) * kDv + r];
-
-    // K and Q rows 16W + r of chunk c (columns 32k + 8q .. +7), zero past the sequence's end
-    auto load_rows = [&](int c, Row8<In> (&kk)[4], Row8<In> (&qq)[4]) {
-        const int nt = min(kC, Tn - c * kC);
-        const int t = 16 * W + r;
-        const long long off = ((long long)(T0 + c * kC + min(t, nt - 1)) * H + h) * kDk + 8 * q;
-        const uint32_t m = mask_if(t < nt);
+        for (int ct = 0; ct < kCT; ++ct)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            kk[k].load(Kg + off + 32 * k);
-            qq[k].load(Qg + off + 32 * k);
-            kk[k].keep(m);
-            qq[k].keep(m);
-        }
-    };
-    Row8<In> ka[4], qa[4];
-    load_rows(0, ka, qa);
+            for (int i = 0; i < 4; ++i) st[u][ct][i] = Sg[(32 * W + 16 * u + 4 * q + i) * kDv + 16 * ct + r];
 
-    for (int c = 0; c < nch; ++c) {
+    using VRaw = typename std::conditional<sizeof(In) == 2, uint32_t, float>::type;
+    // What row tile W of chunk c needs first, loaded one chunk ahead: K and Q rows 16W + r (columns 32k + 8q .. +7,
+    // zero past the sequence's end), the values at rows 16W + 4q + i and the coefficients of those rows.
+    struct Ahead {
+        Row8<In> k[4], q[4];                // raw rows; zeroed past the sequence's end by finish()
+        uint32_t keep;
+        VRaw v[kCT][4];                     // values as loaded (bf16 bits zero-extended, or fp32)
+        float beta, eg, egr;                // row 16W + (lane & 15); rows 16W + 4q + i come by shuffle
+        float glast;
+        u32x4 ta[KS][kTP], pa[KS][kTP];     // T and P pieces of row tile W (A operands, k-steps 0 .. KS-1)
+    };
+    auto load_ahead = [&](int c, Ahead& a) {
         const int nt = min(kC, Tn - c * kC);
         const int tc = T0 + c * kC;
-        const float* wsc = p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats;
-        const float* cf = wsc + kTiles * 256;
-
-        // ---- loads of this chunk's T tiles, values and coefficients; next chunk's K / Q rows
-        float tv[KS][8];
+        const int t = 16 * W + r;
+        const long long off = ((long long)(tc + min(t, nt - 1)) * H + h) * kDk + 8 * q;
+        a.keep = mask_if(t < nt);
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const int b = 2 * k + (q >> 1);
-            const int bc = b <= W ? b : W;
-            const float* tp = wsc + tile_of(W, bc) * 256 + r * 16 + 8 * (q & 1);
-            const f32x4 lo = *reinterpret_cast<const f32x4*>(tp);
-            const f32x4 hi = *reinterpret_cast<const f32x4*>(tp + 4);
-            const uint32_t m = mask_if(b <= W);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                tv[k][e] = __uint_as_float(__float_as_uint(lo[e]) & m);
-                tv[k][4 + e] = __uint_as_float(__float_as_uint(hi[e]) & m);
-            }
+        for (int k = 0; k < 4; ++k) {
+            a.k[k].load(Kg + off + 32 * k);
+            a.q[k].load(Qg + off + 32 * k);
         }
-        float vv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = min(16 * W + 4 * q + i, nt - 1);
-            vv[i] = to_f32(Vg[((long long)(tc + t) * H + h) * kDv + col0 + r]);
-        }
-        const f32x4 beta4 = *reinterpret_cast<const f32x4*>(cf + 16 * W + 4 * q);
-        const f32x4 eg4 = *reinterpret_cast<const f32x4*>(cf + 2 * kC + 16 * W + 4 * q);
-        const f32x4 egr4 = *reinterpret_cast<const f32x4*>(cf + 3 * kC + 16 * W + 4 * q);
-        const float Gt = cf[kC + 16 * W + r];
-        f32x4 Gq[W + 1];
+            const int tv = min(16 * W + 4 * q + i, nt - 1);
+            const In* vrow = Vg + ((long long)(tc + tv) * H + h) * kDv + col0 + r;
 #pragma unroll
-        for (int b = 0; b <= W; ++b) Gq[b] = *reinterpret_cast<const f32x4*>(cf + kC + 16 * b + 4 * q);
-        const float glast = cf[2 * kC + kC - 1];
-        Row8<In> kn[4], qn[4];
-        load_rows(c + 1 < nch ? c + 1 : c, kn, qn);
+            for (int ct = 0; ct < kCT; ++ct) a.v[ct][i] = (VRaw)vrow[16 * ct];
+        }
+        const float* cf = p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats + kCoefOff;
+        a.beta = cf[16 * W + r];
+        a.eg = cf[2 * kC + 16 * W + r];
+        a.egr = cf[3 * kC + 16 * W + r];
+        a.glast = cf[2 * kC + kC - 1];
+        const uint16_t* ws16 = reinterpret_cast<const uint16_t*>(p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats);
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+#pragma unroll
+            for (int pi = 0; pi < kTP; ++pi) {
+                const int e = rt_base(W) + r * rt_width(W) + 32 * k + 8 * q + pi * kPieceElems;
+                a.ta[k][pi] = *reinterpret_cast<const u32x4*>(ws16 + kTOff + e);
+                a.pa[k][pi] = *reinterpret_cast<const u32x4*>(ws16 + kPOff + e);
+            }
+    };
+    // An empty asm that takes every register of `a` as input and output: the loads behind them complete at this
+    // point, and everything computed from them comes after it. Placed before a chunk's output stores, it keeps the
+    // compiler from deferring (or hoisting) that wait: gfx950 counts loads and stores in one in-order counter, so a
+    // wait placed after the stores would also wait for the stores.
+    auto resident = [](Ahead& a) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (sizeof(In) == 2) {
+                asm volatile("" : "+v"(a.k[k].v), "+v"(a.q[k].v));
+            } else {
+                asm volatile("" : "+v"(a.k[k].a), "+v"(a.k[k].b), "+v"(a.q[k].a), "+v"(a.q[k].b));
+            }
+            a.k[k].keep(a.keep);
+            a.q[k].keep(a.keep);
+        }
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(a.v[ct][i]));
+        asm volatile("" : "+v"(a.beta), "+v"(a.eg), "+v"(a.egr), "+v"(a.glast));
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+#pragma unroll
+            for (int pi = 0; pi < kTP; ++pi) asm volatile("" : "+v"(a.ta[k][pi]), "+v"(a.pa[k][pi]));
+    };
+    Ahead cur;
+    load_ahead(0, cur);
+    // the first chunk's data and the initial state complete before the loop, so no wait for them lands inside it
+    resident(cur);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) asm volatile("" : "+v"(st[u][ct]));
+
+    // One chunk: uses `cur` (chunk c), fills `nxt` with chunk c+1. The loop below alternates two buffers, so no
+    // register copy of freshly loaded data (which would wait for the load) is ever needed.
+    auto step = [&](int c, Ahead& cur, Ahead& nxt) __attribute__((always_inline)) {
+        const int nt = min(kC, Tn - c * kC);
+        const int tc = T0 + c * kC;
+        // everything chunk c+1 reads from global memory is requested now and first used at the end of this chunk
+        // (before this chunk's output stores are issued, so that wait never includes store completions)
+        load_ahead(c + 1 < nch ? c + 1 : c, nxt);
 
         // ---- A1: state pieces -> LDS [piece][column][dk]
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const float x[4] = {st[u][0], st[u][1], st[u][2], st[u][3]};
-            u32x2 pc[kNS];
-            split4(x, pc);
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int pi = 0; pi < kNS; ++pi)
-                *reinterpret_cast<u32x2*>(sp + (pi * kCols + r) * kStateRow + 32 * W + 16 * u + 4 * q) = pc[pi];
-        }
+            for (int ct = 0; ct < kCT; ++ct) {
+                const float x[4] = {st[u][ct][0], st[u][ct][1], st[u][ct][2], st[u][ct][3]};
+                u32x2 pc[kNS];
+                split4(x, pc);
+#pragma unroll
+                for (int pi = 0; pi < kNS; ++pi)
+                    *reinterpret_cast<u32x2*>(xrow(sp, kStateRow, pi, ct) + 32 * W + 16 * u + 4 * q) = pc[pi];
+            }
         lds_barrier();
 
-        // ---- A2: X = K S and Q S for row tile W; Y = beta (V - e^G X) -> LDS; K rows and K^T -> LDS
-        f32x4 x = {0.f, 0.f, 0.f, 0.f}, qs = {0.f, 0.f, 0.f, 0.f};
+        // ---- A2: X = K S and Q S for row tile W; Y = beta (V - e^G X) -> LDS; K^T -> LDS
+        f32x4 x[kCT], qs[kCT];
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) x[ct] = qs[ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            u32x4 sb[kNS];
+            u32x4 ok[KP], oq[KP];
+            cur.k[k].pieces(ok);
+            cur.q[k].pieces(oq);
 #pragma unroll
-            for (int pi = 0; pi < kNS; ++pi)
-                sb[pi] = *reinterpret_cast<const u32x4*>(sp + (pi * kCols + r) * kStateRow + 32 * k + 8 * q);
-            u32x4 pa[KP];
-            ka[k].pieces(pa);
-            x = mma(pa, sb, x);
-            qa[k].pieces(pa);
-            qs = mma(pa, sb, qs);
+            for (int ct = 0; ct < kCT; ++ct) {
+                u32x4 sb[kNS];
+#pragma unroll
+                for (int pi = 0; pi < kNS; ++pi)
+                    sb[pi] = *reinterpret_cast<const u32x4*>(xrow(sp, kStateRow, pi, ct) + 32 * k + 8 * q);
+                x[ct] = mma(ok, sb, x[ct]);
+                qs[ct] = mma(oq, sb, qs[ct]);
+            }
         }
-        {
+        float beta4[4], eg4[4], egr4[4];  // coefficients of rows 16W + 4q + i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            beta4[i] = __shfl(cur.beta, 4 * q + i);
+            eg4[i] = __shfl(cur.eg, 4 * q + i);
+            egr4[i] = __shfl(cur.egr, 4 * q + i);
+        }
+#pragma unroll
+        for (int ct = 0; ct < kCT; ++ct) {
             float y[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) y[i] = beta4[i] * (vv[i] - eg4[i] * x[i]);
+            for (int i = 0; i < 4; ++i) y[i] = beta4[i] * (to_f32(cur.v[ct][i]) - eg4[i] * x[ct][i]);
             u32x2 pc[kNS];
             split4(y, pc);
 #pragma unroll
             for (int pi = 0; pi < kNS; ++pi)
-                *reinterpret_cast<u32x2*>(yp + (pi * kCols + r) * kPieceRow + 16 * W + 4 * q) = pc[pi];
+                *reinterpret_cast<u32x2*>(xrow(yp, kPieceRow, pi, ct) + 16 * W + 4 * q) = pc[pi];
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            In* dst = kr + (16 * W + r) * L::kKr + 32 * k + 8 * q;
-            if constexpr (sizeof(In) == 2) {
-                *reinterpret_cast<u32x4*>(dst) = ka[k].v;
-            } else {
-                *reinterpret_cast<f32x4*>(dst) = ka[k].a;
-                *reinterpret_cast<f32x4*>(dst + 4) = ka[k].b;
-            }
+        for (int k = 0; k < 4; ++k)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) kt[(32 * k + 8 * q + e) * L::kKt + 16 * W + r] = ka[k].raw(e);
-        }
+            for (int e = 0; e < 8; ++e) kt[(32 * k + 8 * q + e) * L::kKt + 16 * W + r] = cur.k[k].raw(e);
         lds_barrier();
 
-        // ---- C: vn = T Y (row tile W); P^T tiles; vn and e^{G_last-G} vn -> LDS
-        f32x4 vn = {0.f, 0.f, 0.f, 0.f};
+        // ---- C: vn = T Y (row tile W); vn and e^{G_last-G} vn -> LDS
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            u32x4 ta[kNS], yb[kNS];
-            split8(tv[k], ta);
+        for (int ct = 0; ct < kCT; ++ct) {
+            f32x4 vn = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int pi = 0; pi < kNS; ++pi)
-                yb[pi] = *reinterpret_cast<const u32x4*>(yp + (pi * kCols + r) * kPieceRow + 32 * k + 8 * q);
-            vn = mma(ta, yb, vn);
-        }
-        // P^T tile b: rows t' = 16b + 4q + i, column t = 16W + r; kept where t' <= t
-        float pt[2 * KS][4];
+            for (int k = 0; k < KS; ++k) {
+                u32x4 yb[kNS];
 #pragma unroll
-        for (int b = 0; b < 2 * KS; ++b) {
-            if (b <= W) {
-                f32x4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    Row8<In> kb;
-                    const In* src = kr + (16 * b + r) * L::kKr + 32 * k + 8 * q;
-                    if constexpr (sizeof(In) == 2) {
-                        kb.v = *reinterpret_cast<const u32x4*>(src);
-                    } else {
-                        kb.a = *reinterpret_cast<const f32x4*>(src);
-                        kb.b = *reinterpret_cast<const f32x4*>(src + 4);
-                    }
-                    u32x4 pa[KP], pb[KP];
-                    kb.pieces(pa);
-                    qa[k].pieces(pb);
-                    a = mma(pa, pb, a);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tp = 16 * b + 4 * q + i;
-                    pt[b][i] = tp <= 16 * W + r ? a[i] * expf(Gt - Gq[b][i]) : 0.f;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) pt[b][i] = 0.f;
+                for (int pi = 0; pi < kNS; ++pi)
+                    yb[pi] = *reinterpret_cast<const u32x4*>(xrow(yp, kPieceRow, pi, ct) + 32 * k + 8 * q);
+                vn = mma(cur.ta[k], yb, vn);
             }
-        }
-        {
             float a4[4], b4[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 a4[i] = vn[i];
                 b4[i] = egr4[i] * vn[i];
             }
-            u32x2 pa[kNS], pb[kNS];
-            split4(a4, pa);
-            split4(b4, pb);
+            u32x2 pva[kNS], pvb[kNS];
+            split4(a4, pva);
+            split4(b4, pvb);
 #pragma unroll
             for (int pi = 0; pi < kNS; ++pi) {
-                *reinterpret_cast<u32x2*>(vp + (pi * kCols + r) * kPieceRow + 16 * W + 4 * q) = pa[pi];
-                *reinterpret_cast<u32x2*>(vq + (pi * kCols + r) * kPieceRow + 16 * W + 4 * q) = pb[pi];
+                *reinterpret_cast<u32x2*>(xrow(vp, kPieceRow, pi, ct) + 16 * W + 4 * q) = pva[pi];
+                *reinterpret_cast<u32x2*>(xrow(vq, kPieceRow, pi, ct) + 16 * W + 4 * q) = pvb[pi];
             }
         }
+        const float glast = cur.glast;
+        resident(nxt);                    // complete the look-ahead loads here, ahead of this chunk's stores
         lds_barrier();
 
-        // ---- D: o = e^G Q S + P vn (P as A operand in the accumulator's k order); state update
-        f32x4 o;
+        // ---- D: o = e^G Q S + P vn; state update S = e^{G_last} S + K^T (e^{G_last-G} vn)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = eg4[i] * qs[i];
+        for (int ct = 0; ct < kCT; ++ct) {
+            f32x4 o;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            const float pv[8] = {pt[2 * k][0], pt[2 * k][1], pt[2 * k][2], pt[2 * k][3],
-                                 pt[2 * k + 1][0], pt[2 * k + 1][1], pt[2 * k + 1][2], pt[2 * k + 1][3]};
-            u32x4 pa[kNS], vb[kNS];
-            split8(pv, pa);
+            for (int i = 0; i < 4; ++i) o[i] = eg4[i] * qs[ct][i];
 #pragma unroll
-            for (int pi = 0; pi < kNS; ++pi) {
-                const uint16_t* base = vp + (pi * kCols + r) * kPieceRow + 32 * k + 4 * q;
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(base);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(base + 16);
-                vb[pi] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
+            for (int k = 0; k < KS; ++k) {
+                u32x4 vb[kNS];
+#pragma unroll
+                for (int pi = 0; pi < kNS; ++pi)
+                    vb[pi] = *reinterpret_cast<const u32x4*>(xrow(vp, kPieceRow, pi, ct) + 32 * k + 8 * q);
+                o = mma(cur.pa[k], vb, o);
             }
-            o = mma(pa, vb, o);
+            float* orow = p.out + ((long long)(tc + 16 * W + 4 * q) * H + h) * kDv + col0 + 16 * ct + r;
+            if (nt == kC) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) orow[(long long)i * H * kDv] = o[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (16 * W + 4 * q + i < nt) orow[(long long)i * H * kDv] = o[i];
+            }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = 16 * W + 4 * q + i;
-            if (t < nt) p.out[((long long)(tc + t) * H + h) * kDv + col0 + r] = o[i];
-        }
-        u32x4 qb[2][kNS];
+        for (int k = 0; k < 2; ++k) {
+            Row8<In> kb[2];
 #pragma unroll
-        for (int k = 0; k < 2; ++k)
-#pragma unroll
-            for (int pi = 0; pi < kNS; ++pi)
-                qb[k][pi] = *reinterpret_cast<const u32x4*>(vq + (pi * kCols + r) * kPieceRow + 32 * k + 8 * q);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            f32x4 a;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = glast * st[u][i];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                Row8<In> kb;
+            for (int u = 0; u < 2; ++u) {
                 const In* src = kt + (32 * W + 16 * u + r) * L::kKt + 32 * k + 8 * q;
                 if constexpr (sizeof(In) == 2) {
-                    kb.v = *reinterpret_cast<const u32x4*>(src);
+                    kb[u].v = *reinterpret_cast<const u32x4*>(src);
                 } else {
-                    kb.a = *reinterpret_cast<const f32x4*>(src);
-                    kb.b = *reinterpret_cast<const f32x4*>(src + 4);
+                    kb[u].a = *reinterpret_cast<const f32x4*>(src);
+                    kb[u].b = *reinterpret_cast<const f32x4*>(src + 4);
                 }
-                u32x4 pa[KP];
-                kb.pieces(pa);
-                a = mma(pa, qb[k], a);
             }
-            st[u] = a;
-        }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            ka[k] = kn[k];
-            qa[k] = qn[k];
+            for (int ct = 0; ct < kCT; ++ct) {
+                u32x4 qb[kNS];
+#pragma unroll
+                for (int pi = 0; pi < kNS; ++pi)
+                    qb[pi] = *reinterpret_cast<const u32x4*>(xrow(vq, kPieceRow, pi, ct) + 32 * k + 8 * q);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    if (k == 0)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) st[u][ct][i] *= glast;
+                    u32x4 op[KP];
+                    kb[u].pieces(op);
+                    st[u][ct] = mma(op, qb, st[u][ct]);
+                }
+            }
         }
+    };
+    Ahead other;
+    for (int c = 0; c < nch; c += 2) {
+        step(c, cur, other);
+        if (c + 1 < nch) step(c + 1, other, cur);
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Sg[(32 * W + 16 * u + 4 * q + i) * kDv + r] = st[u][i];
+        for (int ct = 0; ct < kCT; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Sg[(32 * W + 16 * u + 4 * q + i) * kDv + 16 * ct + r] = st[u][ct][i];
 }
 
-// bf16 inputs: 68 KiB of LDS, two workgroups per CU (256 registers per lane); fp32 inputs stage K in fp32: one.
-template <typename In, int WPE = sizeof(In) == 2 ? 2 : 1>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void delta_chunk_scan(DeltaArgs p) {
+// 86 KiB of LDS (bf16 inputs; 103 KiB for fp32): one workgroup per CU, one wave per SIMD with 512 registers.
+template <typename In>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void delta_chunk_scan(DeltaArgs p) {
     extern __shared__ __align__(16) char lds[];
-    // All 8 slices of one (sequence, head) get ids congruent mod 8: with round-robin dispatch over the XCDs they
-    // share one L2, where their common K / Q / T reads hit.
+    // All slices of one (sequence, head) get ids congruent mod 8: with round-robin dispatch over the XCDs they
+    // share one L2, where their common K / Q / T / P reads hit.
     const int id = blockIdx.x;
-    const int slice = (id >> 3) & (kSlices - 1);
-    const int pair = ((id >> 6) << 3) | (id & 7);
+    const int slice = (id >> 3) % kSlices;
+    const int pair = (id / (8 * kSlices)) * 8 + (id & 7);
     if (pair >= p.n_pairs) return;
     const int s = pair / p.H, h = pair % p.H;
     switch (threadIdx.x >> 6) {

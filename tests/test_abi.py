@@ -109,7 +109,7 @@ def test_workspace_size_formula(lib):
 def test_gated_delta_arguments_checked_on_host(lib):
     fake = 4096
     ws = lib.lib.rk_gated_delta_workspace_bytes(256, 16)
-    assert ws == 256 * 16 * (10 * 256 + 4 * 64) * 4 and lib.lib.rk_gated_delta_workspace_bytes(-1, 16) == 0
+    assert ws == 256 * 16 * (2 * 3 * 3072 * 2 + 4 * 64 * 4) and lib.lib.rk_gated_delta_workspace_bytes(-1, 16) == 0
 
     def call(**kw):
         a = dict(out=fake, S=fake, stride=16 * 128 * 128, q=fake, k=fake, v=fake, dt=1, beta=fake, g=fake, cu=fake,
