@@ -72,9 +72,15 @@ def time_region(fn, steps: int, warmup: int, stream) -> float:
     return t0.elapsed_time(t1) / steps
 
 
+USE_GRAPHS = True
+
+
 def graph_time(fn, steps: int, stream) -> float:
-    """Average ms per step of `steps` calls of fn captured in one HIP graph (no host work between launches)."""
+    """Average ms per step of `steps` calls of fn captured in one HIP graph (no host work between launches); with
+    --no-graph (counter-collection runs) the eager back-to-back rate instead."""
     import torch
+    if not USE_GRAPHS:
+        return time_region(fn, steps, 0, stream)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for _ in range(steps):
@@ -225,18 +231,7 @@ def bench_deltanet(args, backend):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for _ in range(args.steps):
-            step()
-    graph.replay()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    graph.replay()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / args.steps
+    ms = graph_time(step, args.steps, stream)
     nbytes = case.algorithmic_bytes()
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] c2: {ms * 1e3:.2f} us per step, {gbs:.0f} GB/s algorithmic")
@@ -384,7 +379,10 @@ def main() -> int:
     ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches only (for counter collection)")
     args = ap.parse_args()
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graph
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the sequences of a batch shard across GPUs with no exchange, so N GPUs run N independent copies "

@@ -92,3 +92,17 @@ def test_pool_states_one_launch(backend):
     for st, rf in zip(states, refs):
         assert rel_err(st.S, rf.S) < 1e-5
         assert torch.equal(st.conv_tail.cpu(), rf.conv_tail)
+
+
+
+
+
+def test_batch_sizes_back_to_back(backend):
+    """Calls of different batch sizes back to back on one pool (rows 0 .. B-1 of a 10-row pool) each match the
+    oracle and touch only their own rows."""
+    for batch in (8, 3, 8):
+        case = wl.c2_deltanet_step(seed=40 + batch, batch=batch, max_seqs=10)
+        want_out, want_S, want_conv = oracle_step(case)
+        got_out, got_S, got_conv = gpu_step(backend, case)
+        assert rel_err(got_out, want_out) < 1e-5 and rel_err(got_S, want_S) < 1e-5
+        assert torch.equal(got_conv, want_conv)
