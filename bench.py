@@ -95,14 +95,19 @@ def graph_time(fn, steps: int, stream) -> float:
     return t0.elapsed_time(t1) / steps
 
 
-def cpu_time(fn, runs: int = 3) -> float:
+CPU_SAMPLE_S = 10.0
+
+
+def cpu_time(fn, runs: int = 3) -> tuple[float, int, float]:
+    """Median seconds per call of fn on the host cores, over at least `runs` calls after a warm-up and until about
+    CPU_SAMPLE_S seconds of calls have run (a bounded sample). Returns (median, calls, total seconds)."""
     fn()                                   # warm-up
     ts = []
-    for _ in range(runs):
+    while len(ts) < runs or (sum(ts) < CPU_SAMPLE_S and len(ts) < 10000):
         t = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t)
-    return statistics.median(ts)
+    return statistics.median(ts), len(ts), sum(ts)
 
 
 def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
@@ -177,10 +182,10 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
                                             case.block_size, case.window)
             backend_ref.gate(o, case.gate)
 
-        t = cpu_time(cpu_run)
+        t, calls, total = cpu_time(cpu_run)
         cpu = {"value": B / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
                "sample": f"the full {workload_name} batch ({B} sequences, {int(case.lens.sum())} positions): "
-                         f"median of 3 runs after 1 warm-up, {t:.3f} s per batch"}
+                         f"median of {calls} runs after 1 warm-up ({total:.1f} s in all), {t:.4f} s per batch"}
     return {
         "metric": "decode attn tokens/s @ batch 64 + achieved HBM GB/s (% of 8 TB/s), 1 GPU",
         "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -243,9 +248,10 @@ def bench_deltanet(args, backend):
         def cpu_run():
             backend_ref.deltanet_decode_batch(case.qkv, case.z, case.b, case.a, states, 0, case.conv_w, case.A_log,
                                               case.dt_bias, case.norm_w, case.eps, case.dims)
-        t = cpu_time(cpu_run, runs=5)
+        t, calls, total = cpu_time(cpu_run, runs=5)
         cpu = {"value": B / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-               "sample": f"one batch-{B} step, median of 5 after 1 warm-up, {t * 1e3:.2f} ms"}
+               "sample": f"one batch-{B} step (state carried between calls), median of {calls} calls after 1 "
+                         f"warm-up ({total:.1f} s in all), {t * 1e3:.2f} ms per step"}
     return {
         "metric": "DeltaNet decode step tokens/s @ batch 8 + achieved HBM GB/s (% of 8 TB/s), 1 GPU",
         "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -285,15 +291,18 @@ def bench_prefill(args, backend):
         # sample: the shortest segment, scaled to the whole batch by flops
         s = min(range(len(case.starts)), key=lambda i: case.lengths()[i] * (case.starts[i] + case.lengths()[i]))
         lo, hi = case.cu_seqlens[s], case.cu_seqlens[s + 1]
-        one = wl.PrefillCase(case.q[lo:hi], case.k_new[lo:hi], case.v_new[lo:hi], case.gate[lo:hi], case.k_pool,
-                             case.v_pool, case.tables[s:s + 1], [0, hi - lo], [case.starts[s]], case.block_size)
-        t = cpu_time(lambda: prefill_ref.packed_prefill(one.q, one.k_new, one.v_new, one.k_pool.clone(),
-                                                        one.v_pool.clone(), one.tables, one.cu_seqlens, one.starts,
-                                                        one.block_size, one.gate), runs=1)
+        one = wl.PrefillCase(case.q[lo:hi], case.k_new[lo:hi], case.v_new[lo:hi], case.gate[lo:hi],
+                             case.k_pool.clone(), case.v_pool.clone(), case.tables[s:s + 1], [0, hi - lo],
+                             [case.starts[s]], case.block_size)
+        # repeated calls rewrite the same rows into the cloned pool: every call does identical work
+        t, calls, total = cpu_time(lambda: prefill_ref.packed_prefill(one.q, one.k_new, one.v_new, one.k_pool,
+                                                                      one.v_pool, one.tables, one.cu_seqlens,
+                                                                      one.starts, one.block_size, one.gate), runs=1)
         t_full = t * flops / one.flops()
         cpu = {"value": N / t_full, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-               "sample": f"segment {s} alone ({hi - lo} new tokens on a {case.starts[s]}-token prefix), "
-                         f"{t:.2f} s, scaled to the whole pack by flops"}
+               "sample": f"segment {s} alone ({hi - lo} new tokens on a {case.starts[s]}-token prefix): median of "
+                         f"{calls} calls ({total:.1f} s in all), {t:.3f} s per call, scaled to the whole pack by "
+                         f"flops"}
     return {
         "metric": "packed prefill attention tokens/s (config 5) + TFLOP/s (% of bf16 MFMA peak), 1 GPU",
         "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -351,11 +360,12 @@ def bench_chunked_delta(args, backend):
         torch.set_num_threads(cpu_threads())
         lo, hi = cu[0], cu[1]
         f = lambda x: x[lo:hi].float()
-        t = cpu_time(lambda: ops_ref.gated_delta_chunked(f(case.q), f(case.k), f(case.v), f(case.beta), f(case.g),
-                                                         case.S[0].clone()), runs=1)
+        t, calls, total = cpu_time(lambda: ops_ref.gated_delta_chunked(f(case.q), f(case.k), f(case.v), f(case.beta),
+                                                                       f(case.g), case.S[0].clone()), runs=1)
         t_full = t * n
         cpu = {"value": N / t_full, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-               "sample": f"sequence 0 alone ({hi - lo} tokens, {H} heads), {t:.2f} s, times {n} sequences"}
+               "sample": f"sequence 0 alone ({hi - lo} tokens, {H} heads): median of {calls} calls ({total:.1f} s "
+                         f"in all), {t:.3f} s per call, times {n} sequences"}
     return {
         "metric": "chunked gated delta prefill tokens/s (config 4) + TFLOP/s (% of bf16 MFMA peak), 1 GPU",
         "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

@@ -10,13 +10,15 @@ path.
 
 Pinning status (what checks each function; see tests/test_oracle.py):
   ops_ref.attention            float64 brute force from absolute positions; reference invariants (S = 1 -> v,
-                               q-scale 30 finite, window edges); committed fixtures tests/golden/attention_*.npz
+                               q-scale 30 finite, window edges); committed fixtures tests/golden/paged_decode.npz,
+                               prefill_attention.npz
   backend_ref.paged_attention  closed-form address map (brute gather) bit-exact; paged == contiguous exactly
   ops_ref.causal_conv1d        float64 brute force; torch.nn.functional.conv1d depthwise (transformers'
                                causal_conv1d_update formulation)
   ops_ref.l2norm, rms_norm_gated  float64 closed forms; transformers l2norm
   ops_ref.gated_delta_recurrent  float64 brute force; transformers torch_recurrent_gated_delta_rule (fixtures)
   ops_ref.gated_delta_chunked  == recurrent (float64); transformers torch_chunk_gated_delta_rule (fixtures);
+                               float64 brute force at dk = dv = 128 (tests/golden/delta_rule_128.npz);
                                special cases S0 = 0, T < 64 padding, beta = g = 0 leaves S unchanged
   backend_ref.deltanet_decode  float64 brute-force step (conv, norms, gates, delta rule, gated norm)
   prefill_ref.packed_prefill   float64 brute force per segment; packed == per-segment
