@@ -158,13 +158,6 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Workgroup barrier ordering LDS only: outstanding global loads are not waited for.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Sequence owning global chunk gc: the last s with cu_chunks[s] <= gc (empty sequences own no chunk).
 __device__ __forceinline__ int seq_of_chunk(const DeltaArgs& p, int gc) {
     int lo = 0, hi = p.n_seqs;

@@ -6,25 +6,30 @@
 // ((tables[i][s / bs] * bs + s % bs) * Hkv + kvh) * D (attention.metal:115).
 //
 // Design (split over positions, then a merge):
-//   * Work unit = one 16-position tile of one sequence. Sequence b gets n(b) = max(1, round(units(b) NW / U))
-//     split workgroups (U = all tiles, NW = the target workgroup count) that take equal contiguous parts of its
-//     tiles, so every workgroup streams about U / NW tiles however unequal the lengths are, never crosses a
-//     sequence, and writes exactly one partial (m, l, acc) per kv-head.
+//   * Work unit = one 16-position tile of one sequence. The tiles of the whole batch, in (sequence, tile) order,
+//     are cut into NW equal contiguous ranges (stream-K): workgroup w takes global tiles [U w / NW, U (w + 1) / NW)
+//     of the U in all, so every workgroup streams the same number of tiles however unequal the lengths are. A range
+//     may cross sequence boundaries; the workgroup writes one partial (m, l, acc) per kv-head for each sequence it
+//     touches, into slot w + b (unique: a later workgroup never touches an earlier sequence). NW is sized so that
+//     the whole grid is resident at once (no second wave of workgroups).
 //   * A split workgroup has one wave per kv-head; the waves walk the same tiles, so the interleaved halves of every
 //     pool row ([bs][Hkv][D]) are fetched together. Each wave serves all G = Hq/Hkv query heads of its kv-head, so
 //     every K/V byte is read from HBM once.
 //   * QK^T on MFMA (v_mfma_f32_16x16x32_bf16): A = the G query rows split exactly into three bf16 parts
-//     (q = hi + mid + lo, kept in LDS), B = 16 keys x 32 dims. bf16 keys are exact MFMA operands; fp32 keys are split
-//     the same way (three MFMA passes), so both pool types get fp32-accurate scores, and a bf16 pool gives bit for
-//     bit the result of the fp32 pool holding the widened values (the extra passes only add exact zeros).
-//   * Loads are software-pipelined: the next tile's keys are issued after this tile's MFMAs and its values after
-//     this tile's PV, so every wave always has a tile's K or V in flight. When tiles align with blocks
-//     (block_size % 16 == 0) one vector load fetches the block numbers of 64 tiles.
+//     (q = hi + mid + lo, built in LDS by the whole wave when a sequence starts), B = 16 keys x 32 dims. bf16 keys
+//     are exact MFMA operands; fp32 keys are split the same way (three MFMA passes), so both pool types get
+//     fp32-accurate scores, and a bf16 pool gives bit for bit the result of the fp32 pool holding the widened values
+//     (the extra passes only add exact zeros).
+//   * Loads are software-pipelined: each register set of keys (values) is refilled with the next tile's as soon as
+//     this tile's MFMA operands (widened values) are taken from it, so a wave has the next tile in flight for
+//     nearly the whole of this tile's compute, also across a sequence boundary. One
+//     vector load per 64 tiles fetches each tile's sequence, position and (block_size % 16 == 0) block number.
 //   * Online softmax in base 2 (scores pre-scaled by log2(e)/sqrt(D)); row max by DPP inside 16-lane rows.
 //   * PV on the VALU in fp32: each lane owns 8 consecutive dims of one position row (coalesced 16/32-byte loads);
 //     probabilities are broadcast through LDS.
-//   * Merge kernel: one workgroup per (sequence, kv-head) combines its partials (m, l, acc) in workgroup order,
-//     divides, applies the optional sigmoid gate and writes [B, Hq, D].
+//   * Merge kernel: one workgroup per (sequence, kv-head) finds the sequence's workgroups in closed form from the
+//     same tile prefix sums, combines their partials in workgroup order, divides, applies the optional sigmoid gate
+//     and writes [B, Hq, D].
 // Bounds: lens are clamped to max_nb * bs and table entries to [0, num_blocks), so a malformed table cannot make a
 // load leave the pool. Positions outside [s0, len) are never used: their scores are replaced (not added) by -inf and
 // their V values by 0 before the FMA, so a NaN-poisoned block outside the window cannot leak in.
@@ -39,6 +44,11 @@ namespace {
 constexpr int kMaxBatch = 1024;
 constexpr int kMaxKvHeads = 4;     // one wave per kv head in a split workgroup of at most 256 threads
 constexpr int kTile = 16;
+// Waves of a split workgroup: 8 (two per SIMD, <= 256 VGPRs each) for up to 4 query heads per kv-head, 4 (one per
+// SIMD) for the register-heavier 8-head instances. It depends on the shape only, never on the pool dtype, so that a
+// bf16 pool and an fp32 pool holding the same (widened) values are cut and combined identically and give bit-equal
+// outputs (the fp32-pool instance at D = 256 spills some registers to do so).
+constexpr int waves_per_group(int GP) { return GP == 4 ? 8 : 4; }
 
 struct DecodeArgs {
     float* part;
@@ -50,6 +60,7 @@ struct DecodeArgs {
     const int32_t* lens;
     const float* gate;
     int B, Hq, Hkv, G, bs, max_nb, num_blocks, window, NW;
+    int NG;         // groups of Hkv waves in a split workgroup
     float qscale;   // log2(e) / sqrt(D)
 };
 
@@ -81,45 +92,37 @@ __device__ __forceinline__ long long kv_row(const int32_t* table, int s, int bs,
     return ((long long)(blk * (long long)bs + s % bs) * Hkv + kvh) * D;
 }
 
-// Workgroup plan, computed by one wave: wg0[b] = first split workgroup of sequence b (exclusive prefix of
-// n(b) = units ? max(1, round(units * NW / U)) : 0), wg0[B] = workgroups in use. Returns U (all tiles).
-__device__ long long plan_workgroups(const DecodeArgs& a, int* wg0) {
+// Tile prefix sums, computed by one wave: P[0] = 0, P[b + 1] = P[b] + units(b); with Ls, also Ls[b] = the clamped
+// length of sequence b. Returns U = P[B] (all tiles).
+__device__ int plan_prefix(const DecodeArgs& a, int* P, int* Ls = nullptr) {
     const int lane = threadIdx.x & 63;
-    long long U = 0;
-    for (int b0 = 0; b0 < a.B; b0 += 64) {
-        const int b = b0 + lane;
-        int x = b < a.B ? seq_range(a, b).units : 0;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
-        U += x;
-    }
     int carry = 0;
     for (int b0 = 0; b0 < a.B; b0 += 64) {
         const int b = b0 + lane;
-        const int units = b < a.B ? seq_range(a, b).units : 0;
-        int x = 0;
-        if (units > 0) {
-            const long long r = ((long long)units * a.NW + U / 2) / U;
-            x = r < 1 ? 1 : (int)r;
-        }
+        const SeqRange sr = b < a.B ? seq_range(a, b) : SeqRange{0, 0, 0, 0};
+        if (Ls && b < a.B) Ls[b] = sr.L;
+        int x = sr.units;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const int y = __shfl_up(x, off);
             if (lane >= off) x += y;
         }
-        if (b < a.B) wg0[b + 1] = carry + x;
+        if (b < a.B) P[b + 1] = carry + x;
         carry += __shfl(x, 63);
     }
-    if (lane == 0) wg0[0] = 0;
-    return U;
+    if (lane == 0) P[0] = 0;
+    return carry;
 }
 
-// largest b with wg0[b] <= w (wg0 non-decreasing, wg0[0] = 0)
-__device__ __forceinline__ int seq_of_workgroup(const int* wg0, int B, int w) {
+// First global tile of workgroup w's range (U tiles over NW workgroups).
+__device__ __forceinline__ int range_lo(int U, int NW, int w) { return (int)((long long)U * w / NW); }
+
+// Sequence of global tile g (0 <= g < P[B]): the largest b in [0, B) with P[b] <= g, which has P[b + 1] > g.
+__device__ __forceinline__ int seq_of_tile(const int* P, int B, int g) {
     int lo = 0, hi = B - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (wg0[mid] <= w) lo = mid; else hi = mid - 1;
+        if (P[mid] <= g) lo = mid; else hi = mid - 1;
     }
     return lo;
 }
@@ -191,6 +194,9 @@ struct KVLoad<float> {
     }
 };
 
+// LDS bytes of the per-sequence plan of a split workgroup: tile prefix sums [B + 1] and clamped lengths [B].
+constexpr int seq_lds_bytes(int B) { return ((2 * B + 1) * 4 + 15) & ~15; }
+
 // LDS bytes one wave of the split kernel uses: the query A operands (NT x NIT x 64 lanes x 16 B), the 16 x GP
 // probabilities of the current tile and the GP rescale factors.
 template <int D, int GP>
@@ -224,17 +230,17 @@ struct TileRows<NVI, TPI, LPT, false> {
 
 template <int NVI, int TPI, int LPT, bool ALIGNED>
 __device__ __forceinline__ TileRows<NVI, TPI, LPT, ALIGNED> tile_rows(const DecodeArgs& a, const int32_t* table,
-                                                                        const SeqRange& sr, int tbase, int blk,
-                                                                        int kvh, int D, int lane) {
+                                                                        int s0, int L, int tbase, int blk, int kvh,
+                                                                        int D, int lane) {
     TileRows<NVI, TPI, LPT, ALIGNED> r;
-    r.partial = tbase < sr.s0 || tbase + kTile > sr.L;
+    r.partial = tbase < s0 || tbase + kTile > L;
     const int tk = tbase + (lane & 15);
-    r.kvalid = tk >= sr.s0 && tk < sr.L;
+    r.kvalid = tk >= s0 && tk < L;
     r.vmask = 0;
 #pragma unroll
     for (int vi = 0; vi < NVI; ++vi) {
         const int tv = tbase + vi * TPI + lane / LPT;
-        r.vmask |= (uint32_t)(tv >= sr.s0 && tv < sr.L) << vi;
+        r.vmask |= (uint32_t)(tv >= s0 && tv < L) << vi;
     }
     if constexpr (ALIGNED) {
         // rows past the length are still rows of the allocated block: no clamping needed for addressing
@@ -243,22 +249,25 @@ __device__ __forceinline__ TileRows<NVI, TPI, LPT, ALIGNED> tile_rows(const Deco
         r.vbase = ((row0 + lane / LPT) * a.Hkv + kvh) * D + (lane % LPT) * 8;
         r.vstride = (long long)TPI * a.Hkv * D;
     } else {
-        const int tkc = tk < sr.s0 ? sr.s0 : (tk >= sr.L ? sr.L - 1 : tk);
+        const int tkc = tk < s0 ? s0 : (tk >= L ? L - 1 : tk);
         r.krow = kv_row(table, tkc, a.bs, a.Hkv, kvh, D, a.num_blocks);
 #pragma unroll
         for (int vi = 0; vi < NVI; ++vi) {
             const int tv = tbase + vi * TPI + lane / LPT;
-            const int tvc = tv < sr.s0 ? sr.s0 : (tv >= sr.L ? sr.L - 1 : tv);
+            const int tvc = tv < s0 ? s0 : (tv >= L ? L - 1 : tv);
             r.vr[vi] = kv_row(table, tvc, a.bs, a.Hkv, kvh, D, a.num_blocks) + (lane % LPT) * 8;
         }
     }
     return r;
 }
 
-// One workgroup = Hkv waves, wave k serving kv-head k: the waves of a workgroup walk the same tiles, so both halves
-// of every interleaved pool row ([bs][Hkv][D]) are fetched together.
-template <typename T, int D, int GP, bool ALIGNED>
-__global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
+// One workgroup = NG groups of Hkv waves (NG = WPG / Hkv, WPG = waves_per_group()); wave g * Hkv + k serves
+// kv-head k for group g. The Hkv waves of a group walk the same tiles, so both halves of every interleaved pool row ([bs][Hkv][D]) are
+// fetched together. Within each sequence segment of the workgroup's range, group g takes the segment's tiles
+// g, g + NG, g + 2 NG, ...; at the segment's end the groups' (m, l, acc) states are combined through LDS and one
+// partial per kv-head is written.
+template <typename T, int D, int GP, bool ALIGNED, int WPG>
+__global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     using LD = KVLoad<T>;
     constexpr int NIT = D / 32;              // MFMA k-steps per tile
     constexpr int NT = (3 * GP + 15) / 16;   // A tiles: 3 query splits x GP heads, 16 rows each
@@ -267,76 +276,213 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
     constexpr int NVI = kTile / TPI;         // V steps per tile
     constexpr int KS = LD::KS;
     constexpr int HB = GP / 4;               // head blocks of 4 in the score layout
+    constexpr int QV = (GP * D / 4 + 63) / 64;   // float4 query pieces per lane when a sequence starts
+    constexpr int REC = GP * D + 2 * GP;     // floats of one (acc, m, l) record
+    static_assert(REC * 4 <= NT * NIT * 64 * 16, "a combine record must fit in the wave's query operand area");
 
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int lane = threadIdx.x & 63;
-    const int kvh = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6;
+    const int kvh = wave % a.Hkv;
+    const int g = wave / a.Hkv;
+    const int NG = a.NG;
     const int w = blockIdx.x;
     const int row = lane & 15;     // MFMA row / column owned by this lane
     const int grp = lane >> 4;     // k-slot group (operands) / row block (accumulator)
 
-    int* wg0 = reinterpret_cast<int*>(smem);
-    char* wl = smem + (((a.B + 1) * 4 + 15) & ~15) + kvh * wave_lds_bytes<D, GP>();
+    int* P = reinterpret_cast<int*>(smem);          // tile prefix sums [B + 1]
+    int* Ls = P + a.B + 1;                           // clamped lengths [B]
+    char* wl = smem + seq_lds_bytes(a.B) + wave * wave_lds_bytes<D, GP>();
     u32x4* qop = reinterpret_cast<u32x4*>(wl);
     float* p_lds = reinterpret_cast<float*>(wl + NT * NIT * 64 * 16);
     float* alpha_lds = p_lds + kTile * GP;
+    // record of wave ww for the segment combine: the start of its query operand area (re-staged after a combine)
+    auto crec = [&](int ww) {
+        return reinterpret_cast<float*>(smem + seq_lds_bytes(a.B) + ww * wave_lds_bytes<D, GP>());
+    };
+    float* myrec = reinterpret_cast<float*>(wl);
 
-    if (kvh == 0) plan_workgroups(a, wg0);
+    // query operand rows that no (split, head) pair fills are zero (again after every combine)
+    auto zero_q = [&]() {
+#pragma unroll
+        for (int i = 0; i < NT * NIT; ++i) qop[i * 64 + lane] = u32x4{0u, 0u, 0u, 0u};
+    };
+    if (wave == 0) plan_prefix(a, P, Ls);
+    zero_q();
     __syncthreads();
-    if (w >= wg0[a.B]) return;
-    const int b = seq_of_workgroup(wg0, a.B, w);
-    const int r = w - wg0[b], nwg = wg0[b + 1] - wg0[b];
-    const SeqRange sr = seq_range(a, b);
-    const int ta = (int)((long long)sr.units * r / nwg), tb = (int)((long long)sr.units * (r + 1) / nwg);
-    const int n_here = tb - ta;
-    const int32_t* table = a.tables + (long long)b * a.max_nb;
-    const int tile0 = sr.t0 + ta;
+    const int U = P[a.B];
+    const int lo = range_lo(U, a.NW, w), hi = range_lo(U, a.NW, w + 1);
+    if (lo >= hi) return;                            // uniform over the workgroup: no barrier is left waiting
+    const int bA = seq_of_tile(P, a.B, lo), bZ = seq_of_tile(P, a.B, hi - 1);
 
-    // ---- query rows of (b, kvh) requested first; split into MFMA operands once the first tile's loads are out
-    float4 qx[NT][NIT][2];
-#pragma unroll
-    for (int tt = 0; tt < NT; ++tt) {
-        const int m = 16 * tt + row;
-        const int h = m % GP;
-        const bool valid = m / GP < 3 && h < a.G;
-        const float* qh = a.q + ((long long)b * a.Hq + kvh * a.G + (valid ? h : 0)) * D;
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int d = 32 * it + 8 * grp;
-            qx[tt][it][0] = *reinterpret_cast<const float4*>(qh + d);
-            qx[tt][it][1] = *reinterpret_cast<const float4*>(qh + d + 4);
+    // segment of sequence b inside the range: range-relative tiles [sa, sb); group g's tiles in it
+    auto seg_lo = [&](int b) { const int x = P[b]; return (x > lo ? x : lo) - lo; };
+    auto seg_hi = [&](int b) { const int x = P[b + 1]; return (x < hi ? x : hi) - lo; };
+    auto my_count = [&](int b) {
+        const int len = seg_hi(b) - seg_lo(b);
+        return len > g ? (len - g + NG - 1) / NG : 0;
+    };
+    int my_total = 0;
+    for (int b = bA; b <= bZ; ++b) my_total += my_count(b);
+
+    // per-lane description of this group's tile list entry j0 + lane: sequence, first position, clamped length,
+    // first visible position and (ALIGNED) physical block
+    int b_l = 0, tpos_l = 0, L_l = 0, s0_l = 0, blk_l = 0;
+    auto refill = [&](int j0) {
+        int e = j0 + lane;
+        e = e < my_total ? e : my_total - 1;
+        int b = bA, k = 0;
+        for (int bb = bA; bb <= bZ; ++bb) {          // uniform loop; each lane keeps the segment holding entry e
+            const int c = my_count(bb);
+            if (e >= 0 && e < c) { b = bb; k = e; }
+            e -= c;
         }
-    }
+        const int gt = lo + seg_lo(b) + g + k * NG;  // global tile
+        const int L = Ls[b];
+        const int s0 = (a.window > 0 && L > a.window) ? L - a.window : 0;
+        b_l = b;
+        L_l = L;
+        s0_l = s0;
+        tpos_l = (s0 / kTile + gt - P[b]) * kTile;
+        if (ALIGNED) {
+            const int blk = a.tables[(long long)b * a.max_nb + tpos_l / a.bs];   // < ceil(L / bs) <= max_nb
+            blk_l = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+        }
+    };
+    auto rows_of = [&](int jj) {
+        const int b = __builtin_amdgcn_readlane(b_l, jj);
+        const int blk = ALIGNED ? __builtin_amdgcn_readlane(blk_l, jj) : 0;
+        return tile_rows<NVI, TPI, LPT, ALIGNED>(a, a.tables + (long long)b * a.max_nb,
+                                                  __builtin_amdgcn_readlane(s0_l, jj),
+                                                  __builtin_amdgcn_readlane(L_l, jj),
+                                                  __builtin_amdgcn_readlane(tpos_l, jj), blk, kvh, D, lane);
+    };
 
     float m_run[4], l_run[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.0f; }
     float acc[GP][8];
+    auto reset = [&]() {
 #pragma unroll
-    for (int h = 0; h < GP; ++h)
+        for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.0f; }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
-
-    // block of each tile (ALIGNED): lane j holds the table entry of tile seg + j; tiles are walked in segments of 64
-    // so the inner loop never reloads it
-    int blk_lane = 0;
-    auto refill = [&](int seg) {
-        if (!ALIGNED) return;
-        const int t = (tile0 + seg + lane) * kTile;
-        const int j = seg + lane < n_here ? t / a.bs : 0;
-        const int blk = table[j < a.max_nb ? j : 0];
-        blk_lane = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
-    };
-    auto rows_of = [&](int seg, int ti) {
-        const int blk = ALIGNED ? __builtin_amdgcn_readlane(blk_lane, ti) : 0;
-        return tile_rows<NVI, TPI, LPT, ALIGNED>(a, table, sr, (tile0 + seg + ti) * kTile, blk, kvh, D, lane);
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
     };
 
-    for (int seg = 0; seg < n_here; seg += 64) {
-        const int nseg = n_here - seg < 64 ? n_here - seg : 64;
-        refill(seg);
-        TileRows<NVI, TPI, LPT, ALIGNED> cur = rows_of(seg, 0);
-        typename LD::Vec kv[NIT], vv[NVI];
+    // Query operands. Row m = s * GP + h of the A tiles holds split s of head h, scaled by log2(e)/sqrt(D); element
+    // (it, grp, e) of a row is dim 32 it + 8 grp + e. The queries of the next sequence this wave has tiles in are
+    // fetched into registers (coalesced: 4 consecutive dims per lane and step) a whole segment ahead, so a sequence
+    // switch waits on no load; there the pieces are split and scattered into the operand layout.
+    float4 qn[QV];
+    auto fetch_q = [&](int b) {
+        const float* qb = a.q + ((long long)b * a.Hq + (long long)kvh * a.G) * D;
+#pragma unroll
+        for (int k = 0; k < QV; ++k) {
+            const int e4 = lane + 64 * k;
+            qn[k] = e4 < a.G * (D / 4) ? *reinterpret_cast<const float4*>(qb + 4 * e4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto stage_q = [&]() {
+#pragma unroll
+        for (int k = 0; k < QV; ++k) {
+            const int e4 = lane + 64 * k;
+            if (e4 < a.G * (D / 4)) {
+                const int h = (4 * e4) / D, d = (4 * e4) % D;
+                const Split3 s0 = split3(qn[k].x * a.qscale), s1 = split3(qn[k].y * a.qscale);
+                const Split3 s2 = split3(qn[k].z * a.qscale), s3 = split3(qn[k].w * a.qscale);
+                const uint32_t pc[3][2] = {{pack_hi2(s0.hi, s1.hi), pack_hi2(s2.hi, s3.hi)},
+                                           {pack_hi2(s0.mid, s1.mid), pack_hi2(s2.mid, s3.mid)},
+                                           {pack_hi2(s0.lo, s1.lo), pack_hi2(s2.lo, s3.lo)}};
+#pragma unroll
+                for (int s = 0; s < 3; ++s) {
+                    const int m = s * GP + h;
+                    const int idx = ((m / 16) * NIT + d / 32) * 64 + (m % 16) + 16 * ((d % 32) / 8);
+                    u32x2* dst = reinterpret_cast<u32x2*>(reinterpret_cast<char*>(qop + idx) + 8 * ((d % 8) / 4));
+                    *dst = u32x2{pc[s][0], pc[s][1]};
+                }
+            }
+        }
+        wave_lds_sync();
+    };
+    // the next sequence after b (exclusive) in which this wave has tiles, or -1
+    auto next_mine = [&](int b) {
+        for (int bb = b + 1; bb <= bZ; ++bb)
+            if (my_count(bb) > 0) return bb;
+        return -1;
+    };
+
+    // Segment end: every wave leaves its (acc, m, l) in LDS; then wave (g, kvh) combines slice g of kv-head kvh's
+    // GP x D outputs over the NG groups (a group with no tile in the segment holds m = -inf, l = 0, acc = 0) and
+    // writes it to the partial of (workgroup w, sequence b, kv-head) in slot w + b: acc [GP][D], m [GP], l [GP].
+    auto combine = [&](int b) {
+#pragma unroll
+        for (int h = 0; h < GP; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float x = acc[h][e];
+                if (TPI >= 8) x += dpp_f32<0x128>(x);   // lanes l and l ^ 8 share dims when a row is 8 lanes
+                if (TPI >= 4) x += __shfl_xor(x, 16);
+                x += __shfl_xor(x, 32);
+                acc[h][e] = x;
+            }
+        if (lane < LPT) {
+#pragma unroll
+            for (int h = 0; h < GP; ++h) {
+                float4* dst = reinterpret_cast<float4*>(myrec + h * D + lane * 8);
+                dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+                dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+            }
+        }
+        float lsum[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lsum[i] = row16_sum(l_run[i]);
+        if (grp < HB && row == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                myrec[GP * D + 4 * grp + i] = m_run[i];
+                myrec[GP * D + GP + 4 * grp + i] = lsum[i];
+            }
+        }
+        lds_barrier();
+        float* slot = a.part + ((long long)(w + b) * a.Hkv + kvh) * REC;
+        const int SL = GP * D / NG;                  // outputs of this wave's slice (a multiple of 4)
+        for (int e = g * SL + 4 * lane; e < (g + 1) * SL; e += 256) {
+            const int h = e / D;
+            float mx = -INFINITY;
+            for (int gg = 0; gg < NG; ++gg) mx = fmaxf(mx, crec(gg * a.Hkv + kvh)[GP * D + h]);
+            float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int gg = 0; gg < NG; ++gg) {
+                const float* r = crec(gg * a.Hkv + kvh);
+                const float sc = fast_exp2(r[GP * D + h] - mx);
+                const float4 x = *reinterpret_cast<const float4*>(r + e);
+                num.x = fmaf(sc, x.x, num.x);
+                num.y = fmaf(sc, x.y, num.y);
+                num.z = fmaf(sc, x.z, num.z);
+                num.w = fmaf(sc, x.w, num.w);
+            }
+            *reinterpret_cast<float4*>(slot + e) = num;
+        }
+        if (g == 0 && lane < GP) {
+            float mx = -INFINITY, den = 0.0f;
+            for (int gg = 0; gg < NG; ++gg) mx = fmaxf(mx, crec(gg * a.Hkv + kvh)[GP * D + lane]);
+            for (int gg = 0; gg < NG; ++gg) {
+                const float* r = crec(gg * a.Hkv + kvh);
+                den = fmaf(fast_exp2(r[GP * D + lane] - mx), r[GP * D + GP + lane], den);
+            }
+            slot[GP * D + lane] = mx;
+            slot[GP * D + GP + lane] = den;
+        }
+        lds_barrier();                                // every record is read: the areas hold query operands again
+        zero_q();
+    };
+
+    reset();
+    typename LD::Vec kv[NIT], vv[NVI];
+    TileRows<NVI, TPI, LPT, ALIGNED> cur;
+    int j0 = 0;                                      // first entry held by the lane arrays
+    if (my_total > 0) {
+        refill(0);
+        cur = rows_of(0);
         // issue order K then V, here and in the loop, so that waiting for a tile's keys never waits for its values
         // (the scheduling barriers keep the compiler from reordering the two groups of loads)
         __builtin_amdgcn_sched_barrier(0);
@@ -346,34 +492,37 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
         __builtin_amdgcn_sched_barrier(0);
-
-        if (seg == 0) {
-            // operands: row r of A tile tt holds split (m / GP) of head (m % GP), m = 16 tt + r, scaled by
-            // log2(e)/sqrt(D); each lane reads back only its own operands, so no barrier is needed
-#pragma unroll
-            for (int tt = 0; tt < NT; ++tt) {
-                const int s = (16 * tt + row) / GP;
-                const bool valid = s < 3 && (16 * tt + row) % GP < a.G;
-#pragma unroll
-                for (int it = 0; it < NIT; ++it) {
-                    const float xs[8] = {qx[tt][it][0].x, qx[tt][it][0].y, qx[tt][it][0].z, qx[tt][it][0].w,
-                                         qx[tt][it][1].x, qx[tt][it][1].y, qx[tt][it][1].z, qx[tt][it][1].w};
-                    uint32_t bits[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const Split3 sp = split3(valid ? xs[e] * a.qscale : 0.0f);
-                        bits[e] = s == 0 ? sp.hi : (s == 1 ? sp.mid : sp.lo);
-                    }
-                    u32x4 op;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) op[j] = pack_hi2(bits[2 * j], bits[2 * j + 1]);
-                    qop[(tt * NIT + it) * 64 + lane] = op;
-                }
-            }
+        fetch_q(next_mine(bA - 1));
+    }
+    int j = 0;                                       // this group's next tile list entry
+    for (int b = bA; b <= bZ; ++b) {
+        if (seg_hi(b) == seg_lo(b)) continue;        // an empty sequence inside the range: no partial
+        const int cnt = my_count(b);
+        if (cnt > 0) {
+            stage_q();
+            const int bn = next_mine(b);
+            if (bn >= 0) fetch_q(bn);
         }
+        for (int k = 0; k < cnt; ++k, ++j) {
+            // the next entry's rows: from the lane arrays, refilled when the next entry starts a new 64-entry chunk
+            // (the refill's table load makes that one prefetch wait); the last entry re-requests its own rows,
+            // which hit in L2
+            const TileRows<NVI, TPI, LPT, ALIGNED> cur_now = cur;
+            TileRows<NVI, TPI, LPT, ALIGNED> nxt;
+            if (j + 1 >= my_total) {
+                nxt = cur_now;
+            } else {
+                if (j + 1 - j0 == 64) {
+                    j0 += 64;
+                    refill(j0);
+                }
+                nxt = rows_of(j + 1 - j0);
+            }
 
-        for (int ti = 0; ti < nseg; ++ti) {
-            // ---- scores: S[m][n] = sum_d A[m][d] * K[n][d]
+            // ---- scores: S[m][n] = sum_d A[m][d] * K[n][d]. Each key register set is refilled with the next
+            // tile's keys as soon as its MFMA operands are built, so the next tile is in flight while this one
+            // computes. Issued unconditionally: a conditional issue would make every later wait for this tile's
+            // values a wait for all outstanding loads.
             f32x4 sacc[NT];
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) sacc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -381,21 +530,15 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
             for (int it = 0; it < NIT; ++it) {
                 u32x4 kb[KS];
                 LD::key_operands(kv[it], kb);
+                __builtin_amdgcn_sched_barrier(0);
+                kv[it] = LD::load(a.kp, nxt.krow + 32 * it + 8 * grp);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
                     for (int tt = 0; tt < NT; ++tt)
                         sacc[tt] = mfma16x16x32(qop[(tt * NIT + it) * 64 + lane], kb[ks], sacc[tt]);
             }
-
-            // ---- keys of the next tile go in flight now. Issued unconditionally (the last tile of a segment
-            // re-requests its own rows, which hit in L2): a conditional issue would make every later wait for this
-            // tile's values a wait for all outstanding loads.
-            const TileRows<NVI, TPI, LPT, ALIGNED> nxt = rows_of(seg, ti + 1 < nseg ? ti + 1 : ti);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, nxt.krow + 32 * it + 8 * grp);
-            __builtin_amdgcn_sched_barrier(0);
 
             // sum the three query splits: lane (grp, row) then holds heads 4 * (grp % HB) + i of position row
             float sc[4];
@@ -406,7 +549,7 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
                 for (int tt = 1; tt < NT; ++tt) x += sacc[tt][i];
                 if (GP == 4) x += __shfl_xor(x, 16);
                 x += __shfl_xor(x, 32);
-                sc[i] = cur.kvalid ? x : -INFINITY;
+                sc[i] = cur_now.kvalid ? x : -INFINITY;
             }
 
             // ---- online softmax (base 2) per head over the 16 positions of this row
@@ -439,13 +582,16 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[h][e] *= alh[h];
             // values of hidden positions become 0 (branch-free: a branch here would make the compiler wait for
-            // every outstanding load, including the next tile's keys)
-#pragma unroll
-            for (int vi = 0; vi < NVI; ++vi) LD::keep_if(vv[vi], cur.vvalid(vi));
+            // every outstanding load, including the next tile's keys); each value register set is refilled with
+            // the next tile's values as soon as it is widened
 #pragma unroll
             for (int vi = 0; vi < NVI; ++vi) {
                 float vf[8];
+                LD::keep_if(vv[vi], cur_now.vvalid(vi));
                 LD::widen(vv[vi], vf);
+                __builtin_amdgcn_sched_barrier(0);
+                vv[vi] = LD::load(a.vp, nxt.vrow(vi));
+                __builtin_amdgcn_sched_barrier(0);
                 const int pos = vi * TPI + lane / LPT;
                 float ph[GP];
 #pragma unroll
@@ -458,131 +604,121 @@ __global__ __launch_bounds__(256) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(ph[h], vf[e], acc[h][e]);
             }
-
-            // ---- values of the next tile go in flight now
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, nxt.vrow(vi));
-            __builtin_amdgcn_sched_barrier(0);
             cur = nxt;
             wave_lds_sync();   // p_lds / alpha_lds are rewritten by the next tile
         }
-    }
-
-    // ---- the partial of (workgroup w, kv-head): acc [GP][D], then m [GP], l [GP]
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float x = acc[h][e];
-            if (TPI >= 8) x += dpp_f32<0x128>(x);   // lanes l and l ^ 8 share dims when a row is 8 lanes
-            if (TPI >= 4) x += __shfl_xor(x, 16);
-            x += __shfl_xor(x, 32);
-            acc[h][e] = x;
-        }
-    float* slot = a.part + ((long long)w * a.Hkv + kvh) * (GP * (D + 2));
-    if (lane < LPT) {
-#pragma unroll
-        for (int h = 0; h < GP; ++h) {
-            float4* dst = reinterpret_cast<float4*>(slot + h * D + lane * 8);
-            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-        }
-    }
-    float lsum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lsum[i] = row16_sum(l_run[i]);
-    if (grp < HB && row == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            slot[GP * D + 4 * grp + i] = m_run[i];
-            slot[GP * D + GP + 4 * grp + i] = lsum[i];
-        }
+        combine(b);
+        reset();
     }
 }
 
-// One workgroup per (sequence, kv-head) pair: combines the partials of the sequence's split workgroups
-// [wg0[b], wg0[b + 1]) in workgroup order with a running maximum. For each chunk of up to 32 partials the
-// accumulators, maxima and sums are all requested before any is used (one memory round trip per chunk), then
-// M' = max(M, m_w), num = num * 2^(M - M') + sum_w 2^(m_w - M') acc_w, den likewise with l_w; out = num / den.
-constexpr int kMergeThreads = 512;
+// One workgroup per (sequence, kv-head); each thread owns float4 outputs of the G x D block. Sequence b owns global
+// tiles [P[b], P[b + 1]); the split workgroups whose ranges meet it are w_first = the one holding tile P[b] ..
+// w_last = the one holding tile P[b + 1] - 1 (empty ranges in between, possible only when NW > U, are skipped),
+// with partials in slots w + b. The gate is requested with the plan; the partials are combined in workgroup order,
+// up to kMergeCh per memory round trip (every load of a chunk is issued before any is used), with a running
+// maximum: M' = max(M, m_w), num = num 2^(M - M') + sum_w 2^(m_w - M') acc_w, den likewise with l_w;
+// out = num / den.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeCh = 8;
 
 template <int D, int GP>
 __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a) {
     constexpr int kT = kMergeThreads;
-    constexpr int NO = (GP * D + kT - 1) / kT;      // outputs per thread (upper bound)
-    constexpr int kCh = NO <= 2 ? 32 : 16;           // partials per memory round trip
-    __shared__ int wg0[kMaxBatch + 1];
-    __shared__ float ml[kCh][2][GP];
+    constexpr int NO = (GP * D / 4 + kT - 1) / kT;   // float4 outputs per thread (upper bound)
+    constexpr int REC = GP * D + 2 * GP;
+    __shared__ int P[kMaxBatch + 1];
     const int tid = threadIdx.x;
-    const int pair = blockIdx.x;
-    const int b = pair / a.Hkv, kvh = pair % a.Hkv;
-    if (tid < 64) plan_workgroups(a, wg0);
-    __syncthreads();
-    const int w0 = wg0[b], nwg = wg0[b + 1] - wg0[b];
-    float* out = a.out + ((long long)b * a.Hq + kvh * a.G) * D;
-    if (nwg == 0) {                                  // empty sequence (length 0)
-        for (int i = tid; i < a.G * D; i += kT) out[i] = 0.0f;
-        return;
-    }
-    const long long stride = GP * (D + 2);
-    auto slot_of = [&](int w) { return ((long long)w * a.Hkv + kvh) * stride; };
-
-    int off[NO], hk[NO];                 // this thread's outputs i = tid + k * kT: offset h * D + d, head h
-    float M[NO], num[NO], den[NO];
+    const int b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
+    const int n4 = a.G * (D / 4);
+    const long long obase = ((long long)b * a.Hq + (long long)kvh * a.G) * D;
+    float4 gv[NO];
 #pragma unroll
     for (int k = 0; k < NO; ++k) {
         const int i = tid + k * kT;
-        const int ic = i < a.G * D ? i : 0;
-        hk[k] = ic / D;
-        off[k] = ic;
-        M[k] = -INFINITY;
-        num[k] = 0.0f;
-        den[k] = 0.0f;
+        gv[k] = a.gate && i < n4 ? *reinterpret_cast<const float4*>(a.gate + obase + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (int c0 = 0; c0 < nwg; c0 += kCh) {
-        const int n_in = min(kCh, nwg - c0);
-        // all loads of the chunk first (indices clamped to the chunk's last partial)
-        float v[kCh][NO];
+    if (tid < 64) plan_prefix(a, P);
+    __syncthreads();
+    const int U = P[a.B], pb = P[b], pe = P[b + 1];
+    float4* out = reinterpret_cast<float4*>(a.out + obase);
+    if (pe == pb) {                                  // empty sequence (length 0)
+        for (int i = tid; i < n4; i += kT) out[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    const int wf = (int)(((long long)(pb + 1) * a.NW - 1) / U);
+    const int wlast = (int)(((long long)pe * a.NW - 1) / U);
+
+    int off[NO], hk[NO];                 // this thread's float4 outputs i = tid + k kT: element offset, head
+    float M[NO], den[NO];
+    float4 num[NO];
 #pragma unroll
-        for (int j = 0; j < kCh; ++j) {
-            const long long base = slot_of(w0 + c0 + min(j, n_in - 1));
+    for (int k = 0; k < NO; ++k) {
+        const int i = tid + k * kT;
+        const int ic = i < n4 ? i : 0;
+        off[k] = 4 * ic;
+        hk[k] = (4 * ic) / D;
+        M[k] = -INFINITY;
+        den[k] = 0.0f;
+        num[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int w0 = wf; w0 <= wlast; w0 += kMergeCh) {
+        float4 v[kMergeCh][NO];
+        float mj[kMergeCh][NO], lj[kMergeCh][NO];
+        bool use[kMergeCh];
 #pragma unroll
-            for (int k = 0; k < NO; ++k) v[j][k] = a.part[base + off[k]];
+        for (int j = 0; j < kMergeCh; ++j) {
+            const int wj = w0 + j;
+            use[j] = wj <= wlast && range_lo(U, a.NW, wj + 1) > range_lo(U, a.NW, wj);
+            if (wj <= wlast) {                       // uniform: loads past the sequence's last partial are skipped
+                const float* base = a.part + ((long long)(wj + b) * a.Hkv + kvh) * REC;
+#pragma unroll
+                for (int k = 0; k < NO; ++k) {
+                    v[j][k] = *reinterpret_cast<const float4*>(base + off[k]);
+                    mj[j][k] = base[GP * D + hk[k]];
+                    lj[j][k] = base[GP * D + GP + hk[k]];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < NO; ++k) {
+                    v[j][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    mj[j][k] = -INFINITY;
+                    lj[j][k] = 0.0f;
+                }
+            }
         }
-        for (int t = tid; t < kCh * 2 * GP; t += kT) {
-            const int j = t / (2 * GP), rr = t % (2 * GP);
-            ml[j][rr / GP][rr % GP] = a.part[slot_of(w0 + c0 + min(j, n_in - 1)) + GP * D + rr];
-        }
-        __syncthreads();
 #pragma unroll
         for (int k = 0; k < NO; ++k) {
             float mx = M[k];
 #pragma unroll
-            for (int j = 0; j < kCh; ++j) mx = j < n_in ? fmaxf(mx, ml[j][0][hk[k]]) : mx;
-            const float rs = fast_exp2(M[k] - mx);      // 0 on the first chunk (M = -inf, mx finite)
-            float nk = num[k] * rs, dk = den[k] * rs;
+            for (int j = 0; j < kMergeCh; ++j) mx = use[j] ? fmaxf(mx, mj[j][k]) : mx;
+            const float rs = fast_exp2(M[k] - mx);   // 0 on the first chunk (M = -inf, mx finite)
+            float4 nk = make_float4(num[k].x * rs, num[k].y * rs, num[k].z * rs, num[k].w * rs);
+            float dk = den[k] * rs;
 #pragma unroll
-            for (int j = 0; j < kCh; ++j) {
-                const float sc = fast_exp2(ml[j][0][hk[k]] - mx);
-                const float tn = fmaf(sc, v[j][k], nk), td = fmaf(sc, ml[j][1][hk[k]], dk);
-                nk = j < n_in ? tn : nk;                 // a select: clamped duplicates never enter
-                dk = j < n_in ? td : dk;
+            for (int j = 0; j < kMergeCh; ++j) {
+                const float sc = use[j] ? fast_exp2(mj[j][k] - mx) : 0.0f;
+                nk.x = fmaf(sc, v[j][k].x, nk.x);
+                nk.y = fmaf(sc, v[j][k].y, nk.y);
+                nk.z = fmaf(sc, v[j][k].z, nk.z);
+                nk.w = fmaf(sc, v[j][k].w, nk.w);
+                dk = fmaf(sc, lj[j][k], dk);
             }
             num[k] = nk;
             den[k] = dk;
             M[k] = mx;
         }
-        __syncthreads();
     }
 #pragma unroll
     for (int k = 0; k < NO; ++k) {
         const int i = tid + k * kT;
-        if (i >= a.G * D) break;
-        float o = num[k] / den[k];
+        if (i >= n4) break;
+        float4 o = make_float4(num[k].x / den[k], num[k].y / den[k], num[k].z / den[k], num[k].w / den[k]);
         if (a.gate) {
-            const float gv = a.gate[(long long)b * a.Hq * D + (long long)kvh * a.G * D + i];
-            o = o * (1.0f / (1.0f + expf(-gv)));
+            o.x *= 1.0f / (1.0f + expf(-gv[k].x));
+            o.y *= 1.0f / (1.0f + expf(-gv[k].y));
+            o.z *= 1.0f / (1.0f + expf(-gv[k].z));
+            o.w *= 1.0f / (1.0f + expf(-gv[k].w));
         }
         out[i] = o;
     }
@@ -594,13 +730,15 @@ typedef void (*MergeFn)(DecodeArgs);
 template <typename T, bool ALIGNED>
 SplitFn pick_split(int D, int GP) {
     if (GP == 4) {
-        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED>;
-        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED>;
-        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED>;
+        constexpr int W = waves_per_group(4);
+        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED, W>;
+        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED, W>;
+        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED, W>;
     } else {
-        if (D == 64) return paged_decode_split<T, 64, 8, ALIGNED>;
-        if (D == 128) return paged_decode_split<T, 128, 8, ALIGNED>;
-        if (D == 256) return paged_decode_split<T, 256, 8, ALIGNED>;
+        constexpr int W = waves_per_group(8);
+        if (D == 64) return paged_decode_split<T, 64, 8, ALIGNED, W>;
+        if (D == 128) return paged_decode_split<T, 128, 8, ALIGNED, W>;
+        if (D == 256) return paged_decode_split<T, 256, 8, ALIGNED, W>;
     }
     return nullptr;
 }
@@ -610,11 +748,16 @@ SplitFn pick_split(int kv_dtype, bool aligned, int D, int GP) {
     return aligned ? pick_split<float, true>(D, GP) : pick_split<float, false>(D, GP);
 }
 
-int split_lds_bytes(int B, int Hkv, int D, int GP) {
+int groups_of(int Hkv, int GP) {
+    const int wpg = waves_per_group(GP);
+    return wpg / Hkv > 0 ? wpg / Hkv : 1;
+}
+
+int split_lds_bytes(int B, int Hkv, int D, int GP, int NG) {
     int per_wave = 0;
     if (GP == 4) per_wave = D == 64 ? wave_lds_bytes<64, 4>() : D == 128 ? wave_lds_bytes<128, 4>() : wave_lds_bytes<256, 4>();
     else per_wave = D == 64 ? wave_lds_bytes<64, 8>() : D == 128 ? wave_lds_bytes<128, 8>() : wave_lds_bytes<256, 8>();
-    return (((B + 1) * 4 + 15) & ~15) + Hkv * per_wave;
+    return seq_lds_bytes(B) + NG * Hkv * per_wave;
 }
 
 MergeFn pick_merge(int D, int GP) {
@@ -630,25 +773,28 @@ MergeFn pick_merge(int D, int GP) {
     return nullptr;
 }
 
-// Workgroups of the split phase (Hkv waves each): the tile count's upper bound, capped so that about
-// kWavesPerCU waves per compute unit are resident. RK_PAGED_DECODE_WAVES_PER_CU overrides the cap (tuning).
-constexpr int kWavesPerCU = 6;
-
-int split_groups(int B, int Hkv, int block_size, int max_nb) {
-    static int per_cu = [] {
+// Workgroups of the split phase (NG groups of Hkv waves): enough for about one tile per group at the tile count's
+// upper bound, capped at the waves per compute unit that stay resident all at once: 8 for 8-wave workgroups (two
+// per SIMD), 4 for 4-wave ones (their registers allow one per SIMD). RK_PAGED_DECODE_WAVES_PER_CU overrides the cap
+// (tuning).
+int split_groups(int B, int Hkv, int block_size, int max_nb, int GP) {
+    static int per_cu_env = [] {
         const char* e = getenv("RK_PAGED_DECODE_WAVES_PER_CU");
-        const int v = e ? atoi(e) : 0;
-        return v > 0 ? v : kWavesPerCU;
+        return e ? atoi(e) : 0;
     }();
+    const int wpg = waves_per_group(GP);
+    const int per_cu = per_cu_env > 0 ? per_cu_env : (wpg == 8 ? 8 : 4);
     const long long upper = (long long)B * (((long long)max_nb * block_size + kTile - 1) / kTile);
     int cus = device_cus();
     if (cus <= 0) cus = 256;
-    const long long cap = (long long)cus * per_cu / Hkv;
-    long long nw = upper < cap ? upper : cap;
+    const int ng = groups_of(Hkv, GP);
+    const long long cap = (long long)cus * per_cu / (ng * Hkv);
+    const long long want = (upper + ng - 1) / ng;
+    long long nw = want < cap ? want : cap;
     return (int)(nw < 1 ? 1 : nw);
 }
 
-// n(b) <= units(b) NW / U + 1, so at most NW + B split workgroups are ever used: the grid and the partials.
+// Partial slots w + b: w < NW and b < B, so NW + B - 1 slots are ever written.
 size_t workspace_bytes(int B, int Hkv, int D, int GP, int NW) {
     return (size_t)(NW + (size_t)B) * Hkv * GP * (D + 2) * sizeof(float);
 }
@@ -663,6 +809,8 @@ int validate(const float* out, const float* q, const void* kp, const void* vp, i
     if (D != 64 && D != 128 && D != 256) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: head_dim %d not in {64,128,256}", D);
     if (bs < 1 || max_nb < 1 || num_blocks < 1) return fail(RK_ERR_ARG, "rk_paged_decode: block_size %d, max_nb %d, num_blocks %d", bs, max_nb, num_blocks);
     if (window < 0) return fail(RK_ERR_ARG, "rk_paged_decode: window %d < 0", window);
+    if ((long long)B * (((long long)max_nb * bs + kTile - 1) / kTile) >= (1ll << 31))
+        return fail(RK_ERR_ARG, "rk_paged_decode: %d sequences x %d blocks of %d positions exceed 2^31 tiles", B, max_nb, bs);
     if (kv_dtype != RK_F32 && kv_dtype != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode: kv dtype %d", kv_dtype);
     return RK_OK;
 }
@@ -677,7 +825,7 @@ extern "C" {
 size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_size, int max_nb) {
     if (B < 1 || Hkv < 1 || Hq < Hkv || block_size < 1 || max_nb < 1) return 0;
     const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
-    return workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb));
+    return workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb, GP));
 }
 
 int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
@@ -690,7 +838,7 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     if (phase != 0 && phase != 1) return fail(RK_ERR_ARG, "rk_paged_decode_phase: phase %d", phase);
     const int G = Hq / Hkv;
     const int GP = G <= 4 ? 4 : 8;
-    const int NW = split_groups(B, Hkv, block_size, max_nb);
+    const int NW = split_groups(B, Hkv, block_size, max_nb, GP);
     const size_t need = workspace_bytes(B, Hkv, D, GP, NW);
     if (!workspace || workspace_bytes_ < need)
         return fail(RK_ERR_WORKSPACE, "rk_paged_decode: workspace %zu bytes < %zu needed", workspace_bytes_, need);
@@ -705,12 +853,15 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     a.lens = lens;
     a.gate = gate;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = G; a.bs = block_size; a.max_nb = max_nb;
-    a.num_blocks = num_blocks; a.window = window; a.NW = NW;
+    a.num_blocks = num_blocks; a.window = window; a.NW = NW; a.NG = groups_of(Hkv, GP);
     a.qscale = kLog2e / sqrtf((float)D);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (phase == 0) {
         SplitFn fn = pick_split(kv_dtype, block_size % kTile == 0, D, GP);
-        hipLaunchKernelGGL(fn, dim3(NW + B), dim3(64 * Hkv), split_lds_bytes(B, Hkv, D, GP), s, a);
+        const int lds = split_lds_bytes(B, Hkv, D, GP, a.NG);
+        rc = allow_dynamic_lds(reinterpret_cast<const void*>(fn), lds);
+        if (rc) return rc;
+        hipLaunchKernelGGL(fn, dim3(NW), dim3(64 * a.NG * Hkv), lds, s, a);
         return check_launch("paged_decode_split");
     }
     hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
