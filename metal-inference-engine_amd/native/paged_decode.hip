@@ -44,6 +44,7 @@ namespace {
 constexpr int kMaxBatch = 1024;
 constexpr int kMaxKvHeads = 4;     // one wave per kv head in a split workgroup of at most 256 threads
 constexpr int kTile = 16;
+constexpr int kStash = 2;   // segments per split workgroup whose records wait in LDS until the range is done
 // Waves of a split workgroup: 8 (two per SIMD, <= 256 VGPRs each) for up to 4 query heads per kv-head, 4 (one per
 // SIMD) for the register-heavier 8-head instances. It depends on the shape only, never on the pool dtype, so that a
 // bf16 pool and an fp32 pool holding the same (widened) values are cut and combined identically and give bit-equal
@@ -300,7 +301,6 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     auto crec = [&](int ww) {
         return reinterpret_cast<float*>(smem + seq_lds_bytes(a.B) + ww * wave_lds_bytes<D, GP>());
     };
-    float* myrec = reinterpret_cast<float*>(wl);
 
     // query operand rows that no (split, head) pair fills are zero (again after every combine)
     auto zero_q = [&]() {
@@ -411,10 +411,11 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         return -1;
     };
 
-    // Segment end: every wave leaves its (acc, m, l) in LDS; then wave (g, kvh) combines slice g of kv-head kvh's
-    // GP x D outputs over the NG groups (a group with no tile in the segment holds m = -inf, l = 0, acc = 0) and
-    // writes it to the partial of (workgroup w, sequence b, kv-head) in slot w + b: acc [GP][D], m [GP], l [GP].
-    auto combine = [&](int b) {
+    // A segment's result per wave is a record (acc [GP][D], m [GP], l [GP]) in LDS. write_record reduces this
+    // wave's state across its lanes into `rec`; combine_slice merges slice g of kv-head kvh's GP x D outputs over
+    // the NG groups' records of one segment (a group with no tile in the segment holds m = -inf, l = 0, acc = 0)
+    // into the partial `dst` = slot w + b of the workspace, same layout; group 0 also writes m and l.
+    auto write_record = [&](float* rec) {
 #pragma unroll
         for (int h = 0; h < GP; ++h)
 #pragma unroll
@@ -428,9 +429,9 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         if (lane < LPT) {
 #pragma unroll
             for (int h = 0; h < GP; ++h) {
-                float4* dst = reinterpret_cast<float4*>(myrec + h * D + lane * 8);
-                dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-                dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+                float4* d4 = reinterpret_cast<float4*>(rec + h * D + lane * 8);
+                d4[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+                d4[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
             }
         }
         float lsum[4];
@@ -439,20 +440,20 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         if (grp < HB && row == 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                myrec[GP * D + 4 * grp + i] = m_run[i];
-                myrec[GP * D + GP + 4 * grp + i] = lsum[i];
+                rec[GP * D + 4 * grp + i] = m_run[i];
+                rec[GP * D + GP + 4 * grp + i] = lsum[i];
             }
         }
-        lds_barrier();
-        float* slot = a.part + ((long long)(w + b) * a.Hkv + kvh) * REC;
+    };
+    auto combine_slice = [&](auto rec_of, float* dst) {
         const int SL = GP * D / NG;                  // outputs of this wave's slice (a multiple of 4)
         for (int e = g * SL + 4 * lane; e < (g + 1) * SL; e += 256) {
             const int h = e / D;
             float mx = -INFINITY;
-            for (int gg = 0; gg < NG; ++gg) mx = fmaxf(mx, crec(gg * a.Hkv + kvh)[GP * D + h]);
+            for (int gg = 0; gg < NG; ++gg) mx = fmaxf(mx, rec_of(gg * a.Hkv + kvh)[GP * D + h]);
             float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
             for (int gg = 0; gg < NG; ++gg) {
-                const float* r = crec(gg * a.Hkv + kvh);
+                const float* r = rec_of(gg * a.Hkv + kvh);
                 const float sc = fast_exp2(r[GP * D + h] - mx);
                 const float4 x = *reinterpret_cast<const float4*>(r + e);
                 num.x = fmaf(sc, x.x, num.x);
@@ -460,21 +461,31 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
                 num.z = fmaf(sc, x.z, num.z);
                 num.w = fmaf(sc, x.w, num.w);
             }
-            *reinterpret_cast<float4*>(slot + e) = num;
+            *reinterpret_cast<float4*>(dst + e) = num;
         }
         if (g == 0 && lane < GP) {
             float mx = -INFINITY, den = 0.0f;
-            for (int gg = 0; gg < NG; ++gg) mx = fmaxf(mx, crec(gg * a.Hkv + kvh)[GP * D + lane]);
+            for (int gg = 0; gg < NG; ++gg) mx = fmaxf(mx, rec_of(gg * a.Hkv + kvh)[GP * D + lane]);
             for (int gg = 0; gg < NG; ++gg) {
-                const float* r = crec(gg * a.Hkv + kvh);
+                const float* r = rec_of(gg * a.Hkv + kvh);
                 den = fmaf(fast_exp2(r[GP * D + lane] - mx), r[GP * D + GP + lane], den);
             }
-            slot[GP * D + lane] = mx;
-            slot[GP * D + GP + lane] = den;
+            dst[GP * D + lane] = mx;
+            dst[GP * D + GP + lane] = den;
         }
-        lds_barrier();                                // every record is read: the areas hold query operands again
-        zero_q();
     };
+
+    // Segments that end inside the range: each wave stashes its record in LDS and goes straight on to its next
+    // tile, with no barrier (the groups' tile counts in a segment differ by one, so a combine barrier there would
+    // idle some groups for a tile); the stashed segments are combined with the last one when the range is done.
+    // Up to kStash segments are stashed; any further one is combined at its end.
+    auto stash_rec = [&](int s, int ww) {
+        return reinterpret_cast<float*>(smem + seq_lds_bytes(a.B) + NG * a.Hkv * wave_lds_bytes<D, GP>()) +
+               (s * NG * a.Hkv + ww) * REC;
+    };
+    int stashed_b[kStash];
+    int n_stashed = 0;
+    auto part_of = [&](int b) { return a.part + ((long long)(w + b) * a.Hkv + kvh) * REC; };
 
     reset();
     typename LD::Vec kv[NIT], vv[NVI];
@@ -607,7 +618,22 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
             cur = nxt;
             wave_lds_sync();   // p_lds / alpha_lds are rewritten by the next tile
         }
-        combine(b);
+        if (b < bZ && n_stashed < kStash) {           // uniform over the workgroup
+            write_record(stash_rec(n_stashed, wave));
+            stashed_b[n_stashed++] = b;
+        } else {
+            // the records of this segment go in the query operand areas (re-staged at the next segment start)
+            write_record(reinterpret_cast<float*>(wl));
+            lds_barrier();
+            for (int s = 0; s < n_stashed; ++s)
+                combine_slice([&](int ww) { return stash_rec(s, ww); }, part_of(stashed_b[s]));
+            n_stashed = 0;
+            combine_slice([&](int ww) { return crec(ww); }, part_of(b));
+            if (b < bZ) {                             // more segments follow: the areas hold query operands again
+                lds_barrier();
+                zero_q();
+            }
+        }
         reset();
     }
 }
@@ -757,7 +783,7 @@ int split_lds_bytes(int B, int Hkv, int D, int GP, int NG) {
     int per_wave = 0;
     if (GP == 4) per_wave = D == 64 ? wave_lds_bytes<64, 4>() : D == 128 ? wave_lds_bytes<128, 4>() : wave_lds_bytes<256, 4>();
     else per_wave = D == 64 ? wave_lds_bytes<64, 8>() : D == 128 ? wave_lds_bytes<128, 8>() : wave_lds_bytes<256, 8>();
-    return seq_lds_bytes(B) + NG * Hkv * per_wave;
+    return seq_lds_bytes(B) + NG * Hkv * per_wave + kStash * NG * Hkv * (GP * D + 2 * GP) * 4;
 }
 
 MergeFn pick_merge(int D, int GP) {
