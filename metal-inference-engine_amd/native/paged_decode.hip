@@ -118,14 +118,17 @@ __device__ int plan_prefix(const DecodeArgs& a, int* P, int* Ls = nullptr) {
 // First global tile of workgroup w's range (U tiles over NW workgroups).
 __device__ __forceinline__ int range_lo(int U, int NW, int w) { return (int)((long long)U * w / NW); }
 
-// Sequence of global tile g (0 <= g < P[B]): the largest b in [0, B) with P[b] <= g, which has P[b + 1] > g.
+// Sequence of global tile g (0 <= g < P[B], g the same in every lane): the largest b in [0, B) with P[b] <= g,
+// which has P[b + 1] > g. P is non-decreasing from P[0] = 0, so b = #{b' in [1, B) : P[b'] <= g}: one ballot per 64
+// sequences, with independent LDS reads (a binary search would chain log2(B) dependent ones).
 __device__ __forceinline__ int seq_of_tile(const int* P, int B, int g) {
-    int lo = 0, hi = B - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (P[mid] <= g) lo = mid; else hi = mid - 1;
+    const int lane = threadIdx.x & 63;
+    int b = 0;
+    for (int c = 1; c < B; c += 64) {
+        const int bb = c + lane;
+        b += __popcll(__ballot(bb < B && P[bb] <= g));
     }
-    return lo;
+    return b;
 }
 
 template <typename T>
