@@ -47,11 +47,29 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     const int t = threadIdx.x;
     const int bi = blockIdx.x / p.H, h = blockIdx.x % p.H;
     const int H = p.H, C = p.C;
+
+    // ---- 0. every small input first, the state after them: one in-order counter serves loads and stores, so a
+    // load issued after the state stores could only be waited for together with them
+    const int part = t / kDK, j = t % kDK;
+    const int c = part == 0 ? h * kDK + j : (part == 1 ? H * kDK + h * kDK + j : 2 * H * kDK + h * kDV + (j & (kDV - 1)));
+    const float x = t < 3 * kDK ? p.qkv[(long long)bi * C + c] : 0.0f;
+    const float4 w = t < 3 * kDK ? *reinterpret_cast<const float4*>(p.conv_w + (long long)c * kTaps)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float b_in = p.b[(long long)bi * H + h], a_in = p.a[(long long)bi * H + h];
+    const float dtb = p.dt_bias[h], alog = p.A_log[h];
+    const float zj = t < kDV ? p.z[(long long)bi * H * kDV + h * kDV + t] : 0.0f;
+    const float nw = t < kDV ? p.norm_w[t] : 0.0f;
     const long long seq = p.seq[bi];
     float* Sh = p.S + (((seq * p.n_linear + p.slot) * H + h) * kDK) * kDV;
     float* tail = p.conv + (seq * p.n_linear + p.slot) * (long long)(kTaps - 1) * C;
+    float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
+    if (t < 3 * kDK) {
+        h0 = tail[c];
+        h1 = tail[C + c];
+        h2 = tail[2 * C + c];
+    }
 
-    // ---- 1. state tile of this thread, loaded first
+    // ---- 1. state tile of this thread
     const int cg = t & 31, rg = t >> 5;       // columns 4*cg .. 4*cg+3, rows 8*rg .. 8*rg+7
     float4 s[8];
 #pragma unroll
@@ -59,11 +77,6 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
 
     // ---- 2. causal conv (taps 0..2 = tail, tap 3 = current token) + SiLU for the head's 384 channels
     if (t < 3 * kDK) {
-        const int part = t / kDK, j = t % kDK;
-        const int c = part == 0 ? h * kDK + j : (part == 1 ? H * kDK + h * kDK + j : 2 * H * kDK + h * kDV + j);
-        const float x = p.qkv[(long long)bi * C + c];
-        const float h0 = tail[c], h1 = tail[C + c], h2 = tail[2 * C + c];
-        const float4 w = *reinterpret_cast<const float4*>(p.conv_w + (long long)c * kTaps);
         float y = __fmul_rn(h0, w.x);
         y = __fadd_rn(y, __fmul_rn(h1, w.y));
         y = __fadd_rn(y, __fmul_rn(h2, w.z));
@@ -88,10 +101,10 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
         qn[t] = __fmul_rn(__fmul_rn(us[t], inv_q), 1.0f / sqrtf((float)kDK));
         kn[t] = __fmul_rn(us[kDK + t], inv_k);
     }
-    const float beta = 1.0f / (1.0f + expf(-p.b[(long long)bi * H + h]));
-    const float ab = p.a[(long long)bi * H + h] + p.dt_bias[h];
+    const float beta = 1.0f / (1.0f + expf(-b_in));
+    const float ab = a_in + dtb;
     const float sp = ab > 20.0f ? ab : log1pf(expf(ab));
-    const float g = -expf(p.A_log[h]) * sp;
+    const float g = -expf(alog) * sp;
     const float decay = expf(g);
     __syncthreads();
 
@@ -149,9 +162,8 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     __syncthreads();
     if (t < kDV) {
         const float rstd = 1.0f / sqrtf((wsum[4] + wsum[5]) / (float)kDV + p.eps);
-        const float zj = p.z[(long long)bi * H * kDV + h * kDV + t];
         const float silu = zj / (1.0f + expf(-zj));
-        p.out[(long long)bi * H * kDV + h * kDV + t] = __fmul_rn(__fmul_rn(__fmul_rn(o, rstd), p.norm_w[t]), silu);
+        p.out[(long long)bi * H * kDV + h * kDV + t] = __fmul_rn(__fmul_rn(__fmul_rn(o, rstd), nw), silu);
     }
 }
 
