@@ -7,13 +7,11 @@
 // src/ops.py:65-104, src/models/packing.py:21-31). Here:
 //   1. prefill_kv_write: the new K/V rows go into the pool first (rounded to the pool's type), so attention reads
 //      exactly what the reference's gather reads back.
-//   2. prefill_attention: one workgroup per (segment, block of 32 queries, kv-head), one wave per query head of the
-//      group. Key tiles of 64 positions are staged in LDS (K as rows, V transposed to [dim][key]) and shared by the
-//      G waves. Per wave the scores are computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16_bf16 (A = 32 keys
-//      x 16 dims from LDS, B = 16 dims x 32 queries from registers), so each lane owns one query column: the online
-//      softmax needs one cross-lane exchange, and the probabilities, rounded to bf16, are already in the B-operand
-//      layout of the second product O^T += V^T P^T (A = 32 dims x 16 keys from LDS). fp32 accumulation throughout;
-//      operands are bf16 (q, k, v as stored; p rounded), so results carry bf16-level error.
+//   2. prefill_attention: one workgroup per (segment, block of 32 queries, kv-head): one consumer wave per query
+//      head of the group (MFMA products and online softmax) and as many producer waves, which stream the key range
+//      through a 2-stage LDS ring with 6 tiles of 32 keys in flight in their registers (details at the kernel).
+//      fp32 accumulation throughout; operands are bf16 (q, k, v as stored; p rounded), so results carry bf16-level
+//      error.
 //   3. The output is divided by the softmax sum, gated and written as fp32 [N, Hq, D].
 // Bounds: key positions past a segment's length are clamped for addressing (and masked), table entries clamped to
 // the pool, query rows past the segment clamped for loading (and not stored).
@@ -26,7 +24,6 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBQ = 32;    // queries per wave
-constexpr int kBK = 64;    // keys per tile
 constexpr int kKPad = 8;   // bf16 padding of a K row in LDS (16 bytes)
 constexpr int kVPad = 8;   // bf16 padding of a V^T row in LDS
 
@@ -119,18 +116,67 @@ __global__ __launch_bounds__(256) void prefill_kv_write(PrefillArgs a, int D) {
     }
 }
 
-// ---- 2. attention. blockDim = G * 64 = 256 (one wave per query head of kv-head blockIdx.y), work item blockIdx.x.
-// One wave per SIMD: 512 registers per lane hold the O^T accumulators, the Q^T operands and the prefetched tile.
-template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_attention(PrefillArgs a) {
+// ---- 2. attention: a warp-specialised pipeline. blockDim = 2 G * 64 (G = 4): waves 0 .. G-1 are consumers (query
+// head kvh * G + wave, the work item's 32 queries), waves G .. 2G-1 are producers. Keys go in tiles of kBKP = 32.
+// Producers keep DEPTH tiles of K / V rows in flight in their registers (8 rows x 8 dims per lane and tile; the
+// block ids of the whole key range are cached in LDS first, so no table load ever sits between two tiles), and
+// per tile move the oldest one into a 2-stage LDS ring (K as rows, V transposed to [dim][key], both rounded to
+// bf16), then request the tile DEPTH ahead. Consumers compute S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = 32 keys
+// x 16 dims from LDS, B = 16 dims x 32 queries from registers), so each lane owns one query column: the online
+// softmax needs one cross-lane exchange, and the probabilities, rounded to bf16, are already the B operand of
+// O^T += V^T P^T (A = 32 dims x 16 keys from LDS). One LDS-only barrier per tile hands the stages over; it never
+// waits for the producers' outstanding loads. fp32 accumulation; bf16 operands (q, k, v as stored, p rounded).
+constexpr int kBKP = 32;        // keys per tile
+constexpr int kStages = 2;      // LDS ring stages
+constexpr int kTabCache = 4096; // block ids cached in LDS (max_nb above it takes the table from global memory)
+
+template <typename TP>
+struct PoolRow;                 // 8 consecutive pool elements of one row, as loaded (converted when staged)
+template <>
+struct PoolRow<uint16_t> {
+    static constexpr int kDepth = 6;
+    u32x4 w;
+    __device__ void load(const void* base, long long off) {
+        w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
+    }
+    __device__ u32x4 bf16() const { return w; }
+};
+template <>
+struct PoolRow<float> {
+    static constexpr int kDepth = 2;
+    u32x4 w0, w1;
+    __device__ void load(const void* base, long long off) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(base) + off);
+        w0 = p[0];
+        w1 = p[1];
+    }
+    __device__ u32x4 bf16() const {
+        u32x4 r;
+        r[0] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w0[0])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w0[1])) << 16);
+        r[1] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w0[2])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w0[3])) << 16);
+        r[2] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w1[0])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w1[1])) << 16);
+        r[3] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w1[2])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w1[3])) << 16);
+        return r;
+    }
+};
+
+template <int D, typename TP, bool TAB_LDS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attention(PrefillArgs a) {
     constexpr int NKS = D / 16;          // k-steps of S^T (dims)
     constexpr int NDT = D / 32;          // 32-row tiles of O^T (dims)
     constexpr int KROW = D + kKPad;      // LDS K row stride (bf16)
-    constexpr int VROW = kBK + kVPad;    // LDS V^T row stride (bf16)
-    constexpr int KBUF = kBK * KROW, VBUF = D * VROW;
-    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];   // [2][K tile] then [2][V^T tile]
+    constexpr int VROW = kBKP + kVPad;   // LDS V^T row stride (bf16)
+    constexpr int KBUF = kBKP * KROW, VBUF = D * VROW;
+    constexpr int DEPTH = PoolRow<TP>::kDepth;
+    constexpr int NJ = (kBKP / 8) * (D / 8);   // 8 x 8 jobs per tile, for K and for V
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    int* tab = reinterpret_cast<int*>(smem);                                  // [kTabCache] when TAB_LDS
+    uint16_t* kst = reinterpret_cast<uint16_t*>(smem + (TAB_LDS ? kTabCache * 4 : 0));   // [kStages][K tile]
+    uint16_t* vst = kst + kStages * KBUF;                                     // [kStages][V^T tile]
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthr = blockDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.G;
+    const bool producer = wave >= G;
     const int kvh = blockIdx.y;
     const int item = a.work[blockIdx.x];
     const int seg = item >> 16, qblk = item & 0xffff;
@@ -138,63 +184,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int nq = min(kBQ, a.cu[seg + 1] - row0);
     const int p0 = a.start[seg] + qblk * kBQ;       // position of the block's first query
     const int n_keys = p0 + nq;                      // keys 0 .. p0 + nq - 1
+    const int n_tiles = (n_keys + kBKP - 1) / kBKP;
     const int32_t* table = a.tables + (long long)seg * a.max_nb;
-    const int head = kvh * a.G + wave;
-    const int col = lane & 31, kg = lane >> 5;      // query column, k-slot group
-    const int qpos = p0 + (col < nq ? col : nq - 1);
 
-    // ---- Q^T operands (B of S^T): lane holds q[query col][d = 16 ks + 8 kg .. + 8]
-    u32x4 qop[NKS];
-    {
-        const long long base = ((long long)(row0 + (col < nq ? col : nq - 1)) * a.Hq + head) * D;
-#pragma unroll
-        for (int t = 0; t < NKS; ++t) qop[t] = load8_bf16(a.q, base + 16 * t + 8 * kg, a.q_dtype);
+    if (TAB_LDS) {
+        const int nb = (n_keys + a.bs - 1) / a.bs;  // <= max_nb <= kTabCache
+        for (int i = tid; i < nb; i += blockDim.x) {
+            const int blk = table[i];
+            tab[i] = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+        }
     }
 
-    f32x16 o[NDT];
+    // ---- producer state: job = 8 keys x 8 dims of K (lanes nV ..) or V (lanes 0 .. NJ-1) per tile
+    const int pl = tid - G * 64;
+    const bool is_v = pl < NJ;
+    const int job = is_v ? pl : pl - NJ;
+    const bool has_job = producer && job < NJ;
+    const int kgp = job / (D / 8), dc = job % (D / 8);
+    PoolRow<TP> buf[DEPTH][8];
+    auto issue = [&](int tile, PoolRow<TP> (&slot)[8]) {
+        const void* base = is_v ? a.vp : a.kp;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) o[t] = f32x16{};
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    // staging: a thread moves jobs of 8 keys x 8 dims (K as 8 row pieces, V transposed in registers)
-    constexpr int kJobs = (kBK / 8) * (D / 8);
-    constexpr int kMaxJobs = (kJobs + 255) / 256;    // per thread (the workgroup has 4 waves)
-    u32x4 kr[kMaxJobs][8], vr[kMaxJobs][8];
-    auto fetch = [&](int tile) {
-        const int k0 = tile * kBK;
-#pragma unroll
-        for (int jb = 0; jb < kMaxJobs; ++jb) {
-            const int job = tid + jb * nthr;
-            if (job >= kJobs) break;
-            const int kgp = job / (D / 8), dc = job % (D / 8);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                int pos = k0 + 8 * kgp + j;
-                pos = pos < n_keys ? pos : n_keys - 1;
-                const long long off = pool_row(a, table, pos, kvh, D) + 8 * dc;
-                kr[jb][j] = load8_bf16(a.kp, off, a.pool_dtype);
-                vr[jb][j] = load8_bf16(a.vp, off, a.pool_dtype);
+        for (int j = 0; j < 8; ++j) {
+            int pos = tile * kBKP + 8 * kgp + j;
+            pos = pos < n_keys ? pos : n_keys - 1;   // tiles past the end re-read the last key (never used)
+            int blk;
+            if (TAB_LDS) {
+                blk = tab[pos / a.bs];
+            } else {
+                blk = table[pos / a.bs];
+                blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
             }
+            slot[j].load(base, (((long long)blk * a.bs + pos % a.bs) * a.Hkv + kvh) * D + 8 * dc);
         }
     };
-    auto stash = [&](int buf) {
-        uint16_t* ks = lds + buf * KBUF;
-        uint16_t* vt = lds + 2 * KBUF + buf * VBUF;
+    auto stash = [&](const PoolRow<TP> (&slot)[8], int stage) {
+        if (!is_v) {
+            uint16_t* ks = kst + stage * KBUF;
 #pragma unroll
-        for (int jb = 0; jb < kMaxJobs; ++jb) {
-            const int job = tid + jb * nthr;
-            if (job >= kJobs) break;
-            const int kgp = job / (D / 8), dc = job % (D / 8);
+            for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(&ks[(8 * kgp + j) * KROW + 8 * dc]) = slot[j].bf16();
+        } else {
+            uint16_t* vt = vst + stage * VBUF;
+            u32x4 v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(&ks[(8 * kgp + j) * KROW + 8 * dc]) = kr[jb][j];
+            for (int j = 0; j < 8; ++j) v[j] = slot[j].bf16();
             // transpose: output e (dim 8 dc + e) gathers element e of the 8 key rows
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 u32x4 t;
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
-                    const uint32_t lo = e & 1 ? vr[jb][2 * jj][e / 2] >> 16 : vr[jb][2 * jj][e / 2] & 0xffffu;
-                    const uint32_t hi = e & 1 ? vr[jb][2 * jj + 1][e / 2] >> 16 : vr[jb][2 * jj + 1][e / 2] & 0xffffu;
+                    const uint32_t lo = e & 1 ? v[2 * jj][e / 2] >> 16 : v[2 * jj][e / 2] & 0xffffu;
+                    const uint32_t hi = e & 1 ? v[2 * jj + 1][e / 2] >> 16 : v[2 * jj + 1][e / 2] & 0xffffu;
                     t[jj] = lo | (hi << 16);
                 }
                 *reinterpret_cast<u32x4*>(&vt[(8 * dc + e) * VROW + 8 * kgp]) = t;
@@ -202,58 +243,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
     };
 
-    const int n_tiles = (n_keys + kBK - 1) / kBK;
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    for (int tile = 0; tile < n_tiles; ++tile) {
-        const int k0 = tile * kBK;
-        const uint16_t* ks = lds + (tile & 1) * KBUF;
-        const uint16_t* vt = lds + 2 * KBUF + (tile & 1) * VBUF;
-        if (tile + 1 < n_tiles) fetch(tile + 1);   // in flight during this tile's products
+    // ---- consumer state
+    const int head = kvh * G + (producer ? 0 : wave);
+    const int col = lane & 31, kg = lane >> 5;      // query column, k-slot group
+    const int qpos = p0 + (col < nq ? col : nq - 1);
+    u32x4 qop[NKS];                                  // Q^T operands: q[query col][d = 16 t + 8 kg .. + 8]
+    f32x16 o[NDT];
+    float m_run = -INFINITY, l_run = 0.0f;
 
-        // ---- S^T = K Q^T for the 64 keys (two 32-key tiles)
-        f32x16 s[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int t = 0; t < NKS; ++t) {
-                const u32x4 ka = *reinterpret_cast<const u32x4*>(&ks[(32 * mt + col) * KROW + 16 * t + 8 * kg]);
-                s[mt] = mfma32(ka, qop[t], s[mt]);
-            }
+    if (TAB_LDS) __syncthreads();                    // the block ids are in LDS
 
+    auto consume = [&](int tile, int stage) {
+        const int k0 = tile * kBKP;
+        const uint16_t* ks = kst + stage * KBUF;
+        const uint16_t* vt = vst + stage * VBUF;
+        // ---- S^T = K Q^T for the 32 keys
+        f32x16 s = f32x16{};
+#pragma unroll
+        for (int t = 0; t < NKS; ++t) {
+            const u32x4 ka = *reinterpret_cast<const u32x4*>(&ks[col * KROW + 16 * t + 8 * kg]);
+            s = mfma32(ka, qop[t], s);
+        }
         // ---- mask, scale (base 2), online softmax over this lane's query column
         float tmax = -INFINITY;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = k0 + 32 * mt + 8 * (r / 4) + 4 * kg + (r % 4);
-                const float v = key <= qpos ? s[mt][r] * a.qscale : -INFINITY;
-                s[mt][r] = v;
-                tmax = fmaxf(tmax, v);
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 8 * (r / 4) + 4 * kg + (r % 4);
+            const float v = key <= qpos ? s[r] * a.qscale : -INFINITY;
+            s[r] = v;
+            tmax = fmaxf(tmax, v);
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const float m_new = fmaxf(m_run, tmax);     // finite: key 0 <= qpos is in the first tile
         const float alpha = fast_exp2(m_run - m_new);
         float psum = 0.0f;
-        u32x4 pop[4];                                // B operands of the 4 key k-steps
+        u32x4 pop[2];                                // B operands of the 2 key k-steps
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int half = 0; half < 2; ++half) {
+            float pv[8];
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                float pv[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    pv[e] = fast_exp2(s[mt][8 * half + e] - m_new);
-                    psum += pv[e];
-                }
-                u32x4 w;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    w[j] = (uint32_t)f32_to_bf16_rne(pv[2 * j]) | ((uint32_t)f32_to_bf16_rne(pv[2 * j + 1]) << 16);
-                pop[2 * mt + half] = w;
+            for (int e = 0; e < 8; ++e) {
+                pv[e] = fast_exp2(s[8 * half + e] - m_new);
+                psum += pv[e];
             }
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                w[j] = (uint32_t)f32_to_bf16_rne(pv[2 * j]) | ((uint32_t)f32_to_bf16_rne(pv[2 * j + 1]) << 16);
+            pop[half] = w;
+        }
         psum += __shfl_xor(psum, 32);
         l_run = l_run * alpha + psum;
         m_run = m_new;
@@ -261,22 +299,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int t = 0; t < NDT; ++t) o[t] *= alpha;
         }
-
-        // ---- O^T += V^T P^T: k-step (mt, half) covers keys 32 mt + 16 half + 8 (e / 4) + 4 kg + e % 4
+        // ---- O^T += V^T P^T: k-step u covers keys 16 u + 8 (e / 4) + 4 kg + e % 4
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             const uint16_t* vrow = &vt[(32 * dt + col) * VROW];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int kb = 32 * (u >> 1) + 16 * (u & 1) + 4 * kg;
+            for (int u = 0; u < 2; ++u) {
+                const int kb = 16 * u + 4 * kg;
                 const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + kb);
                 const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + kb + 8);
                 const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
                 o[dt] = mfma32(va, pop[u], o[dt]);
             }
         }
-        if (tile + 1 < n_tiles) stash((tile + 1) & 1);   // the other buffer: last read two tiles ago
-        __syncthreads();
+    };
+
+    // The two roles run separate loops with one LDS-only barrier per tile each (plus one after the prologue), so
+    // the barriers pair up and neither role's registers are live in the other's loop.
+    if (producer) {
+        // tile t lives in slot t % DEPTH, then in stage t % 2 (DEPTH is even: both compile-time in the unrolled
+        // inner loop); at tile t the slot of tile t + 1 goes to LDS and is refilled with tile t + 1 + DEPTH
+        static_assert(DEPTH % kStages == 0, "slot and stage of a tile must be compile-time in the unrolled loop");
+        if (has_job) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) issue(d, buf[d]);
+            stash(buf[0], 0);
+            issue(DEPTH, buf[0]);
+        }
+        lds_barrier();
+        for (int i = 0; i < n_tiles; i += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                const int t = i + d;
+                if (t >= n_tiles) break;             // uniform over the workgroup
+                if (has_job && t + 1 < n_tiles) {
+                    stash(buf[(d + 1) % DEPTH], (d + 1) % kStages);
+                    issue(t + 1 + DEPTH, buf[(d + 1) % DEPTH]);
+                }
+                lds_barrier();
+            }
+        }
+        return;
+    }
+    {
+        const long long base = ((long long)(row0 + (col < nq ? col : nq - 1)) * a.Hq + head) * D;
+#pragma unroll
+        for (int t = 0; t < NKS; ++t) qop[t] = load8_bf16(a.q, base + 16 * t + 8 * kg, a.q_dtype);
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) o[t] = f32x16{};
+    }
+    lds_barrier();
+    for (int t = 0; t < n_tiles; ++t) {
+        consume(t, t & (kStages - 1));
+        lds_barrier();
     }
 
     // ---- out[row0 + col][head][d] = O^T[d][col] / l (* sigmoid(gate)); lanes of both k-slot groups hold rows
@@ -337,13 +412,21 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     hipLaunchKernelGGL(prefill_kv_write, dim3((unsigned)ceil_div((size_t)threads, 256)), dim3(256), 0, s, a, D);
     int rc = check_launch("prefill_kv_write");
     if (rc) return rc;
-    const size_t lds = 2 * (size_t)(kBK * (D + kKPad) + D * (kBK + kVPad)) * sizeof(uint16_t);
+    const bool tab_lds = max_nb <= kTabCache;
+    const size_t lds = (tab_lds ? kTabCache * 4 : 0) +
+                       (size_t)kStages * (kBKP * (D + kKPad) + D * (kBKP + kVPad)) * sizeof(uint16_t);
+    const dim3 grid(n_work, Hkv), block(2 * 64 * a.G);
+    typedef void (*AttnFn)(PrefillArgs);
+    AttnFn fn;
     if (D == 256) {
-        if (int rc2 = allow_dynamic_lds((const void*)prefill_attention<256>, lds)) return rc2;
-        hipLaunchKernelGGL(prefill_attention<256>, dim3(n_work, Hkv), dim3(64 * a.G), lds, s, a);
+        if (pool_dtype == RK_BF16) fn = tab_lds ? prefill_attention<256, uint16_t, true> : prefill_attention<256, uint16_t, false>;
+        else fn = tab_lds ? prefill_attention<256, float, true> : prefill_attention<256, float, false>;
     } else {
-        hipLaunchKernelGGL(prefill_attention<128>, dim3(n_work, Hkv), dim3(64 * a.G), lds, s, a);
+        if (pool_dtype == RK_BF16) fn = tab_lds ? prefill_attention<128, uint16_t, true> : prefill_attention<128, uint16_t, false>;
+        else fn = tab_lds ? prefill_attention<128, float, true> : prefill_attention<128, float, false>;
     }
+    if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
+    hipLaunchKernelGGL(fn, grid, block, lds, s, a);
     return check_launch("prefill_attention");
 }
 
