@@ -9,7 +9,7 @@
 //      exactly what the reference's gather reads back.
 //   2. prefill_attention: one workgroup per (segment, block of 32 queries, kv-head): one consumer wave per query
 //      head of the group (MFMA products and online softmax) and as many producer waves, which stream the key range
-//      through a 2-stage LDS ring with 6 tiles of 32 keys in flight in their registers (details at the kernel).
+//      through a 2-stage LDS ring with 4 tiles of 32 keys in flight in their registers (details at the kernel).
 //      fp32 accumulation throughout; operands are bf16 (q, k, v as stored; p rounded), so results carry bf16-level
 //      error.
 //   3. The output is divided by the softmax sum, gated and written as fp32 [N, Hq, D].
@@ -25,7 +25,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBQ = 32;    // queries per wave
 constexpr int kKPad = 8;   // bf16 padding of a K row in LDS (16 bytes)
-constexpr int kVPad = 8;   // bf16 padding of a V^T row in LDS
+constexpr int kVPad = 4;   // bf16 padding of a V^T row in LDS: rows of 18 dwords (= 2 mod 4) put 16
+                           // consecutive rows' 8-byte pieces on distinct bank pairs
 
 struct PrefillArgs {
     float* out;                 // [N, Hq, D]
@@ -42,6 +43,7 @@ struct PrefillArgs {
     int q_dtype, new_dtype, pool_dtype;
     int S, n_work, N, Hq, Hkv, G, bs, max_nb, num_blocks;
     float qscale;               // log2(e) / sqrt(D)
+    uint32_t bs_recip;          // ceil(2^32 / bs): pos / bs = mulhi(pos, bs_recip) for pos * bs < 2^32
 };
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -129,12 +131,16 @@ __global__ __launch_bounds__(256) void prefill_kv_write(PrefillArgs a, int D) {
 constexpr int kBKP = 32;        // keys per tile
 constexpr int kStages = 2;      // LDS ring stages
 constexpr int kTabCache = 4096; // block ids cached in LDS (max_nb above it takes the table from global memory)
+constexpr float kLazy = 8.0f;   // log2 headroom before the running maximum is raised
 
 template <typename TP>
 struct PoolRow;                 // 8 consecutive pool elements of one row, as loaded (converted when staged)
 template <>
 struct PoolRow<uint16_t> {
-    static constexpr int kDepth = 6;
+#ifndef RK_PREFILL_DEPTH
+#define RK_PREFILL_DEPTH 4
+#endif
+    static constexpr int kDepth = RK_PREFILL_DEPTH;
     u32x4 w;
     __device__ void load(const void* base, long long off) {
         w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
@@ -168,7 +174,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int VROW = kBKP + kVPad;   // LDS V^T row stride (bf16)
     constexpr int KBUF = kBKP * KROW, VBUF = D * VROW;
     constexpr int DEPTH = PoolRow<TP>::kDepth;
-    constexpr int NJ = (kBKP / 8) * (D / 8);   // 8 x 8 jobs per tile, for K and for V
+    constexpr int NJ = (kBKP / 4) * (D / 8);   // jobs of 4 keys x 8 dims per tile
     extern __shared__ __attribute__((aligned(16))) char smem[];
     int* tab = reinterpret_cast<int*>(smem);                                  // [kTabCache] when TAB_LDS
     uint16_t* kst = reinterpret_cast<uint16_t*>(smem + (TAB_LDS ? kTabCache * 4 : 0));   // [kStages][K tile]
@@ -195,51 +201,73 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
 
-    // ---- producer state: job = 8 keys x 8 dims of K (lanes nV ..) or V (lanes 0 .. NJ-1) per tile
+    // ---- producer state: per tile a producer lane moves job = 4 keys x 8 dims of both K and V (4 + 4 row pieces
+    // of 16 bytes), the same code for every lane: a branch between K and V work would make the compiler wait for
+    // all loads in flight where the branches join
     const int pl = tid - G * 64;
-    const bool is_v = pl < NJ;
-    const int job = is_v ? pl : pl - NJ;
-    const bool has_job = producer && job < NJ;
-    const int kgp = job / (D / 8), dc = job % (D / 8);
-    PoolRow<TP> buf[DEPTH][8];
+    const int job = pl;                              // 0 .. NJ-1 in use
+    const bool has_job = producer && __builtin_amdgcn_readfirstlane(job) < NJ;   // whole waves: uniform
+    // K and V pieces use different lane orders, each chosen for conflict-free LDS writes: for K consecutive lanes
+    // take consecutive dim chunks of one key group (16-byte pieces of the same rows, contiguous); for V consecutive
+    // lanes take consecutive key groups of one dim chunk (their 8-byte V^T writes at key 4 kq of rows 8 dc + e
+    // spread over all banks; dim-chunk-major lanes would put 16 lanes on 2 bank groups)
+    const int kqk = job / (D / 8), dck = job % (D / 8);
+    const int kqv = job % (kBKP / 4), dcv = job / (kBKP / 4);
+    PoolRow<TP> buf[DEPTH][8];                       // [0..3] K rows of keys 4 kqk + j, [4..7] V rows of 4 kqv + j
+    // the 4 keys of a job: one block lookup and one base address when they lie in one block (block_size % 4 == 0:
+    // rows then differ by a constant stride), one per key otherwise
+    const bool rows4 = a.bs % 4 == 0;
+    const long long rstride = (long long)a.Hkv * D;
     auto issue = [&](int tile, PoolRow<TP> (&slot)[8]) {
-        const void* base = is_v ? a.vp : a.kp;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            int pos = tile * kBKP + 8 * kgp + j;
-            pos = pos < n_keys ? pos : n_keys - 1;   // tiles past the end re-read the last key (never used)
+        // pos = b * bs + r with b = mulhi(pos, ceil(2^32 / bs)): exact because pos * bs < 2^32 (checked on the host)
+        auto row_of = [&](int pos) {
+            const int b = (int)__umulhi((uint32_t)pos, a.bs_recip);
             int blk;
             if (TAB_LDS) {
-                blk = tab[pos / a.bs];
+                blk = tab[b];
             } else {
-                blk = table[pos / a.bs];
+                blk = table[b];
                 blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
             }
-            slot[j].load(base, (((long long)blk * a.bs + pos % a.bs) * a.Hkv + kvh) * D + 8 * dc);
-        }
+            return (long long)blk * a.bs + (pos - b * a.bs);
+        };
+        auto group = [&](int kq, int dc, const void* base, PoolRow<TP>* rows) {
+            const int p4 = tile * kBKP + 4 * kq;
+            if (rows4) {
+                // tiles past the end re-read the last key (never used); a clamped group of 4 stays in its block
+                const int pos = p4 + 3 < n_keys ? p4 : (n_keys - 1) / 4 * 4;
+                const long long off = (row_of(pos) * a.Hkv + kvh) * D + 8 * dc;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rows[j].load(base, off + j * rstride);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    int pos = p4 + j;
+                    pos = pos < n_keys ? pos : n_keys - 1;
+                    rows[j].load(base, (row_of(pos) * a.Hkv + kvh) * D + 8 * dc);
+                }
+            }
+        };
+        group(kqk, dck, a.kp, slot);
+        group(kqv, dcv, a.vp, slot + 4);
     };
     auto stash = [&](const PoolRow<TP> (&slot)[8], int stage) {
-        if (!is_v) {
-            uint16_t* ks = kst + stage * KBUF;
+        uint16_t* ks = kst + stage * KBUF;
+        uint16_t* vt = vst + stage * VBUF;
+        u32x4 v[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(&ks[(8 * kgp + j) * KROW + 8 * dc]) = slot[j].bf16();
-        } else {
-            uint16_t* vt = vst + stage * VBUF;
-            u32x4 v[8];
+        for (int j = 0; j < 4; ++j) {
+            *reinterpret_cast<u32x4*>(&ks[(4 * kqk + j) * KROW + 8 * dck]) = slot[j].bf16();
+            v[j] = slot[4 + j].bf16();
+        }
+        // transpose: V^T row 8 dc + e gets element e of the 4 key rows (8 bytes); one byte permute per word picks
+        // the same 16-bit half (low for even e, high for odd e) of two rows
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = slot[j].bf16();
-            // transpose: output e (dim 8 dc + e) gathers element e of the 8 key rows
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                u32x4 t;
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const uint32_t lo = e & 1 ? v[2 * jj][e / 2] >> 16 : v[2 * jj][e / 2] & 0xffffu;
-                    const uint32_t hi = e & 1 ? v[2 * jj + 1][e / 2] >> 16 : v[2 * jj + 1][e / 2] & 0xffffu;
-                    t[jj] = lo | (hi << 16);
-                }
-                *reinterpret_cast<u32x4*>(&vt[(8 * dc + e) * VROW + 8 * kgp]) = t;
-            }
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t sel = e & 1 ? 0x07060302u : 0x05040100u;
+            const uint32_t w0 = __builtin_amdgcn_perm(v[1][e / 2], v[0][e / 2], sel);
+            const uint32_t w1 = __builtin_amdgcn_perm(v[3][e / 2], v[2][e / 2], sel);
+            *reinterpret_cast<u32x2*>(&vt[(8 * dcv + e) * VROW + 4 * kqv]) = u32x2{w0, w1};
         }
     };
 
@@ -264,18 +292,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const u32x4 ka = *reinterpret_cast<const u32x4*>(&ks[col * KROW + 16 * t + 8 * kg]);
             s = mfma32(ka, qop[t], s);
         }
-        // ---- mask, scale (base 2), online softmax over this lane's query column
-        float tmax = -INFINITY;
+        // ---- mask (only tiles reaching past the block's first query hold keys above any query), online softmax
+        // over this lane's query column in base 2 with the scale folded into the exponent's FMA. The running
+        // maximum m is raised only when a tile's maximum exceeds it by more than kLazy: p = 2^(s - m) then stays
+        // <= 2^kLazy (exact in fp32, representable in bf16), and the accumulators are rescaled only when some
+        // column's m moves, which after the first tiles is rare.
+        if (k0 + kBKP - 1 > p0) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 8 * (r / 4) + 4 * kg + (r % 4);
-            const float v = key <= qpos ? s[r] * a.qscale : -INFINITY;
-            s[r] = v;
-            tmax = fmaxf(tmax, v);
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r / 4) + 4 * kg + (r % 4);
+                s[r] = key <= qpos ? s[r] : -INFINITY;
+            }
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);     // finite: key 0 <= qpos is in the first tile
-        const float alpha = fast_exp2(m_run - m_new);
+        float tmax = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.qscale;
+        const float m_new = tmax > m_run + kLazy ? tmax : m_run;   // finite: key 0 <= qpos is in the first tile
         float psum = 0.0f;
         u32x4 pop[2];                                // B operands of the 2 key k-steps
 #pragma unroll
@@ -283,22 +316,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             float pv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                pv[e] = fast_exp2(s[8 * half + e] - m_new);
+                pv[e] = fast_exp2(fmaf(s[8 * half + e], a.qscale, -m_new));
                 psum += pv[e];
             }
             u32x4 w;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                w[j] = (uint32_t)f32_to_bf16_rne(pv[2 * j]) | ((uint32_t)f32_to_bf16_rne(pv[2 * j + 1]) << 16);
+            for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2_rne(pv[2 * j], pv[2 * j + 1]);
             pop[half] = w;
         }
         psum += __shfl_xor(psum, 32);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (__any(alpha != 1.0f)) {
+        if (__any(m_new != m_run)) {
+            const float alpha = fast_exp2(m_run - m_new);   // 0 on the first tile (m_run = -inf)
+            l_run *= alpha;
 #pragma unroll
             for (int t = 0; t < NDT; ++t) o[t] *= alpha;
         }
+        l_run += psum;
+        m_run = m_new;
         // ---- O^T += V^T P^T: k-step u covers keys 16 u + 8 (e / 4) + 4 kg + e % 4
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
@@ -314,66 +348,90 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
 
-    // The two roles run separate loops with one LDS-only barrier per tile each (plus one after the prologue), so
-    // the barriers pair up and neither role's registers are live in the other's loop.
+    // The two roles run separate loops with the same number of LDS-only barriers: one after the prologue and one per
+    // iteration, n_iter = n_tiles rounded up to a multiple of DEPTH. Neither role's registers are live in the other's
+    // loop, and the producers' loop body has no branch at all, so the compiler can count their loads in flight
+    // exactly (a branch there makes it wait for all of them).
+    const int n_iter = (n_tiles + DEPTH - 1) / DEPTH * DEPTH;
     if (producer) {
-        // tile t lives in slot t % DEPTH, then in stage t % 2 (DEPTH is even: both compile-time in the unrolled
-        // inner loop); at tile t the slot of tile t + 1 goes to LDS and is refilled with tile t + 1 + DEPTH
-        static_assert(DEPTH % kStages == 0, "slot and stage of a tile must be compile-time in the unrolled loop");
-        if (has_job) {
-#pragma unroll
-            for (int d = 0; d < DEPTH; ++d) issue(d, buf[d]);
-            stash(buf[0], 0);
-            issue(DEPTH, buf[0]);
+        if (!has_job) {                              // whole waves without a share of the tile (D = 128)
+            for (int k = 0; k <= n_iter; ++k) lds_barrier();
+            return;
         }
+        // tile t lives in slot t % DEPTH, then in stage t % 2 (DEPTH is even: both compile-time in the unrolled
+        // inner loop); at iteration t the slot of tile t + 1 goes to LDS and is refilled with tile t + 1 + DEPTH.
+        // Tiles from n_tiles on read the last key again and fill stages nobody reads.
+        static_assert(DEPTH % kStages == 0, "slot and stage of a tile must be compile-time in the unrolled loop");
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) issue(d, buf[d]);
+        stash(buf[0], 0);
+        issue(DEPTH, buf[0]);
         lds_barrier();
-        for (int i = 0; i < n_tiles; i += DEPTH) {
+        for (int i = 0; i < n_iter; i += DEPTH) {
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
-                const int t = i + d;
-                if (t >= n_tiles) break;             // uniform over the workgroup
-                if (has_job && t + 1 < n_tiles) {
-                    stash(buf[(d + 1) % DEPTH], (d + 1) % kStages);
-                    issue(t + 1 + DEPTH, buf[(d + 1) % DEPTH]);
-                }
+                stash(buf[(d + 1) % DEPTH], (d + 1) % kStages);
+                issue(i + d + 1 + DEPTH, buf[(d + 1) % DEPTH]);
                 lds_barrier();
             }
         }
         return;
     }
     {
-        const long long base = ((long long)(row0 + (col < nq ? col : nq - 1)) * a.Hq + head) * D;
+        // one branch on the dtype around all the loads, so they are all in flight together
+        const long long base = ((long long)(row0 + (col < nq ? col : nq - 1)) * a.Hq + head) * D + 8 * kg;
+        if (a.q_dtype == RK_BF16) {
+            const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q) + base;
 #pragma unroll
-        for (int t = 0; t < NKS; ++t) qop[t] = load8_bf16(a.q, base + 16 * t + 8 * kg, a.q_dtype);
+            for (int t = 0; t < NKS; ++t) qop[t] = *reinterpret_cast<const u32x4*>(qb + 16 * t);
+        } else {
+            const float* qf = reinterpret_cast<const float*>(a.q) + base;
+            float4 x[NKS][2];
+#pragma unroll
+            for (int t = 0; t < NKS; ++t) {
+                x[t][0] = *reinterpret_cast<const float4*>(qf + 16 * t);
+                x[t][1] = *reinterpret_cast<const float4*>(qf + 16 * t + 4);
+            }
+#pragma unroll
+            for (int t = 0; t < NKS; ++t)
+                qop[t] = u32x4{pack_bf16x2_rne(x[t][0].x, x[t][0].y), pack_bf16x2_rne(x[t][0].z, x[t][0].w),
+                               pack_bf16x2_rne(x[t][1].x, x[t][1].y), pack_bf16x2_rne(x[t][1].z, x[t][1].w)};
+        }
 #pragma unroll
         for (int t = 0; t < NDT; ++t) o[t] = f32x16{};
     }
     lds_barrier();
-    for (int t = 0; t < n_tiles; ++t) {
-        consume(t, t & (kStages - 1));
+    for (int t = 0; t < n_iter; ++t) {
+        if (t < n_tiles) consume(t, t & (kStages - 1));
         lds_barrier();
     }
 
-    // ---- out[row0 + col][head][d] = O^T[d][col] / l (* sigmoid(gate)); lanes of both k-slot groups hold rows
+    // The gate values of a 32-dim block are requested together (one branch per block, not per element: a
+    // branch per element would make every gate load a round trip of its own).
     if (col < nq) {
         const float inv = 1.0f / l_run;
         const long long orow = (long long)(row0 + col) * a.Hq + head;
+        const float* gp = a.gate ? a.gate + orow * D : nullptr;
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+        for (int dt = 0; dt < NDT; ++dt) {
+            float4 gv[4];
+            if (gp) {
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) gv[r4] = *reinterpret_cast<const float4*>(gp + 32 * dt + 8 * r4 + 4 * kg);
+            }
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int d = 32 * dt + 8 * r4 + 4 * kg;
-                float v[4];
+                float v[4] = {o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
+                              o[dt][4 * r4 + 3] * inv};
+                if (gp) {
+                    const float g[4] = {gv[r4].x, gv[r4].y, gv[r4].z, gv[r4].w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[i] = o[dt][4 * r4 + i] * inv;
-                    if (a.gate) {
-                        const float g = a.gate[orow * D + d + i];
-                        v[i] = v[i] * (1.0f / (1.0f + expf(-g)));
-                    }
+                    for (int i = 0; i < 4; ++i) v[i] = v[i] * (1.0f / (1.0f + expf(-g[i])));
                 }
                 *reinterpret_cast<float4*>(a.out + orow * D + d) = make_float4(v[0], v[1], v[2], v[3]);
             }
+        }
     }
 }
 
@@ -398,6 +456,9 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
         return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d query heads over %d kv heads (built for groups of 4)",
                     Hq, Hkv);
     if (D != 128 && D != 256) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: head_dim %d not in {128, 256}", D);
+    if ((unsigned long long)max_nb * block_size * block_size >= (1ull << 32))
+        return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d blocks of %d positions (positions x block size must stay "
+                    "below 2^32)", max_nb, block_size);
     for (int dt : {q_dtype, new_dtype, pool_dtype})
         if (dt != RK_F32 && dt != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: dtype %d", dt);
     PrefillArgs a;
@@ -407,6 +468,7 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     a.S = S; a.n_work = n_work; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.bs = block_size;
     a.max_nb = max_nb; a.num_blocks = num_blocks;
     a.qscale = kLog2e / sqrtf((float)D);
+    a.bs_recip = (uint32_t)(0xffffffffu / (uint32_t)block_size + 1u);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const long long threads = (long long)N * (Hkv * D / 8);
     hipLaunchKernelGGL(prefill_kv_write, dim3((unsigned)ceil_div((size_t)threads, 256)), dim3(256), 0, s, a, D);

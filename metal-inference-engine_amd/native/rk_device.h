@@ -34,6 +34,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Two fp32 values -> packed bf16 pair (element 0 in the low 16 bits), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950. For finite inputs this is the rule of f32_to_bf16_rne.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float x0, float x1) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{x0, x1}), bf16x2_t));
+}
+
 // Pack the top halves (truncated bf16 patterns) of two fp32 bit patterns: element 0 in the low 16 bits.
 __device__ __forceinline__ uint32_t pack_hi2(uint32_t e0, uint32_t e1) {
     return (e0 >> 16) | (e1 & 0xffff0000u);
