@@ -120,14 +120,16 @@ __global__ __launch_bounds__(256) void prefill_kv_write(PrefillArgs a, int D) {
 
 // ---- 2. attention: a warp-specialised pipeline. blockDim = 2 G * 64 (G = 4): waves 0 .. G-1 are consumers (query
 // head kvh * G + wave, the work item's 32 queries), waves G .. 2G-1 are producers. Keys go in tiles of kBKP = 32.
-// Producers keep DEPTH tiles of K / V rows in flight in their registers (8 rows x 8 dims per lane and tile; the
-// block ids of the whole key range are cached in LDS first, so no table load ever sits between two tiles), and
-// per tile move the oldest one into a 2-stage LDS ring (K as rows, V transposed to [dim][key], both rounded to
-// bf16), then request the tile DEPTH ahead. Consumers compute S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = 32 keys
-// x 16 dims from LDS, B = 16 dims x 32 queries from registers), so each lane owns one query column: the online
-// softmax needs one cross-lane exchange, and the probabilities, rounded to bf16, are already the B operand of
-// O^T += V^T P^T (A = 32 dims x 16 keys from LDS). One LDS-only barrier per tile hands the stages over; it never
-// waits for the producers' outstanding loads. fp32 accumulation; bf16 operands (q, k, v as stored, p rounded).
+// Producers keep DEPTH tiles of K / V rows in flight in their registers (per lane and tile 4 keys x 8 dims of K and
+// of V; the block ids of the whole key range are cached in LDS first, so no table load ever sits between two
+// tiles), and per tile move the oldest one into a 2-stage LDS ring (K as rows, V transposed to [dim][key], both
+// rounded to bf16; the lane orders and row paddings keep every LDS write and read free of bank conflicts), then
+// request the tile DEPTH ahead. Consumers compute S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = 32 keys x 16 dims
+// from LDS, B = 16 dims x 32 queries from registers), so each lane owns one query column: the online softmax needs
+// one cross-lane exchange, and the probabilities, rounded to bf16, are already the B operand of O^T += V^T P^T
+// (A = 32 dims x 16 keys from LDS). Operand reads from LDS run two k-steps (one 32-dim block) ahead of the MFMAs
+// that use them. One LDS-only barrier per tile hands the stages over; it never waits for the producers'
+// outstanding loads. fp32 accumulation; bf16 operands (q, k, v as stored, p rounded).
 constexpr int kBKP = 32;        // keys per tile
 constexpr int kStages = 2;      // LDS ring stages
 constexpr int kTabCache = 4096; // block ids cached in LDS (max_nb above it takes the table from global memory)
@@ -285,12 +287,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int k0 = tile * kBKP;
         const uint16_t* ks = kst + stage * KBUF;
         const uint16_t* vt = vst + stage * VBUF;
-        // ---- S^T = K Q^T for the 32 keys
+        // ---- S^T = K Q^T for the 32 keys; the K operands of the next two k-steps are requested before this
+        // pair's MFMAs, so four LDS reads are in flight and the MFMA chain does not wait on each one
         f32x16 s = f32x16{};
+        const uint16_t* krow = &ks[col * KROW + 8 * kg];
+        u32x4 ka0 = *reinterpret_cast<const u32x4*>(krow), ka1 = *reinterpret_cast<const u32x4*>(krow + 16);
 #pragma unroll
-        for (int t = 0; t < NKS; ++t) {
-            const u32x4 ka = *reinterpret_cast<const u32x4*>(&ks[col * KROW + 16 * t + 8 * kg]);
-            s = mfma32(ka, qop[t], s);
+        for (int t = 0; t < NKS; t += 2) {
+            u32x4 nb0 = ka0, nb1 = ka1;
+            if (t + 2 < NKS) {
+                nb0 = *reinterpret_cast<const u32x4*>(krow + 16 * (t + 2));
+                nb1 = *reinterpret_cast<const u32x4*>(krow + 16 * (t + 3));
+            }
+            __builtin_amdgcn_sched_barrier(0);       // keep the reads ahead of the MFMAs that do not need them
+            s = mfma32(ka0, qop[t], s);
+            s = mfma32(ka1, qop[t + 1], s);
+            __builtin_amdgcn_sched_barrier(0);
+            ka0 = nb0;
+            ka1 = nb1;
         }
         // ---- mask (only tiles reaching past the block's first query hold keys above any query), online softmax
         // over this lane's query column in base 2 with the scale folded into the exponent's FMA. The running
@@ -334,17 +348,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         l_run += psum;
         m_run = m_new;
         // ---- O^T += V^T P^T: k-step u covers keys 16 u + 8 (e / 4) + 4 kg + e % 4
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
+        // (the V^T operands of the next 32-dim block are requested before this block's MFMAs)
+        auto vread = [&](int dt, u32x4 (&va)[2]) {
             const uint16_t* vrow = &vt[(32 * dt + col) * VROW];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int kb = 16 * u + 4 * kg;
                 const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + kb);
                 const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + kb + 8);
-                const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
-                o[dt] = mfma32(va, pop[u], o[dt]);
+                va[u] = u32x4{lo[0], lo[1], hi[0], hi[1]};
             }
+        };
+        u32x4 vcur[2], vnext[2];
+        vread(0, vcur);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            if (dt + 1 < NDT) vread(dt + 1, vnext);
+            __builtin_amdgcn_sched_barrier(0);
+            o[dt] = mfma32(vcur[0], pop[0], o[dt]);
+            o[dt] = mfma32(vcur[1], pop[1], o[dt]);
+            __builtin_amdgcn_sched_barrier(0);
+            vcur[0] = vnext[0];
+            vcur[1] = vnext[1];
         }
     };
 
