@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 1
+#define RK_ABI_VERSION 2
 
 /* status codes */
 #define RK_OK 0
@@ -99,11 +99,13 @@ int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float
  *   attention reads, then query i of segment s attends causally to positions 0 .. start[s] + i.
  *   work [n_work] int32: (segment << 16) | query block (blocks of 32 queries), in the order to schedule them
  *   (longest key range first balances the grid); every block of every segment must appear once.
- *   gate NULL or [N, Hq*D] fp32. Group size Hq / Hkv = 4, D in {128, 256}. bf16 MFMA operands, fp32 accumulation. */
+ *   gate NULL or [N, Hq*D] in gate_dtype (RK_F32 or RK_BF16, read as stored). Group size Hq / Hkv = 4, D in {128, 256},
+ *   max_nb * block_size^2 < 2^32. bf16 MFMA operands, fp32 accumulation. */
 int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, const void* v_new, int new_dtype,
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
-                     int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const float* gate, void* stream);
+                     int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
+                     void* stream);
 
 /* ---- P3: chunked gated delta rule (64-token chunks, WY / UT form) for packed prefill of the linear-attention
  * layers. Replaces Backend.gated_delta with T > 1 (TorchBackend.gated_delta -> ops.gated_delta_chunked,

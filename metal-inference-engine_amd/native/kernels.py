@@ -206,7 +206,7 @@ def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos
     as_kv = lambda t: t if t.dtype in KV_DTYPES else t.float()
     q, k_new, v_new = as_kv(q).contiguous(), as_kv(k_new).contiguous(), as_kv(v_new).to(as_kv(k_new).dtype).contiguous()
     if gate is not None:
-        gate = gate.to(torch.float32).contiguous()
+        gate = (gate if gate.dtype in KV_DTYPES else gate.float()).contiguous()   # bf16 / fp32 read as stored
         if gate.numel() != N * Hq * d:
             raise ValueError(f"{name}: gate has {gate.numel()} elements, expected {N * Hq * d}")
     if out is None:
@@ -221,7 +221,8 @@ def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos
                 v_new.data_ptr(), DTYPE_CODES[k_new.dtype], k_pool.data_ptr(), v_pool.data_ptr(),
                 DTYPE_CODES[k_pool.dtype], tables.data_ptr(), tables.shape[1], meta.data_ptr(),
                 meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq, Hkv, d, bs, NB,
-                gate.data_ptr() if gate is not None else None, _stream(dev))
+                gate.data_ptr() if gate is not None else None,
+                DTYPE_CODES[gate.dtype] if gate is not None else DTYPE_CODES[torch.float32], _stream(dev))
     return out
 
 

@@ -39,7 +39,8 @@ struct PrefillArgs {
     const int32_t* cu;          // [S + 1] new-row offsets
     const int32_t* start;       // [S] absolute position of each segment's first new token
     const int32_t* work;        // [n_work] (segment << 16) | query block, longest first
-    const float* gate;          // [N, Hq * D] or null
+    const void* gate;           // [N, Hq * D] gate_dtype, or null
+    int gate_dtype;
     int q_dtype, new_dtype, pool_dtype;
     int S, n_work, N, Hq, Hkv, G, bs, max_nb, num_blocks;
     float qscale;               // log2(e) / sqrt(D)
@@ -436,11 +437,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (col < nq) {
         const float inv = 1.0f / l_run;
         const long long orow = (long long)(row0 + col) * a.Hq + head;
-        const float* gp = a.gate ? a.gate + orow * D : nullptr;
+        const bool has_gate = a.gate != nullptr;
+        const bool gate16 = a.gate_dtype == RK_BF16;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             float4 gv[4];
-            if (gp) {
+            if (has_gate && gate16) {
+                const uint16_t* gp = reinterpret_cast<const uint16_t*>(a.gate) + orow * D;
+                u32x2 w[4];
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) w[r4] = *reinterpret_cast<const u32x2*>(gp + 32 * dt + 8 * r4 + 4 * kg);
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    gv[r4] = make_float4(bf16_lo(w[r4][0]), bf16_hi(w[r4][0]), bf16_lo(w[r4][1]), bf16_hi(w[r4][1]));
+            } else if (has_gate) {
+                const float* gp = reinterpret_cast<const float*>(a.gate) + orow * D;
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) gv[r4] = *reinterpret_cast<const float4*>(gp + 32 * dt + 8 * r4 + 4 * kg);
             }
@@ -449,7 +460,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const int d = 32 * dt + 8 * r4 + 4 * kg;
                 float v[4] = {o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
                               o[dt][4 * r4 + 3] * inv};
-                if (gp) {
+                if (has_gate) {
                     const float g[4] = {gv[r4].x, gv[r4].y, gv[r4].z, gv[r4].w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) v[i] = v[i] * (1.0f / (1.0f + expf(-g[i])));
@@ -470,7 +481,8 @@ extern "C" {
 int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, const void* v_new, int new_dtype,
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
-                     int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const float* gate, void* stream) {
+                     int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
+                     void* stream) {
     if (N == 0) return RK_OK;
     if (!out || !q || !k_new || !v_new || !k_pool || !v_pool || !tables || !cu_seqlens || !start_pos || !work)
         return fail(RK_ERR_ARG, "rk_paged_prefill: null pointer");
@@ -484,11 +496,11 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     if ((unsigned long long)max_nb * block_size * block_size >= (1ull << 32))
         return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d blocks of %d positions (positions x block size must stay "
                     "below 2^32)", max_nb, block_size);
-    for (int dt : {q_dtype, new_dtype, pool_dtype})
+    for (int dt : {q_dtype, new_dtype, pool_dtype, gate ? gate_dtype : RK_F32})
         if (dt != RK_F32 && dt != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: dtype %d", dt);
     PrefillArgs a;
     a.out = out; a.q = q; a.k_new = k_new; a.v_new = v_new; a.kp = k_pool; a.vp = v_pool; a.tables = tables;
-    a.cu = cu_seqlens; a.start = start_pos; a.work = work; a.gate = gate;
+    a.cu = cu_seqlens; a.start = start_pos; a.work = work; a.gate = gate; a.gate_dtype = gate_dtype;
     a.q_dtype = q_dtype; a.new_dtype = new_dtype; a.pool_dtype = pool_dtype;
     a.S = S; a.n_work = n_work; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.bs = block_size;
     a.max_nb = max_nb; a.num_blocks = num_blocks;

@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 RK_F32, RK_BF16 = 0, 1
 ERROR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "workspace too small", 4: "HIP runtime error"}
@@ -29,7 +29,8 @@ SIGNATURES = {
     "rk_kv_write": (c_int, [P, P, c_int, P, P, P, c_int] + [c_int] * 5 + [P]),
     "rk_kv_gather": (c_int, [P, P, P, P, c_int, P] + [c_int] * 7 + [P]),
     "rk_deltanet_decode": (c_int, [P] * 12 + [c_int] * 7 + [c_float, P]),
-    "rk_paged_prefill": (c_int, [P, P, c_int, P, P, c_int, P, P, c_int, P, c_int, P, P, P] + [c_int] * 8 + [P, P]),
+    "rk_paged_prefill": (c_int, [P, P, c_int, P, P, c_int, P, P, c_int, P, c_int, P, P, P] + [c_int] * 8
+                         + [P, c_int, P]),
     "rk_gated_delta_workspace_bytes": (c_size_t, [c_int, c_int]),
     "rk_gated_delta_chunked": (c_int, [P, P, c_longlong, P, P, P, c_int, P, P, P, P, P] + [c_int] * 5
                                + [P, c_size_t, P]),
