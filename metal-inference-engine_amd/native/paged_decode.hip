@@ -281,6 +281,12 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     constexpr int KS = LD::KS;
     constexpr int HB = GP / 4;               // head blocks of 4 in the score layout
     constexpr int QV = (GP * D / 4 + 63) / 64;   // float4 query pieces per lane when a sequence starts
+    // register sets for keys (KB of the NIT k-steps) and values (VB of the NVI steps): a whole tile, the next one
+    // in flight; for fp32 pools at D = 256 half a tile (the sets are refilled with the tile's second half, then
+    // the next tile's first half), which keeps the workgroup at two waves per SIMD without spilling. The
+    // arithmetic and its order do not change.
+    constexpr bool kHalf = sizeof(T) == 4 && D == 256;
+    constexpr int KB = kHalf ? NIT / 2 : NIT, VB = kHalf ? NVI / 2 : NVI;
     constexpr int REC = GP * D + 2 * GP;     // floats of one (acc, m, l) record
     static_assert(REC * 4 <= NT * NIT * 64 * 16, "a combine record must fit in the wave's query operand area");
 
@@ -491,7 +497,7 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     auto part_of = [&](int b) { return a.part + ((long long)(w + b) * a.Hkv + kvh) * REC; };
 
     reset();
-    typename LD::Vec kv[NIT], vv[NVI];
+    typename LD::Vec kv[KB], vv[VB];
     TileRows<NVI, TPI, LPT, ALIGNED> cur;
     int j0 = 0;                                      // first entry held by the lane arrays
     if (my_total > 0) {
@@ -501,10 +507,10 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         // (the scheduling barriers keep the compiler from reordering the two groups of loads)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
+        for (int it = 0; it < KB; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int vi = 0; vi < NVI; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
+        for (int vi = 0; vi < VB; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
         __builtin_amdgcn_sched_barrier(0);
         fetch_q(next_mine(bA - 1));
     }
@@ -543,9 +549,10 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 u32x4 kb[KS];
-                LD::key_operands(kv[it], kb);
+                LD::key_operands(kv[it % KB], kb);
                 __builtin_amdgcn_sched_barrier(0);
-                kv[it] = LD::load(a.kp, nxt.krow + 32 * it + 8 * grp);
+                kv[it % KB] = LD::load(a.kp, it + KB < NIT ? cur_now.krow + 32 * (it + KB) + 8 * grp
+                                                          : nxt.krow + 32 * (it + KB - NIT) + 8 * grp);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
@@ -601,10 +608,10 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
             for (int vi = 0; vi < NVI; ++vi) {
                 float vf[8];
-                LD::keep_if(vv[vi], cur_now.vvalid(vi));
-                LD::widen(vv[vi], vf);
+                LD::keep_if(vv[vi % VB], cur_now.vvalid(vi));
+                LD::widen(vv[vi % VB], vf);
                 __builtin_amdgcn_sched_barrier(0);
-                vv[vi] = LD::load(a.vp, nxt.vrow(vi));
+                vv[vi % VB] = LD::load(a.vp, vi + VB < NVI ? cur_now.vrow(vi + VB) : nxt.vrow(vi + VB - NVI));
                 __builtin_amdgcn_sched_barrier(0);
                 const int pos = vi * TPI + lane / LPT;
                 float ph[GP];
