@@ -14,7 +14,8 @@ over the whole batch (split-K kernel + merge/gate kernel), inputs already reside
 
 Other workloads print the same record for: c1, the config-1 decode (parity/latency case); c2, the config-2 DeltaNet
 decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache); c4, the config-4
-chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention.
+chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention; lp, the
+DeltaNet prefill companions (fused conv / norms / beta, g front and the gated RMSNorm) on the config-4 batch.
 Timing: W untimed warm-up steps, then K timed steps captured in one HIP graph and replayed between two events
 after a device synchronize (the eager, Python-issued rate is reported beside it).
 """
@@ -381,12 +382,115 @@ def bench_chunked_delta(args, backend):
     }
 
 
+def bench_linear_prefill(args, backend):
+    """The DeltaNet prefill companions on the config-4 batch: one step = the fused front (conv + split + l2norm +
+    beta / g, conv tails handed over) and the gated RMSNorm over 4 x 4096 packed tokens; the whole layer (front +
+    chunked delta rule + norm) is timed beside it."""
+    import torch
+    import workloads as wl
+    from native import kernels
+    from native.rocm_native import RK_F32, load
+    from state import to_device
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    case = wl.lp_linear_prefill()
+    c = case.to(dev)
+    H, dk, dv, _ = case.dims
+    C, K = case.conv_w.shape
+    N = case.y.shape[0]
+    cu = case.cu_seqlens
+    n = len(cu) - 1
+    cuc = [0]
+    for a, b in zip(cu, cu[1:]):
+        cuc.append(cuc[-1] + -(-(b - a) // kernels.DELTA_CHUNK))
+    meta = to_device(torch.tensor(cu + cuc + list(range(n)), dtype=torch.int32), dev)
+    seqs = meta.data_ptr() + 4 * (2 * n + 2)
+    lib = load()
+    ws = torch.empty(lib.lib.rk_gated_delta_workspace_bytes(cuc[-1], H), dtype=torch.uint8, device=dev)
+    qkv, z, b, a = c.cols()
+    q = torch.empty(N, H, dk, dtype=torch.float32, device=dev)
+    k, v = torch.empty_like(q), torch.empty(N, H, dv, dtype=torch.float32, device=dev)
+    beta, g = torch.empty(N, H, dtype=torch.float32, device=dev), torch.empty(N, H, dtype=torch.float32, device=dev)
+    o = torch.empty(N, H, dv, dtype=torch.float32, device=dev)
+    out = torch.empty(N * H, dv, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    sp = lambda: torch.cuda.current_stream(dev).cuda_stream
+
+    def front():      # conv tails are handed over in place each step; their values do not change the work
+        lib.call("rk_deltanet_prefill_front", q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                 g.data_ptr(), qkv.data_ptr(), b.data_ptr(), a.data_ptr(), RK_F32, qkv.stride(0), c.conv.data_ptr(),
+                 c.conv.stride(0), c.conv_w.data_ptr(), c.A_log.data_ptr(), c.dt_bias.data_ptr(), meta.data_ptr(),
+                 seqs, n, N, H, dk, dv, K, sp())
+
+    def norm():
+        lib.call("rk_rms_norm_gated", out.data_ptr(), o.data_ptr(), z.data_ptr(), RK_F32, z.stride(0), H,
+                 c.norm_w.data_ptr(), N * H, dv, case.eps, sp())
+
+    def delta():
+        lib.call("rk_gated_delta_chunked", o.data_ptr(), c.S.data_ptr(), c.S.stride(0), q.data_ptr(), k.data_ptr(),
+                 v.data_ptr(), RK_F32, beta.data_ptr(), g.data_ptr(), meta.data_ptr(), meta.data_ptr() + 4 * (n + 1),
+                 seqs, n, cuc[-1], H, dk, dv, ws.data_ptr(), ws.numel(), sp())
+
+    def step():
+        front()
+        norm()
+
+    def layer():
+        front()
+        delta()
+        norm()
+
+    for _ in range(args.warmup):
+        layer()
+    torch.cuda.synchronize()
+    ms_front = graph_time(front, args.steps, stream)
+    ms_norm = graph_time(norm, args.steps, stream)
+    ms = graph_time(step, args.steps, stream)
+    ms_layer = graph_time(layer, max(1, args.steps // 5), stream)
+    fb, nb = case.front_bytes(), case.norm_bytes()
+    gbs = fb / (ms_front * 1e-3) / 1e9
+    log(f"[bench] lp: front {ms_front * 1e3:.1f} us ({gbs:.0f} GB/s, {gbs / HBM_PEAK_GBS:.1%}), norm "
+        f"{ms_norm * 1e3:.1f} us ({nb / (ms_norm * 1e-3) / 1e9:.0f} GB/s), companions {ms * 1e3:.1f} us, whole layer "
+        f"{ms_layer * 1e3:.1f} us")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import backend_ref, ops_ref
+        torch.set_num_threads(cpu_threads())
+        lo, hi = cu[0], cu[1]
+        xq, xz, xb, xa = (t[lo:hi] for t in case.cols())
+        o_cpu = torch.randn(hi - lo, H, dv, generator=torch.Generator().manual_seed(0))
+
+        def cpu_run():
+            backend_ref.linear_attention_front(xq, xb, xa, case.conv[0], case.conv_w, case.A_log, case.dt_bias,
+                                               case.dims)
+            ops_ref.rms_norm_gated(o_cpu.reshape(-1, dv), xz.reshape(-1, dv), case.norm_w, case.eps)
+        t, calls, total = cpu_time(cpu_run, runs=3)
+        cpu = {"value": (hi - lo) / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"segment 0 alone ({hi - lo} tokens): conv + split + l2norm + beta / g and the gated "
+                         f"RMSNorm, median of {calls} calls ({total:.1f} s in all), {t * 1e3:.1f} ms per call"}
+    return {
+        "metric": "DeltaNet prefill companions tokens/s (config-4 batch) + achieved HBM GB/s (% of 8 TB/s), 1 GPU",
+        "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded)",
+        "config": {"workload": "linear-attention prefill around the delta rule: 4 x 4096 packed tokens, fp32 in_proj "
+                               "output, conv 4 over 6144 channels, 16 heads x 128, states in place",
+                   "tokens": N, "front_bytes": fb, "norm_bytes": nb, "front_ms": ms_front, "norm_ms": ms_norm,
+                   "layer_ms": ms_layer, "layer_tokens_per_s": N / (ms_layer * 1e-3)},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": traffic_for("deltanet_prefill_front/lp"),
+                     "kernel": "prefill_front_kernel + tail_handoff_kernel", "bytes_per_launch": fb,
+                     "avg_ms": ms_front},
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (for counter collection)")
@@ -424,6 +528,8 @@ def main() -> int:
         rec = bench_prefill(args, backend)
     elif args.workload == "c4":
         rec = bench_chunked_delta(args, backend)
+    elif args.workload == "lp":
+        rec = bench_linear_prefill(args, backend)
     else:
         rec = bench_deltanet(args, backend)
     print(json.dumps(rec), flush=True)

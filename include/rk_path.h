@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 2
+#define RK_ABI_VERSION 3
 
 /* status codes */
 #define RK_OK 0
@@ -123,6 +123,38 @@ int rk_gated_delta_chunked(float* out, float* S, long long s_stride, const void*
                            int in_dtype, const float* beta, const float* g, const int32_t* cu_seqlens,
                            const int32_t* cu_chunks, const int32_t* seq_index, int n_seqs, int total_chunks, int H,
                            int dk, int dv, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- DeltaNet prefill companions: the rest of a linear-attention segment's prefill around P3
+ * (src/models/qwen3_5.py:144-162). fp32 outputs; x_dtype / z_dtype RK_F32 or RK_BF16 (read as stored).
+ *
+ * rk_causal_conv1d replaces Backend.causal_conv1d (ops.causal_conv1d, src/ops.py:127-139) for one segment:
+ *   x: row t (t < T) at x + t * x_ld, C channels; tail [K-1, C] fp32; w [C, K] fp32 (tap K-1 multiplies the
+ *   current token). hist = [tail rounded to x's dtype; x]; u [T, C] fp32 = silu(sum_j hist[t + j] * w[:, j]);
+ *   new_tail [K-1, C] in x_dtype = the last K-1 rows of hist. 2 <= K <= 8.
+ *
+ * rk_deltanet_prefill_front fuses, for n_seqs packed segments (rows cu_seqlens[s] .. cu_seqlens[s+1]-1, device
+ * int32 [n_seqs + 1]), the conv, the q/k/v split, l2norm (src/ops.py:115-117), q * 1/sqrt(dk), beta = sigmoid(b)
+ * and g = -exp(A_log) * softplus(a + dt_bias) of src/models/qwen3_5.py:145-155, and the conv-state update of :159:
+ *   qkv / b / a: row n at ptr + n * ld (x_dtype; C = 2*H*dk + H*dv, H and H channels) -- the columns of the fused
+ *   in_proj output; q, k [N, H, dk], v [N, H, dv], beta, g [N, H] fp32 (the inputs of rk_gated_delta_chunked).
+ *   Segment s's conv tail is [K-1, C] fp32 at conv_state + seq_index[s] * conv_stride: read as the old tail and
+ *   overwritten with the new one (in x's dtype, widened). seq_index NULL: zero tails, conv_state untouched.
+ *   Indices of non-empty segments must be distinct. dk = dv = 128, 2 <= K <= 4; qkv and conv_state 8-byte (fp32) /
+ *   4-byte (bf16) aligned with even strides.
+ *
+ * rk_rms_norm_gated replaces Backend.rms_norm_gated (ops.rms_norm_gated, src/ops.py:120-124):
+ *   out [rows, dv] fp32 = x * (1 / sqrt(mean(x^2) + eps)) * w * silu(z); x [rows, dv] fp32, w [dv] fp32; row r of
+ *   z at z + (r / z_group) * z_ld + (r % z_group) * dv (contiguous: z_group 1, z_ld dv). dv in {64, 128, 256, 512};
+ *   x, out, w, z and z_ld aligned to dv / 64 elements. */
+int rk_causal_conv1d(float* u, void* new_tail, const void* x, int x_dtype, long long x_ld, const float* tail,
+                     const float* w, int T, int C, int K, void* stream);
+int rk_deltanet_prefill_front(float* q, float* k, float* v, float* beta, float* g, const void* qkv, const void* b,
+                              const void* a, int x_dtype, long long ld, float* conv_state, long long conv_stride,
+                              const float* conv_w, const float* A_log, const float* dt_bias,
+                              const int32_t* cu_seqlens, const int32_t* seq_index, int n_seqs, int N, int H, int dk,
+                              int dv, int conv_k, void* stream);
+int rk_rms_norm_gated(float* out, const float* x, const void* z, int z_dtype, long long z_ld, int z_group,
+                      const float* w, int rows, int dv, float eps, void* stream);
 
 #ifdef __cplusplus
 }

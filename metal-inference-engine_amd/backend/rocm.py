@@ -15,6 +15,10 @@ Method -> kernel:
                          KV write-back, causal attention over prefix + new tokens, fused gate)
   gated_delta[_packed]   rk_gated_delta_chunked (P3; the chunked delta rule of the linear-attention prefill,
                          src/models/qwen3_5.py:157, for one sequence or many packed sequences per launch pair)
+  causal_conv1d          rk_causal_conv1d (src/ops.py:127-139)
+  rms_norm_gated         rk_rms_norm_gated (src/ops.py:120-124)
+  deltanet_prefill       rk_deltanet_prefill_front + rk_gated_delta_chunked + rk_rms_norm_gated: a whole packed
+                         linear-attention prefill (src/models/qwen3_5.py:144-162) in four launches
 """
 import torch
 
@@ -114,6 +118,48 @@ class RocmBackend:
                                                          conv_w, A_log, dt_bias, norm_w, eps, dims)
                               for i, st in enumerate(states)])
         return kernels.deltanet_decode(qkv, z, b, a, conv, S, seqs, slot, conv_w, A_log, dt_bias, norm_w, eps, dims)
+
+    # ---- DeltaNet prefill companions
+    def causal_conv1d(self, x, tail, w):
+        """Backend.causal_conv1d (src/backend/base.py:44-45): x [T, C], tail [K-1, C], w [C, K] -> (silu(conv)
+        [T, C] fp32, new tail [K-1, C] in x's dtype), ops.causal_conv1d (src/ops.py:127-139)."""
+        return kernels.causal_conv1d(x, tail, w)
+
+    def rms_norm_gated(self, x, z, w, eps):
+        """Backend.rms_norm_gated (src/backend/base.py:50-51): x, z [rows, dv] -> fp32 [rows, dv],
+        ops.rms_norm_gated (src/ops.py:120-124)."""
+        return kernels.rms_norm_gated(x, z, w, eps)
+
+    def deltanet_prefill(self, qkv, z, b, a, states, slot, cu_seqlens, conv_w, A_log, dt_bias, norm_w, eps, dims):
+        """Packed prefill of one linear-attention layer, every segment at once (the per-segment loop of
+        src/models/qwen3_5.py:144-162): conv + split + l2norm + beta / g (one fused launch, conv tails handed over
+        in the state), the chunked delta rule (P3) and the gated RMSNorm -> [N, H * dv] fp32.
+        qkv [N, C], z [N, H * dv], b, a [N, H] may be column slices of the fused in_proj output (strided rows).
+        Rows cu_seqlens[i] .. cu_seqlens[i+1]-1 belong to states[i] (HybridStates of one HybridPool, or a single
+        standalone state), whose slot `slot` is updated; states None: zero initial states, nothing stored (the
+        reference's `state is None` branch)."""
+        H, dk, dv, _ = dims
+        cu = [int(x) for x in cu_seqlens]
+        n = len(cu) - 1
+        N = qkv.shape[0]
+        if states is None:
+            conv = seqs = None
+            S = torch.zeros(n, H, dk, dv, dtype=torch.float32, device=self.device)
+        else:
+            if len(states) != n:
+                raise ValueError(f"deltanet_prefill: {n} segments but {len(states)} states")
+            pool = getattr(states[0], "pool", None)
+            if pool is not None and all(getattr(st, "pool", None) is pool for st in states):
+                conv, S, seqs = pool.conv[:, slot], pool.S[:, slot], pool.seq_index(states)
+            elif n == 1:
+                conv, S, seqs = states[0].conv_tail[slot].unsqueeze(0), states[0].S[slot].unsqueeze(0), self._seq0
+            else:
+                return torch.cat([self.deltanet_prefill(qkv[lo:hi], z[lo:hi], b[lo:hi], a[lo:hi], [st], slot,
+                                                        [0, hi - lo], conv_w, A_log, dt_bias, norm_w, eps, dims)
+                                  for st, lo, hi in zip(states, cu, cu[1:])])
+        q, k, v, beta, g = kernels.deltanet_prefill_front(qkv, b, a, conv, seqs, conv_w, A_log, dt_bias, cu, dims)
+        o = kernels.gated_delta_chunked(q, k, v, beta, g, S, cu, seqs)
+        return kernels.rms_norm_gated(o.view(N * H, dv), z, norm_w, eps).view(N, H * dv)
 
     def sync(self) -> None:
         torch.cuda.synchronize(self.device)

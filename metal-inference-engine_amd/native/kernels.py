@@ -280,3 +280,128 @@ def gated_delta_chunked(q, k, v, beta, g, S, cu_seqlens, seq_index=None, out=Non
              meta.data_ptr() + 4 * (n_seqs + 1), seq_index.data_ptr() if seq_index is not None else None, n_seqs,
              cuc[-1], H, dk, dv, ws.data_ptr(), ws.numel(), _stream(dev))
     return out
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """A 2-D view whose rows are unit-stride (any row stride): kept as is, or copied when the columns are strided."""
+    return t if t.stride(1) == 1 else t.contiguous()
+
+
+def causal_conv1d(x, tail, w) -> tuple[torch.Tensor, torch.Tensor]:
+    """Backend.causal_conv1d for one segment (rk_causal_conv1d): x [T, C] (fp32 or bf16 read as stored; rows may be
+    strided, as the qkv columns of a fused projection output), tail [K-1, C], w [C, K]
+    -> (silu(conv) [T, C] fp32, new tail [K-1, C] in x's dtype)."""
+    name = "causal_conv1d"
+    if x.dim() != 2 or tail.dim() != 2 or w.dim() != 2:
+        raise ValueError(f"{name}: x {tuple(x.shape)}, tail {tuple(tail.shape)}, w {tuple(w.shape)}")
+    T, C = x.shape
+    K = w.shape[1]
+    if w.shape[0] != C or tail.shape != (K - 1, C):
+        raise ValueError(f"{name}: x [{T}, {C}], tail {tuple(tail.shape)}, w {tuple(w.shape)}")
+    dev = _need_cuda(name, x, tail, w)
+    if x.dtype not in KV_DTYPES:
+        x = x.float()
+    x = _rows(x)
+    tail = tail.to(device=dev, dtype=torch.float32).contiguous()
+    w = w.to(device=dev, dtype=torch.float32).contiguous()
+    u = torch.empty(T, C, dtype=torch.float32, device=dev)
+    new_tail = torch.empty(K - 1, C, dtype=x.dtype, device=dev)
+    load().call("rk_causal_conv1d", u.data_ptr(), new_tail.data_ptr(), x.data_ptr(), DTYPE_CODES[x.dtype],
+                x.stride(0), tail.data_ptr(), w.data_ptr(), T, C, K, _stream(dev))
+    return u, new_tail
+
+
+def deltanet_prefill_front(qkv, b, a, conv_state, seq_index, conv_w, A_log, dt_bias, cu_seqlens, dims):
+    """Conv + split + l2norm + beta / g for packed segments, with the conv-state update (rk_deltanet_prefill_front)
+    -> (q, k [N, H, dk], v [N, H, dv], beta, g [N, H]), all fp32: the inputs of gated_delta_chunked.
+    qkv [N, C], b, a [N, H]: fp32 or bf16 (one dtype), rows may be strided (the column slices of the fused in_proj
+    output). cu_seqlens: host list of n_seqs + 1 row offsets, or a device int32 tensor of them.
+    conv_state: fp32 tails indexed along dim 0 (each [K-1, C] contiguous), segment i uses conv_state[seq_index[i]]
+    (seq_index device int32 [n_seqs]) and leaves the new tail there; conv_state None: zero tails, nothing written."""
+    name = "deltanet_prefill_front"
+    H, dk, dv, key_dim = dims
+    if key_dim != H * dk:
+        raise ValueError(f"{name}: key_dim {key_dim} != H * dk = {H * dk}")
+    N, C = qkv.shape
+    if C != 2 * key_dim + H * dv or b.shape != (N, H) or a.shape != (N, H):
+        raise ValueError(f"{name}: qkv {tuple(qkv.shape)} (expected {2 * key_dim + H * dv} channels), "
+                         f"b {tuple(b.shape)}, a {tuple(a.shape)}")
+    K = conv_w.shape[1]
+    if conv_w.shape != (C, K):
+        raise ValueError(f"{name}: conv_w {tuple(conv_w.shape)}, expected [{C}, K]")
+    dev = _need_cuda(name, qkv, b, a)
+    if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type == "cuda":
+        cu_dev = cu_seqlens
+        if cu_dev.dtype != torch.int32 or cu_dev.dim() != 1:
+            raise ValueError(f"{name}: device cu_seqlens must be int32 [n_seqs + 1]")
+        n_seqs = cu_dev.numel() - 1
+    else:
+        cu = [int(x) for x in cu_seqlens]
+        if len(cu) < 2 or cu[0] != 0 or cu[-1] != N or any(hi < lo for lo, hi in zip(cu, cu[1:])):
+            raise ValueError(f"{name}: cu_seqlens {cu[:8]}... must be non-decreasing offsets from 0 to {N}")
+        n_seqs = len(cu) - 1
+        from state import to_device
+        cu_dev = to_device(torch.tensor(cu, dtype=torch.int32), dev)
+    if conv_state is not None:
+        if conv_state.dtype != torch.float32 or conv_state.dim() != 3 or conv_state.shape[1:] != (K - 1, C) or \
+                conv_state.stride()[1:] != (C, 1):
+            raise ValueError(f"{name}: conv state {tuple(conv_state.shape)} {conv_state.dtype} must be fp32 "
+                             f"[n, {K - 1}, {C}] with contiguous inner dims")
+        _need_cuda(name, conv_state, seq_index)
+        if seq_index.dtype != torch.int32 or seq_index.numel() != n_seqs:
+            raise ValueError(f"{name}: seq_index must be int32 [{n_seqs}]")
+    if not (qkv.dtype == b.dtype == a.dtype and qkv.dtype in KV_DTYPES):
+        qkv, b, a = qkv.float(), b.float(), a.float()
+    qkv, b, a = _rows(qkv), _rows(b), _rows(a)
+    if not (qkv.stride(0) == b.stride(0) == a.stride(0)) or qkv.stride(0) % 2 or \
+            qkv.data_ptr() % (2 * qkv.element_size()):
+        packed = torch.cat([qkv, b, a], dim=1)            # one row stride for the three inputs, aligned rows
+        if packed.shape[1] % 2:
+            packed = torch.nn.functional.pad(packed, (0, 1))
+        qkv, b, a = packed[:, :C], packed[:, C:C + H], packed[:, C + H:C + 2 * H]
+    f = lambda t: t.to(device=dev, dtype=torch.float32).contiguous()
+    conv_w, A_log, dt_bias = f(conv_w), f(A_log), f(dt_bias)
+    q = torch.empty(N, H, dk, dtype=torch.float32, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty(N, H, dv, dtype=torch.float32, device=dev)
+    beta = torch.empty(N, H, dtype=torch.float32, device=dev)
+    g = torch.empty_like(beta)
+    load().call("rk_deltanet_prefill_front", q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), g.data_ptr(),
+                qkv.data_ptr(), b.data_ptr(), a.data_ptr(), DTYPE_CODES[qkv.dtype], qkv.stride(0),
+                conv_state.data_ptr() if conv_state is not None else None,
+                conv_state.stride(0) if conv_state is not None else 0, conv_w.data_ptr(), A_log.data_ptr(),
+                dt_bias.data_ptr(), cu_dev.data_ptr(), seq_index.data_ptr() if conv_state is not None else None,
+                n_seqs, N, H, dk, dv, K, _stream(dev))
+    return q, k, v, beta, g
+
+
+def rms_norm_gated(x, z, w, eps: float, out=None) -> torch.Tensor:
+    """Backend.rms_norm_gated (rk_rms_norm_gated): x [rows, dv] -> x * rsqrt(mean(x^2) + eps) * w * silu(z), fp32.
+    z [rows, dv], or [rows / G, G * dv] (G heads per row with any row stride: the z columns of a fused projection
+    output, without the copy a reshape to [rows, dv] would make); fp32 or bf16 read as stored."""
+    name = "rms_norm_gated"
+    if x.dim() != 2 or z.dim() != 2:
+        raise ValueError(f"{name}: x {tuple(x.shape)}, z {tuple(z.shape)}")
+    rows, dv = x.shape
+    if z.shape[1] % dv or z.shape[0] * (z.shape[1] // dv) != rows or w.numel() != dv:
+        raise ValueError(f"{name}: x {tuple(x.shape)}, z {tuple(z.shape)}, w {tuple(w.shape)}")
+    group = z.shape[1] // dv
+    dev = _need_cuda(name, x, z)
+    per = dv // 64                                        # the kernel's vector width (elements)
+    al = lambda t: t.data_ptr() % (per * t.element_size()) == 0
+    x = x.to(torch.float32).contiguous()
+    if not al(x):
+        x = x.clone()
+    if z.dtype not in KV_DTYPES:
+        z = z.float()
+    z = _rows(z)
+    if not al(z) or z.stride(0) % per:
+        z = z.contiguous() if not z.is_contiguous() else z.clone()
+    w = w.to(device=dev, dtype=torch.float32).contiguous()
+    if not al(w):
+        w = w.clone()
+    if out is None:
+        out = torch.empty(rows, dv, dtype=torch.float32, device=dev)
+    load().call("rk_rms_norm_gated", out.data_ptr(), x.data_ptr(), z.data_ptr(), DTYPE_CODES[z.dtype],
+                z.stride(0), group, w.data_ptr(), rows, dv, float(eps), _stream(dev))
+    return out

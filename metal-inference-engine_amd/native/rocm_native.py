@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 RK_F32, RK_BF16 = 0, 1
 ERROR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "workspace too small", 4: "HIP runtime error"}
@@ -34,6 +34,10 @@ SIGNATURES = {
     "rk_gated_delta_workspace_bytes": (c_size_t, [c_int, c_int]),
     "rk_gated_delta_chunked": (c_int, [P, P, c_longlong, P, P, P, c_int, P, P, P, P, P] + [c_int] * 5
                                + [P, c_size_t, P]),
+    "rk_causal_conv1d": (c_int, [P, P, P, c_int, c_longlong, P, P, c_int, c_int, c_int, P]),
+    "rk_deltanet_prefill_front": (c_int, [P] * 8 + [c_int, c_longlong, P, c_longlong] + [P] * 5 + [c_int] * 6
+                                  + [P]),
+    "rk_rms_norm_gated": (c_int, [P, P, P, c_int, c_longlong, c_int, P, c_int, c_int, c_float, P]),
 }
 
 

@@ -10,7 +10,7 @@ counters, and converters from rocprofv3 CSV output to the short text summaries a
           <name>=<pattern>:<fetch.csv>:<write.csv> ...
       HBM bytes per launch of the kernels whose names contain <pattern> (summed over kernels when the pattern
       matches several per step), from one FETCH_SIZE pass and one WRITE_SIZE pass (KiB per dispatch), each scaled
-      by what the same counter reads for the copy kernel.
+      by what the same counter reads for the copy kernel. Entries for other names already in <out.json> are kept.
 """
 import csv
 import json
@@ -59,8 +59,13 @@ def traffic(out_json: str, copy_mib: int, copy_fetch: str, copy_write: str, spec
     cf, _ = _per_dispatch(copy_fetch, "MulFunctor", "FETCH_SIZE")      # the copy, not the fill that made its input
     cw, _ = _per_dispatch(copy_write, "MulFunctor", "WRITE_SIZE")
     f_scale, w_scale = nbytes / (cf * 1024), nbytes / (cw * 1024)
-    out = {"_calibration": {"copy_bytes": nbytes, "fetch_kib": cf, "write_kib": cw, "fetch_scale": f_scale,
-                            "write_scale": w_scale}}
+    # entries of other workloads already in the file are kept (each was scaled by the calibration of its own run)
+    try:
+        out = json.loads(open(out_json).read())
+    except FileNotFoundError:
+        out = {}
+    out["_calibration"] = {"copy_bytes": nbytes, "fetch_kib": cf, "write_kib": cw, "fetch_scale": f_scale,
+                           "write_scale": w_scale}
     for spec in specs:
         name, rest = spec.split("=", 1)
         pattern, fetch_csv, write_csv = rest.split(":")

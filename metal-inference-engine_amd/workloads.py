@@ -293,3 +293,70 @@ def chunked_delta_case(lengths: list[int], H: int = DN_HEADS, dtype=torch.bfloat
 def c4_chunked_delta(seed: int = 4) -> ChunkedDeltaCase:
     """Config 4: batch 4 x 4096 tokens, 16 heads, dk = dv = 128, bf16 inputs, fp32 state starting at zero."""
     return chunked_delta_case([4096] * 4, seed=seed)
+
+
+@dataclass
+class LinearPrefillCase:
+    """Packed prefill of one linear-attention layer around the delta rule (src/models/qwen3_5.py:128-162): the fused
+    in_proj output y [N, C | H*dv | H | H] (qkv, z, beta logits, a; fp32, as the reference's linear returns), the
+    layer's conv_w [C, K], A_log, dt_bias [H], norm_w [dv], segment offsets cu_seqlens, and per-segment states
+    S [n, H, dk, dv], conv [n, K-1, C] fp32."""
+    y: torch.Tensor
+    conv_w: torch.Tensor
+    A_log: torch.Tensor
+    dt_bias: torch.Tensor
+    norm_w: torch.Tensor
+    S: torch.Tensor
+    conv: torch.Tensor
+    cu_seqlens: list
+    eps: float = 1e-6
+    dims: tuple = (DN_HEADS, DN_DK, DN_DV, KEY_DIM)
+
+    def to(self, device) -> "LinearPrefillCase":
+        f = lambda t: t.to(device)
+        return LinearPrefillCase(f(self.y), f(self.conv_w), f(self.A_log), f(self.dt_bias), f(self.norm_w),
+                                 f(self.S), f(self.conv), list(self.cu_seqlens), self.eps, self.dims)
+
+    def cols(self):
+        """(qkv, z, b, a): the column slices of y (strided rows), as the model takes them."""
+        H, _, dv, _ = self.dims
+        C = self.conv_w.shape[0]
+        return self.y[:, :C], self.y[:, C:C + H * dv], self.y[:, -2 * H:-H], self.y[:, -H:]
+
+    def front_bytes(self) -> int:
+        """Algorithmic HBM bytes of the fused front (conv + split + norms + beta / g + tail handoff): the qkv, b, a
+        columns read once, q, k, v, beta, g written once (fp32), conv_w read, each segment's tail read and written."""
+        N = self.y.shape[0]
+        H, dk, dv, _ = self.dims
+        C, K = self.conv_w.shape
+        xb = self.y.element_size()
+        per_token = (C + 2 * H) * xb + (2 * H * dk + H * dv + 2 * H) * 4
+        return N * per_token + C * K * 4 + 2 * (len(self.cu_seqlens) - 1) * (K - 1) * C * 4
+
+    def norm_bytes(self) -> int:
+        """rms_norm_gated: x [N*H, dv] fp32 and z read, out written, norm_w read."""
+        N = self.y.shape[0]
+        H, _, dv, _ = self.dims
+        return N * H * dv * (4 + self.y.element_size() + 4) + dv * 4
+
+
+def linear_prefill_case(lengths: list[int], dtype=torch.float32, seed: int = 0) -> LinearPrefillCase:
+    """y ~ N(0, 1) (a column block * 3 to reach softplus's linear range), conv_w = 0.5 N, A_log, dt_bias = 0.5 N,
+    norm_w = 1 + 0.1 N, states S = 0.05 N and conv tails N(0, 1)."""
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s, scale=1.0: scale * torch.randn(*s, generator=gen)
+    N, H, C = sum(lengths), DN_HEADS, CONV_DIM
+    y = r(N, C + H * DN_DV + 2 * H)
+    y[:, -H:] *= 3.0
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    return LinearPrefillCase(y.to(dtype), r(C, CONV_K, scale=0.5), r(H, scale=0.5), r(H, scale=0.5),
+                             1.0 + r(DN_DV, scale=0.1), r(len(lengths), H, DN_DK, DN_DV, scale=0.05),
+                             r(len(lengths), CONV_K - 1, C), cu)
+
+
+def lp_linear_prefill(seed: int = 6) -> LinearPrefillCase:
+    """The config-4 batch (4 x 4096 tokens, 16 heads x 128 x 128, conv 4 over 6144 channels) one step earlier: the
+    fp32 in_proj output of a linear-attention layer, before conv, norms and the delta rule."""
+    return linear_prefill_case([4096] * 4, seed=seed)

@@ -19,7 +19,7 @@ def deltanet_decode(qkv, z, b, a, state, slot, conv_w, A_log, dt_bias, norm_w, e
     """One token of one DeltaNet layer, torch_ref.py:61-73. Returns [1, H * dv]; updates state.conv_tail[slot] and
     state.S[slot] in place."""
     H, dk, dv, key_dim = dims
-    u, state.conv_tail[slot] = ops_ref.causal_conv1d(qkv.float(), state.conv_tail[slot], conv_w)
+    u, state.conv_tail[slot] = ops_ref.causal_conv1d(qkv, state.conv_tail[slot], conv_w)   # qkv as given (:65)
     q = ops_ref.l2norm(u[:, :key_dim].reshape(1, H, dk).float()) * (1.0 / dk ** 0.5)
     k = ops_ref.l2norm(u[:, key_dim:2 * key_dim].reshape(1, H, dk).float())
     v = u[:, 2 * key_dim:].reshape(1, H, dv).float()
@@ -34,6 +34,52 @@ def deltanet_decode_batch(qkv, z, b, a, states, slot, conv_w, A_log, dt_bias, no
     """One sequence at a time (torch_ref.py:90-93) -> [B, H * dv]."""
     return torch.cat([deltanet_decode(qkv[i:i + 1], z[i:i + 1], b[i:i + 1], a[i:i + 1], st, slot, conv_w, A_log,
                                       dt_bias, norm_w, eps, dims) for i, st in enumerate(states)])
+
+
+def linear_attention_front(qkv, b, a, tail, conv_w, A_log, dt_bias, dims):
+    """One prefill segment's conv, split, beta / g and l2norm, src/models/qwen3_5.py:145-155
+    -> (q, k [T, H, dk], v [T, H, dv], beta, g [T, H], new conv tail [K-1, C] in qkv's dtype)."""
+    H, dk, dv, key_dim = dims
+    T = qkv.shape[0]
+    u, new_tail = ops_ref.causal_conv1d(qkv, tail, conv_w)                 # conv BEFORE the split (:145)
+    q = u[:, :key_dim].reshape(T, H, dk)
+    k = u[:, key_dim:2 * key_dim].reshape(T, H, dk)
+    v = u[:, 2 * key_dim:].reshape(T, H, dv)
+    beta = torch.sigmoid(b.float())
+    ab = a.float() + dt_bias
+    g = -torch.exp(A_log) * torch.where(ab > 20, ab, torch.log1p(torch.exp(ab)))
+    q = ops_ref.l2norm(q.float()) * (1.0 / dk ** 0.5)
+    k = ops_ref.l2norm(k.float())
+    return q, k, v.float(), beta, g, new_tail
+
+
+def linear_attention_segments(qkv, z, b, a, states, slot, cu, conv_w, A_log, dt_bias, norm_w, eps, dims):
+    """The per-segment loop of src/models/qwen3_5.py:136-162 (projections excluded): rows cu[i] .. cu[i+1]-1 belong
+    to states[i] (updated in place at [slot]), or to a fresh zero state when states is None (nothing stored).
+    A one-token segment with a state takes the decode step (:139-143). Returns [N, H * dv]."""
+    H, dk, dv, key_dim = dims
+    K, C = conv_w.shape[1], conv_w.shape[0]
+    outs = []
+    for i, (lo, hi) in enumerate(zip(cu, cu[1:])):
+        T = hi - lo
+        if T == 0:
+            continue
+        st = states[i] if states is not None else None
+        if T == 1 and st is not None:
+            outs.append(deltanet_decode(qkv[lo:hi], z[lo:hi], b[lo:hi], a[lo:hi], st, slot, conv_w, A_log, dt_bias,
+                                        norm_w, eps, dims))
+            continue
+        tail = st.conv_tail[slot] if st is not None else torch.zeros(K - 1, C)
+        q, k, v, beta, g, new_tail = linear_attention_front(qkv[lo:hi], b[lo:hi], a[lo:hi], tail, conv_w, A_log,
+                                                            dt_bias, dims)
+        S = st.S[slot] if st is not None else torch.zeros(H, dk, dv)
+        o, S = gated_delta(q, k, v, beta, g, S)
+        if st is not None:
+            st.S[slot] = S
+            st.conv_tail[slot] = new_tail
+        o = ops_ref.rms_norm_gated(o.reshape(T * H, dv), z[lo:hi].reshape(T * H, dv), norm_w, eps)
+        outs.append(o.reshape(T, H * dv))
+    return torch.cat(outs)
 
 
 def paged_gather(k_pool, v_pool, table_row, n: int, block_size: int, window: int | None = None):

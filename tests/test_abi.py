@@ -122,3 +122,35 @@ def test_gated_delta_arguments_checked_on_host(lib):
     assert call(dt=7) == 2 and "dtype" in lib.last_error()
     assert call(stride=128) == 1 and "stride" in lib.last_error()
     assert call(wsb=ws - 1) == 3 and "workspace" in lib.last_error()
+
+
+def test_deltanet_prefill_companions_checked_on_host(lib):
+    fake = 4096
+    C = 6144
+
+    def front(**kw):
+        a = dict(q=fake, k=fake, v=fake, beta=fake, g=fake, qkv=fake, b=fake, a=fake, dt=1, ld=C + 2048 + 32,
+                 conv=fake, cs=3 * C, w=fake, A=fake, dtb=fake, cu=fake, idx=fake, n=4, N=100, H=16, dk=128, dv=128,
+                 K=4)
+        a.update(kw)
+        return lib.lib.rk_deltanet_prefill_front(*a.values(), None)
+
+    assert front(qkv=None) == 1 and "null pointer" in lib.last_error()
+    assert front(conv=None) == 1 and "null pointer" in lib.last_error()
+    assert front(dk=64) == 2 and "dk 64" in lib.last_error()
+    assert front(dt=5) == 2 and "dtype 5" in lib.last_error()
+    assert front(K=9) == 1 and "conv kernel 9" in lib.last_error()
+    assert front(ld=C - 2) == 1 and "row stride" in lib.last_error()
+    assert front(cs=3 * C - 2) == 1 and "state stride" in lib.last_error()
+    assert front(ld=C + 1) == 1 and "aligned" in lib.last_error()
+    assert front(qkv=fake + 2, dt=0) == 1 and "aligned" in lib.last_error()
+    assert front(N=0) == 0                                           # nothing to do
+    assert lib.lib.rk_causal_conv1d(fake, fake, fake, 0, C, fake, fake, 5, C, 1, None) == 1
+    assert "K 1" in lib.last_error()
+    assert lib.lib.rk_causal_conv1d(fake, fake, fake, 0, C - 1, fake, fake, 5, C, 4, None) == 1
+    assert lib.lib.rk_causal_conv1d(fake, fake, fake, 3, C, fake, fake, 5, C, 4, None) == 2
+    assert lib.lib.rk_rms_norm_gated(fake, fake, fake, 0, 128, 1, fake, 10, 96, 1e-6, None) == 1
+    assert "dv 96" in lib.last_error()
+    assert lib.lib.rk_rms_norm_gated(fake, fake, fake, 0, 16 * 128 - 1, 16, fake, 32, 128, 1e-6, None) == 1
+    assert lib.lib.rk_rms_norm_gated(fake, fake, fake, 2, 128, 1, fake, 10, 128, 1e-6, None) == 2
+    assert lib.lib.rk_rms_norm_gated(None, None, None, 0, 128, 1, None, 0, 128, 1e-6, None) == 0

@@ -186,3 +186,72 @@ def test_softplus_threshold_is_torch_softplus():
     ab = torch.tensor([-30.0, -1.0, 0.0, 5.0, 19.99, 20.0, 20.01, 50.0])
     mine = torch.where(ab > 20, ab, torch.log1p(torch.exp(ab)))
     assert torch.allclose(mine, torch.nn.functional.softplus(ab), rtol=1e-6, atol=0)
+
+
+# ---------------------------------------------------------------- DeltaNet prefill segment (qwen3_5.py:136-162)
+
+def _dn_layer(seed, H=2, dk=8, dv=8, K=4):
+    g_ = torch.Generator().manual_seed(seed)
+    C = 2 * H * dk + H * dv
+    r = lambda *s, scale=1.0: scale * torch.randn(*s, generator=g_)
+    return dict(conv_w=r(C, K, scale=0.5), A_log=r(H, scale=0.5), dt_bias=r(H, scale=0.5),
+                norm_w=1.0 + r(dv, scale=0.1), eps=1e-6, dims=(H, dk, dv, H * dk)), C, g_
+
+
+def test_prefill_segment_equals_chained_decode_steps():
+    """One T-token prefill (chunked delta rule, conv over [tail; x], tail handoff) must equal T decode steps (the
+    recurrent path pinned by the deltanet_step fixture) token by token: outputs, final S and conv tail."""
+    layer, C, g_ = _dn_layer(11)
+    H, dk, dv, _ = layer["dims"]
+    T = 9
+    qkv, z = torch.randn(T, C, generator=g_), torch.randn(T, H * dv, generator=g_)
+    b, a = torch.randn(T, H, generator=g_), torch.randn(T, H, generator=g_)
+    S0, tail0 = 0.05 * torch.randn(1, H, dk, dv, generator=g_), torch.randn(1, 3, C, generator=g_)
+    pre = SlotState(S0.clone(), tail0.clone())
+    out = backend_ref.linear_attention_segments(qkv, z, b, a, [pre], 0, [0, T], **layer)
+    step = SlotState(S0.clone(), tail0.clone())
+    outs = [backend_ref.deltanet_decode(qkv[i:i + 1], z[i:i + 1], b[i:i + 1], a[i:i + 1], step, 0, **layer)
+            for i in range(T)]
+    assert rel_err(out, torch.cat(outs)) < 1e-5
+    assert rel_err(pre.S, step.S) < 1e-5
+    assert torch.equal(pre.conv_tail, step.conv_tail)
+
+
+@pytest.mark.parametrize("split", [1, 2, 5])
+def test_prefill_split_in_two_equals_one_prefill(split):
+    """A segment prefilled in two pieces (state and conv tail carried) equals the same tokens in one piece; a short
+    second piece (fewer tokens than the conv's K - 1) keeps part of the old tail."""
+    layer, C, g_ = _dn_layer(12)
+    H, dk, dv, _ = layer["dims"]
+    T = 7
+    qkv, z = torch.randn(T, C, generator=g_), torch.randn(T, H * dv, generator=g_)
+    b, a = torch.randn(T, H, generator=g_), torch.randn(T, H, generator=g_)
+    S0, tail0 = 0.05 * torch.randn(1, H, dk, dv, generator=g_), torch.randn(1, 3, C, generator=g_)
+    one = SlotState(S0.clone(), tail0.clone())
+    o1 = backend_ref.linear_attention_segments(qkv, z, b, a, [one], 0, [0, T], **layer)
+    two = SlotState(S0.clone(), tail0.clone())
+    o2 = torch.cat([backend_ref.linear_attention_segments(qkv[lo:hi], z[lo:hi], b[lo:hi], a[lo:hi], [two], 0,
+                                                          [0, hi - lo], **layer)
+                    for lo, hi in ((0, split), (split, T))])
+    assert rel_err(o2, o1) < 1e-5 and rel_err(two.S, one.S) < 1e-5
+    assert torch.equal(two.conv_tail, one.conv_tail)
+    assert torch.equal(one.conv_tail[0], qkv[T - 3:])           # the new tail is the last K - 1 raw inputs
+
+
+def test_prefill_tail_shorter_than_kernel():
+    """T = 2 < K - 1 = 3: the new tail is [old tail row 2; x0; x1], the conv of token 0 reads tail rows 0-2."""
+    layer, C, g_ = _dn_layer(13)
+    H, dk, dv, key_dim = layer["dims"]
+    qkv, tail = torch.randn(2, C, generator=g_), torch.randn(3, C, generator=g_)
+    q, k, v, beta, g, new_tail = backend_ref.linear_attention_front(qkv, torch.zeros(2, H), torch.zeros(2, H), tail,
+                                                                    layer["conv_w"], layer["A_log"],
+                                                                    layer["dt_bias"], layer["dims"])
+    assert torch.equal(new_tail, torch.cat([tail[2:], qkv]))
+    w = layer["conv_w"].double()
+    y0 = (tail[0].double() * w[:, 0] + tail[1].double() * w[:, 1] + tail[2].double() * w[:, 2]
+          + qkv[0].double() * w[:, 3])
+    u0 = y0 / (1 + torch.exp(-y0))
+    assert rel_err(v[0].reshape(-1), u0[2 * key_dim:]) < 1e-6
+    qn = u0[:key_dim].reshape(H, dk)
+    assert rel_err(q[0], qn / qn.norm(dim=-1, keepdim=True) / dk ** 0.5) < 1e-5
+    assert torch.allclose(beta, torch.full_like(beta, 0.5))
