@@ -15,7 +15,8 @@ over the whole batch (split-K kernel + merge/gate kernel), inputs already reside
 Other workloads print the same record for: c1, the config-1 decode (parity/latency case); c2, the config-2 DeltaNet
 decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache); c4, the config-4
 chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention; lp, the
-DeltaNet prefill companions (fused conv / norms / beta, g front and the gated RMSNorm) on the config-4 batch.
+DeltaNet prefill companions (fused conv / norms / beta, g front and the gated RMSNorm) on the config-4 batch; ap,
+the config-3 decode attention layer with its q / k norm, RoPE and KV write (rk_attn_prep) in front.
 Timing: W untimed warm-up steps, then K timed steps captured in one HIP graph and replayed between two events
 after a device synchronize (the eager, Python-issued rate is reported beside it).
 """
@@ -151,7 +152,8 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
     ws = kernels.workspace(dev, need)
     argsets = [(0, o.data_ptr(), c.q.data_ptr(), c.k_pool.data_ptr(), c.v_pool.data_ptr(),
                 kernels.DTYPE_CODES[c.k_pool.dtype], c.tables.data_ptr(), c.lens.data_ptr(), B, Hq, Hkv, d, bs, max_nb,
-                NB, int(c.window or 0), c.gate.data_ptr(), ws.data_ptr(), ws.numel(), stream.cuda_stream)
+                NB, int(c.window or 0), c.gate.data_ptr(), c.gate.stride(0), ws.data_ptr(), ws.numel(),
+                stream.cuda_stream)
                for o, c in zip(outs, sets)]
     fn = lib.lib.rk_paged_decode_phase
     j = [0]
@@ -485,12 +487,102 @@ def bench_linear_prefill(args, backend):
     }
 
 
+def bench_attn_prep(args, backend):
+    """The decode attention layer at config 3 with its pre-processing: rk_attn_prep (q / k RMSNorm, partial RoPE,
+    KV write of the 64 new tokens) + the paged decode with the fused gate. The prep kernel is also timed at the
+    config-5 prefill size (N packed tokens, q / k / v written out), where it is bandwidth-bound."""
+    import torch
+    import workloads as wl
+    from native import kernels
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    Hq, Hkv, d, rot, theta = wl.HQ, wl.HKV, wl.HEAD_DIM, 64, 1e7
+    case = wl.c3_paged_decode()
+    B, bs = case.q.shape[0], case.block_size
+    gen = torch.Generator().manual_seed(12)
+    y = torch.randn(B, (2 * Hq + 2 * Hkv) * d, generator=gen)
+    qw, kw = 1 + 0.1 * torch.randn(d, generator=gen), 1 + 0.1 * torch.randn(d, generator=gen)
+    pos = (case.lens - 1).to(torch.int32)
+    last = pos.long()
+    slots = case.tables.long().gather(1, (last // bs)[:, None])[:, 0] * bs + last % bs
+    log(f"[bench] ap: copying inputs to {dev}")
+    sets = []
+    for i in range(args.sets):
+        c = case.to(dev)
+        if i:
+            c.k_pool, c.v_pool = c.k_pool.clone(), c.v_pool.clone()
+        sets.append(c)
+    yd, qwd, kwd, posd, slotsd = y.to(dev), qw.to(dev), kw.to(dev), pos.to(dev), slots.to(dev)
+    torch.cuda.synchronize()
+    it = [0]
+
+    def prep():
+        c = sets[it[0] % len(sets)]
+        return backend.attention_prep(yd, qwd, kwd, 1e-6, posd, theta, rot, (Hq, Hkv, d), c.k_pool, c.v_pool, slotsd)
+
+    def layer():
+        c = sets[it[0] % len(sets)]
+        it[0] += 1
+        q, gate = backend.attention_prep(yd, qwd, kwd, 1e-6, posd, theta, rot, (Hq, Hkv, d), c.k_pool, c.v_pool,
+                                         slotsd)
+        backend.paged_attention(q, c.k_pool, c.v_pool, c.tables, c.lens, bs, gate=gate)
+
+    for _ in range(args.warmup):
+        layer()
+    torch.cuda.synchronize()
+    ms_prep = graph_time(prep, args.steps, stream)
+    ms = graph_time(layer, args.steps, stream)
+    # prefill size: the config-5 packed tokens, q / k / v written out (the paged prefill writes the pool itself)
+    c5 = wl.c5_prefill()
+    N = c5.q.shape[0]
+    yp = torch.randn(N, (2 * Hq + 2 * Hkv) * d, generator=gen).to(dev)
+    posp = torch.randint(0, 16384, (N,), generator=gen, dtype=torch.int32).to(dev)
+    ms_pf = graph_time(lambda: kernels.attn_prep(yp, qwd, kwd, 1e-6, posp, theta, rot, (Hq, Hkv, d)), args.steps,
+                       stream)
+    pf_bytes = N * (Hq + 2 * Hkv) * d * (4 + 4) + N * 4 + 2 * d * 4
+    pf_gbs = pf_bytes / (ms_pf * 1e-3) / 1e9
+    log(f"[bench] ap: prep {ms_prep * 1e3:.1f} us at B = {B}, prep + decode {ms * 1e3:.1f} us; prep at N = {N}: "
+        f"{ms_pf * 1e3:.1f} us ({pf_gbs:.0f} GB/s, {pf_gbs / HBM_PEAK_GBS:.1%})")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import backend_ref
+        torch.set_num_threads(cpu_threads())
+        kp, vp = case.k_pool.clone(), case.v_pool.clone()
+        blocks, offsets = (slots // bs), (slots % bs)
+
+        def cpu_run():
+            q, k, v, gate = backend_ref.attention_prep(y, qw, kw, 1e-6, pos, theta, rot, (Hq, Hkv, d))
+            kp[blocks, offsets] = k.to(kp.dtype)
+            vp[blocks, offsets] = v.to(vp.dtype)
+            o = backend_ref.paged_attention(q, kp, vp, case.tables, case.lens, bs)
+            backend_ref.gate(o.reshape(B, Hq * d), gate)
+        t, calls, total = cpu_time(cpu_run)
+        cpu = {"value": B / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"the full config-3 batch ({B} sequences): norms, RoPE, KV write, paged attention, gate; "
+                         f"median of {calls} runs ({total:.1f} s in all), {t:.4f} s per batch"}
+    return {
+        "metric": "decode attention layer tokens/s @ batch 64 (q/k norm + RoPE + KV write + paged attention + gate), "
+                  "1 GPU",
+        "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded)",
+        "config": {"workload": "config 3 decode batch with the layer's pre-processing: fp32 projection rows, "
+                               "8/2 heads x 256, 64 rotary dims, theta 1e7, bf16 pool", "prep_ms": ms_prep,
+                   "prefill_prep_tokens": N, "prefill_prep_ms": ms_pf, "prefill_prep_bytes": pf_bytes},
+        "roofline": {"bound": "hbm", "achieved": pf_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": pf_gbs / HBM_PEAK_GBS, "traffic": traffic_for("attn_prep/ap"),
+                     "kernel": "attn_prep_kernel (at the config-5 prefill size)", "bytes_per_launch": pf_bytes,
+                     "avg_ms": ms_pf},
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (for counter collection)")
@@ -530,6 +622,8 @@ def main() -> int:
         rec = bench_chunked_delta(args, backend)
     elif args.workload == "lp":
         rec = bench_linear_prefill(args, backend)
+    elif args.workload == "ap":
+        rec = bench_attn_prep(args, backend)
     else:
         rec = bench_deltanet(args, backend)
     print(json.dumps(rec), flush=True)

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 3
+#define RK_ABI_VERSION 4
 
 /* status codes */
 #define RK_OK 0
@@ -46,20 +46,21 @@ int rk_device_info(int* compute_units, char* arch, int arch_len);
  *   k_pool, v_pool: one layer of the pool, [num_blocks, block_size, Hkv, D], kv_dtype RK_F32 or RK_BF16
  *   tables [B, max_nb] int32 (rows 0-padded), lens [B] int32 (positions 0..lens[i]-1 are read)
  *   window 0 = none, else each sequence reads only positions lens[i]-window .. lens[i]-1
- *   gate   NULL or [B, Hq*D] fp32: out *= sigmoid(gate)
+ *   gate   NULL or B rows of Hq*D fp32, row i at gate + i * gate_ld (gate_ld >= Hq*D, a multiple of 4; the gate
+ *          columns of a projection output are read in place): out *= sigmoid(gate)
  *   workspace: rk_paged_decode_workspace_bytes(...) bytes of device memory (split-K partials); no zeroing needed.
  * D in {64, 128, 256}; Hq / Hkv <= 8; B <= 1024. */
 size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_size, int max_nb);
 int rk_paged_decode(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
                     const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
-                    int max_nb, int num_blocks, int window, const float* gate, void* workspace,
+                    int max_nb, int num_blocks, int window, const float* gate, long long gate_ld, void* workspace,
                     size_t workspace_bytes, void* stream);
 /* The two launches of rk_paged_decode, separately (phase 0: split-K partials into the workspace; phase 1: merge,
  * gate, write out). Used to time the dominant phase on its own; rk_paged_decode == phase 0 then phase 1. */
 int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
                           int kv_dtype, const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D,
                           int block_size, int max_nb, int num_blocks, int window, const float* gate,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          long long gate_ld, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- paged KV cache write (scatter) and read (gather)
  * rk_kv_write replaces PagedKVPool.write_batch / PagedSequence.write (src/state.py:131-134, 163-170):
@@ -155,6 +156,23 @@ int rk_deltanet_prefill_front(float* q, float* k, float* v, float* beta, float* 
                               int dv, int conv_k, void* stream);
 int rk_rms_norm_gated(float* out, const float* x, const void* z, int z_dtype, long long z_ld, int z_group,
                       const float* w, int rows, int dv, float eps, void* stream);
+
+/* ---- The steps of a gated-attention layer between its projection and attention, one launch: per-head RMSNorm of
+ * q and k with (1 + w) weights (ops.rms_norm, src/ops.py:7-15), RoPE over the first `rot` dims of q and k
+ * (ops.rope, src/ops.py:27-54), and, for decode, the write of the new K / V rows into the paged pool
+ * (PagedKVPool.write_batch, src/state.py:131-134) -- src/models/qwen3_5.py:251-262 (decode) and :100-110 (prefill).
+ *   y: row n at y + n * ld (y_dtype RK_F32 / RK_BF16): [Hq*d q | Hkv*d k | Hkv*d v | ...] (the gate columns that
+ *   follow are not read); q_w, k_w [d] fp32 = 1 + q_norm.weight / k_norm.weight; positions [N] int32;
+ *   inv_freq [rot / 2] fp32 = ops.rope_inv_freq(theta, rot), computed on the host.
+ *   q_out [N, Hq, d] fp32. k_out, v_out: NULL or [N, Hkv, d] fp32 (normed + rotated k; v as is).
+ *   slots: NULL, or [N] int64 pool rows (block * block_size + offset): k and v are written into one layer's
+ *   k_pool / v_pool [num_blocks, block_size, Hkv, d] (pool_dtype; fp32 -> bf16 rounds to nearest even); a slot
+ *   outside the pool is skipped.
+ * d in {64, 128, 256}; rot = 0 or 2 * (d / 64) * a power of 2, at most d; y 4 * (d / 64)-byte aligned (fp32). */
+int rk_attn_prep(float* q_out, float* k_out, float* v_out, void* k_pool, void* v_pool, int pool_dtype,
+                 const int64_t* slots, int num_blocks, int block_size, const void* y, int y_dtype, long long ld,
+                 const float* q_w, const float* k_w, float eps, const int32_t* positions, const float* inv_freq,
+                 int rot, int N, int Hq, int Hkv, int d, void* stream);
 
 #ifdef __cplusplus
 }

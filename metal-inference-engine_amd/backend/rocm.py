@@ -19,6 +19,8 @@ Method -> kernel:
   rms_norm_gated         rk_rms_norm_gated (src/ops.py:120-124)
   deltanet_prefill       rk_deltanet_prefill_front + rk_gated_delta_chunked + rk_rms_norm_gated: a whole packed
                          linear-attention prefill (src/models/qwen3_5.py:144-162) in four launches
+  attention_prep         rk_attn_prep: q / k RMSNorm + partial RoPE (+ the decode KV write) of a gated-attention
+                         layer (src/models/qwen3_5.py:251-262, 100-110) in one launch
 """
 import torch
 
@@ -160,6 +162,20 @@ class RocmBackend:
         q, k, v, beta, g = kernels.deltanet_prefill_front(qkv, b, a, conv, seqs, conv_w, A_log, dt_bias, cu, dims)
         o = kernels.gated_delta_chunked(q, k, v, beta, g, S, cu, seqs)
         return kernels.rms_norm_gated(o.view(N * H, dv), z, norm_w, eps).view(N, H * dv)
+
+    # ---- gated-attention pre-processing
+    def attention_prep(self, y, q_w, k_w, eps, positions, theta, rot, dims, k_pool=None, v_pool=None, slots=None):
+        """The steps between a gated-attention layer's fused projection and its attention, one launch
+        (src/models/qwen3_5.py:251-262 for decode, :100-110 for prefill): per-head q / k RMSNorm with the (1 + w)
+        weights q_w / k_w, RoPE over the first `rot` dims at `positions` (int32 [N]), and, given one pool layer and
+        int64 slots (block * block_size + offset, as write_batch addresses rows), the new K / V rows written there.
+        y [N, (2 Hq + 2 Hkv) d]; dims (Hq, Hkv, d). Returns (q [N, Hq, d] fp32, gate) with a pool, else
+        (q, k, v, gate); gate is the column slice of y (no copy)."""
+        Hq, Hkv, d = dims
+        gate = y[:, (Hq + 2 * Hkv) * d:]
+        if k_pool is None:
+            return (*kernels.attn_prep(y, q_w, k_w, eps, positions, theta, rot, dims), gate)
+        return kernels.attn_prep(y, q_w, k_w, eps, positions, theta, rot, dims, k_pool, v_pool, slots), gate
 
     def sync(self) -> None:
         torch.cuda.synchronize(self.device)

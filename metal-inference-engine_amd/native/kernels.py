@@ -48,10 +48,12 @@ def paged_decode(q, k_pool, v_pool, tables, lens, block_size: int, window: int |
                  out=None, phase: int | None = None) -> torch.Tensor:
     """Batched decode attention over one layer of a paged pool (rk_paged_decode). q [B, Hq, d] -> [B, Hq, d] fp32.
     k_pool / v_pool [num_blocks, block_size, Hkv, d] fp32 or bf16; tables [B, max_nb] int32; lens [B] int32;
-    gate None or [B, Hq * d] (out *= sigmoid(gate)). phase 0 / 1 runs one of the two launches (for timing)."""
+    gate None or [B, Hq * d] (out *= sigmoid(gate); rows may be strided). phase 0 / 1 runs one of the two launches
+    (for timing)."""
     name = "paged_attention"
     if k_pool.dtype != v_pool.dtype or k_pool.dtype not in KV_DTYPES:
-        raise TypeError(f"{name}: keys and values must both be float32 or bfloat16, not {k_pool.dtype} / {v_pool.dtype}")
+        raise TypeError(f"{name}: keys and values must both be float32 or bfloat16, not "
+                        f"{k_pool.dtype} / {v_pool.dtype}")
     if q.dim() != 3 or k_pool.dim() != 4 or k_pool.shape != v_pool.shape:
         raise ValueError(f"{name}: q {tuple(q.shape)}, pools {tuple(k_pool.shape)} / {tuple(v_pool.shape)}")
     B, Hq, d = q.shape
@@ -67,9 +69,14 @@ def paged_decode(q, k_pool, v_pool, tables, lens, block_size: int, window: int |
     _contig(name, tables, "tables"); _contig(name, lens, "lens")
     q = q.to(torch.float32).contiguous()
     if gate is not None:
-        gate = gate.to(torch.float32).contiguous()
-        if gate.numel() != B * Hq * d:
-            raise ValueError(f"{name}: gate has {gate.numel()} elements, expected {B * Hq * d}")
+        # rows of Hq * d fp32 at any 16-byte-aligned stride (the gate columns of a projection output: no copy)
+        gate = gate.to(torch.float32)
+        if gate.dim() != 2:
+            gate = gate.reshape(B, -1)
+        if gate.shape != (B, Hq * d):
+            raise ValueError(f"{name}: gate {tuple(gate.shape)}, expected [{B}, {Hq * d}]")
+        if gate.stride(1) != 1 or gate.stride(0) % 4 or gate.data_ptr() % 16:
+            gate = gate.contiguous() if not gate.is_contiguous() else gate.clone()
         _need_cuda(name, q, gate)
     if out is None:
         out = torch.empty(B, Hq, d, dtype=torch.float32, device=dev)
@@ -79,7 +86,8 @@ def paged_decode(q, k_pool, v_pool, tables, lens, block_size: int, window: int |
     ws = workspace(dev, need)
     args = (out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype],
             tables.data_ptr(), lens.data_ptr(), B, Hq, Hkv, d, bs, max_nb, NB, int(window or 0),
-            gate.data_ptr() if gate is not None else None, ws.data_ptr(), ws.numel(), _stream(dev))
+            gate.data_ptr() if gate is not None else None, gate.stride(0) if gate is not None else 0, ws.data_ptr(),
+            ws.numel(), _stream(dev))
     if phase is None:
         lib.call("rk_paged_decode", *args)
     else:
@@ -405,3 +413,66 @@ def rms_norm_gated(x, z, w, eps: float, out=None) -> torch.Tensor:
     load().call("rk_rms_norm_gated", out.data_ptr(), x.data_ptr(), z.data_ptr(), DTYPE_CODES[z.dtype],
                 z.stride(0), group, w.data_ptr(), rows, dv, float(eps), _stream(dev))
     return out
+
+
+_inv_freq: dict[tuple, torch.Tensor] = {}
+
+
+def rope_inv_freq(theta: float, rot: int, dev: torch.device) -> torch.Tensor:
+    """1 / theta^(i / (rot/2)), computed once in fp32 on the host (as the reference computes it, src/ops.py:27-33:
+    the same bits whatever device runs the rotation) and cached on the device."""
+    key = (float(theta), int(rot), str(dev))
+    t = _inv_freq.get(key)
+    if t is None:
+        half = rot // 2
+        t = (1.0 / (theta ** (torch.arange(0, half, dtype=torch.float32) / half))).to(dev)
+        _inv_freq[key] = t
+    return t
+
+
+def attn_prep(y, q_w, k_w, eps: float, positions, theta: float, rot: int, dims, k_pool=None, v_pool=None,
+              slots=None):
+    """q / k RMSNorm (1 + w weights given), partial RoPE and the KV write of a gated-attention layer (rk_attn_prep).
+    y [N, >= (Hq + 2 Hkv) d] (fp32 or bf16; rows may be strided: the fused projection output); positions [N] int32
+    (device); dims (Hq, Hkv, d). With k_pool / v_pool (one layer [num_blocks, bs, Hkv, d]) and slots ([N] int64
+    device, block * bs + offset) the new K / V rows go into the pool and q [N, Hq, d] fp32 is returned; without,
+    (q, k, v) fp32 are returned."""
+    name = "attn_prep"
+    Hq, Hkv, d = dims
+    if y.dim() != 2 or y.shape[1] < (Hq + 2 * Hkv) * d or q_w.numel() != d or k_w.numel() != d:
+        raise ValueError(f"{name}: y {tuple(y.shape)}, norm weights {q_w.numel()} / {k_w.numel()} for {dims}")
+    if not 0 <= rot <= d:
+        raise ValueError(f"{name}: rotary dims {rot} of {d}")
+    N = y.shape[0]
+    dev = _need_cuda(name, y, positions)
+    if positions.dtype != torch.int32 or positions.numel() != N:
+        raise ValueError(f"{name}: positions must be int32 [{N}]")
+    if y.dtype not in KV_DTYPES:
+        y = y.float()
+    y = _rows(y)
+    if y.data_ptr() % (d // 64 * y.element_size()) or y.stride(0) % (d // 64):
+        y = y.contiguous() if not y.is_contiguous() else y.clone()
+    f = lambda t: t.to(device=dev, dtype=torch.float32).contiguous()
+    q_w, k_w = f(q_w), f(k_w)
+    inv = rope_inv_freq(theta, rot, dev) if rot else None
+    q = torch.empty(N, Hq, d, dtype=torch.float32, device=dev)
+    lib = load()
+    common = (y.data_ptr(), DTYPE_CODES[y.dtype], y.stride(0), q_w.data_ptr(), k_w.data_ptr(), float(eps),
+              positions.data_ptr(), inv.data_ptr() if inv is not None else None, int(rot), N, Hq, Hkv, d, _stream(dev))
+    if k_pool is None:
+        k = torch.empty(N, Hkv, d, dtype=torch.float32, device=dev)
+        v = torch.empty_like(k)
+        lib.call("rk_attn_prep", q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, RK_F32, None, 0, 0, *common)
+        return q, k, v
+    if k_pool.dtype != v_pool.dtype or k_pool.dtype not in KV_DTYPES:
+        raise TypeError(f"{name}: keys and values must both be float32 or bfloat16, not "
+                        f"{k_pool.dtype} / {v_pool.dtype}")
+    if k_pool.dim() != 4 or k_pool.shape != v_pool.shape or k_pool.shape[2:] != (Hkv, d):
+        raise ValueError(f"{name}: pools {tuple(k_pool.shape)} / {tuple(v_pool.shape)} for {dims}")
+    _need_cuda(name, k_pool, v_pool, slots)
+    _contig(name, k_pool, "k_pool"); _contig(name, v_pool, "v_pool")
+    if slots.dtype != torch.int64 or slots.numel() != N:
+        raise ValueError(f"{name}: slots must be int64 [{N}]")
+    lib.call("rk_attn_prep", q.data_ptr(), None, None, k_pool.data_ptr(), v_pool.data_ptr(),
+             DTYPE_CODES[k_pool.dtype], slots.contiguous().data_ptr(), k_pool.shape[0], k_pool.shape[1], *common)
+    return q

@@ -60,6 +60,7 @@ struct DecodeArgs {
     const int32_t* tables;
     const int32_t* lens;
     const float* gate;
+    long long gate_ld;  // elements between the gate rows of consecutive sequences
     int B, Hq, Hkv, G, bs, max_nb, num_blocks, window, NW;
     int NG;         // groups of Hkv waves in a split workgroup
     float qscale;   // log2(e) / sqrt(D)
@@ -668,11 +669,12 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
     const int b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
     const int n4 = a.G * (D / 4);
     const long long obase = ((long long)b * a.Hq + (long long)kvh * a.G) * D;
+    const float* grow = a.gate ? a.gate + (long long)b * a.gate_ld + (long long)kvh * a.G * D : nullptr;
     float4 gv[NO];
 #pragma unroll
     for (int k = 0; k < NO; ++k) {
         const int i = tid + k * kT;
-        gv[k] = a.gate && i < n4 ? *reinterpret_cast<const float4*>(a.gate + obase + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        gv[k] = grow && i < n4 ? *reinterpret_cast<const float4*>(grow + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (tid < 64) plan_prefix(a, P);
     __syncthreads();
@@ -867,10 +869,13 @@ size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_
 int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
                           int kv_dtype, const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D,
                           int block_size, int max_nb, int num_blocks, int window, const float* gate,
-                          void* workspace, size_t workspace_bytes_, void* stream) {
+                          long long gate_ld, void* workspace, size_t workspace_bytes_, void* stream) {
     int rc = validate(out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
                       num_blocks, window);
     if (rc) return rc;
+    if (gate && (gate_ld < (long long)Hq * D || gate_ld % 4 || reinterpret_cast<uintptr_t>(gate) % 16))
+        return fail(RK_ERR_ARG, "rk_paged_decode: gate rows of %lld elements (>= %d, a multiple of 4, 16-byte "
+                    "aligned)", gate_ld, Hq * D);
     if (phase != 0 && phase != 1) return fail(RK_ERR_ARG, "rk_paged_decode_phase: phase %d", phase);
     const int G = Hq / Hkv;
     const int GP = G <= 4 ? 4 : 8;
@@ -888,6 +893,7 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     a.tables = tables;
     a.lens = lens;
     a.gate = gate;
+    a.gate_ld = gate_ld;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = G; a.bs = block_size; a.max_nb = max_nb;
     a.num_blocks = num_blocks; a.window = window; a.NW = NW; a.NG = groups_of(Hkv, GP);
     a.qscale = kLog2e / sqrtf((float)D);
@@ -906,13 +912,13 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
 
 int rk_paged_decode(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
                     const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
-                    int max_nb, int num_blocks, int window, const float* gate, void* workspace,
+                    int max_nb, int num_blocks, int window, const float* gate, long long gate_ld, void* workspace,
                     size_t workspace_bytes_, void* stream) {
     int rc = rk_paged_decode_phase(0, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size,
-                                   max_nb, num_blocks, window, gate, workspace, workspace_bytes_, stream);
+                                   max_nb, num_blocks, window, gate, gate_ld, workspace, workspace_bytes_, stream);
     if (rc) return rc;
     return rk_paged_decode_phase(1, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size,
-                                 max_nb, num_blocks, window, gate, workspace, workspace_bytes_, stream);
+                                 max_nb, num_blocks, window, gate, gate_ld, workspace, workspace_bytes_, stream);
 }
 
 }  // extern "C"

@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 RK_F32, RK_BF16 = 0, 1
 ERROR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "workspace too small", 4: "HIP runtime error"}
@@ -24,8 +24,9 @@ SIGNATURES = {
     "rk_abi_version": (c_int, []),
     "rk_device_info": (c_int, [P, c_char_p, c_int]),
     "rk_paged_decode_workspace_bytes": (c_size_t, [c_int] * 6),
-    "rk_paged_decode": (c_int, [P, P, P, P, c_int, P, P] + [c_int] * 8 + [P, P, c_size_t, P]),
-    "rk_paged_decode_phase": (c_int, [c_int, P, P, P, P, c_int, P, P] + [c_int] * 8 + [P, P, c_size_t, P]),
+    "rk_paged_decode": (c_int, [P, P, P, P, c_int, P, P] + [c_int] * 8 + [P, c_longlong, P, c_size_t, P]),
+    "rk_paged_decode_phase": (c_int, [c_int, P, P, P, P, c_int, P, P] + [c_int] * 8
+                              + [P, c_longlong, P, c_size_t, P]),
     "rk_kv_write": (c_int, [P, P, c_int, P, P, P, c_int] + [c_int] * 5 + [P]),
     "rk_kv_gather": (c_int, [P, P, P, P, c_int, P] + [c_int] * 7 + [P]),
     "rk_deltanet_decode": (c_int, [P] * 12 + [c_int] * 7 + [c_float, P]),
@@ -38,6 +39,8 @@ SIGNATURES = {
     "rk_deltanet_prefill_front": (c_int, [P] * 8 + [c_int, c_longlong, P, c_longlong] + [P] * 5 + [c_int] * 6
                                   + [P]),
     "rk_rms_norm_gated": (c_int, [P, P, P, c_int, c_longlong, c_int, P, c_int, c_int, c_float, P]),
+    "rk_attn_prep": (c_int, [P, P, P, P, P, c_int, P, c_int, c_int, P, c_int, c_longlong, P, P, c_float, P, P]
+                     + [c_int] * 5 + [P]),
 }
 
 

@@ -82,6 +82,23 @@ def linear_attention_segments(qkv, z, b, a, states, slot, cu, conv_w, A_log, dt_
     return torch.cat(outs)
 
 
+def attention_prep(y, q_w, k_w, eps, positions, theta, rot, dims):
+    """The gated-attention layer's steps between its projection and attention, src/models/qwen3_5.py:251-259
+    (decode; then write_batch, :262) and :100-110 (prefill): per-head RMSNorm of q and k with the (1 + w) weights, RoPE over the first `rot`
+    dims of q and k together, v and the gate split off. y [N, (2 Hq + 2 Hkv) d] -> (q [N, Hq, d], k, v [N, Hkv, d],
+    gate [N, Hq d]) fp32 (k and v are what write_batch then stores)."""
+    Hq, Hkv, d = dims
+    N = y.shape[0]
+    q = ops_ref.rms_norm(y[:, :Hq * d].reshape(N, Hq, d), q_w, eps)
+    k = ops_ref.rms_norm(y[:, Hq * d:(Hq + Hkv) * d].reshape(N, Hkv, d), k_w, eps)
+    v = y[:, (Hq + Hkv) * d:(Hq + 2 * Hkv) * d].reshape(N, Hkv, d).float()
+    gate = y[:, (Hq + 2 * Hkv) * d:]
+    qk = ops_ref.rope(torch.cat([q[..., :rot], k[..., :rot]], dim=1).contiguous(), positions, theta)
+    q = torch.cat([qk[:, :Hq], q[..., rot:]], dim=-1)
+    k = torch.cat([qk[:, Hq:], k[..., rot:]], dim=-1)
+    return q, k, v, gate
+
+
 def paged_gather(k_pool, v_pool, table_row, n: int, block_size: int, window: int | None = None):
     """The positions a decode query reads, gathered through one block-table row (torch_ref.py:81-86)."""
     nb = -(-n // block_size)

@@ -34,6 +34,30 @@ def attention(q, k, v, causal: bool = True, window: int | None = None) -> torch.
     return (scores @ vh).transpose(0, 1)                          # ops.py:103-104
 
 
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """x / sqrt(mean(x^2) + eps) * weight over the last dim, src/ops.py:7-15 (weight already 1 + w for Qwen3.5)."""
+    x32 = x.float()
+    rms = torch.sqrt(torch.mean(x32 * x32, dim=-1, keepdim=True) + eps)
+    return (x32 / rms) * weight.float()
+
+
+def rope_inv_freq(theta: float, d: int) -> torch.Tensor:
+    """1 / theta^(i / (d/2)) for i < d/2, fp32 on the CPU, src/ops.py:27-33."""
+    half = d // 2
+    return 1.0 / (theta ** (torch.arange(0, half, dtype=torch.float32) / half))
+
+
+def rope(x: torch.Tensor, positions: torch.Tensor, theta: float) -> torch.Tensor:
+    """Rotary embedding with the rotate_half pairing (i, i + d/2), src/ops.py:35-54. x [T, H, d], positions [T]."""
+    d = x.shape[-1]
+    half = d // 2
+    angles = positions.float()[:, None] * rope_inv_freq(theta, d)[None, :]
+    cos, sin = torch.cos(angles)[:, None, :], torch.sin(angles)[:, None, :]
+    x32 = x.float()
+    a, b = x32[..., :half], x32[..., half:]
+    return torch.cat((a * cos - b * sin, a * sin + b * cos), dim=-1)
+
+
 def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """x * rsqrt(sum(x^2) + eps) over the last dim, src/ops.py:115-117."""
     return x * torch.rsqrt((x * x).sum(-1, keepdim=True) + eps)

@@ -59,22 +59,28 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_null_pointer_is_an_argument_error(lib):
-    rc = lib.lib.rk_paged_decode(None, None, None, None, 1, None, None, 1, 8, 2, 256, 16, 1, 1, 0, None, None, 0,
+    rc = lib.lib.rk_paged_decode(None, None, None, None, 1, None, None, 1, 8, 2, 256, 16, 1, 1, 0, None, 0, None, 0,
                                  None)
     assert rc == 1 and "null pointer" in lib.last_error()
 
 
 def test_unsupported_shapes_are_refused(lib):
     fake = 4096                            # never dereferenced: validation fails first
-    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 8, 2, 96, 16, 1, 1, 0, None, fake, 1 << 20,
-                                 None)
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 8, 2, 96, 16, 1, 1, 0, None, 0, fake,
+                                 1 << 20, None)
     assert rc == 2 and "head_dim 96" in lib.last_error()
-    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 7, fake, fake, 1, 8, 2, 256, 16, 1, 1, 0, None, fake, 1 << 20,
-                                 None)
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 7, fake, fake, 1, 8, 2, 256, 16, 1, 1, 0, None, 0, fake,
+                                 1 << 20, None)
     assert rc == 2 and "dtype" in lib.last_error()
-    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 9, 2, 256, 16, 1, 1, 0, None, fake, 1 << 20,
-                                 None)
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 9, 2, 256, 16, 1, 1, 0, None, 0, fake,
+                                 1 << 20, None)
     assert rc == 1
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 8, 2, 256, 16, 1, 1, 0, fake, 8 * 256 - 4,
+                                 fake, 1 << 20, None)
+    assert rc == 1 and "gate rows" in lib.last_error()
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 8, 2, 256, 16, 1, 1, 0, fake, 8 * 256 + 2,
+                                 fake, 1 << 20, None)
+    assert rc == 1 and "gate rows" in lib.last_error()
     args = [fake] * 12 + [8, 16, 64, 64, 4, 1, 0, ctypes.c_float(1e-6), None]
     assert lib.lib.rk_deltanet_decode(*args) == 2 and "dk 64" in lib.last_error()
     args = [fake] * 12 + [8, 16, 128, 128, 4, 2, 2, ctypes.c_float(1e-6), None]
@@ -83,8 +89,8 @@ def test_unsupported_shapes_are_refused(lib):
 
 def test_too_small_workspace_is_refused(lib):
     fake = 4096
-    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 64, 8, 2, 256, 16, 512, 20000, 0, None, fake,
-                                 16, None)
+    rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 64, 8, 2, 256, 16, 512, 20000, 0, None, 0,
+                                 fake, 16, None)
     assert rc == 3 and "workspace" in lib.last_error()
 
 
@@ -154,3 +160,26 @@ def test_deltanet_prefill_companions_checked_on_host(lib):
     assert lib.lib.rk_rms_norm_gated(fake, fake, fake, 0, 16 * 128 - 1, 16, fake, 32, 128, 1e-6, None) == 1
     assert lib.lib.rk_rms_norm_gated(fake, fake, fake, 2, 128, 1, fake, 10, 128, 1e-6, None) == 2
     assert lib.lib.rk_rms_norm_gated(None, None, None, 0, 128, 1, None, 0, 128, 1e-6, None) == 0
+
+
+def test_attn_prep_checked_on_host(lib):
+    fake = 4096
+
+    def call(**kw):
+        a = dict(q=fake, k=None, v=None, kp=fake, vp=fake, pdt=1, slots=fake, nb=256, bs=16, y=fake, ydt=0,
+                 ld=12 * 256 + 8 * 256, qw=fake, kw=fake, eps=1e-6, pos=fake, inv=fake, rot=64, N=64, Hq=8, Hkv=2,
+                 d=256)
+        a.update(kw)
+        return lib.lib.rk_attn_prep(*a.values(), None)
+
+    assert call(q=None) == 1 and "null pointer" in lib.last_error()
+    assert call(kp=None) == 1 and "null pointer" in lib.last_error()
+    assert call(inv=None) == 1 and "null pointer" in lib.last_error()
+    assert call(d=96) == 2 and "head_dim 96" in lib.last_error()
+    assert call(rot=48) == 2 and "rotary dims 48" in lib.last_error()
+    assert call(rot=512) == 2
+    assert call(ld=11 * 256) == 1 and "row stride" in lib.last_error()
+    assert call(ydt=3) == 2 and "dtypes" in lib.last_error()
+    assert call(pdt=4) == 2
+    assert call(y=fake + 4) == 1 and "aligned" in lib.last_error()
+    assert call(N=0) == 0

@@ -255,3 +255,71 @@ def test_prefill_tail_shorter_than_kernel():
     qn = u0[:key_dim].reshape(H, dk)
     assert rel_err(q[0], qn / qn.norm(dim=-1, keepdim=True) / dk ** 0.5) < 1e-5
     assert torch.allclose(beta, torch.full_like(beta, 0.5))
+
+
+# ---------------------------------------------------------------- q/k norm + partial RoPE (qwen3_5.py:251-259)
+
+def test_rms_norm_is_transformers_qwen35_rmsnorm():
+    """ops.rms_norm with the (1 + w) weight == transformers' Qwen3_5RMSNorm (x * rsqrt(...) * (1 + w)) to rounding."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as hf
+    g_ = torch.Generator().manual_seed(31)
+    x, w = torch.randn(7, 3, 256, generator=g_) * 3, 0.1 * torch.randn(256, generator=g_)
+    norm = hf.Qwen3_5RMSNorm(256, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(w)
+        want = norm(x)
+    assert rel_err(ops_ref.rms_norm(x, 1.0 + w, 1e-6), want) < 1e-6
+
+
+def test_rope_is_transformers_apply_rotary_pos_emb():
+    """Partial RoPE over the first 64 of 256 dims, theta 1e7: the oracle's rope on the rotated slice equals
+    transformers' apply_rotary_pos_emb with cos / sin of the same angles (inv_freq as transformers computes it)."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as hf
+    g_ = torch.Generator().manual_seed(32)
+    T, Hq, Hkv, d, rot, theta = 9, 8, 2, 256, 64, 1e7
+    q, k = torch.randn(T, Hq, d, generator=g_), torch.randn(T, Hkv, d, generator=g_)
+    pos = torch.tensor([0, 1, 2, 100, 4095, 4096, 16383, 20000, 123457], dtype=torch.int32)
+    inv = 1.0 / (theta ** (torch.arange(0, rot, 2, dtype=torch.float) / rot))
+    assert torch.equal(inv, ops_ref.rope_inv_freq(theta, rot))
+    emb = torch.cat([pos.float()[:, None] * inv[None], pos.float()[:, None] * inv[None]], dim=-1)
+    hq, hk = hf.apply_rotary_pos_emb(q.transpose(0, 1), k.transpose(0, 1), emb.cos(), emb.sin(), unsqueeze_dim=0)
+    qk = ops_ref.rope(torch.cat([q[..., :rot], k[..., :rot]], dim=1), pos, theta)
+    assert torch.equal(qk[:, :Hq], hq.transpose(0, 1)[..., :rot])
+    assert torch.equal(qk[:, Hq:], hk.transpose(0, 1)[..., :rot])
+
+
+def test_rope_invariants():
+    """Position 0 is the identity; every pair keeps its length; rotating by p then by s equals rotating by p + s
+    (to the rounding of the angles); a float64 rotation of the same fp32 angles agrees."""
+    g_ = torch.Generator().manual_seed(33)
+    x = torch.randn(4, 3, 64, generator=g_)
+    zero = torch.zeros(4, dtype=torch.int32)
+    assert torch.equal(ops_ref.rope(x, zero, 1e7), x)
+    pos = torch.tensor([1, 7, 300, 5000], dtype=torch.int32)
+    y = ops_ref.rope(x, pos, 1e7)
+    pair = lambda t: t[..., :32] ** 2 + t[..., 32:] ** 2
+    assert torch.allclose(pair(y), pair(x), rtol=1e-5, atol=1e-6)
+    yy = ops_ref.rope(ops_ref.rope(x, pos, 1e7), pos, 1e7)
+    assert rel_err(yy, ops_ref.rope(x, 2 * pos, 1e7)) < 1e-4
+    ang = (pos.float()[:, None] * ops_ref.rope_inv_freq(1e7, 64)[None]).double()[:, None, :]
+    a, b = x[..., :32].double(), x[..., 32:].double()
+    want = torch.cat([a * ang.cos() - b * ang.sin(), a * ang.sin() + b * ang.cos()], dim=-1)
+    assert rel_err(y, want) < 1e-6
+
+
+def test_attention_prep_splits_norms_and_rotates():
+    """The composition of qwen3_5.py:251-259 on a small layer: v and the gate are untouched slices, dims past `rot`
+    are only normalised, and the rotated q / k heads equal rope(rms_norm(...)) head by head."""
+    g_ = torch.Generator().manual_seed(34)
+    N, Hq, Hkv, d, rot = 5, 4, 2, 32, 8
+    y = torch.randn(N, (2 * Hq + 2 * Hkv) * d, generator=g_)
+    qw, kw = 1 + 0.1 * torch.randn(d, generator=g_), 1 + 0.1 * torch.randn(d, generator=g_)
+    pos = torch.tensor([0, 3, 9, 27, 81], dtype=torch.int32)
+    q, k, v, gate = backend_ref.attention_prep(y, qw, kw, 1e-6, pos, 1e4, rot, (Hq, Hkv, d))
+    assert torch.equal(v, y[:, (Hq + Hkv) * d:(Hq + 2 * Hkv) * d].reshape(N, Hkv, d))
+    assert torch.equal(gate, y[:, (Hq + 2 * Hkv) * d:])
+    qn = ops_ref.rms_norm(y[:, :Hq * d].reshape(N, Hq, d), qw, 1e-6)
+    assert torch.equal(q[..., rot:], qn[..., rot:])
+    assert torch.equal(q[..., :rot], ops_ref.rope(qn[..., :rot], pos, 1e4))
+    kn = ops_ref.rms_norm(y[:, Hq * d:(Hq + Hkv) * d].reshape(N, Hkv, d), kw, 1e-6)
+    assert torch.equal(k[..., :rot], ops_ref.rope(kn[..., :rot], pos, 1e4))
