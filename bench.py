@@ -16,7 +16,8 @@ Other workloads print the same record for: c1, the config-1 decode (parity/laten
 decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache); c4, the config-4
 chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention; lp, the
 DeltaNet prefill companions (fused conv / norms / beta, g front and the gated RMSNorm) on the config-4 batch; ap,
-the config-3 decode attention layer with its q / k norm, RoPE and KV write (rk_attn_prep) in front.
+the config-3 decode attention layer with its q / k norm, RoPE and KV write (rk_attn_prep) in front; wd, the
+sliding-window decode (window 4096) through the grouped pool's rings.
 Timing: W untimed warm-up steps, then K timed steps captured in one HIP graph and replayed between two events
 after a device synchronize (the eager, Python-issued rate is reported beside it).
 """
@@ -166,8 +167,7 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
 
     split_ms = time_region(split, args.steps, args.warmup, stream)
     kv = case.kv_bytes()
-    nb = (case.lens.long() + bs - 1) // bs
-    split_bytes = kv + B * Hq * d * 4 + 4 * int(nb.sum()) + 4 * B
+    split_bytes = kv + B * Hq * d * 4 + 4 * case.table_entries() + 4 * B
     achieved = split_bytes / (split_ms * 1e-3) / 1e9
     step_gbs = case.algorithmic_bytes() / (ms * 1e-3) / 1e9
     log(f"[bench] {workload_name}: step {ms * 1e3:.1f} us in a graph ({step_gbs:.0f} GB/s algorithmic), "
@@ -582,7 +582,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (for counter collection)")
@@ -616,6 +616,16 @@ def main() -> int:
                                  {"workload": "config 1: paged GQA decode, batch 1, fp32 KV, 512 positions"})
         rec["metric"] = "decode attn tokens/s @ batch 1 (config 1 latency case), 1 GPU"
         rec["dtype"] = "f32"
+    elif args.workload == "wd":
+        case = wl.wd_windowed_decode()
+        rec = bench_paged_decode(case, args, backend, "wd",
+                                 {"workload": "sliding-window decode through the grouped pool: batch 64, 16/4 heads "
+                                              "x 128, window 4096, bf16 KV in per-sequence rings, lengths "
+                                              "U[128, 8192] (config 3's), sigmoid gate",
+                                  "batch": 64, "window": wl.WD_WINDOW, "visible_positions":
+                                      int(case.lens.long().clamp(max=wl.WD_WINDOW).sum()),
+                                  "units": case.meta["units"], "kv_bytes": case.kv_bytes()})
+        rec["metric"] = "sliding-window decode attn tokens/s @ batch 64 (grouped pool rings) + achieved HBM GB/s, 1 GPU"
     elif args.workload == "c5":
         rec = bench_prefill(args, backend)
     elif args.workload == "c4":

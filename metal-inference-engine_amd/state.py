@@ -5,7 +5,9 @@ Layouts kept exactly, because the HIP kernels index them in place:
                       [2, ...] buffer (src/state.py:11-17, 106-114);
   * block tables     int32 [B, max_nb], rows padded with 0; lens int32 [B] (src/state.py:119-129);
   * DeltaNet slots   S: [max_seqs, n_linear, H, dk, dv] fp32, conv: [max_seqs, n_linear, K-1, C] fp32
-                      (src/state.py:420-429); a slot is zeroed when released (src/state.py:467-470).
+                      (src/state.py:420-429); a slot is zeroed when released (src/state.py:467-470);
+  * grouped pool     k, v: [G, units, block_size, n_kv_heads, head_dim] for layer groups with sliding-window rings
+                      (src/state.py:195-359); one group slot is a paged layer as above.
 Allocation is host-side bookkeeping (free list, all-or-nothing growth). KV scatter and gather run as HIP kernels
 when the pool is on a GPU (librk_path.so: rk_kv_write / rk_kv_gather) and as torch indexing on the CPU.
 """
@@ -213,6 +215,195 @@ class PagedSequence:
     def bytes_used(self) -> int:
         p = self.pool
         return 2 * len(self.block_table) * p.k[0, 0].numel() * p.k.shape[0] * p.k.element_size()
+
+
+def _write_layer(k_layer: torch.Tensor, v_layer: torch.Tensor, slots: torch.Tensor, k: torch.Tensor,
+                 v: torch.Tensor) -> None:
+    """k, v [n, Hkv, d] into rows slots = unit * block_size + offset of one pool layer [units, bs, Hkv, d]: the HIP
+    scatter on a GPU, torch indexing on the CPU."""
+    if k_layer.is_cuda:
+        from native.kernels import kv_write
+        kv_write(k_layer, v_layer, slots, k, v)
+    else:
+        k_layer.view(-1, *k_layer.shape[2:])[slots.long()] = k.to(k_layer.dtype)
+        v_layer.view(-1, *v_layer.shape[2:])[slots.long()] = v.to(v_layer.dtype)
+
+
+class GroupedKVPool:
+    """Paged KV for a model whose layers look back different distances (src/state.py:195-262; Tiny Aya: 9 full and
+    27 sliding-window layers), so the sliding layers' memory stops growing past the window.
+
+    Layers are grouped G = gcd(#full, #sliding) at a time (full groups first, then sliding groups); the pool's unit
+    is one block of one group's G layers, k / v [G, units, block_size, Hkv, d], and one allocator hands units to all
+    groups (units = num_blocks x groups, so num_blocks still counts blocks of every layer). Per sequence a full group
+    holds one unit per block; a sliding group a ring of R = ceil((W + max_chunk + bs - 2) / bs) units with logical
+    block b in slot b % R, enough for every block one forward of at most max_chunk tokens reads or writes. A layer of
+    the pool, k[slot] [units, bs, Hkv, d], has the paged layout the decode kernel reads, through the group's table
+    (by absolute block; entries before a sliding window are pad_block and never read). poison=True (tests): a ring
+    slot taking a new block is first filled with NaN, so a stale read shows."""
+
+    def __init__(self, layer_windows: list, n_kv_heads: int, head_dim: int, num_blocks: int, block_size: int = 16,
+                 max_chunk: int = 512, device="cpu", dtype: torch.dtype = torch.float32, poison: bool = False):
+        full = [i for i, w in enumerate(layer_windows) if w is None]
+        sliding = [i for i, w in enumerate(layer_windows) if w is not None]
+        windows = sorted({w for w in layer_windows if w is not None})
+        if len(windows) > 1:
+            raise ValueError(f"one sliding window size per model, not {windows}")
+        self.window = windows[0] if windows else None
+        G = math.gcd(len(full), len(sliding))
+        self.groups = [full[i:i + G] for i in range(0, len(full), G)] + \
+            [sliding[i:i + G] for i in range(0, len(sliding), G)]
+        self.sliding = [False] * (len(full) // G) + [True] * (len(sliding) // G)
+        self.layer_map = {layer: (g, j) for g, members in enumerate(self.groups) for j, layer in enumerate(members)}
+        self.n_groups, self.block_size, self.poison = len(self.groups), block_size, poison
+        self.ring = math.ceil((self.window + max_chunk + block_size - 2) / block_size) if self.window else None
+        self.k, self.v = kv_buffers((G, num_blocks * self.n_groups, block_size, n_kv_heads, head_dim), device, dtype)
+        self.allocator = BlockAllocator(num_blocks * self.n_groups)
+        self.unit_bytes = 2 * self.k[:, 0].numel() * self.k.element_size()
+        self.max_step_units = self.n_groups          # a decode step adds at most one unit per group
+        self.pad_block = 0
+
+    def blocks_for(self, n: int) -> int:
+        """Units a sequence of n positions holds: one per block in a full group, at most R in a sliding one."""
+        nb = math.ceil(n / self.block_size)
+        return sum(min(self.ring, nb) if sl else nb for sl in self.sliding)
+
+    def new_sequence(self) -> "WindowedSequence":
+        return WindowedSequence(self)
+
+    def batch_layout(self, seqs: list["WindowedSequence"], starts: list[int]):
+        """One decode step (a new token per sequence at starts[i], units reserved), as device tensors: per group the
+        unit each new token goes to (blocks [groups, B] int64, ring slots retagged), offsets [B] int64, per group
+        every sequence's table by absolute block (tables [groups, B, max_nb] int32, 0-padded; a sliding group's
+        entries before the window are pad_block), lens [B] int32 = starts + 1."""
+        bs, W = self.block_size, self.window
+        width = max(math.ceil((p + 1) / bs) for p in starts)
+        blocks = [[s.unit(g, p // bs, write=True) for s, p in zip(seqs, starts)] for g in range(self.n_groups)]
+        tables = []
+        for g, sl in enumerate(self.sliding):
+            rows = []
+            for s, p in zip(seqs, starts):
+                first = max(0, p + 1 - W) // bs if sl else 0
+                row = [self.pad_block] * first + [s.unit(g, b) for b in range(first, math.ceil((p + 1) / bs))]
+                rows.append(row + [self.pad_block] * (width - len(row)))
+            tables.append(rows)
+        out = (torch.tensor(blocks, dtype=torch.int64), torch.tensor([p % bs for p in starts], dtype=torch.int64),
+               torch.tensor(tables, dtype=torch.int32), torch.tensor([p + 1 for p in starts], dtype=torch.int32))
+        return tuple(to_device(t, self.k.device) for t in out)
+
+    def write_batch(self, slot: int, blocks: torch.Tensor, offsets: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+        """k, v [B, Hkv, d]: one new token per sequence, for the layer at `slot` of one group (blocks: that group's
+        row of batch_layout's blocks)."""
+        _write_layer(self.k[slot], self.v[slot], _slots(blocks, offsets, self.block_size), k, v)
+
+
+class WindowedSequence:
+    """One sequence's view of a GroupedKVPool (src/state.py:265-359): a table of units per full group, a ring of
+    units per sliding group with the logical block each ring slot holds (its tag). Same interface as PagedSequence;
+    block_table is the first group's table."""
+
+    def __init__(self, pool: GroupedKVPool):
+        self.pool = pool
+        self.tables: list[list[int]] = [[] for _ in range(pool.n_groups)]
+        self.tags: list[list[int]] = [[] for _ in range(pool.n_groups)]
+        self.length = 0
+        self.shared = 0                   # blocks 0 .. shared-1 of every group belong to a borrowed prefix
+
+    @property
+    def block_table(self) -> list[int]:
+        return self.tables[0]
+
+    def check_forward(self, start: int, end: int) -> None:
+        """Refuse, before anything moves, a forward whose blocks (the first query's window .. the last token) do not
+        fit in the ring (a chunk longer than the pool's max_chunk)."""
+        p = self.pool
+        if p.ring is None:
+            return
+        span = math.ceil(end / p.block_size) - max(0, start - p.window + 1) // p.block_size
+        if span > p.ring:
+            raise ValueError(f"a forward from position {start} to {end} spans {span} blocks, more than the "
+                             f"{p.ring}-block ring (chunks of at most the pool's max_chunk tokens)")
+
+    def reserve(self, end: int) -> None:
+        """Take every unit positions < end need, all or nothing (as PagedSequence.reserve)."""
+        p = self.pool
+        need = p.blocks_for(end) - sum(len(t) for t in self.tables)
+        if need <= 0:
+            return
+        if need > p.allocator.num_free:
+            raise OutOfBlocks(f"need {need} more KV units, only {p.allocator.num_free} free")
+        nb = math.ceil(end / p.block_size)
+        for g, sl in enumerate(p.sliding):
+            want = min(p.ring, nb) if sl else nb
+            while len(self.tables[g]) < want:
+                self.tables[g].append(p.allocator.allocate())
+                self.tags[g].append(-1)
+
+    def borrow(self, pin: "WindowedSequence", n: int) -> None:
+        """Start this empty sequence from the first n blocks of `pin` (same pool, rings not yet wrapped), shared
+        read-only: never written through (unit) or freed (free) by this sequence."""
+        p = self.pool
+        if self.length or any(self.tables) or pin.pool is not p or n * p.block_size > pin.length or \
+                any(sl and pin.tags[g][:n] != list(range(n)) for g, sl in enumerate(p.sliding)):
+            raise ValueError("borrow needs an empty sequence and a sequence of the same pool holding blocks 0..n-1")
+        self.tables = [t[:n] for t in pin.tables]
+        self.tags = [t[:n] for t in pin.tags]
+        self.length, self.shared = n * p.block_size, n
+
+    def unit(self, g: int, b: int, write: bool = False) -> int:
+        """The unit holding logical block b of group g. Writing to a sliding group's block retags its ring slot
+        (poisoning it first when the pool asks); reading a block the ring no longer holds raises."""
+        p = self.pool
+        i = b % p.ring if p.sliding[g] else b
+        if write and i < self.shared:
+            raise RuntimeError(f"a write to block {b} of group {g} would overwrite a shared prefix")
+        if not p.sliding[g]:
+            return self.tables[g][b]
+        if self.tags[g][i] != b:
+            if not write:
+                raise RuntimeError(f"block {b} of group {g} is no longer in the ring (slot {i} holds "
+                                   f"{self.tags[g][i]})")
+            if p.poison:
+                p.k[:, self.tables[g][i]] = float("nan")
+                p.v[:, self.tables[g][i]] = float("nan")
+            self.tags[g][i] = b
+        return self.tables[g][i]
+
+    def write(self, layer: int, start: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        end = start + k.shape[0]
+        self.reserve(end)
+        g, slot = self.pool.layer_map[layer]
+        bs = self.pool.block_size
+        slots = torch.tensor([self.unit(g, t // bs, write=True) * bs + t % bs for t in range(start, end)],
+                             dtype=torch.int64)
+        _write_layer(self.pool.k[slot], self.pool.v[slot], to_device(slots, self.pool.k.device), k, v)
+
+    def read(self, layer: int, end: int, lo: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+        """Positions lo .. end-1 of one layer, gathered into contiguous [end - lo, Hkv, d]."""
+        g, slot = self.pool.layer_map[layer]
+        bs = self.pool.block_size
+        b0, nb = lo // bs, math.ceil(end / bs)
+        units = [self.unit(g, b) for b in range(b0, nb)]
+        kl, vl = self.pool.k[slot], self.pool.v[slot]
+        if kl.is_cuda:
+            from native.kernels import kv_gather
+            table = to_device(torch.tensor([self.pool.pad_block] * b0 + units, dtype=torch.int32), kl.device)
+            return kv_gather(kl, vl, table, lo, end)
+        idx = torch.tensor(units, dtype=torch.int64)
+        rows = slice(lo - b0 * bs, end - b0 * bs)
+        return kl[idx].flatten(0, 1)[rows], vl[idx].flatten(0, 1)[rows]
+
+    def advance(self, n: int) -> None:
+        self.length += n
+
+    def free(self) -> None:
+        self.pool.allocator.free([u for t in self.tables for u in t[self.shared:]])   # a borrowed prefix stays
+        self.tables = [[] for _ in range(self.pool.n_groups)]
+        self.tags = [[] for _ in range(self.pool.n_groups)]
+        self.length = self.shared = 0
+
+    def bytes_used(self) -> int:
+        return (sum(len(t) for t in self.tables) - self.shared * len(self.tables)) * self.pool.unit_bytes
 
 
 class HybridState:

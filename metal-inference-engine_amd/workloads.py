@@ -42,11 +42,18 @@ class PagedDecodeCase:
             L = L.clamp(max=self.window)
         return int(L.sum()) * Hkv * d * self.k_pool.element_size() * 2
 
+    def table_entries(self) -> int:
+        """Block-table entries one decode call reads: the blocks holding each sequence's visible positions."""
+        L = self.lens.long()
+        nb = (L + self.block_size - 1) // self.block_size
+        if self.window:
+            nb = nb - (L - self.window).clamp(min=0) // self.block_size
+        return int(nb.sum())
+
     def algorithmic_bytes(self) -> int:
         """KV read once + q, gate, out (fp32) + the table entries and lens actually read."""
         B, Hq, d = self.q.shape
-        nb = (self.lens.long() + self.block_size - 1) // self.block_size
-        return self.kv_bytes() + B * Hq * d * 4 * 3 + 4 * int(nb.sum()) + 4 * B
+        return self.kv_bytes() + B * Hq * d * 4 * 3 + 4 * self.table_entries() + 4 * B
 
 
 def _tables_from_perm(perm: list[int], nbs: list[int]) -> torch.Tensor:
@@ -102,6 +109,35 @@ def c3_paged_decode(seed: int = 3, batch: int = 64) -> PagedDecodeCase:
     case = paged_decode_case(lens, num_blocks, kv_dtype=torch.bfloat16, seed=seed + 1000)
     case.meta["config"] = "c3"
     return case
+
+
+WD_WINDOW, WD_HQ, WD_HKV, WD_DIM = 4096, 16, 4, 128
+
+
+def wd_windowed_decode(seed: int = 7, batch: int = 64) -> PagedDecodeCase:
+    """Sliding-window decode through the grouped pool (Tiny Aya's sliding layers: 16 query / 4 kv heads x 128, a
+    4096-token window, bf16 KV): config 3's batch shape (lengths U[128, 8192]), each sequence's ring of
+    R = ceil((W + 512 + 14) / 16) units written through for all its blocks (so longer sequences have wrapped), the
+    decode step's tables from GroupedKVPool.batch_layout. The pool holds the rings only (one sliding layer group)."""
+    from state import GroupedKVPool
+    lens = c3_lens(seed, batch)
+    gen = torch.Generator().manual_seed(seed)
+    probe = GroupedKVPool([WD_WINDOW], WD_HKV, WD_DIM, num_blocks=1, block_size=BLOCK, dtype=torch.bfloat16)
+    units = sum(probe.blocks_for(n) for n in lens)
+    pool = GroupedKVPool([WD_WINDOW], WD_HKV, WD_DIM, num_blocks=units, block_size=BLOCK, dtype=torch.bfloat16)
+    seqs = [pool.new_sequence() for _ in lens]
+    for s, n in zip(seqs, lens):
+        s.reserve(n)
+        for b in range(math.ceil(n / BLOCK)):         # every block of the history written through the ring
+            s.unit(0, b, write=True)
+        s.length = n - 1
+    _, _, tables, lens_t = pool.batch_layout(seqs, [n - 1 for n in lens])
+    pool.k[0].copy_(torch.randn(pool.k[0].shape, generator=gen))
+    pool.v[0].copy_(torch.randn(pool.v[0].shape, generator=gen))
+    q = torch.randn(batch, WD_HQ, WD_DIM, generator=gen)
+    gate = torch.randn(batch, WD_HQ * WD_DIM, generator=gen)
+    return PagedDecodeCase(q, gate, pool.k[0], pool.v[0], tables[0], lens_t, BLOCK, WD_WINDOW,
+                           {"config": "wd", "lens": lens, "units": units, "ring": pool.ring})
 
 
 @dataclass

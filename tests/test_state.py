@@ -130,3 +130,91 @@ def test_standalone_state_fork_and_free():
     assert float(st.S.sum()) > 0 and twin.length == 5
     st.free()
     assert float(st.S.abs().sum()) == 0
+
+
+# ---------------------------------------------------------------- grouped pool with sliding-window rings
+
+def test_grouped_pool_random_chunks_against_a_dict_oracle():
+    """Random chunk schedules up to max_chunk over 8 layers (6 sliding, 2 full): every read of a layer's window
+    returns exactly what was written at those positions, stale ring slots are NaN-poisoned yet never read, every
+    group holds exactly min(R, blocks) / blocks units, an oversized chunk is refused, and free returns every unit."""
+    import random
+    from state import GroupedKVPool
+    rnd = random.Random(1)
+    for W, bs, C in ((8, 4, 3), (8, 4, 7), (6, 3, 4), (5, 4, 4), (5, 3, 7), (16, 16, 16)):
+        layers = [W, W, W, None] * 2
+        pool = GroupedKVPool(layers, 1, 2, num_blocks=64, block_size=bs, max_chunk=C, poison=True)
+        assert pool.groups == [[3, 7], [0, 1], [2, 4], [5, 6]] and pool.sliding == [False, True, True, True]
+        seq, written, pos = pool.new_sequence(), {}, 0
+        for _ in range(30):
+            n = rnd.randint(1, C)
+            seq.check_forward(pos, pos + n)
+            for layer, w in enumerate(layers):
+                k, v = torch.randn(n, 1, 2), torch.randn(n, 1, 2)
+                seq.write(layer, pos, k, v)
+                for j in range(n):
+                    written[layer, pos + j] = (k[j], v[j])
+                lo = max(0, pos - w + 1) if w else 0
+                K, V = seq.read(layer, pos + n, lo)
+                assert torch.equal(K, torch.stack([written[layer, t][0] for t in range(lo, pos + n)]))
+                assert torch.equal(V, torch.stack([written[layer, t][1] for t in range(lo, pos + n)]))
+            seq.advance(n)
+            pos += n
+            nb = -(-pos // bs)
+            assert [len(t) for t in seq.tables] == [min(pool.ring, nb) if sl else nb for sl in pool.sliding]
+            assert pool.allocator.num_free + sum(map(len, seq.tables)) == pool.allocator.num_blocks
+        with pytest.raises(ValueError):
+            seq.check_forward(pos, pos + C + bs + W)
+        seq.free()
+        assert pool.allocator.num_free == pool.allocator.num_blocks
+
+
+def test_grouped_pool_reserve_is_all_or_nothing():
+    from state import GroupedKVPool, OutOfBlocks
+    pool = GroupedKVPool([8, 8, 8, None] * 2, 1, 2, num_blocks=3, block_size=4, max_chunk=4)
+    a, b = pool.new_sequence(), pool.new_sequence()
+    a.reserve(8)
+    with pytest.raises(OutOfBlocks):
+        b.reserve(12)
+    assert b.tables == [[], [], [], []] and pool.allocator.num_free == 4
+    assert pool.blocks_for(8) == 8 and pool.blocks_for(100) == 25 + 3 * pool.ring
+
+
+def test_grouped_batch_layout_and_windowed_decode_on_the_cpu():
+    """batch_layout of a sliding group: entries before the window are pad_block, the new token's unit is retagged
+    (poisoned when it takes a new block), and the oracle's windowed paged attention over those tables, with every
+    stale slot NaN, equals attention over exactly the window's positions."""
+    from oracle import backend_ref, ops_ref
+    from state import GroupedKVPool
+    W, bs, Hq, Hkv, d = 10, 4, 4, 2, 8
+    pool = GroupedKVPool([W, None], Hkv, d, num_blocks=64, block_size=bs, max_chunk=4, poison=True)
+    g_sl, slot = pool.layer_map[0]
+    assert pool.sliding[g_sl]
+    lens = [1, 5, 11, 23, 40]
+    seqs, hist = [pool.new_sequence() for _ in lens], []
+    gen = torch.Generator().manual_seed(3)
+    for s, n in zip(seqs, lens):                    # history of n - 1 tokens written in chunks of <= max_chunk
+        K, V = torch.randn(n, Hkv, d, generator=gen), torch.randn(n, Hkv, d, generator=gen)
+        for t in range(0, n - 1, 4):
+            e = min(n - 1, t + 4)
+            s.check_forward(t, e)
+            s.write(0, t, K[t:e], V[t:e])
+            s.advance(e - t)
+        hist.append((K, V))
+    starts = [n - 1 for n in lens]
+    for s, p in zip(seqs, starts):
+        s.reserve(p + 1)
+    blocks, offsets, tables, lens_t = pool.batch_layout(seqs, starts)
+    for i, (s, p) in enumerate(zip(seqs, starts)):
+        first = max(0, p + 1 - W) // bs
+        assert tables[g_sl, i, :first].tolist() == [pool.pad_block] * first
+        assert int(blocks[g_sl, i]) == s.unit(g_sl, p // bs)
+    k_new = torch.stack([K[-1] for K, _ in hist])
+    v_new = torch.stack([V[-1] for _, V in hist])
+    pool.write_batch(slot, blocks[g_sl], offsets, k_new, v_new)
+    q = torch.randn(len(lens), Hq, d, generator=gen)
+    out = backend_ref.paged_attention(q, pool.k[slot], pool.v[slot], tables[g_sl], lens_t, bs, window=W)
+    assert torch.isfinite(out).all()
+    want = torch.cat([ops_ref.attention(q[i:i + 1], K[max(0, n - W):], V[max(0, n - W):])
+                      for i, ((K, V), n) in enumerate(zip(hist, lens))])
+    assert torch.allclose(out, want, rtol=0, atol=1e-6)
