@@ -17,7 +17,8 @@ decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB
 chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention; lp, the
 DeltaNet prefill companions (fused conv / norms / beta, g front and the gated RMSNorm) on the config-4 batch; ap,
 the config-3 decode attention layer with its q / k norm, RoPE and KV write (rk_attn_prep) in front; wd, the
-sliding-window decode (window 4096) through the grouped pool's rings.
+sliding-window decode (window 4096) through the grouped pool's rings; mv, every linear of a Qwen3.5-2B decode step at
+batch 8 (INT4 layers, INT8 head).
 Timing: W untimed warm-up steps, then K timed steps captured in one HIP graph and replayed between two events
 after a device synchronize (the eager, Python-issued rate is reported beside it).
 """
@@ -577,12 +578,98 @@ def bench_attn_prep(args, backend):
     }
 
 
+QWEN35_2B = {"layers": 24, "linear_layers": 18, "hidden": 2048, "intermediate": 6144, "vocab": 248320,
+             "in_proj": 8224, "qkvg": 5120}
+
+
+def bench_linears(args, backend):
+    """Every linear of one Qwen3.5-2B decode step at batch 8 (the reference's INT4 policy: INT4 layers, INT8 tied
+    head; src/quant.py:115-121): per layer the mixer's input projection (DeltaNet in_proj [8224, 2048] on 18 layers,
+    attention qkvg [5120, 2048] on 6) and output projection [2048, 2048], the MLP's gate_up [12288, 2048] and down
+    [2048, 6144]; then the head [248320, 2048]. Weights are random codes / scales generated on the GPU (a bandwidth
+    workload: the values do not change the work); one step = the 97 rk_linear_rows launches, in a HIP graph."""
+    import torch
+    from quant import QuantTensor
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    c = QWEN35_2B
+    M, H, I = 8, c["hidden"], c["intermediate"]
+    gen = torch.Generator(device=dev).manual_seed(14)
+
+    def qt(N, K, scheme):
+        if scheme == "int8":
+            data = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+        else:
+            data = torch.randint(0, 256, (N, K // 2), generator=gen, device=dev, dtype=torch.uint8)
+        scales = (torch.rand(N, K // 32, generator=gen, device=dev) * 1e-3 + 1e-4).to(torch.float16)
+        mins = (torch.rand(N, K // 32, generator=gen, device=dev) * -0.01).to(torch.float16) if scheme == "int4" else None
+        return QuantTensor(scheme, data, scales, (N, K), 32, mins)
+
+    mats = []
+    for i in range(c["layers"]):
+        mixer_in = c["in_proj"] if i % 4 != 3 else c["qkvg"]       # 3 of every 4 layers are DeltaNet
+        mats += [qt(mixer_in, H, "int4"), qt(H, H, "int4"), qt(2 * I, H, "int4"), qt(H, I, "int4")]
+    mats.append(qt(c["vocab"], H, "int8"))
+    wbytes = sum(m.nbytes for m in mats)
+    xs = {K: torch.randn(M, K, generator=gen, device=dev) for K in (H, I)}
+    outs = [torch.empty(M, m.shape[0], device=dev) for m in mats]
+    from native import kernels
+    torch.cuda.synchronize()
+
+    def step():
+        for m, o in zip(mats, outs):
+            kernels.linear_rows(xs[m.shape[1]], m, out=o)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ms = graph_time(step, max(1, args.steps // 5), stream)
+    head = mats[-1]
+    ms_head = graph_time(lambda: kernels.linear_rows(xs[H], head, out=outs[-1]), args.steps, stream)
+    io = sum(M * (m.shape[1] + m.shape[0]) * 4 for m in mats)
+    gbs = (wbytes + io) / (ms * 1e-3) / 1e9
+    head_gbs = head.nbytes / (ms_head * 1e-3) / 1e9
+    log(f"[bench] mv: {ms * 1e3:.1f} us per step of {len(mats)} linears ({wbytes / 1e9:.2f} GB of weights, "
+        f"{gbs:.0f} GB/s = {gbs / HBM_PEAK_GBS:.1%}); head alone {ms_head * 1e3:.1f} us ({head_gbs:.0f} GB/s)")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import quant_ref
+        torch.set_num_threads(cpu_threads())
+        layer = [m.to("cpu") for m in mats[:4]]
+        xc = {K: v.cpu() for K, v in xs.items()}
+
+        def cpu_run():
+            for m in layer:
+                quant_ref.linear(xc[m.shape[1]], quant_ref.dequantize(m.scheme, m.data, m.scales, m.mins))
+        t, calls, total = cpu_time(cpu_run, runs=3)
+        lbytes = sum(m.nbytes for m in layer)
+        t_step = t * wbytes / lbytes
+        cpu = {"value": M / t_step, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"one DeltaNet layer's 4 linears (dequantize + fp32 matmul, {lbytes / 1e6:.1f} MB of weights): "
+                         f"median of {calls} calls ({total:.1f} s in all), {t * 1e3:.1f} ms, scaled by weight bytes to "
+                         f"the step ({wbytes / lbytes:.1f}x)"}
+    return {
+        "metric": "decode-step linears tokens/s @ batch 8 (Qwen3.5-2B shapes, INT4 + INT8 head) + achieved HBM GB/s, "
+                  "1 GPU",
+        "value": M / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random codes and scales)",
+        "config": {"workload": "all 97 linears of a Qwen3.5-2B decode step at batch 8: INT4 (block 32) layers, INT8 "
+                               "head, fp32 activations", "weight_bytes": wbytes, "head_ms": ms_head,
+                   "head_gbs": head_gbs},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": traffic_for("linear_rows/mv"), "kernel": "linear_rows_kernel (97 launches)",
+                     "bytes_per_launch": (wbytes + io) / len(mats), "avg_ms": ms / len(mats)},
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd", "mv"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (for counter collection)")
@@ -634,6 +721,8 @@ def main() -> int:
         rec = bench_linear_prefill(args, backend)
     elif args.workload == "ap":
         rec = bench_attn_prep(args, backend)
+    elif args.workload == "mv":
+        rec = bench_linears(args, backend)
     else:
         rec = bench_deltanet(args, backend)
     print(json.dumps(rec), flush=True)

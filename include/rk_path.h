@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 4
+#define RK_ABI_VERSION 5
 
 /* status codes */
 #define RK_OK 0
@@ -30,6 +30,12 @@ extern "C" {
 /* element types of caller buffers */
 #define RK_F32 0
 #define RK_BF16 1
+
+/* weight matrix types of rk_linear_rows / rk_dequant_rows (src/quant.py:1-10: blocks of 32 weights along a row share
+ * fp16 parameters) */
+#define RK_W_BF16 1 /* bf16 [N, K] */
+#define RK_W_INT8 2 /* int8 q [N, K], fp16 scales [N, K/32]: w = q * scale */
+#define RK_W_INT4 3 /* uint8 [N, K/2] (element 2j low nibble, 2j+1 high), fp16 scales and mins [N, K/32]: w = q * s + m */
 
 /* ---- library / errors (replaces the mr_* status + error-buffer convention of src/native/metal_runtime.mm:20-43) */
 const char* rk_last_error(void);
@@ -173,6 +179,25 @@ int rk_attn_prep(float* q_out, float* k_out, float* v_out, void* k_pool, void* v
                  const int64_t* slots, int num_blocks, int block_size, const void* y, int y_dtype, long long ld,
                  const float* q_w, const float* k_w, float eps, const int32_t* positions, const float* inv_freq,
                  int rot, int N, int Hq, int Hkv, int d, void* stream);
+
+/* ---- Decode-time linears (the other half of a decode step): y [M, N] = x [M, K] @ W^T (+ bias) (+ residual), fp32,
+ * for M <= 16 activation rows. Replaces MetalBackend.linear / _qlinear for batched decode (src/backend/metal.py:59-133;
+ * matvec / qmatvec kernels) with the reference's math: W dequantized as src/quant.py:45-56 (QuantTensor.dequantize),
+ * y = x @ W^T, then + bias, then + residual, each rounded.
+ *   x [M, K] fp32 contiguous, 16-byte aligned; w per w_type (16-byte aligned); scales / mins fp16 [N, K/32] or NULL
+ *   (bf16); bias [N] or NULL; residual [M, N] or NULL; y [M, N]. K a multiple of 32.
+ *   K is cut into splits; when there is more than one, partials (rk_linear_workspace_bytes(M, N, K, w_type) bytes,
+ *   no zeroing needed) receive the splits' sums and counters[ceil(N / 64)] (uint32) count the splits of each 64-row
+ *   block as they finish: counters must be zero before the first call, and every call leaves them zero. Calls that
+ *   share them must be stream-ordered. Results do not depend on timing (partials are added in a fixed order).
+ * rk_dequant_rows: rows of W as fp32 (the reference's dequantize; bit-exact: q * scale then + min, each rounded):
+ *   out [n_rows, K], source row rows[i] (int32, clamped into [0, N)) or row0 + i when rows is NULL. */
+size_t rk_linear_workspace_bytes(int M, int N, int K, int w_type);
+int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w, int w_type, const void* scales,
+                   const void* mins, const float* bias, const float* residual, float* partials,
+                   size_t partial_bytes, uint32_t* counters, int n_counters, void* stream);
+int rk_dequant_rows(float* out, const void* w, int w_type, const void* scales, const void* mins,
+                    const int32_t* rows, int row0, int n_rows, int N, int K, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,6 +21,8 @@ Method -> kernel:
                          linear-attention prefill (src/models/qwen3_5.py:144-162) in four launches
   attention_prep         rk_attn_prep: q / k RMSNorm + partial RoPE (+ the decode KV write) of a gated-attention
                          layer (src/models/qwen3_5.py:251-262, 100-110) in one launch
+  linear, embedding      rk_linear_rows (bf16 / INT8 / INT4 weights, up to 32 rows), rk_dequant_rows (+ a BLAS GEMM
+                         beyond 32 rows; embedding rows), src/backend/metal.py:50-133
 """
 import torch
 
@@ -162,6 +164,20 @@ class RocmBackend:
         q, k, v, beta, g = kernels.deltanet_prefill_front(qkv, b, a, conv, seqs, conv_w, A_log, dt_bias, cu, dims)
         o = kernels.gated_delta_chunked(q, k, v, beta, g, S, cu, seqs)
         return kernels.rms_norm_gated(o.view(N * H, dv), z, norm_w, eps).view(N, H * dv)
+
+    # ---- decode-time linears
+    def linear(self, x, w, b=None, residual=None):
+        """Backend.linear (src/backend/base.py:19-21) on a bf16 weight or a block-quantized QuantTensor
+        (src/backend/metal.py:59-133): up to 32 rows through rk_linear_rows (16 per launch), beyond that an fp32
+        GEMM on row chunks of the weight dequantized by rk_dequant_rows -> [M, N] fp32."""
+        return kernels.linear(x, w, b, residual)
+
+    def embedding(self, table, ids):
+        """Rows of a bf16 or quantized embedding table as fp32 (src/backend/metal.py:50-53)."""
+        from quant import QuantTensor
+        if isinstance(table, QuantTensor) or table.dtype == torch.bfloat16:
+            return kernels.dequantize(table, rows=ids.to(self.device))
+        return table[ids.to(table.device)].float()
 
     # ---- gated-attention pre-processing
     def attention_prep(self, y, q_w, k_w, eps, positions, theta, rot, dims, k_pool=None, v_pool=None, slots=None):

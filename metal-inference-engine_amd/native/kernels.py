@@ -6,7 +6,7 @@ kernel for, src/backend/metal.py:189-195) and turn shape mistakes into ValueErro
 """
 import torch
 
-from native.rocm_native import RK_BF16, RK_F32, load
+from native.rocm_native import RK_BF16, RK_F32, RK_W_BF16, RK_W_INT4, RK_W_INT8, load
 
 DTYPE_CODES = {torch.float32: RK_F32, torch.bfloat16: RK_BF16}
 KV_DTYPES = (torch.float32, torch.bfloat16)
@@ -476,3 +476,124 @@ def attn_prep(y, q_w, k_w, eps: float, positions, theta: float, rot: int, dims, 
     lib.call("rk_attn_prep", q.data_ptr(), None, None, k_pool.data_ptr(), v_pool.data_ptr(),
              DTYPE_CODES[k_pool.dtype], slots.contiguous().data_ptr(), k_pool.shape[0], k_pool.shape[1], *common)
     return q
+
+
+W_TYPES = {"int8": RK_W_INT8, "int4": RK_W_INT4}
+LINEAR_ROWS = 16            # activation rows per rk_linear_rows launch (the MFMA's 16 columns)
+KERNEL_ROWS = 32            # up to here: the matvec kernel in groups of 16; beyond: dequantize + GEMM
+
+
+def _weight_args(w):
+    """(w_type, data, scales, mins, N, K) of a bf16 tensor or a QuantTensor, checked."""
+    from quant import QuantTensor
+    if isinstance(w, QuantTensor):
+        if w.scheme not in W_TYPES or w.block != 32:
+            raise TypeError(f"linear: quantized scheme {w.scheme} / block {w.block} has no kernel")
+        N, K = w.shape
+        if w.data.dtype != (torch.int8 if w.scheme == "int8" else torch.uint8) or \
+                w.data.shape != (N, K if w.scheme == "int8" else K // 2) or w.scales.shape != (N, K // 32) or \
+                w.scales.dtype != torch.float16 or \
+                (w.scheme == "int4" and (w.mins is None or w.mins.shape != (N, K // 32))):
+            raise ValueError(f"linear: malformed {w.scheme} weight {tuple(w.data.shape)} / {tuple(w.scales.shape)}")
+        for t in (w.data, w.scales) + ((w.mins,) if w.mins is not None else ()):
+            _contig("linear", t, "quantized weight parts")
+        return W_TYPES[w.scheme], w.data, w.scales, w.mins, N, K
+    if w.dtype != torch.bfloat16 or w.dim() != 2:
+        raise TypeError(f"linear: weight dtype {w.dtype} has no matvec kernel (bf16 or quantized)")
+    _contig("linear", w, "w")
+    return RK_W_BF16, w, None, None, w.shape[0], w.shape[1]
+
+
+def linear_rows(x, w, bias=None, residual=None, out=None) -> torch.Tensor:
+    """y [M, N] = x [M, K] @ dequant(w)^T (+ bias) (+ residual), fp32, for M <= KERNEL_ROWS (rk_linear_rows, 16 rows
+    per launch): the decode-time linear of src/backend/metal.py:59-133. w: bf16 [N, K] or a QuantTensor."""
+    wt, data, scales, mins, N, K = _weight_args(w)
+    M = x.shape[0]
+    if x.dim() != 2 or x.shape[1] != K or M > KERNEL_ROWS or K % 32:
+        raise ValueError(f"linear: x {tuple(x.shape)} for a [{N}, {K}] weight (M <= {KERNEL_ROWS}, K % 32 == 0)")
+    dev = _need_cuda("linear", x, data)
+    x = x.to(torch.float32).contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    if bias is not None:
+        bias = bias.to(device=dev, dtype=torch.float32).contiguous()
+    if residual is not None:
+        residual = residual.to(device=dev, dtype=torch.float32).contiguous()
+        if residual.shape != (M, N):
+            raise ValueError(f"linear: residual {tuple(residual.shape)}, expected [{M}, {N}]")
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.float32, device=dev)
+    lib = load()
+    cnt = linear_counters(dev, -(-N // 64))
+    for m0 in range(0, M, LINEAR_ROWS):
+        m = min(LINEAR_ROWS, M - m0)
+        need = lib.lib.rk_linear_workspace_bytes(m, N, K, wt)
+        part = workspace(dev, need) if need else None
+        lib.call("rk_linear_rows", out[m0:].data_ptr(), x[m0:].data_ptr(), m, N, K, data.data_ptr(), wt,
+                 scales.data_ptr() if scales is not None else None, mins.data_ptr() if mins is not None else None,
+                 bias.data_ptr() if bias is not None else None,
+                 residual[m0:].data_ptr() if residual is not None else None,
+                 part.data_ptr() if part is not None else None, part.numel() if part is not None else 0,
+                 cnt.data_ptr(), cnt.numel(), _stream(dev))
+    return out
+
+
+_linear_cnt: dict[int, torch.Tensor] = {}
+
+
+def linear_counters(dev: torch.device, n: int) -> torch.Tensor:
+    """rk_linear_rows's per-row-block arrival counters on dev: zero-filled when (re)allocated, and every call leaves
+    them at zero, so one buffer serves all stream-ordered calls."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _linear_cnt.get(idx)
+    if buf is None or buf.numel() < n:
+        buf = torch.zeros(max(n, 1 << 14), dtype=torch.int32, device=dev)
+        _linear_cnt[idx] = buf
+    return buf
+
+
+def dequantize(w, rows=None, row0: int = 0, n_rows: int | None = None) -> torch.Tensor:
+    """Rows of a bf16 / quantized weight as fp32 [n, K] (rk_dequant_rows; bit-exact with the reference's
+    dequantize, src/quant.py:45-56): the given row indices (device int64 / int32 tensor) or rows row0 .. row0+n-1."""
+    wt, data, scales, mins, N, K = _weight_args(w)
+    dev = _need_cuda("dequantize", data)
+    if rows is not None:
+        rows = rows.to(device=dev, dtype=torch.int32).contiguous()
+        n = rows.numel()
+    else:
+        n = N - row0 if n_rows is None else n_rows
+    out = torch.empty(n, K, dtype=torch.float32, device=dev)
+    load().call("rk_dequant_rows", out.data_ptr(), data.data_ptr(), wt,
+                scales.data_ptr() if scales is not None else None, mins.data_ptr() if mins is not None else None,
+                rows.data_ptr() if rows is not None else None, row0, n, N, K, _stream(dev))
+    return out
+
+
+DEQUANT_CHUNK = 1 << 23     # weights expanded per prefill GEMM piece (32 MB fp32), as the reference
+
+
+def linear(x, w, bias=None, residual=None) -> torch.Tensor:
+    """The reference's decode / prefill linear on a bf16 or quantized weight (src/backend/metal.py:59-133): up to 32
+    rows through the matvec kernel, beyond that an fp32 GEMM (the ROCm BLAS through torch) on row chunks of the
+    dequantized weight, so the full-size fp32 weight never exists. fp32 / other-dtype weights: x @ w.T in fp32."""
+    from quant import QuantTensor
+    M = x.shape[0]
+    if not isinstance(w, QuantTensor) and w.dtype != torch.bfloat16:
+        y = x.float() @ w.float().T
+    elif M <= KERNEL_ROWS and w.shape[1] % 32 == 0:
+        return linear_rows(x, w, bias, residual)
+    else:
+        N, K = w.shape
+        x = x.float()
+        y = torch.empty(M, N, dtype=torch.float32, device=x.device)
+        step = max(1, DEQUANT_CHUNK // K)
+        for r in range(0, N, step):
+            n = min(step, N - r)
+            if isinstance(w, QuantTensor) or K % 32 == 0:
+                wr = dequantize(w, row0=r, n_rows=n)
+            else:
+                wr = w[r:r + n].float()
+            y[:, r:r + n] = x @ wr.T
+    if bias is not None:
+        y = y + bias.float()
+    return y + residual.float() if residual is not None else y

@@ -11,9 +11,10 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 RK_F32, RK_BF16 = 0, 1
+RK_W_BF16, RK_W_INT8, RK_W_INT4 = 1, 2, 3
 ERROR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "workspace too small", 4: "HIP runtime error"}
 
 P = c_void_p
@@ -41,6 +42,9 @@ SIGNATURES = {
     "rk_rms_norm_gated": (c_int, [P, P, P, c_int, c_longlong, c_int, P, c_int, c_int, c_float, P]),
     "rk_attn_prep": (c_int, [P, P, P, P, P, c_int, P, c_int, c_int, P, c_int, c_longlong, P, P, c_float, P, P]
                      + [c_int] * 5 + [P]),
+    "rk_linear_workspace_bytes": (c_size_t, [c_int] * 4),
+    "rk_linear_rows": (c_int, [P, P, c_int, c_int, c_int, P, c_int, P, P, P, P, P, c_size_t, P, c_int, P]),
+    "rk_dequant_rows": (c_int, [P, P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
 }
 
 

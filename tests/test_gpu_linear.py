@@ -1,0 +1,84 @@
+"""Parity of the decode-time linears (rk_linear_rows, rk_dequant_rows; RocmBackend.linear / embedding) with the
+oracle's restatement of the reference's math (oracle/quant_ref.py: QuantTensor.dequantize, src/quant.py:45-56, then
+y = x @ w.T + bias + residual in fp32, src/backend/metal.py:59-133).
+
+Bars: dequantized rows bit-exact (q * scale, + min, each rounded, as the reference); linear outputs (fp32) within
+1e-5 relative. Shapes: Qwen3.5-0.8B's qkvg / down / gate_up (the reference's own kernel test shapes,
+tests/test_quant.py:46-55 there), Qwen3.5-2B's, and ragged ones (rows not a multiple of 64, K not a multiple of the
+K-tile)."""
+import pytest
+import torch
+
+import quant
+from helpers import rel_err
+from oracle import quant_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL = 1e-5
+
+
+def weight(kind, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * 0.05 + 0.01
+    if kind == "bf16":
+        return w.to(torch.bfloat16), w.to(torch.bfloat16).float()
+    q = quant.quantize(w, kind)
+    return q, quant_ref.dequantize(q.scheme, q.data, q.scales, q.mins)
+
+
+def to_dev(w):
+    return w.to(DEV) if isinstance(w, quant.QuantTensor) else w.to(DEV)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
+def test_dequant_rows_bit_exact(backend, kind):
+    from native import kernels
+    w, deq = weight(kind, 300, 224, 1)
+    wd = to_dev(w)
+    assert torch.equal(kernels.dequantize(wd).cpu(), deq)
+    rows = torch.tensor([299, 0, 17, 17, 150])
+    assert torch.equal(kernels.dequantize(wd, rows=rows.to(DEV)).cpu(), deq[rows])
+    assert torch.equal(backend.embedding(wd, rows.to(DEV)).cpu(), deq[rows])
+
+
+SHAPES = [(5120, 1024), (1024, 3584), (7168, 1024), (8224, 2048), (2048, 6144), (100, 96), (65, 2080)]
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
+def test_linear_rows_matches_dequantized_reference(backend, kind, N, K):
+    w, deq = weight(kind, N, K, N + K)
+    g = torch.Generator().manual_seed(K)
+    wd = to_dev(w)
+    worst = 0.0
+    for M, with_b, with_r in ((1, False, True), (3, True, False), (8, True, True), (16, False, False),
+                              (20, True, True), (32, False, True)):
+        x = torch.randn(M, K, generator=g)
+        b = torch.randn(N, generator=g) if with_b else None
+        r = torch.randn(M, N, generator=g) if with_r else None
+        want = quant_ref.linear(x, deq, b, r)
+        got = backend.linear(x.to(DEV), wd, None if b is None else b.to(DEV), None if r is None else r.to(DEV))
+        e = rel_err(got, want)
+        worst = max(worst, e)
+        assert e < TOL, f"M {M}: rel {e:.2e}"
+    print(f"linear {kind} {N}x{K}: worst rel {worst:.2e}")
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
+def test_prefill_sized_linear_goes_through_dequantized_gemm(backend, kind):
+    w, deq = weight(kind, 1000, 512, 9)
+    g = torch.Generator().manual_seed(9)
+    x, r = torch.randn(70, 512, generator=g), torch.randn(70, 1000, generator=g)
+    got = backend.linear(x.to(DEV), to_dev(w), residual=r.to(DEV))
+    assert rel_err(got, quant_ref.linear(x, deq, None, r)) < TOL
+
+
+def test_rows_are_independent_of_the_batch(backend):
+    """A row's output does not depend on the other rows launched with it (the reference's batching invariant)."""
+    w, _ = weight("int4", 2048, 2048, 4)
+    wd = to_dev(w)
+    x = torch.randn(16, 2048, generator=torch.Generator().manual_seed(4)).to(DEV)
+    full = backend.linear(x, wd)
+    for i in (0, 7, 15):
+        assert torch.equal(backend.linear(x[i:i + 1], wd), full[i:i + 1])
