@@ -186,10 +186,11 @@ int rk_attn_prep(float* q_out, float* k_out, float* v_out, void* k_pool, void* v
  * y = x @ W^T, then + bias, then + residual, each rounded.
  *   x [M, K] fp32 contiguous, 16-byte aligned; w per w_type (16-byte aligned); scales / mins fp16 [N, K/32] or NULL
  *   (bf16); bias [N] or NULL; residual [M, N] or NULL; y [M, N]. K a multiple of 32.
- *   K is cut into splits; when there is more than one, partials (rk_linear_workspace_bytes(M, N, K, w_type) bytes,
- *   no zeroing needed) receive the splits' sums and counters[ceil(N / 64)] (uint32) count the splits of each 64-row
- *   block as they finish: counters must be zero before the first call, and every call leaves them zero. Calls that
- *   share them must be stream-ordered. Results do not depend on timing (partials are added in a fixed order).
+ *   K is cut into splits of 1024; when there is more than one, partials (rk_linear_workspace_bytes(M, N, K, w_type)
+ *   bytes, no zeroing needed) receive the splits' sums and counters[ceil(N / 16)] (uint32) count the splits of each
+ *   row group as they finish: counters must be zero before the first call, and every call leaves them zero. Calls
+ *   that share them must be stream-ordered. Results depend on neither timing nor M nor N (every output's terms are
+ *   added in an order fixed by K).
  * rk_dequant_rows: rows of W as fp32 (the reference's dequantize; bit-exact: q * scale then + min, each rounded):
  *   out [n_rows, K], source row rows[i] (int32, clamped into [0, N)) or row0 + i when rows is NULL. */
 size_t rk_linear_workspace_bytes(int M, int N, int K, int w_type);

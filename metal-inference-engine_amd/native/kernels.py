@@ -524,7 +524,7 @@ def linear_rows(x, w, bias=None, residual=None, out=None) -> torch.Tensor:
     if out is None:
         out = torch.empty(M, N, dtype=torch.float32, device=dev)
     lib = load()
-    cnt = linear_counters(dev, -(-N // 64))
+    cnt = linear_counters(dev, -(-N // 16))
     for m0 in range(0, M, LINEAR_ROWS):
         m = min(LINEAR_ROWS, M - m0)
         need = lib.lib.rk_linear_workspace_bytes(m, N, K, wt)

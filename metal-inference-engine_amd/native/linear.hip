@@ -6,16 +6,16 @@
 // INT4 w = q * scale + min, q in 0..15, element 2j in the low nibble of byte j, 2j+1 in the high nibble), then
 // y += bias, y += residual, fp32 throughout.
 //
-// Design: y^T [N, M] = W [N, K] x^T [K, M] on MFMA (v_mfma_f32_16x16x32_bf16), a 16-row tile of W against the (up
-// to 16) activation rows as the 16 columns. Weights are exact bf16 operands (bf16 as stored; INT8 and INT4 codes are
-// small integers), activations enter as their exact three-piece bf16 split (x = hi + mid + lo), so every product is
-// exact and accumulates in fp32: fp32-level results (the VALU alternative tops out near 2.5 TB/s of INT4 at 8 rows).
-// One MFMA k-extent is one quantization block, so a block's dot products come out of three MFMAs and its scale (and
-// min, times the block's activation sum) is applied to them on the VALU.
-// Work: workgroups of 4 waves take 64 rows x one K-split of NB blocks (16 or 32), so every matrix gives hundreds of
-// workgroups (a decode step's 2048-row projections too) and each wave requests all its weights at once: no loop
-// over K, no per-tile barrier, whole K-splits in flight. Splits of one row block are added by the last workgroup to
-// finish (see linear_rows_kernel).
+// Design: y [M, N] = X [M, K] W^T on MFMA (v_mfma_f32_16x16x32_bf16): the (up to 16) activation rows are the A
+// operand's 16 rows, a 16-row tile of W the B operand's 16 columns. Weights are exact bf16 operands (bf16 as stored;
+// INT8 and INT4 codes are small integers), activations enter as their exact three-piece bf16 split
+// (x = hi + mid + lo), so every product is exact and accumulates in fp32: fp32-level results (the VALU alternative
+// tops out near 2.5 TB/s of INT4 at 8 rows). One MFMA k-extent is one quantization block, so a block's dot products
+// come out of three MFMAs and its scale (and min, times the block's activation sum) is applied to them on the VALU.
+// Work: a workgroup of 4 waves takes 16, 32 or 64 rows (1, 2 or 4 row tiles, the most that leave 512 workgroups)
+// and a 1024-weight K-split, one quarter of the split per wave, so each wave requests all its weights at once (no
+// loop over K) and reuses every activation piece it reads from LDS across its row tiles. Splits of one row group
+// are added by the last workgroup to finish (see linear_rows_kernel).
 #include "rk_device.h"
 #include "rk_internal.h"
 
@@ -34,133 +34,169 @@ struct LinArgs {
     const float* bias;             // [N] or null
     const float* res;              // [M, N] or null
     float* part;                   // [S, M, N] partial sums (S > 1)
-    uint32_t* cnt;                 // [row blocks] arrival counters, zero between calls (S > 1)
+    uint32_t* cnt;                 // [row groups] arrival counters, zero between calls (S > 1)
     int M, N, K, S;
 };
 
 template <int WT> struct WTraits;
-// DPB: dwords of one lane's MFMA slots of one block (8 weights); BPB: bytes of one block of one row
-template <> struct WTraits<RK_W_BF16> { static constexpr int DPB = 4; static constexpr int BPB = 64; };
-template <> struct WTraits<RK_W_INT8> { static constexpr int DPB = 2; static constexpr int BPB = 32; };
-template <> struct WTraits<RK_W_INT4> { static constexpr int DPB = 1; static constexpr int BPB = 16; };
+// BPB: bytes of one block of one row
+template <> struct WTraits<RK_W_BF16> { static constexpr int BPB = 64; };
+template <> struct WTraits<RK_W_INT8> { static constexpr int BPB = 32; };
+template <> struct WTraits<RK_W_INT4> { static constexpr int BPB = 16; };
 
 __device__ __forceinline__ float half_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-// 8 weights (one lane's MFMA slots of one block) as bf16 bits, from the raw bytes
-template <int WT> struct Slot;
-template <> struct Slot<RK_W_BF16> {
-    u32x4 v;
-    __device__ __forceinline__ void load(const uint8_t* p) { v = *reinterpret_cast<const u32x4*>(p); }
-    __device__ __forceinline__ u32x4 bf16() const { return v; }
-};
-template <> struct Slot<RK_W_INT8> {
-    u32x2 v;
-    __device__ __forceinline__ void load(const uint8_t* p) { v = *reinterpret_cast<const u32x2*>(p); }
-    __device__ __forceinline__ u32x4 bf16() const {
-        // q in [-127, 127]: exact in bf16; the top half of the fp32 value is its bf16 pattern
-        u32x4 o;
+// 8 INT8 codes (one lane's MFMA slots of one block: bytes of lo then hi) as bf16 bits; q in [-127, 127] is exact in
+// bf16, and the top half of the fp32 value is its bf16 pattern
+__device__ __forceinline__ u32x4 int8_bf16(uint32_t lo, uint32_t hi) {
+    u32x4 o;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const uint32_t w = v[h];
-                const float f0 = (float)(int)__builtin_amdgcn_sbfe(w, 16 * e, 8);
-                const float f1 = (float)(int)__builtin_amdgcn_sbfe(w, 16 * e + 8, 8);
-                o[2 * h + e] = pack_hi2(__float_as_uint(f0), __float_as_uint(f1));
-            }
-        return o;
-    }
-};
-template <> struct Slot<RK_W_INT4> {
-    uint32_t v;
-    __device__ __forceinline__ void load(const uint8_t* p) { v = *reinterpret_cast<const uint32_t*>(p); }
-    __device__ __forceinline__ u32x4 bf16() const {
-        // byte j holds elements 2j (low nibble) and 2j+1 (high nibble); q in 0..15 is exact in bf16
-        u32x4 o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float f0 = (float)__builtin_amdgcn_ubfe(v, 8 * j, 4);
-            const float f1 = (float)__builtin_amdgcn_ubfe(v, 8 * j + 4, 4);
-            o[j] = pack_hi2(__float_as_uint(f0), __float_as_uint(f1));
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t w = h ? hi : lo;
+            const float f0 = (float)(int)__builtin_amdgcn_sbfe(w, 16 * e, 8);
+            const float f1 = (float)(int)__builtin_amdgcn_sbfe(w, 16 * e + 8, 8);
+            o[2 * h + e] = pack_hi2(__float_as_uint(f0), __float_as_uint(f1));
         }
-        return o;
+    return o;
+}
+
+// 8 INT4 codes (4 bytes; byte j holds elements 2j in the low nibble, 2j+1 in the high one) as bf16 bits
+__device__ __forceinline__ u32x4 int4_bf16(uint32_t v) {
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float f0 = (float)__builtin_amdgcn_ubfe(v, 8 * j, 4);
+        const float f1 = (float)__builtin_amdgcn_ubfe(v, 8 * j + 4, 4);
+        o[j] = pack_hi2(__float_as_uint(f0), __float_as_uint(f1));
     }
-};
+    return o;
+}
 
-constexpr int kRows = 64;                  // weight rows per workgroup: 4 waves x one 16-row MFMA tile
+// 4 x 4 transpose over the wave's four 16-lane groups: afterwards register d of lane group g holds what register g
+// of lane group d held. v_permlane32_swap exchanges the upper 32 lanes of its first operand with the lower 32 of its
+// second, v_permlane16_swap the odd 16-lane groups of the first with the even ones of the second; all 64 lanes must
+// be active.
+__device__ __forceinline__ u32x4 xpose4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+    const auto s02 = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+    const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    return (u32x4){s01[0], s01[1], s23[0], s23[1]};
+}
 
-// Workgroup (row block rb, K-split sp): rows rb*64 .. +63, blocks sp*NB .. +NB-1. Everything it reads is requested
-// first (activations, then the rows' scales / mins, then all NB blocks of this lane's weights, so the staging wait
-// never includes the weights); the activations' pieces, block sums and the parameters go to LDS behind one barrier;
-// then the NB blocks of MFMAs. With S > 1 splits the workgroup stores its partial sums (device-coherent stores),
-// counts itself in for its row block, and the last to arrive adds the S partials in split order (deterministic,
-// whatever the arrival order), the bias and the residual, and writes y.
-template <int WT, int COLS, int NB>
+constexpr int kWaveBlocks = 8;                     // quantization blocks per wave
+constexpr int kSplitBlocks = 4 * kWaveBlocks;      // blocks per workgroup (its K-split: 1024 weights)
+
+// Workgroup (row group rg, K-split sp): rows rg*16*RT .. +16*RT-1 against blocks sp*32 .. +31; wave w takes blocks
+// 8w .. 8w+7 of the split for all the group's rows (RT 16-row tiles), so the activations a wave reads from LDS feed RT
+// tiles of MFMAs. The MFMA computes D[m][n] = sum_k X[m][k] W[n][k]: activation pieces are the A operand, the
+// weights the B operand, so a lane's four outputs share weight row n = r and one scale (and min) per block, which the
+// lane holds in registers. Each thread requests everything first (its activations for staging, then its rows'
+// scales / mins, then its RT tiles' weight chunks; the staging wait covers the activations only), stages activation
+// pieces and block sums in LDS behind one barrier, runs the MFMAs, and the four waves' sums meet in LDS (added in
+// wave order). With S > 1 splits the workgroup stores its partial sums (device-coherent stores), counts itself in
+// for its row group, and the last to arrive adds the S partials in split order (deterministic, whatever the arrival
+// order), the bias and the residual, and writes y. Every output's summation order depends on K alone.
+template <int WT, int COLS, int RT, bool PV>
 __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     using TR = WTraits<WT>;
-    constexpr int KG = 4 * NB;                     // 8-element k-groups of the workgroup's K-range
     constexpr bool QUANT = WT != RK_W_BF16;
-    constexpr int XI = COLS * KG / 256;            // staging items (8 activations each) per thread
-    constexpr int PB = NB / 4;                     // parameter blocks per thread (4 threads per row)
-    __shared__ __align__(16) u32x4 xs[3 * KG * COLS];
-    __shared__ float xsum[WT == RK_W_INT4 ? COLS * KG : 1];
-    __shared__ __align__(16) float ss[QUANT ? NB * kRows : 4];
-    __shared__ __align__(16) float ms[WT == RK_W_INT4 ? NB * kRows : 4];
+    constexpr int KG = 4 * kSplitBlocks;           // 8-element k-groups of the split
+    constexpr int XI = COLS * KG / 256;            // staged k-groups (8 activations of one row) per thread
+    __shared__ __align__(16) u32x4 xs[3 * KG * COLS];          // [piece][k-group][activation row]
+    __shared__ __align__(16) float bsum_s[WT == RK_W_INT4 ? kSplitBlocks * COLS : 4];   // [block][activation row]
     __shared__ int is_last;
+    static_assert(4 * RT * 64 * sizeof(f32x4) <= sizeof(xs), "wave sums reuse the staging buffer");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, grp = lane >> 4;
-    const int rb = blockIdx.x / a.S, sp = blockIdx.x % a.S;
-    const int row0 = rb * kRows;
+    const int rg = blockIdx.x / a.S, sp = blockIdx.x % a.S;
+    const int row0 = rg * 16 * RT;
     const int nblk = a.K / kQB;
-    const int b0 = sp * NB;
-    const int nb = min(NB, nblk - b0);             // blocks of this workgroup (>= 1)
+    const int b0 = sp * kSplitBlocks;
+    const int nb = min(kSplitBlocks, nblk - b0);   // blocks of this split (>= 1)
+    const int wb0 = b0 + wave * kWaveBlocks;       // this wave's first block
+    const int nbw = max(0, min(kWaveBlocks, nblk - wb0));
 
-    // ---- requests: activations, parameters, weights
-    f32x4 xa[XI], xb[XI];
+    // ---- requests: activations, parameters, weights (in this order, all before any use)
+    // activations: thread k-groups id = tid + 256u, activation row id / KG, k-group id % KG (consecutive lanes read
+    // consecutive 32 bytes)
+    f32x4 xv[XI][2];
 #pragma unroll
     for (int u = 0; u < XI; ++u) {
-        const int i = tid + 256 * u;
-        const int col = i % COLS, kg = i / COLS;
-        const bool ok = col < a.M && kg < 4 * nb;
-        const float* p = a.x + (size_t)min(col, a.M - 1) * a.K + (size_t)kQB * b0 + 8 * min(kg, 4 * nb - 1);
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(p);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(p + 4);
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        xa[u] = ok ? v0 : z;
-        xb[u] = ok ? v1 : z;
+        const int id = tid + 256 * u;
+        const int col = id / KG, kg = id % KG;
+        const f32x4* p = reinterpret_cast<const f32x4*>(a.x + (size_t)min(col, a.M - 1) * a.K + (size_t)kQB * b0 +
+                                                          8 * min(kg, 4 * nb - 1));
+        xv[u][0] = p[0];
+        xv[u][1] = p[1];
     }
-    const int prow = tid % kRows, pq = tid / kRows;            // parameters: row prow, blocks pq*PB .. +PB-1
-    uint16_t sc16[QUANT ? PB : 1], mn16[WT == RK_W_INT4 ? PB : 1];
+    __builtin_amdgcn_sched_barrier(0);
+    // scales / mins of blocks wb0 .. +7 of row 16t + r: PV (K % 256 == 0) one 16-byte load per tile and kind
+    // (wb0 + 8 <= nblk whenever the wave has blocks), else 8 two-byte loads kept unpacked until use
+    u32x4 sc[QUANT && PV ? RT : 1], mn[WT == RK_W_INT4 && PV ? RT : 1];
+    uint32_t sch[QUANT && !PV ? RT : 1][8], mnh[WT == RK_W_INT4 && !PV ? RT : 1][8];
     if constexpr (QUANT) {
-        const size_t base = (size_t)min(row0 + prow, a.N - 1) * nblk + b0;
 #pragma unroll
-        for (int e = 0; e < PB; ++e) {
-            const int j = min(pq * PB + e, nb - 1);
-            sc16[e] = a.scales[base + j];
-            if constexpr (WT == RK_W_INT4) mn16[e] = a.mins[base + j];
+        for (int t = 0; t < RT; ++t) {
+            const size_t rowp = (size_t)min(row0 + 16 * t + r, a.N - 1) * nblk;
+            if constexpr (PV) {
+                const size_t i0 = rowp + min(wb0, nblk - kWaveBlocks);
+                sc[t] = *reinterpret_cast<const u32x4*>(a.scales + i0);
+                if constexpr (WT == RK_W_INT4) mn[t] = *reinterpret_cast<const u32x4*>(a.mins + i0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < kWaveBlocks; ++j) {
+                    const size_t i0 = rowp + min(wb0 + j, nblk - 1);
+                    sch[t][j] = a.scales[i0];
+                    if constexpr (WT == RK_W_INT4) mnh[t][j] = a.mins[i0];
+                }
+            }
         }
     }
-    const uint8_t* wrow = static_cast<const uint8_t*>(a.w) +
-                          (size_t)min(row0 + 16 * wave + r, a.N - 1) * ((size_t)a.K * TR::BPB / kQB) +
-                          (size_t)b0 * TR::BPB + grp * (TR::BPB / 4);
-    Slot<WT> wv[NB];
+    __builtin_amdgcn_sched_barrier(0);
+    // weights, 16 bytes per lane and load: 64 contiguous bytes of each of 16 rows per instruction. bf16: lane group g
+    // loads its own k-group of each block. INT8 / INT4: lane group g loads all of block 4q + g (two / one chunks),
+    // and a 4 x 4 transpose over the lane groups (xpose4) then hands each lane its k-group of blocks 4q .. 4q+3.
+    constexpr int CH = WT == RK_W_INT4 ? 2 : (WT == RK_W_INT8 ? 4 : kWaveBlocks);   // chunks per tile
+    u32x4 raw[RT][CH];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) wv[j].load(wrow + (size_t)min(j, nb - 1) * TR::BPB);
+    for (int t = 0; t < RT; ++t) {
+        const uint8_t* wrow = static_cast<const uint8_t*>(a.w) +
+                              (size_t)min(row0 + 16 * t + r, a.N - 1) * ((size_t)nblk * TR::BPB);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            size_t off;
+            if constexpr (WT == RK_W_BF16) off = (size_t)min(wb0 + c, nblk - 1) * TR::BPB + 16 * grp;
+            else if constexpr (WT == RK_W_INT8) off = (size_t)min(wb0 + 4 * (c >> 1) + grp, nblk - 1) * TR::BPB + 16 * (c & 1);
+            else off = (size_t)min(wb0 + 4 * c + grp, nblk - 1) * TR::BPB;
+            raw[t][c] = *reinterpret_cast<const u32x4*>(wrow + off);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- staging: activation pieces [3][KG][COLS], block sums [COLS][KG], parameters [NB][64 rows]
+    // ---- staging: activation pieces [3][KG][COLS]; block sums [32][COLS] (INT4: the four k-groups of a block sit in
+    // lanes 4i .. 4i+3 and are added pairwise, (s0 + s1) + (s2 + s3), identically in all four)
 #pragma unroll
     for (int u = 0; u < XI; ++u) {
-        const int i = tid + 256 * u;
-        const int col = i % COLS, kg = i / COLS;
-        const float v[8] = {xa[u][0], xa[u][1], xa[u][2], xa[u][3], xb[u][0], xb[u][1], xb[u][2], xb[u][3]};
+        const int id = tid + 256 * u;
+        const int col = id / KG, kg = id % KG;
+        const bool ok = col < a.M && kg < 4 * nb;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = ok ? xv[u][0][e] : 0.0f;
+            v[4 + e] = ok ? xv[u][1][e] : 0.0f;
+        }
         u32x4 pc[3];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const Split3 s0 = split3(v[2 * j]), s1 = split3(v[2 * j + 1]);
-            pc[0][j] = pack_hi2(s0.hi, s1.hi);
-            pc[1][j] = pack_hi2(s0.mid, s1.mid);
-            pc[2][j] = pack_hi2(s0.lo, s1.lo);
+        for (int q = 0; q < 4; ++q) {
+            const Split3 s0 = split3(v[2 * q]), s1 = split3(v[2 * q + 1]);
+            pc[0][q] = pack_hi2(s0.hi, s1.hi);
+            pc[1][q] = pack_hi2(s0.mid, s1.mid);
+            pc[2][q] = pack_hi2(s0.lo, s1.lo);
         }
 #pragma unroll
         for (int p = 0; p < 3; ++p) xs[(p * KG + kg) * COLS + col] = pc[p];
@@ -168,89 +204,126 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
             float sum = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) sum += v[e];
-            xsum[col * KG + kg] = sum;
-        }
-    }
-    if constexpr (QUANT) {
-#pragma unroll
-        for (int e = 0; e < PB; ++e) {
-            ss[(pq * PB + e) * kRows + prow] = half_to_f32(sc16[e]);
-            if constexpr (WT == RK_W_INT4) ms[(pq * PB + e) * kRows + prow] = half_to_f32(mn16[e]);
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            if ((kg & 3) == 0) bsum_s[(kg >> 2) * COLS + col] = sum;
         }
     }
     __syncthreads();
 
-    // ---- MFMAs: block j of this workgroup = MFMA k-extent j; accumulator rows 16 wave + 4 grp + i, column r
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // ---- MFMAs: block wb0 + j; lane (r, grp) supplies activation row r's k-group grp and weight row 16t + r's
+    f32x4 acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
-    const int lr = 16 * wave + 4 * grp;
+    const bool col_ok = COLS == 16 || r < COLS;
+    const int cr = COLS == 16 ? r : (r & (COLS - 1));
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        if (j < nb) {                               // uniform: the last split may hold fewer blocks
-        const int kg = 4 * j + grp;                 // this lane's k-group: k = 32 (b0 + j) + 8 grp .. + 7
-        const bool col_ok = COLS == 16 || r < COLS;
-        const int cr = COLS == 16 ? r : (r & (COLS - 1));
-        const u32x4 p0 = col_ok ? xs[(0 * KG + kg) * COLS + cr] : zero4;
-        const u32x4 p1 = col_ok ? xs[(1 * KG + kg) * COLS + cr] : zero4;
-        const u32x4 p2 = col_ok ? xs[(2 * KG + kg) * COLS + cr] : zero4;
-        const u32x4 av = wv[j].bf16();
-        if constexpr (QUANT) {
-            f32x4 d = mfma16x16x32(av, p0, (f32x4){0.f, 0.f, 0.f, 0.f});
-            d = mfma16x16x32(av, p1, d);
-            d = mfma16x16x32(av, p2, d);
-            const f32x4 sc = *reinterpret_cast<const f32x4*>(&ss[j * kRows + lr]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = fmaf(sc[i], d[i], acc[i]);
+    for (int j = 0; j < kWaveBlocks; ++j) {
+        if (j < nbw) {                              // uniform per wave: the last split may hold fewer blocks
+            const int kg = 4 * (wave * kWaveBlocks + j) + grp;
+            const u32x4 p0 = col_ok ? xs[(0 * KG + kg) * COLS + cr] : zero4;
+            const u32x4 p1 = col_ok ? xs[(1 * KG + kg) * COLS + cr] : zero4;
+            const u32x4 p2 = col_ok ? xs[(2 * KG + kg) * COLS + cr] : zero4;
+            f32x4 bs = {0.f, 0.f, 0.f, 0.f};
             if constexpr (WT == RK_W_INT4) {
-                // block sum of activation column r: four k-group partials, in order
-                const float bsum = col_ok ? ((xsum[cr * KG + 4 * j] + xsum[cr * KG + 4 * j + 1]) +
-                                             xsum[cr * KG + 4 * j + 2]) + xsum[cr * KG + 4 * j + 3]
-                                          : 0.0f;
-                const f32x4 mn = *reinterpret_cast<const f32x4*>(&ms[j * kRows + lr]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[i] = fmaf(mn[i], bsum, acc[i]);
+                if (4 * grp < COLS) bs = *reinterpret_cast<const f32x4*>(&bsum_s[(wave * kWaveBlocks + j) * COLS + 4 * grp]);
             }
-        } else {
-            acc = mfma16x16x32(av, p0, acc);
-            acc = mfma16x16x32(av, p1, acc);
-            acc = mfma16x16x32(av, p2, acc);
-        }
-        }
-    }
-
-    // ---- epilogue: y[m][n] (+ bias, + residual, separately rounded), m = r, n = row0 + lr + i
-    const int n0 = row0 + lr;
-    if (a.S == 1) {
-        if (r < a.M) {
+            if constexpr (WT != RK_W_BF16) {
+                if ((j & 3) == 0) {                 // blocks j .. j+3 arrive in this wave's lane groups
+                    const int q = j >> 2;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int n = n0 + i;
-                if (n < a.N) {
-                    float v = acc[i];
-                    if (a.bias) v = __fadd_rn(v, a.bias[n]);
-                    if (a.res) v = __fadd_rn(v, a.res[(size_t)r * a.N + n]);
-                    a.y[(size_t)r * a.N + n] = v;
+                    for (int t = 0; t < RT; ++t) {
+                        if constexpr (WT == RK_W_INT4) {
+                            const u32x4 c = raw[t][q];
+                            raw[t][q] = xpose4(c[0], c[1], c[2], c[3]);
+                        } else {
+                            // qword k (k-group k of the lane group's block) = dwords (2k, 2k+1) of chunks 2q, 2q+1
+                            const u32x4 c0 = raw[t][2 * q], c1 = raw[t][2 * q + 1];
+                            const u32x4 lo = xpose4(c0[0], c0[2], c1[0], c1[2]);
+                            const u32x4 hi = xpose4(c0[1], c0[3], c1[1], c1[3]);
+                            raw[t][2 * q] = (u32x4){lo[0], hi[0], lo[1], hi[1]};
+                            raw[t][2 * q + 1] = (u32x4){lo[2], hi[2], lo[3], hi[3]};
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const int d = j & 3;
+                u32x4 bw;
+                if constexpr (WT == RK_W_BF16) bw = raw[t][j];
+                else if constexpr (WT == RK_W_INT8)
+                    bw = int8_bf16(raw[t][2 * (j >> 2) + (d >> 1)][2 * (d & 1)], raw[t][2 * (j >> 2) + (d >> 1)][2 * (d & 1) + 1]);
+                else bw = int4_bf16(raw[t][j >> 2][d]);
+                if constexpr (QUANT) {
+                    f32x4 d = mfma16x16x32(p0, bw, (f32x4){0.f, 0.f, 0.f, 0.f});
+                    d = mfma16x16x32(p1, bw, d);
+                    d = mfma16x16x32(p2, bw, d);
+                    const float s = half_to_f32((uint16_t)(PV ? sc[t][j >> 1] >> (16 * (j & 1)) : sch[t][j]));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(s, d[i], acc[t][i]);
+                    if constexpr (WT == RK_W_INT4) {
+                        const float m = half_to_f32((uint16_t)(PV ? mn[t][j >> 1] >> (16 * (j & 1)) : mnh[t][j]));
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(m, bs[i], acc[t][i]);
+                    }
+                } else {
+                    acc[t] = mfma16x16x32(p0, bw, acc[t]);
+                    acc[t] = mfma16x16x32(p1, bw, acc[t]);
+                    acc[t] = mfma16x16x32(p2, bw, acc[t]);
                 }
             }
         }
-        return;
     }
-    if (r < a.M) {
+
+    // ---- the four waves' sums, in wave order; thread (t, l) then owns outputs m = 4(l/16) + i, n = row0 + 16t + l%16
+    __syncthreads();                                // every wave has finished reading the staging buffer
+    f32x4* red = reinterpret_cast<f32x4*>(xs);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (n0 + i < a.N)
-                __hip_atomic_store(&a.part[((size_t)sp * a.M + r) * a.N + n0 + i], acc[i], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+    for (int t = 0; t < RT; ++t) red[(wave * RT + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (tid < RT * 64) {
+        const int t = tid >> 6, l = tid & 63;
+        f32x4 s = red[t * 64 + l];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const f32x4 o = red[(w * RT + t) * 64 + l];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[i] += o[i];
+        }
+        const int n = row0 + 16 * t + (l & 15), m0 = 4 * (l >> 4);
+        if (n < a.N) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + i;
+                if (m < a.M) {
+                    if (a.S == 1) {
+                        float v = s[i];
+                        if (a.bias) v = __fadd_rn(v, a.bias[n]);
+                        if (a.res) v = __fadd_rn(v, a.res[(size_t)m * a.N + n]);
+                        a.y[(size_t)m * a.N + n] = v;
+                    } else {
+                        __hip_atomic_store(&a.part[((size_t)sp * a.M + m) * a.N + n], s[i], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+        }
     }
-    __syncthreads();                                // every partial store of the workgroup has completed
+    if (a.S == 1) return;
+    // every partial store of the workgroup is complete (acknowledged at the device-coherent level: they are
+    // agent-scope atomic stores) before the workgroup counts itself in
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): loads and stores issued so far have completed
+    __syncthreads();
     if (tid == 0) {
-        const uint32_t before = __hip_atomic_fetch_add(&a.cnt[rb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t before = __hip_atomic_fetch_add(&a.cnt[rg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         is_last = before == (uint32_t)(a.S - 1);
     }
     __syncthreads();
     if (!is_last) return;
-    for (int i = tid; i < a.M * kRows; i += 256) {
-        const int m = i / kRows, n = row0 + i % kRows;
+    for (int i = tid; i < a.M * 16 * RT; i += 256) {
+        const int m = i / (16 * RT), n = row0 + i % (16 * RT);
         if (n >= a.N) continue;
         float v = 0.0f;
         for (int q = 0; q < a.S; ++q)
@@ -260,21 +333,24 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
         if (a.res) v = __fadd_rn(v, a.res[(size_t)m * a.N + n]);
         a.y[(size_t)m * a.N + n] = v;
     }
-    if (tid == 0) __hip_atomic_store(&a.cnt[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(&a.cnt[rg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Blocks per workgroup (32 INT8 / INT4 blocks, 16 bf16 blocks: a fixed K-split, so the summation order of an output
-// does not depend on M) and staged activation columns (8 for M <= 8, else 16).
+// Row tiles per workgroup: the most (4; 2 for bf16, whose weight slots are 4x wider than INT4's) that still leave
+// 512 workgroups, down to 1. Staged activation rows: 8 for M <= 8, else 16. Neither changes any output's summation
+// order (blocks in order within a wave, waves in order, splits in order).
 struct LinPlan {
-    int cols, nb, S, row_blocks;
+    int cols, rt, S, groups;
 };
+
 LinPlan lin_plan(int M, int N, int K, int w_type) {
     LinPlan p;
     p.cols = M <= 8 ? 8 : 16;
-    p.nb = w_type == RK_W_BF16 ? 16 : 32;          // never depends on M: a row's sums do not depend on the batch
     const int nblk = K / kQB;
-    p.S = (nblk + p.nb - 1) / p.nb;
-    p.row_blocks = (N + kRows - 1) / kRows;
+    p.S = (nblk + kSplitBlocks - 1) / kSplitBlocks;
+    p.rt = w_type == RK_W_BF16 ? 2 : 4;
+    while (p.rt > 1 && (long long)((N + 16 * p.rt - 1) / (16 * p.rt)) * p.S < 512) p.rt /= 2;
+    p.groups = (N + 16 * p.rt - 1) / (16 * p.rt);
     return p;
 }
 
@@ -343,26 +419,32 @@ int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w,
         return fail(RK_ERR_ARG, "rk_linear_rows: x and w must be 16-byte aligned");
     const LinPlan p = lin_plan(M, N, K, w_type);
     const size_t need = rk_linear_workspace_bytes(M, N, K, w_type);
-    if (need && (!partials || partial_bytes < need || !counters || n_counters < p.row_blocks))
+    if (need && (!partials || partial_bytes < need || !counters || n_counters < p.groups))
         return fail(RK_ERR_WORKSPACE, "rk_linear_rows: partials %zu bytes (need %zu), %d counters (need %d)",
-                    partial_bytes, need, n_counters, p.row_blocks);
-    if ((long long)p.row_blocks * p.S >= (1ll << 31)) return fail(RK_ERR_ARG, "rk_linear_rows: N %d too large", N);
+                    partial_bytes, need, n_counters, p.groups);
+    if ((long long)p.groups * p.S >= (1ll << 31)) return fail(RK_ERR_ARG, "rk_linear_rows: N %d too large", N);
     LinArgs a;
     a.y = y; a.x = x; a.w = w; a.scales = static_cast<const uint16_t*>(scales);
     a.mins = static_cast<const uint16_t*>(mins); a.bias = bias; a.res = residual;
     a.cnt = counters;
     a.part = partials;
     a.M = M; a.N = N; a.K = K; a.S = p.S;
+    // 16-byte parameter loads: K % 256 == 0 and 16-byte aligned scale / min arrays
+    const bool pv = (K / kQB) % kWaveBlocks == 0 && reinterpret_cast<uintptr_t>(scales) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(mins) % 16 == 0;
     using Fn = void (*)(LinArgs);
-    Fn fn;
-    if (p.cols == 8) {
-        fn = w_type == RK_W_BF16 ? linear_rows_kernel<RK_W_BF16, 8, 16>
-             : w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, 8, 32> : linear_rows_kernel<RK_W_INT4, 8, 32>;
-    } else {
-        fn = w_type == RK_W_BF16 ? linear_rows_kernel<RK_W_BF16, 16, 16>
-             : w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, 16, 32> : linear_rows_kernel<RK_W_INT4, 16, 32>;
-    }
-    hipLaunchKernelGGL(fn, dim3((unsigned)(p.row_blocks * p.S)), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    Fn fn = nullptr;
+#define RK_LIN_PICK(C, R, V)                                                                                   \
+    if (p.cols == C && p.rt == R && pv == V)                                                                   \
+        fn = w_type == RK_W_BF16 ? linear_rows_kernel<RK_W_BF16, C, (R > 2 ? 2 : R), V>                        \
+             : w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, C, R, V> : linear_rows_kernel<RK_W_INT4, C, R, V>;
+    RK_LIN_PICK(8, 1, true) RK_LIN_PICK(8, 2, true) RK_LIN_PICK(8, 4, true)
+    RK_LIN_PICK(16, 1, true) RK_LIN_PICK(16, 2, true) RK_LIN_PICK(16, 4, true)
+    RK_LIN_PICK(8, 1, false) RK_LIN_PICK(8, 2, false) RK_LIN_PICK(8, 4, false)
+    RK_LIN_PICK(16, 1, false) RK_LIN_PICK(16, 2, false) RK_LIN_PICK(16, 4, false)
+#undef RK_LIN_PICK
+    if (!fn) return fail(RK_ERR_ARG, "rk_linear_rows: no kernel for %d columns, %d row tiles", p.cols, p.rt);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(p.groups * p.S)), dim3(256), 0, static_cast<hipStream_t>(stream), a);
     return check_launch("linear_rows");
 }
 

@@ -190,7 +190,7 @@ def test_linear_arguments_checked_on_host(lib):
 
     def call(**kw):
         a = dict(y=fake, x=fake, M=8, N=2048, K=2048, w=fake, wt=2, s=fake, m=fake, b=None, r=None, p=fake,
-                 pb=1 << 30, c=fake, nc=32)
+                 pb=1 << 30, c=fake, nc=128)
         a.update(kw)
         return lib.lib.rk_linear_rows(*a.values(), None)
 
@@ -200,11 +200,12 @@ def test_linear_arguments_checked_on_host(lib):
     assert call(wt=3, m=None) == 1 and "null pointer" in lib.last_error()
     assert call(y=fake + 4, x=fake + 8) == 1 and "aligned" in lib.last_error()
     need = lib.lib.rk_linear_workspace_bytes(8, 2048, 2048, 2)
-    assert need == 2 * 8 * 2048 * 4                            # 2 splits of 32 blocks
+    assert need == 2 * 8 * 2048 * 4                            # 2 K-splits of 32 blocks
     assert call(pb=need - 1) == 3 and "partials" in lib.last_error()
-    assert call(nc=31) == 3 and "counters" in lib.last_error()
+    assert call(nc=127) == 3 and "counters" in lib.last_error()    # 128 groups of 16 rows
     assert lib.lib.rk_linear_workspace_bytes(8, 2048, 1024, 2) == 0      # one split: no workspace
-    assert lib.lib.rk_linear_workspace_bytes(12, 2048, 2048, 1) == 4 * 12 * 2048 * 4
+    assert lib.lib.rk_linear_workspace_bytes(12, 2048, 2048, 1) == 2 * 12 * 2048 * 4
+    assert lib.lib.rk_linear_workspace_bytes(3, 100, 6144, 3) == 6 * 3 * 100 * 4
     assert lib.lib.rk_linear_workspace_bytes(12, 2048, 2048, 3) == 2 * 12 * 2048 * 4
     assert call(M=0) == 0
     assert lib.lib.rk_dequant_rows(fake, fake, 2, fake, None, None, 10, 5, 12, 2048, None) == 1
