@@ -42,9 +42,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float x0, float x1) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{x0, x1}), bf16x2_t));
 }
 
-// Pack the top halves (truncated bf16 patterns) of two fp32 bit patterns: element 0 in the low 16 bits.
+// Pack the top halves (truncated bf16 patterns) of two fp32 bit patterns: element 0 in the low 16 bits. One
+// v_perm_b32: result bytes = bytes 2, 3 of e0 then bytes 2, 3 of e1 (selectors 4..7 address the first operand).
 __device__ __forceinline__ uint32_t pack_hi2(uint32_t e0, uint32_t e1) {
-    return (e0 >> 16) | (e1 & 0xffff0000u);
+    return __builtin_amdgcn_perm(e1, e0, 0x07060302u);
 }
 
 // Exact three-way split of an fp32 value into bf16-representable parts x = hi + mid + lo (truncation at every
