@@ -625,12 +625,15 @@ def bench_linears(args, backend):
     torch.cuda.synchronize()
     ms = graph_time(step, max(1, args.steps // 5), stream)
     head = mats[-1]
-    ms_head = graph_time(lambda: kernels.linear_rows(xs[H], head, out=outs[-1]), args.steps, stream)
+    # the head alone (skipped under --no-graph, the counter-collection mode, so that every dispatch is one of a step)
+    ms_head = None if args.no_graph else graph_time(lambda: kernels.linear_rows(xs[H], head, out=outs[-1]),
+                                                     args.steps, stream)
     io = sum(M * (m.shape[1] + m.shape[0]) * 4 for m in mats)
     gbs = (wbytes + io) / (ms * 1e-3) / 1e9
-    head_gbs = head.nbytes / (ms_head * 1e-3) / 1e9
+    head_gbs = head.nbytes / (ms_head * 1e-3) / 1e9 if ms_head else None
+    head_note = f"; head alone {ms_head * 1e3:.1f} us ({head_gbs:.0f} GB/s)" if ms_head else ""
     log(f"[bench] mv: {ms * 1e3:.1f} us per step of {len(mats)} linears ({wbytes / 1e9:.2f} GB of weights, "
-        f"{gbs:.0f} GB/s = {gbs / HBM_PEAK_GBS:.1%}); head alone {ms_head * 1e3:.1f} us ({head_gbs:.0f} GB/s)")
+        f"{gbs:.0f} GB/s = {gbs / HBM_PEAK_GBS:.1%}){head_note}")
     cpu = None
     if not args.no_cpu:
         from oracle import quant_ref

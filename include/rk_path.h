@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 5
+#define RK_ABI_VERSION 6
 
 /* status codes */
 #define RK_OK 0
@@ -199,6 +199,27 @@ int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w,
                    size_t partial_bytes, uint32_t* counters, int n_counters, void* stream);
 int rk_dequant_rows(float* out, const void* w, int w_type, const void* scales, const void* mins,
                     const int32_t* rows, int row0, int n_rows, int N, int K, void* stream);
+
+/* ---- the rest of a decode step (native/decode_ops.hip): the row norms, RoPE and SwiGLU's silu * up
+ * Replace Backend.rms_norm / layer_norm / rope / silu_mul (src/backend/base.py:26-40, the protocol's v1 and v3
+ * methods; MetalBackend.rms_norm / layer_norm / rope / silu_mul, src/backend/metal.py:159-187, 225-230; semantics
+ * ops.rms_norm, ops.layer_norm, ops.rope, ops.silu_mul, src/ops.py:7-54, 107-110). fp32 outputs, contiguous.
+ *
+ * rk_rms_norm: out [rows, D] = (x / sqrt(mean(x^2) + eps)) * w; x rows at x + r * x_ld (RK_F32 / RK_BF16),
+ *   w [D] (RK_F32 / RK_BF16); D a multiple of 4, at most 4096; x, w, out aligned to 4 elements.
+ * rk_layer_norm: out = w * ((x - mean) * (1 / sqrt(var + eps))), no bias; arguments as rk_rms_norm.
+ * rk_rope: out [T, H, d] = x rotated by positions[t] * inv_freq[i] over the pairs (i, i + d/2) (HF rotate_half);
+ *   inv_freq [d/2] fp32 as the reference computes it on the host (ops.rope_inv_freq).
+ * rk_silu_mul: out [rows, F] = (g / (1 + exp(-g))) * u, g rows at gate + r * gate_ld, u at up + r * up_ld (fp32:
+ *   SwiGLU reads the two halves of one [rows, 2F] projection in place). */
+int rk_rms_norm(float* out, const void* x, int x_dtype, long long x_ld, const void* w, int w_dtype, int rows, int D,
+                float eps, void* stream);
+int rk_layer_norm(float* out, const void* x, int x_dtype, long long x_ld, const void* w, int w_dtype, int rows, int D,
+                  float eps, void* stream);
+int rk_rope(float* out, const float* x, const int32_t* positions, const float* inv_freq, int T, int H, int d,
+            void* stream);
+int rk_silu_mul(float* out, const float* gate, long long gate_ld, const float* up, long long up_ld, int rows, int F,
+                void* stream);
 
 #ifdef __cplusplus
 }

@@ -23,6 +23,11 @@ Method -> kernel:
                          layer (src/models/qwen3_5.py:251-262, 100-110) in one launch
   linear, embedding      rk_linear_rows (bf16 / INT8 / INT4 weights, up to 32 rows), rk_dequant_rows (+ a BLAS GEMM
                          beyond 32 rows; embedding rows), src/backend/metal.py:50-133
+  swiglu, silu_mul       rk_linear_rows on the stacked [gate; up] weight, then rk_silu_mul on its two halves in place
+  rms_norm, layer_norm   rk_rms_norm, rk_layer_norm (src/ops.py:7-24)
+  rope                   rk_rope (src/ops.py:27-54)
+  prepare                the reference's weight policy (src/backend/metal.py:43-48): bf16 on the device, or with a
+                         scheme every 2-D weight block-quantized (the tied embedding / head and policy groups INT8)
 """
 import torch
 
@@ -36,7 +41,12 @@ class RocmBackend:
     """Token-mixing backend on one ROCm device. Not thread-safe (one engine thread owns the device, as in the
     reference's scheduler); every launch goes on torch's current stream of that device, without host syncs."""
 
-    def __init__(self, device: str | torch.device = "cuda"):
+    def __init__(self, device: str | torch.device = "cuda", scheme: str | None = None, policy: str | None = None):
+        """scheme None keeps bf16 weights; "int8" / "int4" quantizes every 2-D weight in prepare (or accepts
+        QuantTensors), with the INT4 policy of src/quant.py:115-121 (policy: a configs/quant JSON of groups kept
+        INT8), as MetalBackend(scheme, policy)."""
+        if scheme not in (None, "int8", "int4"):
+            raise ValueError(f"unknown scheme {scheme}")
         if not torch.cuda.is_available():
             raise RuntimeError("RocmBackend needs a ROCm GPU (torch.cuda.is_available() is False)")
         dev = torch.device(device)
@@ -45,8 +55,24 @@ class RocmBackend:
         arch = torch.cuda.get_device_properties(self.device).gcnArchName
         if not arch.startswith("gfx950"):
             raise RuntimeError(f"librk_path.so is built for gfx950 only; device {self.device} is {arch}")
-        self.name = "rocm"
+        from quant import load_policy
+        self.scheme = scheme
+        self.keep_int8 = load_policy(policy)
+        self.weight_dtype = torch.bfloat16
+        self.name = f"rocm-{scheme or 'bf16'}"
         self._seq0 = torch.zeros(1, dtype=torch.int32, device=self.device)
+
+    # ---- weights
+    def prepare(self, w, name=None):
+        """One weight into its resident format (src/backend/metal.py:43-48): a QuantTensor moves to the device;
+        with a scheme, a 2-D weight whose rows are whole blocks is quantized (INT8 for the tied embedding / head and
+        the policy's groups in INT4 mode); anything else is bf16 on the device (src/backend/torch_ref.py:16-17)."""
+        from quant import QuantTensor, quantize, scheme_for
+        if isinstance(w, QuantTensor):
+            return w.to(self.device)
+        if self.scheme and w.ndim == 2 and w.shape[1] % 32 == 0:
+            return quantize(w, scheme_for(name, self.scheme, self.keep_int8)).to(self.device)
+        return w.to(device=self.device, dtype=self.weight_dtype)
 
     # ---- P1: decode attention
     def paged_attention(self, q, k_pool, v_pool, tables, lens, block_size, window=None, gate=None):
@@ -178,6 +204,30 @@ class RocmBackend:
         if isinstance(table, QuantTensor) or table.dtype == torch.bfloat16:
             return kernels.dequantize(table, rows=ids.to(self.device))
         return table[ids.to(table.device)].float()
+
+    def swiglu(self, x, w_gate_up):
+        """silu(x @ gate.T) * (x @ up.T) for w_gate_up = [gate; up] stacked [2F, K] (src/backend/base.py:41-42): one
+        linear over the stacked weight, then silu * up over the two column halves of its output, read in place."""
+        y = self.linear(x, w_gate_up)
+        F = w_gate_up.shape[0] // 2
+        return kernels.silu_mul(y[:, :F], y[:, F:])
+
+    def silu_mul(self, gate, up):
+        """silu(gate) * up, fp32 (src/ops.py:107-110)."""
+        return kernels.silu_mul(gate, up)
+
+    # ---- row norms and rotary embedding
+    def rms_norm(self, x, w, eps):
+        """[..., D] -> (x / sqrt(mean(x^2) + eps)) * w, fp32 (src/ops.py:7-15)."""
+        return kernels.rms_norm(x, w, eps)
+
+    def layer_norm(self, x, w, eps):
+        """LayerNorm without bias over the last dim, fp32 (src/ops.py:18-24; Cohere2)."""
+        return kernels.layer_norm(x, w, eps)
+
+    def rope(self, x, positions, theta):
+        """x [T, H, d] rotated by absolute positions [T] (HF rotate_half pairs), fp32 (src/ops.py:27-54)."""
+        return kernels.rope(x, positions, theta)
 
     # ---- gated-attention pre-processing
     def attention_prep(self, y, q_w, k_w, eps, positions, theta, rot, dims, k_pool=None, v_pool=None, slots=None):

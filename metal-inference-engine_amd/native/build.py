@@ -15,7 +15,7 @@ LIB = HERE / "librk_path.so"
 OBJ_DIR = HERE / "_obj"
 SOURCES = ["rk_abi.cpp", "paged_decode.hip", "kv_cache.hip", "deltanet_step.hip", "paged_prefill.hip",
            "chunked_delta.hip", "deltanet_prefill.hip", "attn_prep.hip",
-           "linear.hip"]
+           "linear.hip", "decode_ops.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 # packed-fp32 VALU forms are switched off for all device code (see the header of rk_device.h)

@@ -597,3 +597,78 @@ def linear(x, w, bias=None, residual=None) -> torch.Tensor:
     if bias is not None:
         y = y + bias.float()
     return y + residual.float() if residual is not None else y
+
+
+NORM_MAX_D = 4096           # rk_rms_norm / rk_layer_norm keep a row in registers: up to 4096 values
+
+
+def _norm(entry: str, x, w, eps: float) -> torch.Tensor:
+    name = entry[3:]
+    D = x.shape[-1]
+    if w.numel() != D or D % 4 or D > NORM_MAX_D:
+        raise ValueError(f"{name}: x {tuple(x.shape)}, w {tuple(w.shape)} (D a multiple of 4, at most {NORM_MAX_D})")
+    dev = _need_cuda(name, x)
+    shape = x.shape
+    if x.dtype not in KV_DTYPES:
+        x = x.float()
+    x = x.reshape(-1, D)
+    if x.stride(1) != 1 or x.stride(0) % 4 or x.data_ptr() % (4 * x.element_size()):
+        x = x.contiguous() if not x.is_contiguous() else x.clone()
+    if w.dtype not in KV_DTYPES:
+        w = w.float()
+    w = w.to(dev).contiguous()
+    if w.data_ptr() % (4 * w.element_size()):
+        w = w.clone()
+    rows = x.shape[0]
+    out = torch.empty(rows, D, dtype=torch.float32, device=dev)
+    load().call(entry, out.data_ptr(), x.data_ptr(), DTYPE_CODES[x.dtype], x.stride(0), w.data_ptr(),
+                DTYPE_CODES[w.dtype], rows, D, float(eps), _stream(dev))
+    return out.view(shape)
+
+
+def rms_norm(x, w, eps: float) -> torch.Tensor:
+    """Backend.rms_norm (rk_rms_norm): [..., D] -> (x / sqrt(mean(x^2) + eps)) * w in fp32 (src/ops.py:7-15); x fp32
+    or bf16 read as stored, rows may be strided; w fp32 or bf16."""
+    return _norm("rk_rms_norm", x, w, eps)
+
+
+def layer_norm(x, w, eps: float) -> torch.Tensor:
+    """Backend.layer_norm (rk_layer_norm): LayerNorm without bias, w * ((x - mean) * rsqrt(var + eps)) in fp32
+    (src/ops.py:18-24)."""
+    return _norm("rk_layer_norm", x, w, eps)
+
+
+def rope(x, positions, theta: float) -> torch.Tensor:
+    """Backend.rope (rk_rope): x [T, H, d] rotated by positions [T] over the pairs (i, i + d/2), fp32 out
+    (src/ops.py:36-54), with the host-computed fp32 inv_freq of the reference (rope_inv_freq)."""
+    if x.dim() != 3 or x.shape[-1] % 2 or positions.numel() != x.shape[0]:
+        raise ValueError(f"rope: x {tuple(x.shape)}, positions {tuple(positions.shape)}")
+    T, H, d = x.shape
+    dev = _need_cuda("rope", x)
+    x = x.to(torch.float32).contiguous()
+    pos = positions.to(device=dev, dtype=torch.int32).contiguous()
+    out = torch.empty_like(x)
+    load().call("rk_rope", out.data_ptr(), x.data_ptr(), pos.data_ptr(), rope_inv_freq(theta, d, dev).data_ptr(),
+                T, H, d, _stream(dev))
+    return out
+
+
+def silu_mul(gate, up) -> torch.Tensor:
+    """Backend.silu_mul (rk_silu_mul): (g / (1 + exp(-g))) * u in fp32 (src/ops.py:107-110). 2-D gate / up may be
+    strided row views (the two halves of one projection output are read in place)."""
+    if gate.shape != up.shape:
+        raise ValueError(f"silu_mul: gate {tuple(gate.shape)}, up {tuple(up.shape)}")
+    dev = _need_cuda("silu_mul", gate, up)
+    shape = gate.shape
+    F = shape[-1] if gate.dim() else 1
+
+    def rows2(t):
+        t = t.to(torch.float32)
+        t = t.reshape(-1, F) if t.dim() != 2 else t
+        return t if t.stride(1) == 1 else t.contiguous()
+
+    g, u = rows2(gate), rows2(up)
+    out = torch.empty(g.shape[0], F, dtype=torch.float32, device=dev)
+    load().call("rk_silu_mul", out.data_ptr(), g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), g.shape[0], F,
+                _stream(dev))
+    return out.view(shape)

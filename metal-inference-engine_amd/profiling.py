@@ -9,7 +9,7 @@ counters, and converters from rocprofv3 CSV output to the short text summaries a
   python metal-inference-engine_amd/profiling.py traffic <out.json> <copy_mib> <copy_fetch.csv> <copy_write.csv>
           <name>=<pattern>:<fetch.csv>:<write.csv> ...
       HBM bytes per launch of the kernels whose names contain <pattern> (summed over kernels when the pattern
-      matches several per step), from one FETCH_SIZE pass and one WRITE_SIZE pass (KiB per dispatch), each scaled
+      matches several per step; averaged over all matching dispatches when it starts with '*'), from one FETCH_SIZE pass and one WRITE_SIZE pass (KiB per dispatch), each scaled
       by what the same counter reads for the copy kernel. Entries for other names already in <out.json> are kept.
 """
 import csv
@@ -43,7 +43,15 @@ def stats_table(stats_csv: str, out_txt: str, command: str) -> None:
 
 
 def _per_dispatch(counter_csv: str, pattern: str, counter: str) -> tuple[float, int]:
-    """Median over steps of the counter summed over the dispatches of one step (kernels matching pattern), KiB."""
+    """Median over steps of the counter summed over the dispatches of one step (kernels matching pattern), KiB.
+    A pattern starting with '*' instead averages over every matching dispatch (a step of many launches of one
+    kernel family over different shapes: the mean bytes per launch)."""
+    if pattern.startswith("*"):
+        vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(counter_csv))
+                if r["Counter_Name"] == counter and pattern[1:] in r["Kernel_Name"]]
+        if not vals:
+            raise SystemExit(f"{counter_csv}: no {counter} rows for kernels matching {pattern[1:]!r}")
+        return sum(vals) / len(vals), len(vals)
     by_kernel = defaultdict(list)
     for r in csv.DictReader(open(counter_csv)):
         if r["Counter_Name"] == counter and pattern in r["Kernel_Name"]:
@@ -72,7 +80,7 @@ def traffic(out_json: str, copy_mib: int, copy_fetch: str, copy_write: str, spec
         f, nf = _per_dispatch(fetch_csv, pattern, "FETCH_SIZE")
         w, nw = _per_dispatch(write_csv, pattern, "WRITE_SIZE")
         fb, wb = f * 1024 * f_scale, w * 1024 * w_scale
-        out[name] = {"kernels": pattern, "fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb,
+        out[name] = {"kernels": pattern.lstrip("*"), "fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb,
                      "dispatches": min(nf, nw)}
     open(out_json, "w").write(json.dumps(out, indent=1) + "\n")
 

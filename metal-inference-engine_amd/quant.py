@@ -7,6 +7,7 @@ Every BLOCK = 32 consecutive weights along a row share fp16 parameters (src/quan
 Blocks never cross rows, so stacking quantized matrices row-wise (fused QKV, gate+up) is exact. Quantizing is a
 one-time host step (loading a checkpoint); the matvec and dequantize run as HIP kernels (native/linear.hip).
 """
+import json
 from dataclasses import dataclass
 
 import torch
@@ -87,3 +88,41 @@ def concat_rows(parts: list):
     mins = torch.cat([p.mins for p in parts]) if parts[0].mins is not None else None
     return QuantTensor(parts[0].scheme, torch.cat([p.data for p in parts]), torch.cat([p.scales for p in parts]),
                        (sum(p.shape[0] for p in parts), parts[0].shape[1]), parts[0].block, mins)
+
+
+# The fused-weight groups of the INT4 precision policy (src/quant.py:92-98): checkpoint components and the fused
+# matrices they are stacked into share one group, so a stacked matrix gets a single scheme.
+POLICY_GROUPS = [
+    (("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+      "self_attn.qkvg.weight", "self_attn.qkv.weight"), "attn_in"),
+    (("mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.gate_up.weight"), "mlp_in"),
+    (("linear_attn.in_proj_qkv.weight", "linear_attn.in_proj_z.weight", "linear_attn.in_proj_b.weight",
+      "linear_attn.in_proj_a.weight", "linear_attn.in_proj.weight"), "linear_in"),
+]
+
+
+def policy_group(name: str) -> str:
+    """The policy id of a weight name (src/quant.py:101-112): the part from 'layers.' on, with a fused-group
+    member's suffix replaced by its group, so checkpoint and fused names of one matrix agree."""
+    i = name.find("layers.")
+    base = name[i:] if i >= 0 else name
+    for suffixes, group in POLICY_GROUPS:
+        for suf in suffixes:
+            if base.endswith(suf):
+                return base[: -len(suf)] + group
+    return base
+
+
+def scheme_for(name, scheme: str, keep_int8: frozenset = frozenset()) -> str:
+    """INT4 mode keeps the tied embedding / output head and the policy's groups at INT8 (src/quant.py:115-121)."""
+    if scheme == "int4" and name is not None and (
+            "embed_tokens" in name or policy_group(name) in {policy_group(k) for k in keep_int8}):
+        return "int8"
+    return scheme
+
+
+def load_policy(path) -> frozenset:
+    """The groups a configs/quant/<model>.json keeps at INT8 (src/quant.py:124-128); empty without a file."""
+    if not path:
+        return frozenset()
+    return frozenset(policy_group(n) for n in json.load(open(path))["keep_int8"])

@@ -41,6 +41,20 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return (x32 / rms) * weight.float()
 
 
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """LayerNorm without bias, src/ops.py:18-24: mean removed first, then weight * (centered * rsqrt(var + eps))."""
+    x32 = x.float()
+    centered = x32 - x32.mean(dim=-1, keepdim=True)
+    variance = centered.pow(2).mean(dim=-1, keepdim=True)
+    return weight.float() * (centered * torch.rsqrt(variance + eps))
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up with silu(g) = g / (1 + e^-g), src/ops.py:107-110."""
+    g = gate.float()
+    return (g / (1.0 + torch.exp(-g))) * up.float()
+
+
 def rope_inv_freq(theta: float, d: int) -> torch.Tensor:
     """1 / theta^(i / (d/2)) for i < d/2, fp32 on the CPU, src/ops.py:27-33."""
     half = d // 2

@@ -210,3 +210,23 @@ def test_linear_arguments_checked_on_host(lib):
     assert call(M=0) == 0
     assert lib.lib.rk_dequant_rows(fake, fake, 2, fake, None, None, 10, 5, 12, 2048, None) == 1
     assert "rows 10 + 5 of 12" in lib.last_error()
+
+
+def test_decode_ops_checked_on_host(lib):
+    fake = 4096
+    L = lib.lib
+    for fn in (L.rk_rms_norm, L.rk_layer_norm):
+        assert fn(fake, None, 0, 2048, fake, 0, 4, 2048, 1e-6, None) == 1                      # null x
+        assert fn(fake, fake, 5, 2048, fake, 0, 4, 2048, 1e-6, None) == 2                      # x dtype
+        assert fn(fake, fake, 0, 2048, fake, 0, 4, 2046, 1e-6, None) == 1                      # D % 4
+        assert fn(fake, fake, 0, 8192, fake, 0, 4, 8192, 1e-6, None) == 1                      # D > 4096
+        assert "4 .. 4096" in lib.last_error()
+        assert fn(fake, fake, 0, 1024, fake, 0, 4, 2048, 1e-6, None) == 1                      # stride < D
+        assert fn(fake + 4, fake, 0, 2048, fake, 0, 4, 2048, 1e-6, None) == 1                  # misaligned out
+        assert fn(fake, fake, 0, 2048, fake, 0, 0, 2048, 1e-6, None) == 0                      # no rows
+    assert L.rk_rope(fake, fake, fake, fake, 3, 2, 63, None) == 1 and "even" in lib.last_error()
+    assert L.rk_rope(fake, fake, None, fake, 3, 2, 64, None) == 1
+    assert L.rk_rope(fake, fake, fake, fake, 0, 2, 64, None) == 0
+    assert L.rk_silu_mul(fake, fake, 100, fake, 200, 4, 128, None) == 1 and "strides" in lib.last_error()
+    assert L.rk_silu_mul(fake, None, 256, fake, 256, 4, 128, None) == 1
+    assert L.rk_silu_mul(fake, fake, 256, fake, 256, 0, 128, None) == 0

@@ -323,3 +323,26 @@ def test_attention_prep_splits_norms_and_rotates():
     assert torch.equal(q[..., :rot], ops_ref.rope(qn[..., :rot], pos, 1e4))
     kn = ops_ref.rms_norm(y[:, Hq * d:(Hq + Hkv) * d].reshape(N, Hkv, d), kw, 1e-6)
     assert torch.equal(k[..., :rot], ops_ref.rope(kn[..., :rot], pos, 1e4))
+
+
+# ---------------------------------------------------------------- the rest of a decode step (src/ops.py:18-24, 107-110)
+
+def test_layer_norm_is_the_library_layer_norm():
+    """ops.layer_norm (no bias) == torch's layer_norm with that weight, to rounding; with weight 1 every row has mean
+    0 and variance 1 (up to eps) -- a dropped centering or a missing eps fails one of them."""
+    g_ = torch.Generator().manual_seed(41)
+    x, w = torch.randn(6, 2048, generator=g_) * 3 + 1.5, torch.randn(2048, generator=g_)
+    want = torch.nn.functional.layer_norm(x, (2048,), w, None, 1e-5)
+    assert rel_err(ops_ref.layer_norm(x, w, 1e-5), want) < 1e-6
+    y = ops_ref.layer_norm(x.double(), torch.ones(2048, dtype=torch.float64), 0.0)
+    assert y.mean(-1).abs().max() < 1e-6 and (y.var(-1, unbiased=False) - 1).abs().max() < 1e-5
+
+
+def test_silu_mul_is_the_library_silu():
+    """silu_mul == torch's silu(g) * u; silu(0) = 0, silu(g) -> g for large g, -> 0 for very negative g."""
+    g_ = torch.Generator().manual_seed(42)
+    g, u = torch.randn(5, 300, generator=g_) * 4, torch.randn(5, 300, generator=g_)
+    assert rel_err(ops_ref.silu_mul(g, u), torch.nn.functional.silu(g) * u) < 1e-6
+    edge = torch.tensor([0.0, 30.0, -30.0, -100.0])
+    out = ops_ref.silu_mul(edge, torch.ones(4))
+    assert out[0] == 0 and abs(out[1] - 30.0) < 1e-6 and abs(out[2]) < 1e-11 and out[3] == 0

@@ -67,3 +67,36 @@ def test_quantize_in_row_chunks_is_bit_identical(monkeypatch):
         parts = quant.quantize(w, scheme)
         monkeypatch.setattr(quant, "CHUNK", 1 << 24)
         assert torch.equal(parts.data, whole.data) and torch.equal(parts.scales, whole.scales)
+
+
+def test_policy_groups_and_int8_exceptions():
+    """The reference's own expectations for the INT4 precision policy (tests/test_quant.py:58-73 of the reference):
+    checkpoint component names and fused names map to one group; a kept fused tensor keeps all its components INT8;
+    the tied embedding stays INT8."""
+    ck = "model.language_model."
+    assert (quant.policy_group(ck + "layers.3.self_attn.q_proj.weight")
+            == quant.policy_group(ck + "layers.3.self_attn.k_proj.weight")
+            == quant.policy_group("layers.3.self_attn.qkvg.weight") == "layers.3.attn_in")
+    assert (quant.policy_group(ck + "layers.5.linear_attn.in_proj_z.weight")
+            == quant.policy_group("layers.5.linear_attn.in_proj.weight") == "layers.5.linear_in")
+    assert (quant.policy_group(ck + "layers.3.mlp.gate_proj.weight")
+            == quant.policy_group("layers.3.mlp.gate_up.weight") == "layers.3.mlp_in")
+    assert quant.policy_group(ck + "layers.3.mlp.down_proj.weight") == "layers.3.mlp.down_proj.weight"
+    assert (quant.policy_group("model.layers.3.self_attn.k_proj.weight")
+            == quant.policy_group("layers.3.self_attn.qkv.weight") == "layers.3.attn_in")
+    keep = frozenset({"layers.3.self_attn.qkvg.weight", "layers.0.linear_attn.in_proj.weight"})
+    kept = ({quant.scheme_for(f"{ck}layers.3.self_attn.{c}_proj.weight", "int4", keep) for c in "qkv"}
+            | {quant.scheme_for(f"{ck}layers.0.linear_attn.in_proj_{c}.weight", "int4", keep)
+               for c in ("qkv", "z", "b", "a")})
+    assert kept == {"int8"}
+    assert quant.scheme_for(ck + "layers.3.mlp.down_proj.weight", "int4", keep) == "int4"
+    assert quant.scheme_for("model.embed_tokens.weight", "int4") == "int8"
+    assert quant.scheme_for("model.embed_tokens.weight", "int8") == "int8"
+    assert quant.scheme_for(None, "int4") == "int4"
+
+
+def test_load_policy(tmp_path):
+    p = tmp_path / "policy.json"
+    p.write_text('{"keep_int8": ["model.language_model.layers.2.mlp.up_proj.weight"]}')
+    assert quant.load_policy(str(p)) == frozenset({"layers.2.mlp_in"})
+    assert quant.load_policy(None) == frozenset()
