@@ -667,12 +667,102 @@ def bench_linears(args, backend):
     }
 
 
+def bench_decode_step(args, backend):
+    """A whole Qwen3.5-2B decode step at batch 8 through RocmBackend (INT4 weights, INT8 tied embedding / head, the
+    reference's policy): the backend calls of Qwen3_5Model.decode_batch (src/models/qwen3_5.py:228-298) for 24 layers
+    (18 DeltaNet, 6 gated attention over bf16 paged KV with histories of 512-4096 positions) plus the head. Weights
+    are random codes / scales generated on the GPU (the values do not change the work); one step is captured in a
+    HIP graph and replayed (the sequences are not advanced, so every replay does the same work)."""
+    import dataclasses
+    import torch
+    import workloads as wl
+    from backend.rocm import RocmBackend
+    dev = backend.device
+    stream = torch.cuda.current_stream(dev)
+    be = RocmBackend(dev, scheme="int4")
+    cfg, B = wl.QWEN35_2B, 8
+    gen = torch.Generator().manual_seed(33)
+    lens = torch.randint(512, 4097, (B,), generator=gen).tolist()
+    log(f"[bench] ds: building the model and states on {dev}")
+    w = wl.random_device_weights(cfg, "int4", dev, seed=31)
+    st = wl.HybridDecodeState(cfg, lens, dev, seed=32)
+    layout = st.layout()
+    tokens = torch.randint(0, cfg.vocab, (B,), generator=gen).to(dev)
+    torch.cuda.synchronize()
+
+    def step():
+        wl.hybrid_decode_step(be, w, st, tokens, layout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ms = graph_time(step, max(1, args.steps // 5), stream)
+    n_full = sum(cfg.is_full(i) for i in range(cfg.layers))
+    wbytes = sum(t.nbytes if hasattr(t, "scheme") else 0 for t in w.values())
+    kv_bytes = n_full * sum(L + 1 for L in lens) * cfg.Hkv * cfg.d * 2 * 2
+    state_bytes = (cfg.layers - n_full) * B * (cfg.H * cfg.dk * cfg.dv * 4 * 2 + (cfg.conv_k - 1) * cfg.conv_dim * 4 * 2)
+    step_bytes = wbytes + kv_bytes + state_bytes
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] ds: {ms * 1e3:.1f} us per decode step at batch {B} ({B / (ms * 1e-3):.0f} tokens/s); "
+        f"{step_bytes / 1e9:.3f} GB per step (weights {wbytes / 1e9:.3f}, KV {kv_bytes / 1e6:.1f} MB, DeltaNet states "
+        f"{state_bytes / 1e6:.1f} MB): {gbs:.0f} GB/s = {gbs / HBM_PEAK_GBS:.1%}")
+    cpu = None
+    if not args.no_cpu:
+        # the oracle on the host: 4 of the 24 layers (3 DeltaNet + 1 attention) and the head, fp32 weights dequantized
+        # once (the reference's CPU path holds fp32 weights), scaled to the 24 layers
+        from oracle import decode_ref, ops_ref, quant_ref
+        torch.set_num_threads(cpu_threads())
+        cfg4 = dataclasses.replace(cfg, layers=4)
+        names = [n for n in wl.hybrid_weight_shapes(cfg4)]
+
+        def host(t):
+            if hasattr(t, "scheme"):
+                return quant_ref.dequantize(t.scheme, t.data.cpu(), t.scales.cpu(),
+                                            t.mins.cpu() if t.mins is not None else None)
+            return t.float().cpu()
+        wh = {n: host(w[n]) for n in names}
+        kh, vh = st.pool.kv.k.cpu(), st.pool.kv.v.cpu()
+        Sh, convh = st.pool.S.cpu(), st.pool.conv.cpu()
+        seq_index = torch.tensor([q.seq for q in st.seqs])
+        lay = [t.cpu() for t in layout]
+        tok = tokens.cpu()
+        h = torch.randn(B, cfg.hidden, generator=gen)
+
+        def run4():
+            decode_ref.hybrid_decode_step(cfg4, wh, kh, vh, Sh, convh, seq_index, st.slot, *lay, tok)
+
+        def head():
+            quant_ref.linear(ops_ref.rms_norm(h, wh["norm.weight"], cfg.eps), wh["embed_tokens.weight"])
+        t4, calls, total = cpu_time(run4)
+        th, _, _ = cpu_time(head)
+        t_step = th + (cfg.layers / 4) * (t4 - th)
+        cpu = {"value": B / t_step, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"the oracle's decode step over 4 of the 24 layers (3 DeltaNet + 1 attention) plus "
+                         f"embedding and head, fp32 weights: median {t4:.3f} s over {calls} calls ({total:.1f} s); "
+                         f"head alone {th:.3f} s; step = head + 6 x (4 layers)"}
+    return {
+        "metric": "decode step tokens/s @ batch 8 (Qwen3.5-2B, INT4 weights, whole step: 24 layers + head) + "
+                  "achieved HBM GB/s, 1 GPU",
+        "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random INT4 / INT8 codes and scales, seeded states and KV)",
+        "config": {"workload": "Qwen3.5-2B decode_batch at batch 8: 18 DeltaNet + 6 gated-attention layers, "
+                               "INT4 linears (INT8 tied head), bf16 paged KV, histories U[512, 4096]",
+                   "lens": lens, "step_bytes": step_bytes, "weight_bytes": wbytes, "kv_bytes": kv_bytes,
+                   "state_bytes": state_bytes},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": None, "kernel": "the whole step (97 linears, 6 paged decodes, 18 DeltaNet steps, "
+                                                "norms, SwiGLU)", "bytes_per_launch": step_bytes, "avg_ms": ms},
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd", "mv"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd", "mv", "ds"])
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (for counter collection)")
@@ -726,6 +816,8 @@ def main() -> int:
         rec = bench_attn_prep(args, backend)
     elif args.workload == "mv":
         rec = bench_linears(args, backend)
+    elif args.workload == "ds":
+        rec = bench_decode_step(args, backend)
     else:
         rec = bench_deltanet(args, backend)
     print(json.dumps(rec), flush=True)

@@ -396,3 +396,188 @@ def lp_linear_prefill(seed: int = 6) -> LinearPrefillCase:
     """The config-4 batch (4 x 4096 tokens, 16 heads x 128 x 128, conv 4 over 6144 channels) one step earlier: the
     fp32 in_proj output of a linear-attention layer, before conv, norms and the delta rule."""
     return linear_prefill_case([4096] * 4, seed=seed)
+
+
+# ---------------------------------------------------------------- a whole hybrid decode step (decode_batch)
+
+@dataclass
+class HybridConfig:
+    """Shapes of a Qwen3.5 hybrid stack (src/models/qwen3_5.py): every 4th layer (i % 4 == 3) full attention with
+    a sigmoid output gate and partial RoPE, the rest Gated DeltaNet; SwiGLU MLPs; tied embedding / head."""
+    layers: int
+    hidden: int
+    intermediate: int
+    vocab: int
+    Hq: int = HQ
+    Hkv: int = HKV
+    d: int = HEAD_DIM
+    rot: int = 64
+    theta: float = 1e7
+    H: int = DN_HEADS
+    dk: int = DN_DK
+    dv: int = DN_DV
+    conv_k: int = CONV_K
+    eps: float = 1e-6
+    block_size: int = BLOCK
+
+    def is_full(self, i: int) -> bool:
+        return i % 4 == 3
+
+    @property
+    def conv_dim(self) -> int:
+        return 2 * self.H * self.dk + self.H * self.dv
+
+    @property
+    def in_proj_rows(self) -> int:
+        return self.conv_dim + self.H * self.dv + 2 * self.H
+
+    @property
+    def qkvg_rows(self) -> int:
+        return (2 * self.Hq + 2 * self.Hkv) * self.d
+
+
+QWEN35_2B = HybridConfig(layers=24, hidden=2048, intermediate=6144, vocab=248320)
+
+
+def hybrid_weight_shapes(cfg: HybridConfig) -> dict:
+    """name -> shape of every weight, named as the reference's fused model tensors (so prepare() applies the same
+    per-tensor precision policy); norm weights are stored as (1 + w), as the model's _vec(one_plus=True) hands them
+    to the backend."""
+    s = {"embed_tokens.weight": (cfg.vocab, cfg.hidden), "norm.weight": (cfg.hidden,)}
+    for i in range(cfg.layers):
+        p = f"layers.{i}."
+        s[p + "input_layernorm.weight"] = (cfg.hidden,)
+        s[p + "post_attention_layernorm.weight"] = (cfg.hidden,)
+        s[p + "mlp.gate_up.weight"] = (2 * cfg.intermediate, cfg.hidden)
+        s[p + "mlp.down_proj.weight"] = (cfg.hidden, cfg.intermediate)
+        if cfg.is_full(i):
+            s[p + "self_attn.qkvg.weight"] = (cfg.qkvg_rows, cfg.hidden)
+            s[p + "self_attn.q_norm.weight"] = (cfg.d,)
+            s[p + "self_attn.k_norm.weight"] = (cfg.d,)
+            s[p + "self_attn.o_proj.weight"] = (cfg.hidden, cfg.Hq * cfg.d)
+        else:
+            s[p + "linear_attn.in_proj.weight"] = (cfg.in_proj_rows, cfg.hidden)
+            s[p + "linear_attn.conv1d.weight"] = (cfg.conv_dim, cfg.conv_k)
+            s[p + "linear_attn.A_log"] = (cfg.H,)
+            s[p + "linear_attn.dt_bias"] = (cfg.H,)
+            s[p + "linear_attn.norm.weight"] = (cfg.dv,)
+            s[p + "linear_attn.out_proj.weight"] = (cfg.hidden, cfg.H * cfg.dv)
+    return s
+
+
+def hybrid_weights(cfg: HybridConfig, seed: int = 0) -> dict:
+    """Seeded fp32 host weights of the stack (random init at the scale of a trained model's)."""
+    gen = torch.Generator().manual_seed(seed)
+    out = {}
+    for name, shape in hybrid_weight_shapes(cfg).items():
+        if name.endswith(("layernorm.weight", "norm.weight", "q_norm.weight", "k_norm.weight")):
+            w = 1.0 + 0.1 * torch.randn(shape, generator=gen)
+        elif name.endswith("conv1d.weight"):
+            w = 0.5 * torch.randn(shape, generator=gen)
+        elif name.endswith(("A_log", "dt_bias")):
+            w = 0.5 * torch.randn(shape, generator=gen)
+        else:
+            w = torch.randn(shape, generator=gen) / math.sqrt(shape[1])
+        out[name] = w
+    return out
+
+
+def random_device_weights(cfg: HybridConfig, scheme: str, dev, seed: int = 0) -> dict:
+    """The same names and shapes drawn directly in the device format (random codes and fp16 scales for the 2-D
+    weights, INT8 for the tied embedding in INT4 mode, per the reference's policy), for models too large to draw in
+    fp32 on the host: a bandwidth workload, where the values do not change the work."""
+    from quant import BLOCK as QB, QuantTensor, scheme_for
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    out = {}
+    for name, shape in hybrid_weight_shapes(cfg).items():
+        if len(shape) == 2 and shape[1] % QB == 0 and not name.endswith("conv1d.weight"):
+            N, K = shape
+            sch = scheme_for(name, scheme)
+            if sch == "int8":
+                data = torch.randint(-127, 128, (N, K), generator=gen, device=dev, dtype=torch.int8)
+            else:
+                data = torch.randint(0, 256, (N, K // 2), generator=gen, device=dev, dtype=torch.uint8)
+            scale = 2.0 / (127 if sch == "int8" else 15) / math.sqrt(K)
+            scales = (torch.rand(N, K // QB, generator=gen, device=dev) * scale + 0.5 * scale).to(torch.float16)
+            mins = (-7.5 * scales.float()).to(torch.float16) if sch == "int4" else None
+            out[name] = QuantTensor(sch, data, scales, (N, K), QB, mins)
+        else:
+            t = torch.randn(shape, generator=gen, device=dev)
+            out[name] = 1.0 + 0.1 * t if name.endswith("norm.weight") else 0.5 * t
+    return out
+
+
+class HybridDecodeState:
+    """The sequences of one decode batch in the reference's pools: a PagedKVPool layer per attention layer (bf16)
+    and a HybridPool slot per sequence (S and conv tails of every DeltaNet layer), with histories of `lens`
+    positions already written (seeded random K / V, S ~ N(0, 0.02^2), tails ~ N(0, 1))."""
+
+    def __init__(self, cfg: HybridConfig, lens: list[int], device, seed: int = 0, kv_dtype=torch.bfloat16):
+        from state import HybridPool, PagedKVPool
+        self.cfg = cfg
+        n_full = sum(cfg.is_full(i) for i in range(cfg.layers))
+        n_linear = cfg.layers - n_full
+        bs = cfg.block_size
+        num_blocks = sum(math.ceil((L + 1) / bs) for L in lens) + 1
+        kv = PagedKVPool(n_full, cfg.Hkv, cfg.d, num_blocks, bs, device=device, dtype=kv_dtype)
+        self.pool = HybridPool(kv, len(lens), n_linear, cfg.H, cfg.dk, cfg.dv, cfg.conv_dim, cfg.conv_k, device)
+        self.seqs = [self.pool.new_sequence() for _ in lens]
+        gen = torch.Generator().manual_seed(seed)
+        for st, L in zip(self.seqs, lens):
+            st.reserve(L + 1)
+            st.kv.length = L
+        kv.k.copy_(torch.randn(kv.k.shape, generator=gen).to(kv_dtype))
+        kv.v.copy_(torch.randn(kv.v.shape, generator=gen).to(kv_dtype))
+        self.pool.S.copy_(0.02 * torch.randn(self.pool.S.shape, generator=gen))
+        self.pool.conv.copy_(torch.randn(self.pool.conv.shape, generator=gen))
+        # layer slots: attention layers index the KV pool, DeltaNet layers the state pool (the model's self.slot)
+        self.slot, nf, nl = [], 0, 0
+        for i in range(cfg.layers):
+            self.slot.append(nf if cfg.is_full(i) else nl)
+            nf, nl = nf + cfg.is_full(i), nl + (not cfg.is_full(i))
+
+    def layout(self):
+        """One step's KV layout (src/models/qwen3_5.py:237-245): write slots, tables, lengths after the step, and
+        the positions of the new tokens."""
+        from state import to_device
+        starts = [st.length for st in self.seqs]
+        kvs = [st.kv for st in self.seqs]
+        blocks, offsets, tables, lens = self.pool.kv.batch_layout(kvs, starts)
+        slots = blocks * self.cfg.block_size + offsets
+        positions = to_device(torch.tensor(starts, dtype=torch.int32), self.pool.S.device)
+        return slots, tables, lens, positions
+
+
+def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Tensor, layout) -> torch.Tensor:
+    """One decode step for the batch through the backend protocol, in the order of Qwen3_5Model.decode_batch
+    (src/models/qwen3_5.py:228-298) -> logits [B, vocab] fp32. The attention layer's q / k norms, partial RoPE and
+    KV write are the one fused attention_prep call, and the output gate is fused into paged_attention; the
+    sequences' lengths are not advanced (a benchmark replays the same step)."""
+    cfg = st.cfg
+    B = tokens.shape[0]
+    slots, tables, lens, positions = layout
+    kv = st.pool.kv
+    h = backend.embedding(w["embed_tokens.weight"], tokens)
+    for i in range(cfg.layers):
+        p = f"layers.{i}."
+        x = backend.rms_norm(h, w[p + "input_layernorm.weight"], cfg.eps)
+        L = st.slot[i]
+        if cfg.is_full(i):
+            a = p + "self_attn."
+            y = backend.linear(x, w[a + "qkvg.weight"])
+            q, gate = backend.attention_prep(y, w[a + "q_norm.weight"], w[a + "k_norm.weight"], cfg.eps, positions,
+                                             cfg.theta, cfg.rot, (cfg.Hq, cfg.Hkv, cfg.d), kv.k[L], kv.v[L], slots)
+            o = backend.paged_attention(q, kv.k[L], kv.v[L], tables, lens, cfg.block_size, gate=gate)
+            h = backend.linear(o.reshape(B, cfg.Hq * cfg.d), w[a + "o_proj.weight"], residual=h)
+        else:
+            a = p + "linear_attn."
+            y = backend.linear(x, w[a + "in_proj.weight"])
+            C, Z, H = cfg.conv_dim, cfg.H * cfg.dv, cfg.H
+            o = backend.deltanet_decode_batch(y[:, :C], y[:, C:C + Z], y[:, C + Z:C + Z + H], y[:, C + Z + H:],
+                                              st.seqs, L, w[a + "conv1d.weight"], w[a + "A_log"], w[a + "dt_bias"],
+                                              w[a + "norm.weight"], cfg.eps, (H, cfg.dk, cfg.dv, H * cfg.dk))
+            h = backend.linear(o, w[a + "out_proj.weight"], residual=h)
+        x = backend.rms_norm(h, w[p + "post_attention_layernorm.weight"], cfg.eps)
+        h = backend.linear(backend.swiglu(x, w[p + "mlp.gate_up.weight"]), w[p + "mlp.down_proj.weight"], residual=h)
+    h = backend.rms_norm(h, w["norm.weight"], cfg.eps)
+    return backend.linear(h, w["embed_tokens.weight"])
