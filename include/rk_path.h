@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 6
+#define RK_ABI_VERSION 7
 
 /* status codes */
 #define RK_OK 0
@@ -86,14 +86,15 @@ int rk_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_poo
  * RMSNorm). Replaces MetalBackend.deltanet_decode_batch + conv_step + gdn_decode (src/backend/metal.py:232-256;
  * src/kernels/deltanet.metal:9-92) with the semantics of TorchBackend.deltanet_decode(_batch)
  * (src/backend/torch_ref.py:61-73, 90-93).
- *   out [B, H*dv] fp32; qkv [B, C] fp32 (C = 2*H*dk + H*dv, pre-conv); z [B, H*dv]; b, a [B, H]
+ *   out [B, H*dv] fp32; qkv [B, C] fp32 (C = 2*H*dk + H*dv, pre-conv), z [B, H*dv], b, a [B, H], row i of each at
+ *   qkv + i*qkv_ld, z + i*z_ld, b / a + i*ba_ld (the column slices of one in_proj output row, read in place)
  *   conv_state [seqs, n_linear, K-1, C] fp32 and S [seqs, n_linear, H, dk, dv] fp32, both updated in place at
  *   [seq_index[i], slot]; conv_w [C, K]; A_log, dt_bias [H]; norm_w [dv]; seq_index [B] int32.
  * dk = dv = 128, K = 4. */
-int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float* b, const float* a,
-                       float* conv_state, float* S, const float* conv_w, const float* A_log, const float* dt_bias,
-                       const float* norm_w, const int32_t* seq_index, int B, int H, int dk, int dv, int conv_k,
-                       int n_linear, int slot, float eps, void* stream);
+int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float* b, const float* a, long long qkv_ld,
+                       long long z_ld, long long ba_ld, float* conv_state, float* S, const float* conv_w,
+                       const float* A_log, const float* dt_bias, const float* norm_w, const int32_t* seq_index, int B,
+                       int H, int dk, int dv, int conv_k, int n_linear, int slot, float eps, void* stream);
 
 /* ---- P4: packed (varlen) prefill attention over the paged pool, with the KV write-back of the new tokens.
  * Replaces, per packed segment, the model's kv.write -> kv.read -> attention(causal) -> * sigmoid(gate) sequence

@@ -37,12 +37,16 @@ __global__ __launch_bounds__(256) void row_norm_kernel(float* __restrict__ out, 
     const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;                        // whole waves leave: no barrier below
     const int nv = D >> 2;                          // 4-float chunks in the row
-    f32x4 v[MAXV];
+    f32x4 v[MAXV], wv[MAXV];
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {                // the row and the weights requested together: one round trip
+        const int c = lane + 64 * i;
+        v[i] = c < nv ? ld4(x, row * ld + 4 * c, x_dtype) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        wv[i] = c < nv ? ld4(w, 4 * c, w_dtype) : (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < MAXV; ++i) {
-        const int c = lane + 64 * i;
-        v[i] = c < nv ? ld4(x, row * ld + 4 * c, x_dtype) : (f32x4){0.f, 0.f, 0.f, 0.f};
         if constexpr (KIND == 0) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) s = __fadd_rn(s, __fmul_rn(v[i][e], v[i][e]));
@@ -75,12 +79,11 @@ __global__ __launch_bounds__(256) void row_norm_kernel(float* __restrict__ out, 
     for (int i = 0; i < MAXV; ++i) {
         const int c = lane + 64 * i;
         if (c < nv) {
-            const f32x4 wv = ld4(w, 4 * c, w_dtype);
             f32x4 o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if constexpr (KIND == 0) o[e] = __fmul_rn(__fdiv_rn(v[i][e], scale), wv[e]);
-                else o[e] = __fmul_rn(wv[e], __fmul_rn(__fsub_rn(v[i][e], mean), scale));
+                if constexpr (KIND == 0) o[e] = __fmul_rn(__fdiv_rn(v[i][e], scale), wv[i][e]);
+                else o[e] = __fmul_rn(wv[i][e], __fmul_rn(__fsub_rn(v[i][e], mean), scale));
             }
             *reinterpret_cast<f32x4*>(out + row * D + 4 * c) = o;
         }

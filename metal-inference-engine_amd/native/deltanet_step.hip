@@ -27,6 +27,7 @@ struct StepArgs {
     const float* z;
     const float* b;
     const float* a;
+    long long qkv_ld, z_ld, ba_ld;   // row strides (elements) of qkv, z, and b / a: column slices of one projection
     float* conv;
     float* S;
     const float* conv_w;
@@ -52,12 +53,12 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     // load issued after the state stores could only be waited for together with them
     const int part = t / kDK, j = t % kDK;
     const int c = part == 0 ? h * kDK + j : (part == 1 ? H * kDK + h * kDK + j : 2 * H * kDK + h * kDV + (j & (kDV - 1)));
-    const float x = t < 3 * kDK ? p.qkv[(long long)bi * C + c] : 0.0f;
+    const float x = t < 3 * kDK ? p.qkv[(long long)bi * p.qkv_ld + c] : 0.0f;
     const float4 w = t < 3 * kDK ? *reinterpret_cast<const float4*>(p.conv_w + (long long)c * kTaps)
                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float b_in = p.b[(long long)bi * H + h], a_in = p.a[(long long)bi * H + h];
+    const float b_in = p.b[(long long)bi * p.ba_ld + h], a_in = p.a[(long long)bi * p.ba_ld + h];
     const float dtb = p.dt_bias[h], alog = p.A_log[h];
-    const float zj = t < kDV ? p.z[(long long)bi * H * kDV + h * kDV + t] : 0.0f;
+    const float zj = t < kDV ? p.z[(long long)bi * p.z_ld + h * kDV + t] : 0.0f;
     const float nw = t < kDV ? p.norm_w[t] : 0.0f;
     const long long seq = p.seq[bi];
     float* Sh = p.S + (((seq * p.n_linear + p.slot) * H + h) * kDK) * kDV;
@@ -174,10 +175,10 @@ using namespace rk;
 
 extern "C" {
 
-int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float* b, const float* a,
-                       float* conv_state, float* S, const float* conv_w, const float* A_log, const float* dt_bias,
-                       const float* norm_w, const int32_t* seq_index, int B, int H, int dk, int dv, int conv_k,
-                       int n_linear, int slot, float eps, void* stream) {
+int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float* b, const float* a, long long qkv_ld,
+                       long long z_ld, long long ba_ld, float* conv_state, float* S, const float* conv_w,
+                       const float* A_log, const float* dt_bias, const float* norm_w, const int32_t* seq_index, int B,
+                       int H, int dk, int dv, int conv_k, int n_linear, int slot, float eps, void* stream) {
     if (!out || !qkv || !z || !b || !a || !conv_state || !S || !conv_w || !A_log || !dt_bias || !norm_w || !seq_index)
         return fail(RK_ERR_ARG, "rk_deltanet_decode: null pointer");
     if (B < 1 || H < 1 || n_linear < 1 || slot < 0 || slot >= n_linear)
@@ -185,8 +186,12 @@ int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float
     if (dk != kDK || dv != kDV || conv_k != kTaps)
         return fail(RK_ERR_UNSUPPORTED, "rk_deltanet_decode: dk %d dv %d conv kernel %d (built for 128/128/4)", dk, dv,
                     conv_k);
+    if (qkv_ld < 2LL * H * dk + (long long)H * dv || z_ld < (long long)H * dv || ba_ld < H)
+        return fail(RK_ERR_ARG, "rk_deltanet_decode: row strides qkv %lld, z %lld, b / a %lld below the rows", qkv_ld,
+                    z_ld, ba_ld);
     StepArgs p;
-    p.out = out; p.qkv = qkv; p.z = z; p.b = b; p.a = a; p.conv = conv_state; p.S = S; p.conv_w = conv_w;
+    p.out = out; p.qkv = qkv; p.z = z; p.b = b; p.a = a; p.qkv_ld = qkv_ld; p.z_ld = z_ld; p.ba_ld = ba_ld;
+    p.conv = conv_state; p.S = S; p.conv_w = conv_w;
     p.A_log = A_log; p.dt_bias = dt_bias; p.norm_w = norm_w; p.seq = seq_index;
     p.B = B; p.H = H; p.C = 2 * H * dk + H * dv; p.n_linear = n_linear; p.slot = slot; p.eps = eps;
     hipLaunchKernelGGL(deltanet_step_kernel, dim3(B * H), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);

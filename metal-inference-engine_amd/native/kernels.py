@@ -158,12 +158,19 @@ def deltanet_decode(qkv, z, b, a, conv_state, S, seq_index, slot: int, conv_w, A
     dev = _need_cuda(name, qkv, S, conv_state)
     _contig(name, S, "S"); _contig(name, conv_state, "conv_state")
     f = lambda t: t.to(device=dev, dtype=torch.float32).contiguous()
-    qkv, z, b, a = f(qkv), f(z), f(b), f(a)
+    # qkv / z / b / a are read in place with their row strides (column slices of one in_proj output row: no copies)
+    rowwise = lambda t: t if t.dtype == torch.float32 and t.device == dev and t.stride(-1) == 1 else f(t)
+    qkv, z, b, a = rowwise(qkv), rowwise(z), rowwise(b), rowwise(a)
+    if z.shape != (B, H * dv) or b.shape != (B, H) or a.shape != (B, H):
+        raise ValueError(f"{name}: z {tuple(z.shape)}, b {tuple(b.shape)}, a {tuple(a.shape)} for batch {B}, {H} heads")
+    ld = lambda t: t.stride(0) if t.shape[0] > 1 else t.shape[1]     # a 1-row view's stride is arbitrary
+    if ld(b) != ld(a):
+        b, a = b.contiguous(), a.contiguous()
     conv_w, A_log, dt_bias, norm_w = f(conv_w), f(A_log), f(dt_bias), f(norm_w)
     seq_index = seq_index.to(device=dev, dtype=torch.int32).contiguous()
     out = torch.empty(B, H * dv, dtype=torch.float32, device=dev)
     load().call("rk_deltanet_decode", out.data_ptr(), qkv.data_ptr(), z.data_ptr(), b.data_ptr(), a.data_ptr(),
-                conv_state.data_ptr(), S.data_ptr(), conv_w.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(),
+                ld(qkv), ld(z), ld(b), conv_state.data_ptr(), S.data_ptr(), conv_w.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(),
                 norm_w.data_ptr(), seq_index.data_ptr(), B, H, dk, dv, K, n_linear, int(slot), float(eps),
                 _stream(dev))
     return out

@@ -653,17 +653,20 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 // tiles [P[b], P[b + 1]); the split workgroups whose ranges meet it are w_first = the one holding tile P[b] ..
 // w_last = the one holding tile P[b + 1] - 1 (empty ranges in between, possible only when NW > U, are skipped),
 // with partials in slots w + b. The gate is requested with the plan; the partials are combined in workgroup order,
-// up to kMergeCh per memory round trip (every load of a chunk is issued before any is used), with a running
-// maximum: M' = max(M, m_w), num = num 2^(M - M') + sum_w 2^(m_w - M') acc_w, den likewise with l_w;
-// out = num / den.
+// up to kMergeCh (8, or 32 / float4 outputs per thread) per memory round trip (every load of a chunk is issued
+// before any is used), with a running maximum: M' = max(M, m_w), num = num 2^(M - M') + sum_w 2^(m_w - M') acc_w,
+// den likewise with l_w; out = num / den.
 constexpr int kMergeThreads = 256;
-constexpr int kMergeCh = 8;
 
-template <int D, int GP>
+template <int D, int GP, bool WIDE>
 __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a) {
     constexpr int kT = kMergeThreads;
     constexpr int NO = (GP * D / 4 + kT - 1) / kT;   // float4 outputs per thread (upper bound)
     constexpr int REC = GP * D + 2 * GP;
+    // partials combined per memory round trip. WIDE (many split workgroups per sequence: small batches over long
+    // sequences give each dozens of partials): 32 / NO, within ~210 registers, one or two round trips; else 8, at
+    // a lighter register budget
+    constexpr int kMergeCh = WIDE ? 32 / NO : 8;
     __shared__ int P[kMaxBatch + 1];
     const int tid = threadIdx.x;
     const int b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
@@ -798,15 +801,27 @@ int split_lds_bytes(int B, int Hkv, int D, int GP, int NG) {
     return seq_lds_bytes(B) + NG * Hkv * per_wave + kStash * NG * Hkv * (GP * D + 2 * GP) * 4;
 }
 
-MergeFn pick_merge(int D, int GP) {
+MergeFn pick_merge(int D, int GP, bool wide) {
+    if (wide) {
+        if (GP == 4) {
+            if (D == 64) return paged_decode_merge<64, 4, true>;
+            if (D == 128) return paged_decode_merge<128, 4, true>;
+            if (D == 256) return paged_decode_merge<256, 4, true>;
+        } else {
+            if (D == 64) return paged_decode_merge<64, 8, true>;
+            if (D == 128) return paged_decode_merge<128, 8, true>;
+            if (D == 256) return paged_decode_merge<256, 8, true>;
+        }
+        return nullptr;
+    }
     if (GP == 4) {
-        if (D == 64) return paged_decode_merge<64, 4>;
-        if (D == 128) return paged_decode_merge<128, 4>;
-        if (D == 256) return paged_decode_merge<256, 4>;
+        if (D == 64) return paged_decode_merge<64, 4, false>;
+        if (D == 128) return paged_decode_merge<128, 4, false>;
+        if (D == 256) return paged_decode_merge<256, 4, false>;
     } else {
-        if (D == 64) return paged_decode_merge<64, 8>;
-        if (D == 128) return paged_decode_merge<128, 8>;
-        if (D == 256) return paged_decode_merge<256, 8>;
+        if (D == 64) return paged_decode_merge<64, 8, false>;
+        if (D == 128) return paged_decode_merge<128, 8, false>;
+        if (D == 256) return paged_decode_merge<256, 8, false>;
     }
     return nullptr;
 }
@@ -906,7 +921,8 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
         hipLaunchKernelGGL(fn, dim3(NW), dim3(64 * a.NG * Hkv), lds, s, a);
         return check_launch("paged_decode_split");
     }
-    hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
+    // more than 8 split workgroups per sequence on average: the wide-chunk merge
+    hipLaunchKernelGGL(pick_merge(D, GP, NW > 8 * B), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
     return check_launch("paged_decode_merge");
 }
 

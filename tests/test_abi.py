@@ -81,10 +81,12 @@ def test_unsupported_shapes_are_refused(lib):
     rc = lib.lib.rk_paged_decode(fake, fake, fake, fake, 1, fake, fake, 1, 8, 2, 256, 16, 1, 1, 0, fake, 8 * 256 + 2,
                                  fake, 1 << 20, None)
     assert rc == 1 and "gate rows" in lib.last_error()
-    args = [fake] * 12 + [8, 16, 64, 64, 4, 1, 0, ctypes.c_float(1e-6), None]
+    args = [fake] * 5 + [6144, 2048, 16] + [fake] * 7 + [8, 16, 64, 64, 4, 1, 0, ctypes.c_float(1e-6), None]
     assert lib.lib.rk_deltanet_decode(*args) == 2 and "dk 64" in lib.last_error()
-    args = [fake] * 12 + [8, 16, 128, 128, 4, 2, 2, ctypes.c_float(1e-6), None]
+    args = [fake] * 5 + [6144, 2048, 16] + [fake] * 7 + [8, 16, 128, 128, 4, 2, 2, ctypes.c_float(1e-6), None]
     assert lib.lib.rk_deltanet_decode(*args) == 1 and "slot 2" in lib.last_error()
+    args = [fake] * 5 + [6143, 2048, 16] + [fake] * 7 + [8, 16, 128, 128, 4, 2, 0, ctypes.c_float(1e-6), None]
+    assert lib.lib.rk_deltanet_decode(*args) == 1 and "row strides" in lib.last_error()
 
 
 def test_too_small_workspace_is_refused(lib):
