@@ -669,7 +669,7 @@ def bench_linears(args, backend):
 
 def bench_decode_step(args, backend):
     """A whole Qwen3.5-2B decode step at batch 8 through RocmBackend (INT4 weights, INT8 tied embedding / head, the
-    reference's policy): the backend calls of Qwen3_5Model.decode_batch (src/models/qwen3_5.py:228-298) for 24 layers
+    reference's policy): the backend calls of Qwen3_5Model.decode_batch (src/models/qwen3_5.py:228-290) for 24 layers
     (18 DeltaNet, 6 gated attention over bf16 paged KV with histories of 512-4096 positions) plus the head. Weights
     are random codes / scales generated on the GPU (the values do not change the work); one step is captured in a
     HIP graph and replayed (the sequences are not advanced, so every replay does the same work)."""

@@ -550,7 +550,7 @@ class HybridDecodeState:
 
 def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Tensor, layout) -> torch.Tensor:
     """One decode step for the batch through the backend protocol, in the order of Qwen3_5Model.decode_batch
-    (src/models/qwen3_5.py:228-298) -> logits [B, vocab] fp32. The attention layer's q / k norms, partial RoPE and
+    (src/models/qwen3_5.py:228-290) -> logits [B, vocab] fp32. The attention layer's q / k norms, partial RoPE and
     KV write are the one fused attention_prep call, and the output gate is fused into paged_attention; the
     sequences' lengths are not advanced (a benchmark replays the same step)."""
     cfg = st.cfg

@@ -1,5 +1,5 @@
 """fp32 CPU restatement of one hybrid decode step, the sequence of backend calls of Qwen3_5Model.decode_batch
-(src/models/qwen3_5.py:228-298), on the oracle's functions. TEST INFRASTRUCTURE ONLY.
+(src/models/qwen3_5.py:228-290), on the oracle's functions. TEST INFRASTRUCTURE ONLY.
 
 Each backend call is replaced by its oracle counterpart: embedding rows, rms_norm (ops.rms_norm), the projections
 (x @ w.T (+ residual) in fp32 on the dequantized weights), the attention layer's q / k norms + partial RoPE

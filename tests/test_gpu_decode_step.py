@@ -1,5 +1,5 @@
 """A whole hybrid decode step through RocmBackend -- the sequence of backend calls of Qwen3_5Model.decode_batch
-(src/models/qwen3_5.py:228-298): embedding, per layer RMSNorm, the attention layer (qkvg projection, fused q / k norm
+(src/models/qwen3_5.py:228-290): embedding, per layer RMSNorm, the attention layer (qkvg projection, fused q / k norm
 + partial RoPE + KV write, paged attention with the fused gate, o_proj + residual) or the DeltaNet layer (in_proj,
 batched recurrent step on the pool's states, out_proj + residual), RMSNorm and the SwiGLU MLP, then the final norm
 and the tied head -- against the same composition on the oracle (oracle/decode_ref.py), on a small 4-layer stack
