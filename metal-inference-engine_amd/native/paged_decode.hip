@@ -653,20 +653,17 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 // tiles [P[b], P[b + 1]); the split workgroups whose ranges meet it are w_first = the one holding tile P[b] ..
 // w_last = the one holding tile P[b + 1] - 1 (empty ranges in between, possible only when NW > U, are skipped),
 // with partials in slots w + b. The gate is requested with the plan; the partials are combined in workgroup order,
-// up to kMergeCh (8, or 32 / float4 outputs per thread) per memory round trip (every load of a chunk is issued
-// before any is used), with a running maximum: M' = max(M, m_w), num = num 2^(M - M') + sum_w 2^(m_w - M') acc_w,
-// den likewise with l_w; out = num / den.
+// up to kMergeCh per memory round trip (every load of a chunk is issued before any is used, with no branch between
+// them), with a running maximum: M' = max(M, m_w), num = num 2^(M - M') + sum_w 2^(m_w - M') acc_w, den likewise
+// with l_w; out = num / den.
 constexpr int kMergeThreads = 256;
 
-template <int D, int GP, bool WIDE>
+template <int D, int GP>
 __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a) {
     constexpr int kT = kMergeThreads;
     constexpr int NO = (GP * D / 4 + kT - 1) / kT;   // float4 outputs per thread (upper bound)
     constexpr int REC = GP * D + 2 * GP;
-    // partials combined per memory round trip. WIDE (many split workgroups per sequence: small batches over long
-    // sequences give each dozens of partials): 32 / NO, within ~210 registers, one or two round trips; else 8, at
-    // a lighter register budget
-    constexpr int kMergeCh = WIDE ? 32 / NO : 8;
+    constexpr int kMergeCh = 8;                       // partials combined per memory round trip
     __shared__ int P[kMaxBatch + 1];
     const int tid = threadIdx.x;
     const int b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
@@ -703,30 +700,29 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
         den[k] = 0.0f;
         num[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    // a workgroup's range can be empty only when there are more split workgroups than tiles; otherwise every
+    // workgroup in [wf, wlast] holds a partial, and no range has to be recomputed per partial
+    const bool sparse = a.NW > U;
     for (int w0 = wf; w0 <= wlast; w0 += kMergeCh) {
         float4 v[kMergeCh][NO];
         float mj[kMergeCh][NO], lj[kMergeCh][NO];
         bool use[kMergeCh];
+        // every load of the chunk first, without branches: slots past wlast re-read wlast's partial (unused)
+#pragma unroll
+        for (int j = 0; j < kMergeCh; ++j) {
+            const int wj = min(w0 + j, wlast);
+            const float* base = a.part + ((long long)(wj + b) * a.Hkv + kvh) * REC;
+#pragma unroll
+            for (int k = 0; k < NO; ++k) {
+                v[j][k] = *reinterpret_cast<const float4*>(base + off[k]);
+                mj[j][k] = base[GP * D + hk[k]];
+                lj[j][k] = base[GP * D + GP + hk[k]];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < kMergeCh; ++j) {
             const int wj = w0 + j;
-            use[j] = wj <= wlast && range_lo(U, a.NW, wj + 1) > range_lo(U, a.NW, wj);
-            if (wj <= wlast) {                       // uniform: loads past the sequence's last partial are skipped
-                const float* base = a.part + ((long long)(wj + b) * a.Hkv + kvh) * REC;
-#pragma unroll
-                for (int k = 0; k < NO; ++k) {
-                    v[j][k] = *reinterpret_cast<const float4*>(base + off[k]);
-                    mj[j][k] = base[GP * D + hk[k]];
-                    lj[j][k] = base[GP * D + GP + hk[k]];
-                }
-            } else {
-#pragma unroll
-                for (int k = 0; k < NO; ++k) {
-                    v[j][k] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    mj[j][k] = -INFINITY;
-                    lj[j][k] = 0.0f;
-                }
-            }
+            use[j] = wj <= wlast && (!sparse || range_lo(U, a.NW, wj + 1) > range_lo(U, a.NW, wj));
         }
 #pragma unroll
         for (int k = 0; k < NO; ++k) {
@@ -801,27 +797,15 @@ int split_lds_bytes(int B, int Hkv, int D, int GP, int NG) {
     return seq_lds_bytes(B) + NG * Hkv * per_wave + kStash * NG * Hkv * (GP * D + 2 * GP) * 4;
 }
 
-MergeFn pick_merge(int D, int GP, bool wide) {
-    if (wide) {
-        if (GP == 4) {
-            if (D == 64) return paged_decode_merge<64, 4, true>;
-            if (D == 128) return paged_decode_merge<128, 4, true>;
-            if (D == 256) return paged_decode_merge<256, 4, true>;
-        } else {
-            if (D == 64) return paged_decode_merge<64, 8, true>;
-            if (D == 128) return paged_decode_merge<128, 8, true>;
-            if (D == 256) return paged_decode_merge<256, 8, true>;
-        }
-        return nullptr;
-    }
+MergeFn pick_merge(int D, int GP) {
     if (GP == 4) {
-        if (D == 64) return paged_decode_merge<64, 4, false>;
-        if (D == 128) return paged_decode_merge<128, 4, false>;
-        if (D == 256) return paged_decode_merge<256, 4, false>;
+        if (D == 64) return paged_decode_merge<64, 4>;
+        if (D == 128) return paged_decode_merge<128, 4>;
+        if (D == 256) return paged_decode_merge<256, 4>;
     } else {
-        if (D == 64) return paged_decode_merge<64, 8, false>;
-        if (D == 128) return paged_decode_merge<128, 8, false>;
-        if (D == 256) return paged_decode_merge<256, 8, false>;
+        if (D == 64) return paged_decode_merge<64, 8>;
+        if (D == 128) return paged_decode_merge<128, 8>;
+        if (D == 256) return paged_decode_merge<256, 8>;
     }
     return nullptr;
 }
@@ -921,8 +905,7 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
         hipLaunchKernelGGL(fn, dim3(NW), dim3(64 * a.NG * Hkv), lds, s, a);
         return check_launch("paged_decode_split");
     }
-    // more than 8 split workgroups per sequence on average: the wide-chunk merge
-    hipLaunchKernelGGL(pick_merge(D, GP, NW > 8 * B), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
+    hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
     return check_launch("paged_decode_merge");
 }
 
