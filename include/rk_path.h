@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 7
+#define RK_ABI_VERSION 8
 
 /* status codes */
 #define RK_OK 0
@@ -200,6 +200,20 @@ int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w,
                    size_t partial_bytes, uint32_t* counters, int n_counters, void* stream);
 int rk_dequant_rows(float* out, const void* w, int w_type, const void* scales, const void* mins,
                     const int32_t* rows, int row0, int n_rows, int N, int K, void* stream);
+
+/* rk_linear_rows_ex: rk_linear_rows with the row stride x_ld of x and an optional input transform applied while x
+ * is staged. RK_X_SILU_MUL: x -> (x / (1 + exp(-x))) * up, up rows at aux + m * aux_ld (ops.silu_mul,
+ * src/ops.py:107-110, with the hardware exp2 and reciprocal): SwiGLU's down projection reading the gate / up halves
+ * of the gate_up output in place, one launch instead of silu_mul then linear (src/models/qwen3_5.py:166-170;
+ * MetalBackend.swiglu / silu_mul / linear, src/backend/metal.py:55-157, 225-230); results equal that composition
+ * within 1e-5. The transform needs M <= 8 and K % 256 == 0 (else RK_ERR_UNSUPPORTED: apply it first).
+ * rk_linear_rows(...) == rk_linear_rows_ex(y, x, K, RK_X_PLAIN, NULL, 0, ...). */
+#define RK_X_PLAIN 0
+#define RK_X_SILU_MUL 1
+int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const float* aux, long long aux_ld, int M,
+                      int N, int K, const void* w, int w_type, const void* scales, const void* mins,
+                      const float* bias, const float* residual, float* partials, size_t partial_bytes,
+                      uint32_t* counters, int n_counters, void* stream);
 
 /* ---- the rest of a decode step (native/decode_ops.hip): the row norms, RoPE and SwiGLU's silu * up
  * Replace Backend.rms_norm / layer_norm / rope / silu_mul (src/backend/base.py:26-40, the protocol's v1 and v3

@@ -24,6 +24,8 @@ Method -> kernel:
   linear, embedding      rk_linear_rows (bf16 / INT8 / INT4 weights, up to 32 rows), rk_dequant_rows (+ a BLAS GEMM
                          beyond 32 rows; embedding rows), src/backend/metal.py:50-133
   swiglu, silu_mul       rk_linear_rows on the stacked [gate; up] weight, then rk_silu_mul on its two halves in place
+  silu_mul_linear        rk_linear_rows_ex: SwiGLU's silu * up applied while the down projection stages its
+                         activations (one launch instead of two)
   rms_norm, layer_norm   rk_rms_norm, rk_layer_norm (src/ops.py:7-24)
   rope                   rk_rope (src/ops.py:27-54)
   prepare                the reference's weight policy (src/backend/metal.py:43-48): bf16 on the device, or with a
@@ -211,6 +213,11 @@ class RocmBackend:
         y = self.linear(x, w_gate_up)
         F = w_gate_up.shape[0] // 2
         return kernels.silu_mul(y[:, :F], y[:, F:])
+
+    def silu_mul_linear(self, gate, up, w, b=None, residual=None):
+        """linear(silu_mul(gate, up), w, b, residual): SwiGLU's down projection (src/models/qwen3_5.py:166-170)
+        reading the gate / up halves of the gate_up output in place, in one launch (rk_linear_rows_ex)."""
+        return kernels.silu_mul_linear(gate, up, w, b, residual)
 
     def silu_mul(self, gate, up):
         """silu(gate) * up, fp32 (src/ops.py:107-110)."""

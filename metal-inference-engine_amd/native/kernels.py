@@ -679,3 +679,44 @@ def silu_mul(gate, up) -> torch.Tensor:
     load().call("rk_silu_mul", out.data_ptr(), g.data_ptr(), g.stride(0), u.data_ptr(), u.stride(0), g.shape[0], F,
                 _stream(dev))
     return out.view(shape)
+
+
+def silu_mul_linear(gate, up, w, bias=None, residual=None) -> torch.Tensor:
+    """linear(silu_mul(gate, up), w, bias, residual) with silu * up applied while rk_linear_rows_ex stages the
+    activations (one launch). gate / up may be strided row views (the halves of one gate_up output). Outside what
+    the fused kernel covers (more than 8 rows, K not a multiple of 256) silu_mul runs as its own kernel first: the
+    same results within 1e-5."""
+    from native.rocm_native import RK_X_SILU_MUL
+    wt, data, scales, mins, N, K = _weight_args(w)
+    M = gate.shape[0]
+    if gate.dim() != 2 or gate.shape[1] != K or up.shape != gate.shape:
+        raise ValueError(f"linear: gate {tuple(gate.shape)}, up {tuple(up.shape)} for a [{N}, {K}] weight")
+    if M > 8 or K % 256:
+        return linear(silu_mul(gate, up), w, bias, residual)
+    dev = _need_cuda("linear", gate, up, data)
+
+    def rows(t):
+        t = t.to(torch.float32)
+        if t.stride(1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16 or (t.shape[0] > 1 and t.stride(0) < K):
+            t = t.contiguous() if not t.is_contiguous() else t.clone()
+        return t
+    g, u = rows(gate), rows(up)
+    g_ld = g.stride(0) if M > 1 else K
+    u_ld = u.stride(0) if M > 1 else K
+    if bias is not None:
+        bias = bias.to(device=dev, dtype=torch.float32).contiguous()
+    if residual is not None:
+        residual = residual.to(device=dev, dtype=torch.float32).contiguous()
+        if residual.shape != (M, N):
+            raise ValueError(f"linear: residual {tuple(residual.shape)}, expected [{M}, {N}]")
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+    lib = load()
+    cnt = linear_counters(dev, -(-N // 16))
+    need = lib.lib.rk_linear_workspace_bytes(M, N, K, wt)
+    part = workspace(dev, need) if need else None
+    lib.call("rk_linear_rows_ex", out.data_ptr(), g.data_ptr(), g_ld, RK_X_SILU_MUL, u.data_ptr(), u_ld, M, N, K,
+             data.data_ptr(), wt, scales.data_ptr() if scales is not None else None,
+             mins.data_ptr() if mins is not None else None, bias.data_ptr() if bias is not None else None,
+             residual.data_ptr() if residual is not None else None, part.data_ptr() if part is not None else None,
+             part.numel() if part is not None else 0, cnt.data_ptr(), cnt.numel(), _stream(dev))
+    return out

@@ -35,6 +35,8 @@ struct LinArgs {
     const float* res;              // [M, N] or null
     float* part;                   // [S, M, N] partial sums (S > 1)
     uint32_t* cnt;                 // [row groups] arrival counters, zero between calls (S > 1)
+    const float* aux;              // XF 1: the up rows (row m at aux + m * aux_ld)
+    long long x_ld, aux_ld;        // row strides (elements) of x and of the up rows
     int M, N, K, S;
 };
 
@@ -99,7 +101,7 @@ constexpr int kSplitBlocks = 4 * kWaveBlocks;      // blocks per workgroup (its 
 // wave order). With S > 1 splits the workgroup stores its partial sums (device-coherent stores), counts itself in
 // for its row group, and the last to arrive adds the S partials in split order (deterministic, whatever the arrival
 // order), the bias and the residual, and writes y. Every output's summation order depends on K alone.
-template <int WT, int COLS, int RT, bool PV>
+template <int WT, int COLS, int RT, bool PV, int XF>
 __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     using TR = WTraits<WT>;
     constexpr bool QUANT = WT != RK_W_BF16;
@@ -123,15 +125,22 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     // ---- requests: activations, parameters, weights (in this order, all before any use)
     // activations: thread k-groups id = tid + 256u, activation row id / KG, k-group id % KG (consecutive lanes read
     // consecutive 32 bytes)
-    f32x4 xv[XI][2];
+    // XF 1: also the up rows
+    f32x4 xv[XI][2], xa[XF != 0 ? XI : 1][2];
 #pragma unroll
     for (int u = 0; u < XI; ++u) {
         const int id = tid + 256 * u;
         const int col = id / KG, kg = id % KG;
-        const f32x4* p = reinterpret_cast<const f32x4*>(a.x + (size_t)min(col, a.M - 1) * a.K + (size_t)kQB * b0 +
-                                                          8 * min(kg, 4 * nb - 1));
+        const size_t row = (size_t)min(col, a.M - 1);
+        const int kk = 8 * min(kg, 4 * nb - 1);
+        const f32x4* p = reinterpret_cast<const f32x4*>(a.x + row * a.x_ld + (size_t)kQB * b0 + kk);
         xv[u][0] = p[0];
         xv[u][1] = p[1];
+        if constexpr (XF == 1) {
+            const f32x4* pu = reinterpret_cast<const f32x4*>(a.aux + row * a.aux_ld + (size_t)kQB * b0 + kk);
+            xa[u][0] = pu[0];
+            xa[u][1] = pu[1];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     // scales / mins of blocks wb0 .. +7 of row 16t + r: PV (K % 256 == 0) one 16-byte load per tile and kind
@@ -189,6 +198,13 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
         for (int e = 0; e < 4; ++e) {
             v[e] = ok ? xv[u][0][e] : 0.0f;
             v[4 + e] = ok ? xv[u][1][e] : 0.0f;
+        }
+        if constexpr (XF == 1) {                    // silu(gate) * up = g / (1 + exp(-g)) * u, hardware exp / rcp
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = 1.0f + __builtin_amdgcn_exp2f(-v[e] * 1.4426950408889634f);
+                v[e] = v[e] * __builtin_amdgcn_rcpf(d) * (ok ? xa[u][e >> 2][e & 3] : 0.0f);
+            }
         }
         u32x4 pc[3];
 #pragma unroll
@@ -405,18 +421,30 @@ size_t rk_linear_workspace_bytes(int M, int N, int K, int w_type) {
     return p.S == 1 ? 0 : (size_t)p.S * M * N * sizeof(float);
 }
 
-int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w, int w_type, const void* scales,
-                   const void* mins, const float* bias, const float* residual, float* partials,
-                   size_t partial_bytes, uint32_t* counters, int n_counters, void* stream) {
+int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const float* aux, long long aux_ld, int M,
+                      int N, int K, const void* w, int w_type, const void* scales, const void* mins,
+                      const float* bias, const float* residual, float* partials, size_t partial_bytes,
+                      uint32_t* counters, int n_counters, void* stream) {
     if (M == 0 || N == 0) return RK_OK;
     const bool quant = w_type == RK_W_INT8 || w_type == RK_W_INT4;
-    if (!y || !x || !w || (quant && !scales) || (w_type == RK_W_INT4 && !mins))
+    if (!y || !x || !w || (quant && !scales) || (w_type == RK_W_INT4 && !mins) || (x_op != RK_X_PLAIN && !aux))
         return fail(RK_ERR_ARG, "rk_linear_rows: null pointer");
     if (w_type != RK_W_BF16 && !quant) return fail(RK_ERR_UNSUPPORTED, "rk_linear_rows: weight type %d", w_type);
     if (M < 0 || M > kCols || N < 0 || K < kQB || K % kQB)
         return fail(RK_ERR_ARG, "rk_linear_rows: M %d (1..%d), N %d, K %d (a multiple of %d)", M, kCols, N, K, kQB);
-    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
-        return fail(RK_ERR_ARG, "rk_linear_rows: x and w must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16 || x_ld < K || x_ld % 4)
+        return fail(RK_ERR_ARG, "rk_linear_rows: x and w must be 16-byte aligned, x rows at a stride >= K of 4n");
+    // 16-byte parameter loads: K % 256 == 0 and 16-byte aligned scale / min arrays
+    const bool pv = (K / kQB) % kWaveBlocks == 0 && reinterpret_cast<uintptr_t>(scales) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(mins) % 16 == 0;
+    if (x_op != RK_X_PLAIN) {
+        if (x_op != RK_X_SILU_MUL) return fail(RK_ERR_ARG, "rk_linear_rows: input transform %d", x_op);
+        if (M > 8 || !pv)
+            return fail(RK_ERR_UNSUPPORTED, "rk_linear_rows: the fused input transform needs M <= 8 and K %% 256 == 0: "
+                        "M %d, K %d", M, K);
+        if (reinterpret_cast<uintptr_t>(aux) % 16 || aux_ld < K || aux_ld % 4)
+            return fail(RK_ERR_ARG, "rk_linear_rows: up rows must be 16-byte aligned, at a stride >= K of 4n");
+    }
     const LinPlan p = lin_plan(M, N, K, w_type);
     const size_t need = rk_linear_workspace_bytes(M, N, K, w_type);
     if (need && (!partials || partial_bytes < need || !counters || n_counters < p.groups))
@@ -428,24 +456,31 @@ int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w,
     a.mins = static_cast<const uint16_t*>(mins); a.bias = bias; a.res = residual;
     a.cnt = counters;
     a.part = partials;
+    a.aux = aux; a.x_ld = x_ld; a.aux_ld = aux_ld;
     a.M = M; a.N = N; a.K = K; a.S = p.S;
-    // 16-byte parameter loads: K % 256 == 0 and 16-byte aligned scale / min arrays
-    const bool pv = (K / kQB) % kWaveBlocks == 0 && reinterpret_cast<uintptr_t>(scales) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(mins) % 16 == 0;
     using Fn = void (*)(LinArgs);
     Fn fn = nullptr;
-#define RK_LIN_PICK(C, R, V)                                                                                   \
-    if (p.cols == C && p.rt == R && pv == V)                                                                   \
-        fn = w_type == RK_W_BF16 ? linear_rows_kernel<RK_W_BF16, C, (R > 2 ? 2 : R), V>                        \
-             : w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, C, R, V> : linear_rows_kernel<RK_W_INT4, C, R, V>;
-    RK_LIN_PICK(8, 1, true) RK_LIN_PICK(8, 2, true) RK_LIN_PICK(8, 4, true)
-    RK_LIN_PICK(16, 1, true) RK_LIN_PICK(16, 2, true) RK_LIN_PICK(16, 4, true)
-    RK_LIN_PICK(8, 1, false) RK_LIN_PICK(8, 2, false) RK_LIN_PICK(8, 4, false)
-    RK_LIN_PICK(16, 1, false) RK_LIN_PICK(16, 2, false) RK_LIN_PICK(16, 4, false)
+#define RK_LIN_PICK(C, R, V, X)                                                                                \
+    if (p.cols == C && p.rt == R && pv == V && x_op == X)                                                      \
+        fn = w_type == RK_W_BF16 ? linear_rows_kernel<RK_W_BF16, C, (R > 2 ? 2 : R), V, X>                     \
+             : w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, C, R, V, X>                                 \
+                                   : linear_rows_kernel<RK_W_INT4, C, R, V, X>;
+    RK_LIN_PICK(8, 1, true, 0) RK_LIN_PICK(8, 2, true, 0) RK_LIN_PICK(8, 4, true, 0)
+    RK_LIN_PICK(16, 1, true, 0) RK_LIN_PICK(16, 2, true, 0) RK_LIN_PICK(16, 4, true, 0)
+    RK_LIN_PICK(8, 1, false, 0) RK_LIN_PICK(8, 2, false, 0) RK_LIN_PICK(8, 4, false, 0)
+    RK_LIN_PICK(16, 1, false, 0) RK_LIN_PICK(16, 2, false, 0) RK_LIN_PICK(16, 4, false, 0)
+    RK_LIN_PICK(8, 1, true, 1) RK_LIN_PICK(8, 2, true, 1) RK_LIN_PICK(8, 4, true, 1)
 #undef RK_LIN_PICK
     if (!fn) return fail(RK_ERR_ARG, "rk_linear_rows: no kernel for %d columns, %d row tiles", p.cols, p.rt);
     hipLaunchKernelGGL(fn, dim3((unsigned)(p.groups * p.S)), dim3(256), 0, static_cast<hipStream_t>(stream), a);
     return check_launch("linear_rows");
+}
+
+int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w, int w_type, const void* scales,
+                   const void* mins, const float* bias, const float* residual, float* partials,
+                   size_t partial_bytes, uint32_t* counters, int n_counters, void* stream) {
+    return rk_linear_rows_ex(y, x, K, RK_X_PLAIN, nullptr, 0, M, N, K, w, w_type, scales, mins, bias, residual, partials,
+                             partial_bytes, counters, n_counters, stream);
 }
 
 int rk_dequant_rows(float* out, const void* w, int w_type, const void* scales, const void* mins,

@@ -551,33 +551,41 @@ class HybridDecodeState:
 def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Tensor, layout) -> torch.Tensor:
     """One decode step for the batch through the backend protocol, in the order of Qwen3_5Model.decode_batch
     (src/models/qwen3_5.py:228-290) -> logits [B, vocab] fp32. The attention layer's q / k norms, partial RoPE and
-    KV write are the one fused attention_prep call, and the output gate is fused into paged_attention; the
-    sequences' lengths are not advanced (a benchmark replays the same step)."""
+    KV write are the one fused attention_prep call, the output gate is fused into paged_attention, and (with a
+    backend that has silu_mul_linear) SwiGLU's silu * up runs inside the down projection; the sequences' lengths
+    are not advanced (a benchmark replays the same step)."""
     cfg = st.cfg
     B = tokens.shape[0]
     slots, tables, lens, positions = layout
     kv = st.pool.kv
+    fused = hasattr(backend, "silu_mul_linear")
+
+    def norm_linear(h, norm_w, wt):
+        return backend.linear(backend.rms_norm(h, norm_w, cfg.eps), wt)
+
     h = backend.embedding(w["embed_tokens.weight"], tokens)
     for i in range(cfg.layers):
         p = f"layers.{i}."
-        x = backend.rms_norm(h, w[p + "input_layernorm.weight"], cfg.eps)
         L = st.slot[i]
         if cfg.is_full(i):
             a = p + "self_attn."
-            y = backend.linear(x, w[a + "qkvg.weight"])
+            y = norm_linear(h, w[p + "input_layernorm.weight"], w[a + "qkvg.weight"])
             q, gate = backend.attention_prep(y, w[a + "q_norm.weight"], w[a + "k_norm.weight"], cfg.eps, positions,
                                              cfg.theta, cfg.rot, (cfg.Hq, cfg.Hkv, cfg.d), kv.k[L], kv.v[L], slots)
             o = backend.paged_attention(q, kv.k[L], kv.v[L], tables, lens, cfg.block_size, gate=gate)
             h = backend.linear(o.reshape(B, cfg.Hq * cfg.d), w[a + "o_proj.weight"], residual=h)
         else:
             a = p + "linear_attn."
-            y = backend.linear(x, w[a + "in_proj.weight"])
+            y = norm_linear(h, w[p + "input_layernorm.weight"], w[a + "in_proj.weight"])
             C, Z, H = cfg.conv_dim, cfg.H * cfg.dv, cfg.H
             o = backend.deltanet_decode_batch(y[:, :C], y[:, C:C + Z], y[:, C + Z:C + Z + H], y[:, C + Z + H:],
                                               st.seqs, L, w[a + "conv1d.weight"], w[a + "A_log"], w[a + "dt_bias"],
                                               w[a + "norm.weight"], cfg.eps, (H, cfg.dk, cfg.dv, H * cfg.dk))
             h = backend.linear(o, w[a + "out_proj.weight"], residual=h)
-        x = backend.rms_norm(h, w[p + "post_attention_layernorm.weight"], cfg.eps)
-        h = backend.linear(backend.swiglu(x, w[p + "mlp.gate_up.weight"]), w[p + "mlp.down_proj.weight"], residual=h)
-    h = backend.rms_norm(h, w["norm.weight"], cfg.eps)
-    return backend.linear(h, w["embed_tokens.weight"])
+        gu = norm_linear(h, w[p + "post_attention_layernorm.weight"], w[p + "mlp.gate_up.weight"])
+        F = gu.shape[1] // 2
+        if fused:
+            h = backend.silu_mul_linear(gu[:, :F], gu[:, F:], w[p + "mlp.down_proj.weight"], residual=h)
+        else:
+            h = backend.linear(backend.silu_mul(gu[:, :F], gu[:, F:]), w[p + "mlp.down_proj.weight"], residual=h)
+    return norm_linear(h, w["norm.weight"], w["embed_tokens.weight"])

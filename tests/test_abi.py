@@ -232,3 +232,22 @@ def test_decode_ops_checked_on_host(lib):
     assert L.rk_silu_mul(fake, fake, 100, fake, 200, 4, 128, None) == 1 and "strides" in lib.last_error()
     assert L.rk_silu_mul(fake, None, 256, fake, 256, 4, 128, None) == 1
     assert L.rk_silu_mul(fake, fake, 256, fake, 256, 0, 128, None) == 0
+
+
+def test_linear_ex_checked_on_host(lib):
+    fake = 4096
+    L = lib.lib
+
+    def call(**kw):
+        a = dict(y=fake, x=fake, xld=4096, op=1, aux=fake + 8192, auxld=4096, M=8, N=2048, K=2048, w=fake, wt=3,
+                 s=fake, m=fake, b=None, r=None, p=fake, pb=1 << 30, c=fake, nc=1024)
+        a.update(kw)
+        return L.rk_linear_rows_ex(*a.values(), None)
+
+    assert call(op=3) == 1 and "input transform 3" in lib.last_error()
+    assert call(aux=None) == 1 and "null pointer" in lib.last_error()
+    assert call(M=9) == 2 and "M <= 8" in lib.last_error()
+    assert call(K=2080, xld=4160, auxld=4160) == 2                  # K % 256 != 0
+    assert call(xld=2047) == 1 and "stride" in lib.last_error()
+    assert call(auxld=100) == 1 and "up rows" in lib.last_error()
+    assert call(M=0) == 0

@@ -85,3 +85,25 @@ def test_rows_are_independent_of_the_batch(backend):
     full = backend.linear(x, wd)
     for i in (0, 7, 15):
         assert torch.equal(backend.linear(x[i:i + 1], wd), full[i:i + 1])
+
+
+@pytest.mark.parametrize("N,K", [(2048, 6144), (1024, 3584), (640, 2048), (96, 256)])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
+def test_silu_mul_fused_into_the_linear(backend, kind, N, K):
+    """silu_mul_linear (rk_linear_rows_ex, RK_X_SILU_MUL) over the two halves of one [M, 2K] gate_up output read in
+    place == linear(silu_mul(gate, up)) on the oracle; more than 8 rows take the two-launch path (same bar); a fused
+    row does not depend on the batch."""
+    from oracle import ops_ref
+    w, deq = weight(kind, N, K, 7 * N + K)
+    g = torch.Generator().manual_seed(K)
+    wd = to_dev(w)
+    for M in (1, 5, 8, 12):
+        y = torch.randn(M, 2 * K, generator=g) * 2
+        r = torch.randn(M, N, generator=g)
+        want = quant_ref.linear(ops_ref.silu_mul(y[:, :K], y[:, K:]), deq, None, r)
+        yd = y.to(DEV)
+        got = backend.silu_mul_linear(yd[:, :K], yd[:, K:], wd, residual=r.to(DEV))
+        assert rel_err(got, want) < TOL, f"M {M}"
+    yd = yd[:8]
+    full = backend.silu_mul_linear(yd[:, :K], yd[:, K:], wd)
+    assert torch.equal(backend.silu_mul_linear(yd[3:4, :K], yd[3:4, K:], wd), full[3:4])
