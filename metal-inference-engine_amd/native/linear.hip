@@ -123,14 +123,14 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     const int nbw = max(0, min(kWaveBlocks, nblk - wb0));
 
     // ---- requests: activations, parameters, weights (in this order, all before any use)
-    // activations: thread k-groups id = tid + 256u, activation row id / KG, k-group id % KG (consecutive lanes read
-    // consecutive 32 bytes)
+    // activations: thread k-groups id = tid + 256u, activation row id % COLS, k-group id / COLS (the row varies
+    // fastest, so consecutive lanes write consecutive 16 bytes of the staging buffer: no LDS bank conflicts)
     // XF 1: also the up rows
     f32x4 xv[XI][2], xa[XF != 0 ? XI : 1][2];
 #pragma unroll
     for (int u = 0; u < XI; ++u) {
         const int id = tid + 256 * u;
-        const int col = id / KG, kg = id % KG;
+        const int col = id % COLS, kg = id / COLS;
         const size_t row = (size_t)min(col, a.M - 1);
         const int kk = 8 * min(kg, 4 * nb - 1);
         const f32x4* p = reinterpret_cast<const f32x4*>(a.x + row * a.x_ld + (size_t)kQB * b0 + kk);
@@ -187,11 +187,11 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- staging: activation pieces [3][KG][COLS]; block sums [32][COLS] (INT4: the four k-groups of a block sit in
-    // lanes 4i .. 4i+3 and are added pairwise, (s0 + s1) + (s2 + s3), identically in all four)
+    // lanes i, i + COLS, i + 2 COLS, i + 3 COLS and are added pairwise, (s0 + s1) + (s2 + s3), identically in all four)
 #pragma unroll
     for (int u = 0; u < XI; ++u) {
         const int id = tid + 256 * u;
-        const int col = id / KG, kg = id % KG;
+        const int col = id % COLS, kg = id / COLS;
         const bool ok = col < a.M && kg < 4 * nb;
         float v[8];
 #pragma unroll
@@ -220,8 +220,8 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
             float sum = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) sum += v[e];
-            sum += __shfl_xor(sum, 1);
-            sum += __shfl_xor(sum, 2);
+            sum += __shfl_xor(sum, COLS);           // the block's k-groups sit COLS lanes apart
+            sum += __shfl_xor(sum, 2 * COLS);
             if ((kg & 3) == 0) bsum_s[(kg >> 2) * COLS + col] = sum;
         }
     }
