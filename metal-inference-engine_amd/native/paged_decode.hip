@@ -649,116 +649,130 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     }
 }
 
-// One workgroup per (sequence, kv-head); each thread owns float4 outputs of the G x D block. Sequence b owns global
-// tiles [P[b], P[b + 1]); the split workgroups whose ranges meet it are w_first = the one holding tile P[b] ..
-// w_last = the one holding tile P[b + 1] - 1 (empty ranges in between, possible only when NW > U, are skipped),
-// with partials in slots w + b. The gate is requested with the plan; the partials are combined in workgroup order,
-// up to kMergeCh per memory round trip (every load of a chunk is issued before any is used, with no branch between
-// them), with a running maximum: M' = max(M, m_w), num = num 2^(M - M') + sum_w 2^(m_w - M') acc_w, den likewise
-// with l_w; out = num / den.
-constexpr int kMergeThreads = 256;
+// One workgroup per (sequence, kv-head). Sequence b owns global tiles [P[b], P[b + 1]); the split workgroups whose
+// ranges meet it are w_first = the one holding tile P[b] .. w_last = the one holding tile P[b + 1] - 1 (empty ranges
+// in between, possible only when NW > U, are skipped), with partials in slots w + b. The workgroup's threads form SL
+// slices of TS threads (TS = GP * D / 4, one float4 output of the GP x D block each); with n partials, the first
+// min(SL, ceil(n / kMergeCh)) slices take consecutive runs of them, so a sequence over many partials (few
+// sequences, many split workgroups) needs up to SL times fewer memory round trips. Within a slice the partials are combined in workgroup order, up to kMergeCh per
+// round trip (every load of a chunk is issued before any is used, with no branch between them), with a running
+// maximum: M' = max(M, m_w), num = num 2^(M - M') + sum_w 2^(m_w - M') acc_w, den likewise with l_w; the slices'
+// (M, num, den) are then combined in slice order the same way, and out = num / den, times the gate.
+constexpr int kMergeThreads = 1024;
 
 template <int D, int GP>
 __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a) {
-    constexpr int kT = kMergeThreads;
-    constexpr int NO = (GP * D / 4 + kT - 1) / kT;   // float4 outputs per thread (upper bound)
+    constexpr int TS = GP * D / 4;                    // threads per slice: one float4 output each
+    constexpr int SL = kMergeThreads / TS;            // slices
+    static_assert(TS <= kMergeThreads && kMergeThreads % TS == 0, "slices tile the workgroup");
     constexpr int REC = GP * D + 2 * GP;
     constexpr int kMergeCh = 8;                       // partials combined per memory round trip
     __shared__ int P[kMaxBatch + 1];
-    const int tid = threadIdx.x;
+    __shared__ float4 num_s[SL > 1 ? SL - 1 : 1][TS];
+    __shared__ float2 md_s[SL > 1 ? SL - 1 : 1][TS];  // (M, den)
+    const int tid = threadIdx.x, sl = tid / TS, ti = tid % TS;
     const int b = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
     const int n4 = a.G * (D / 4);
     const long long obase = ((long long)b * a.Hq + (long long)kvh * a.G) * D;
     const float* grow = a.gate ? a.gate + (long long)b * a.gate_ld + (long long)kvh * a.G * D : nullptr;
-    float4 gv[NO];
-#pragma unroll
-    for (int k = 0; k < NO; ++k) {
-        const int i = tid + k * kT;
-        gv[k] = grow && i < n4 ? *reinterpret_cast<const float4*>(grow + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    const float4 gv = sl == 0 && grow && ti < n4 ? *reinterpret_cast<const float4*>(grow + 4 * ti)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < 64) plan_prefix(a, P);
     __syncthreads();
     const int U = P[a.B], pb = P[b], pe = P[b + 1];
     float4* out = reinterpret_cast<float4*>(a.out + obase);
     if (pe == pb) {                                  // empty sequence (length 0)
-        for (int i = tid; i < n4; i += kT) out[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (sl == 0 && ti < n4) out[ti] = make_float4(0.f, 0.f, 0.f, 0.f);
         return;
     }
     const int wf = (int)(((long long)(pb + 1) * a.NW - 1) / U);
     const int wlast = (int)(((long long)pe * a.NW - 1) / U);
+    // slices in use: one per chunk of partials, up to SL (the rest hold none); partials per slice
+    const int npart = wlast - wf + 1;
+    const int slr = min(SL, (npart + kMergeCh - 1) / kMergeCh);
+    const int per = (npart + slr - 1) / slr;
+    const int s_first = sl < slr ? wf + sl * per : wlast + 1, s_last = min(wlast, s_first + per - 1);
 
-    int off[NO], hk[NO];                 // this thread's float4 outputs i = tid + k kT: element offset, head
-    float M[NO], den[NO];
-    float4 num[NO];
-#pragma unroll
-    for (int k = 0; k < NO; ++k) {
-        const int i = tid + k * kT;
-        const int ic = i < n4 ? i : 0;
-        off[k] = 4 * ic;
-        hk[k] = (4 * ic) / D;
-        M[k] = -INFINITY;
-        den[k] = 0.0f;
-        num[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    const int ic = ti < n4 ? ti : 0;
+    const int off = 4 * ic, hk = (4 * ic) / D;        // this thread's float4 output: element offset, head
+    float M = -INFINITY, den = 0.0f;
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
     // a workgroup's range can be empty only when there are more split workgroups than tiles; otherwise every
     // workgroup in [wf, wlast] holds a partial, and no range has to be recomputed per partial
     const bool sparse = a.NW > U;
-    for (int w0 = wf; w0 <= wlast; w0 += kMergeCh) {
-        float4 v[kMergeCh][NO];
-        float mj[kMergeCh][NO], lj[kMergeCh][NO];
+    for (int w0 = s_first; w0 <= s_last; w0 += kMergeCh) {
+        float4 v[kMergeCh];
+        float mj[kMergeCh], lj[kMergeCh];
         bool use[kMergeCh];
-        // every load of the chunk first, without branches: slots past wlast re-read wlast's partial (unused)
+        // every load of the chunk first, without branches: slots past the slice's last re-read it (unused)
 #pragma unroll
         for (int j = 0; j < kMergeCh; ++j) {
-            const int wj = min(w0 + j, wlast);
+            const int wj = min(w0 + j, s_last);
             const float* base = a.part + ((long long)(wj + b) * a.Hkv + kvh) * REC;
-#pragma unroll
-            for (int k = 0; k < NO; ++k) {
-                v[j][k] = *reinterpret_cast<const float4*>(base + off[k]);
-                mj[j][k] = base[GP * D + hk[k]];
-                lj[j][k] = base[GP * D + GP + hk[k]];
-            }
+            v[j] = *reinterpret_cast<const float4*>(base + off);
+            mj[j] = base[GP * D + hk];
+            lj[j] = base[GP * D + GP + hk];
         }
 #pragma unroll
         for (int j = 0; j < kMergeCh; ++j) {
             const int wj = w0 + j;
-            use[j] = wj <= wlast && (!sparse || range_lo(U, a.NW, wj + 1) > range_lo(U, a.NW, wj));
+            use[j] = wj <= s_last && (!sparse || range_lo(U, a.NW, wj + 1) > range_lo(U, a.NW, wj));
         }
+        float mx = M;
 #pragma unroll
-        for (int k = 0; k < NO; ++k) {
-            float mx = M[k];
+        for (int j = 0; j < kMergeCh; ++j) mx = use[j] ? fmaxf(mx, mj[j]) : mx;
+        // 0 before the first partial (M = -inf): num and den are 0 then, also in a chunk with none to use
+        const float rs = M == -INFINITY ? 0.0f : fast_exp2(M - mx);
+        float4 nk = make_float4(num.x * rs, num.y * rs, num.z * rs, num.w * rs);
+        float dk = den * rs;
 #pragma unroll
-            for (int j = 0; j < kMergeCh; ++j) mx = use[j] ? fmaxf(mx, mj[j][k]) : mx;
-            const float rs = fast_exp2(M[k] - mx);   // 0 on the first chunk (M = -inf, mx finite)
-            float4 nk = make_float4(num[k].x * rs, num[k].y * rs, num[k].z * rs, num[k].w * rs);
-            float dk = den[k] * rs;
+        for (int j = 0; j < kMergeCh; ++j) {
+            const float sc = use[j] ? fast_exp2(mj[j] - mx) : 0.0f;
+            nk.x = fmaf(sc, v[j].x, nk.x);
+            nk.y = fmaf(sc, v[j].y, nk.y);
+            nk.z = fmaf(sc, v[j].z, nk.z);
+            nk.w = fmaf(sc, v[j].w, nk.w);
+            dk = fmaf(sc, lj[j], dk);
+        }
+        num = nk;
+        den = dk;
+        M = mx;
+    }
+    if constexpr (SL > 1) {
+        if (sl > 0) {
+            num_s[sl - 1][ti] = num;
+            md_s[sl - 1][ti] = make_float2(M, den);
+        }
+        __syncthreads();
+        if (sl > 0) return;
+        // slice 0 holds the first partials, so M is finite; a slice without partials has M = -inf and adds 0
+        float mx = M;
 #pragma unroll
-            for (int j = 0; j < kMergeCh; ++j) {
-                const float sc = use[j] ? fast_exp2(mj[j][k] - mx) : 0.0f;
-                nk.x = fmaf(sc, v[j][k].x, nk.x);
-                nk.y = fmaf(sc, v[j][k].y, nk.y);
-                nk.z = fmaf(sc, v[j][k].z, nk.z);
-                nk.w = fmaf(sc, v[j][k].w, nk.w);
-                dk = fmaf(sc, lj[j][k], dk);
-            }
-            num[k] = nk;
-            den[k] = dk;
-            M[k] = mx;
+        for (int q = 0; q < SL - 1; ++q) mx = fmaxf(mx, md_s[q][ti].x);
+        const float rs = fast_exp2(M - mx);
+        num = make_float4(num.x * rs, num.y * rs, num.z * rs, num.w * rs);
+        den *= rs;
+#pragma unroll
+        for (int q = 0; q < SL - 1; ++q) {
+            const float2 md = md_s[q][ti];
+            const float4 nq = num_s[q][ti];
+            const float sc = fast_exp2(md.x - mx);
+            num.x = fmaf(sc, nq.x, num.x);
+            num.y = fmaf(sc, nq.y, num.y);
+            num.z = fmaf(sc, nq.z, num.z);
+            num.w = fmaf(sc, nq.w, num.w);
+            den = fmaf(sc, md.y, den);
         }
     }
-#pragma unroll
-    for (int k = 0; k < NO; ++k) {
-        const int i = tid + k * kT;
-        if (i >= n4) break;
-        float4 o = make_float4(num[k].x / den[k], num[k].y / den[k], num[k].z / den[k], num[k].w / den[k]);
-        if (a.gate) {
-            o.x *= 1.0f / (1.0f + expf(-gv[k].x));
-            o.y *= 1.0f / (1.0f + expf(-gv[k].y));
-            o.z *= 1.0f / (1.0f + expf(-gv[k].z));
-            o.w *= 1.0f / (1.0f + expf(-gv[k].w));
-        }
-        out[i] = o;
+    if (ti >= n4) return;
+    float4 o = make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+    if (a.gate) {
+        o.x *= 1.0f / (1.0f + expf(-gv.x));
+        o.y *= 1.0f / (1.0f + expf(-gv.y));
+        o.z *= 1.0f / (1.0f + expf(-gv.z));
+        o.w *= 1.0f / (1.0f + expf(-gv.w));
     }
+    out[ti] = o;
 }
 
 typedef void (*SplitFn)(DecodeArgs);
