@@ -353,19 +353,20 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
 }
 
 // Row tiles per workgroup: the most (4; 2 for bf16, whose weight slots are 4x wider than INT4's) that still leave
-// 512 workgroups, down to 1. Staged activation rows: 8 for M <= 8, else 16. Neither changes any output's summation
+// min_groups workgroups, down to 1: 512, and 256 for the fused silu * up input, whose workgroups stage twice the
+// activation bytes (gate and up rows), so more weight rows per workgroup pay for them. Staged activation rows: 8 for M <= 8, else 16. Neither changes any output's summation
 // order (blocks in order within a wave, waves in order, splits in order).
 struct LinPlan {
     int cols, rt, S, groups;
 };
 
-LinPlan lin_plan(int M, int N, int K, int w_type) {
+LinPlan lin_plan(int M, int N, int K, int w_type, int min_groups = 512) {
     LinPlan p;
     p.cols = M <= 8 ? 8 : 16;
     const int nblk = K / kQB;
     p.S = (nblk + kSplitBlocks - 1) / kSplitBlocks;
     p.rt = w_type == RK_W_BF16 ? 2 : 4;
-    while (p.rt > 1 && (long long)((N + 16 * p.rt - 1) / (16 * p.rt)) * p.S < 512) p.rt /= 2;
+    while (p.rt > 1 && (long long)((N + 16 * p.rt - 1) / (16 * p.rt)) * p.S < min_groups) p.rt /= 2;
     p.groups = (N + 16 * p.rt - 1) / (16 * p.rt);
     return p;
 }
@@ -445,7 +446,7 @@ int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const 
         if (reinterpret_cast<uintptr_t>(aux) % 16 || aux_ld < K || aux_ld % 4)
             return fail(RK_ERR_ARG, "rk_linear_rows: up rows must be 16-byte aligned, at a stride >= K of 4n");
     }
-    const LinPlan p = lin_plan(M, N, K, w_type);
+    const LinPlan p = lin_plan(M, N, K, w_type, x_op == RK_X_SILU_MUL ? 256 : 512);
     const size_t need = rk_linear_workspace_bytes(M, N, K, w_type);
     if (need && (!partials || partial_bytes < need || !counters || n_counters < p.groups))
         return fail(RK_ERR_WORKSPACE, "rk_linear_rows: partials %zu bytes (need %zu), %d counters (need %d)",
