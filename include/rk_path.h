@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 8
+#define RK_ABI_VERSION 9
 
 /* status codes */
 #define RK_OK 0
@@ -214,6 +214,24 @@ int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const 
                       int N, int K, const void* w, int w_type, const void* scales, const void* mins,
                       const float* bias, const float* residual, float* partials, size_t partial_bytes,
                       uint32_t* counters, int n_counters, void* stream);
+
+/* rk_linear_rows_ex2: rk_linear_rows_ex with two more options, so that a decode layer's RMSNorm needs no launch of
+ * its own (src/models/qwen3_5.py:228-290: every input_layernorm / post_attention_layernorm / final norm reads the
+ * residual stream that the linear before it wrote).
+ *   ss_out (or NULL): also writes, for each output row m and 16-column tile t, the sum of squares of y[m, 16t ..
+ *     16t+15] at ss_out[m * ceil(N / 16) + t] (the tile's 16 squares added as a tree).
+ *   RK_X_RMS_NORM: x -> (x * (1 / sqrt(sum / K + eps))) * norm_w, each step rounded (ops.rms_norm,
+ *     src/ops.py:7-15, with the division by the rms as a product with its reciprocal; Backend.rms_norm,
+ *     src/backend/base.py:26-27), where sum adds row m's K / 16 tile sums of squares at aux + m * aux_ld
+ *     (written by the linear that produced x, with ss_out) in a fixed order; norm_w fp32 [K], 16-byte aligned;
+ *     K <= 2048. Needs M <= 8 and K % 256 == 0 like RK_X_SILU_MUL (else
+ *     RK_ERR_UNSUPPORTED: run rk_rms_norm first). Results equal rk_rms_norm then rk_linear_rows within 1e-5.
+ * No counterpart in the reference as one call: it replaces the pair Backend.rms_norm + Backend.linear. */
+#define RK_X_RMS_NORM 2
+int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, int x_op, const float* aux,
+                       long long aux_ld, const float* norm_w, float eps, int M, int N, int K, const void* w,
+                       int w_type, const void* scales, const void* mins, const float* bias, const float* residual,
+                       float* partials, size_t partial_bytes, uint32_t* counters, int n_counters, void* stream);
 
 /* ---- the rest of a decode step (native/decode_ops.hip): the row norms, RoPE and SwiGLU's silu * up
  * Replace Backend.rms_norm / layer_norm / rope / silu_mul (src/backend/base.py:26-40, the protocol's v1 and v3

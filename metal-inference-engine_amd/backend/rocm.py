@@ -219,6 +219,20 @@ class RocmBackend:
         reading the gate / up halves of the gate_up output in place, in one launch (rk_linear_rows_ex)."""
         return kernels.silu_mul_linear(gate, up, w, b, residual)
 
+    def linear_ss(self, x, w, b=None, residual=None):
+        """linear, also returning the sums of squares of the output's 16-column tiles (or None) for the RMSNorm
+        of the next layer input (rms_norm_linear): the residual-stream producers of a decode step."""
+        return kernels.linear_ss(x, w, b, residual)
+
+    def silu_mul_linear_ss(self, gate, up, w, b=None, residual=None):
+        """silu_mul_linear, also returning the sums of squares of the output's 16-column tiles (or None)."""
+        return kernels.silu_mul_linear_ss(gate, up, w, b, residual)
+
+    def rms_norm_linear(self, x, ss, norm_w, eps, w, b=None, residual=None):
+        """linear(rms_norm(x, norm_w, eps), w, b, residual) in one launch from the sums of squares ss that the
+        linear producing x returned (src/models/qwen3_5.py: every norm of a layer input follows a residual add)."""
+        return kernels.rms_norm_linear(x, ss, norm_w, eps, w, b, residual)
+
     def silu_mul(self, gate, up):
         """silu(gate) * up, fp32 (src/ops.py:107-110)."""
         return kernels.silu_mul(gate, up)

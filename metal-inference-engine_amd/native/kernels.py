@@ -545,6 +545,94 @@ def linear_rows(x, w, bias=None, residual=None, out=None) -> torch.Tensor:
     return out
 
 
+
+def _ex2(x, x_ld: int, w, x_op: int, aux=None, aux_ld: int = 0, norm_w=None, eps: float = 0.0, bias=None,
+         residual=None, want_ss: bool = False):
+    """One rk_linear_rows_ex2 launch over M <= 16 rows: y [M, N] fp32 and, with want_ss, the sums of squares of
+    y's 16-column tiles [M, ceil(N / 16)] (else None)."""
+    wt, data, scales, mins, N, K = _weight_args(w)
+    M = x.shape[0]
+    dev = x.device
+    if bias is not None:
+        bias = bias.to(device=dev, dtype=torch.float32).contiguous()
+    if residual is not None:
+        residual = residual.to(device=dev, dtype=torch.float32).contiguous()
+        if residual.shape != (M, N):
+            raise ValueError(f"linear: residual {tuple(residual.shape)}, expected [{M}, {N}]")
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+    ss = torch.empty(M, -(-N // 16), dtype=torch.float32, device=dev) if want_ss else None
+    lib = load()
+    cnt = linear_counters(dev, -(-N // 16))
+    need = lib.lib.rk_linear_workspace_bytes(M, N, K, wt)
+    part = workspace(dev, need) if need else None
+    lib.call("rk_linear_rows_ex2", out.data_ptr(), ss.data_ptr() if ss is not None else None, x.data_ptr(), x_ld,
+             x_op, aux.data_ptr() if aux is not None else None, aux_ld,
+             norm_w.data_ptr() if norm_w is not None else None, float(eps), M, N, K, data.data_ptr(), wt,
+             scales.data_ptr() if scales is not None else None, mins.data_ptr() if mins is not None else None,
+             bias.data_ptr() if bias is not None else None, residual.data_ptr() if residual is not None else None,
+             part.data_ptr() if part is not None else None, part.numel() if part is not None else 0, cnt.data_ptr(),
+             cnt.numel(), _stream(dev))
+    return out, ss
+
+
+def _rows_k(t, K: int):
+    """fp32 rows with unit column stride, 16-byte aligned, at a row stride >= K of 4n (a copy when not)."""
+    t = t.to(torch.float32)
+    if t.stride(1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16 or (t.shape[0] > 1 and t.stride(0) < K):
+        t = t.contiguous() if not t.is_contiguous() else t.clone()
+    return t, (t.stride(0) if t.shape[0] > 1 else K)
+
+
+def linear_ss(x, w, bias=None, residual=None):
+    """linear(x, w, bias, residual) -> (y, ss): with up to 16 rows (rk_linear_rows_ex2) also the sums of squares of
+    y's 16-column tiles [M, ceil(N / 16)], which let the RMSNorm before the next linear run inside it
+    (rms_norm_linear); beyond 16 rows (or K % 32 != 0) the plain linear and ss = None."""
+    wt, data, scales, mins, N, K = _weight_args(w)
+    M = x.shape[0]
+    if x.dim() != 2 or x.shape[1] != K or M > LINEAR_ROWS or K % 32:
+        return linear(x, w, bias, residual), None
+    _need_cuda("linear", x, data)
+    xr, ld = _rows_k(x, K)
+    from native.rocm_native import RK_X_PLAIN
+    return _ex2(xr, ld, w, RK_X_PLAIN, bias=bias, residual=residual, want_ss=True)
+
+
+def silu_mul_linear_ss(gate, up, w, bias=None, residual=None):
+    """silu_mul_linear -> (y, ss) like linear_ss: one launch with the sums of squares of y's 16-column tiles where
+    the fused kernel covers the shapes, else (silu_mul_linear(...), None)."""
+    wt, data, scales, mins, N, K = _weight_args(w)
+    M = gate.shape[0]
+    if gate.dim() != 2 or gate.shape[1] != K or up.shape != gate.shape or M > 8 or K % 256:
+        return silu_mul_linear(gate, up, w, bias, residual), None
+    _need_cuda("linear", gate, up, data)
+    g, g_ld = _rows_k(gate, K)
+    u, u_ld = _rows_k(up, K)
+    from native.rocm_native import RK_X_SILU_MUL
+    return _ex2(g, g_ld, w, RK_X_SILU_MUL, aux=u, aux_ld=u_ld, bias=bias, residual=residual, want_ss=True)
+
+
+def rms_norm_linear(x, ss, norm_w, eps: float, w, bias=None, residual=None) -> torch.Tensor:
+    """linear(rms_norm(x, norm_w, eps), w, bias, residual) with the norm applied while rk_linear_rows_ex2 stages x
+    (one launch), from ss = the sums of squares of x's 16-column tiles that the linear producing x wrote
+    (linear_ss / silu_mul_linear_ss). Without ss, beyond 8 rows, K % 256 != 0 or K > 2048, and for long matrices
+    (N > 16384: every workgroup recomputes the rows' rms, which costs more than the separate launch there):
+    rms_norm, then linear (the same results within 1e-5)."""
+    wt, data, scales, mins, N, K = _weight_args(w)
+    M = x.shape[0]
+    if (ss is None or x.dim() != 2 or x.shape[1] != K or M > 8 or K % 256 or K > 2048 or N > 16384
+            or ss.shape != (M, K // 16) or norm_w.numel() != K):
+        return linear(rms_norm(x, norm_w, eps), w, bias, residual)
+    _need_cuda("linear", x, ss, norm_w, data)
+    xr, ld = _rows_k(x, K)
+    nw = norm_w.to(torch.float32).contiguous()
+    if nw.data_ptr() % 16:
+        nw = nw.clone()
+    ssr = ss.to(torch.float32).contiguous()
+    from native.rocm_native import RK_X_RMS_NORM
+    y, _ = _ex2(xr, ld, w, RK_X_RMS_NORM, aux=ssr, aux_ld=ssr.stride(0), norm_w=nw, eps=eps, bias=bias,
+                residual=residual)
+    return y
+
 _linear_cnt: dict[int, torch.Tensor] = {}
 
 

@@ -35,10 +35,15 @@ struct LinArgs {
     const float* res;              // [M, N] or null
     float* part;                   // [S, M, N] partial sums (S > 1)
     uint32_t* cnt;                 // [row groups] arrival counters, zero between calls (S > 1)
-    const float* aux;              // XF 1: the up rows (row m at aux + m * aux_ld)
-    long long x_ld, aux_ld;        // row strides (elements) of x and of the up rows
+    const float* aux;              // XF 1: the up rows (row m at aux + m * aux_ld); XF 2: the sums of squares
+    long long x_ld, aux_ld;        // row strides (elements) of x and of aux
+    const float* nw;               // XF 2: the norm weight [K] (fp32)
+    float* ss;                     // [M, ceil(N / 16)] sums of squares of y's 16-column tiles, or null
+    float eps;                     // XF 2
     int M, N, K, S;
 };
+
+constexpr int kMaxSsTiles = 128;   // XF 2: at most 128 sums of squares per row (K <= 2048)
 
 template <int WT> struct WTraits;
 // BPB: bytes of one block of one row
@@ -140,6 +145,23 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
             const f32x4* pu = reinterpret_cast<const f32x4*>(a.aux + row * a.aux_ld + (size_t)kQB * b0 + kk);
             xa[u][0] = pu[0];
             xa[u][1] = pu[1];
+        } else if constexpr (XF == 2) {
+            const f32x4* pw = reinterpret_cast<const f32x4*>(a.nw + (size_t)kQB * b0 + kk);
+            xa[u][0] = pw[0];
+            xa[u][1] = pw[1];
+        }
+    }
+    // XF 2: the sums of squares of the rows this wave normalises (rows wave + 4j), up to 8 per lane, branch-free
+    constexpr int SSR = XF == 2 ? COLS / 4 : 1;
+    float ssv[SSR][kMaxSsTiles / 64];
+    const int n_ss = a.K / 16;
+    if constexpr (XF == 2) {
+#pragma unroll
+        for (int j = 0; j < SSR; ++j) {
+            const size_t row = (size_t)min(wave + 4 * j, a.M - 1);
+#pragma unroll
+            for (int q = 0; q < kMaxSsTiles / 64; ++q)
+                ssv[j][q] = a.aux[row * a.aux_ld + min(lane + 64 * q, n_ss - 1)];
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -186,6 +208,22 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    // XF 2: 1 / rms of each row, rms = sqrt(sum / K + eps), from its tiles' sums of squares (a wave tree, lane 0's
+    // result)
+    __shared__ float rms_s[XF == 2 ? COLS : 1];
+    if constexpr (XF == 2) {
+#pragma unroll
+        for (int j = 0; j < SSR; ++j) {
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kMaxSsTiles / 64; ++q) t += lane + 64 * q < n_ss ? ssv[j][q] : 0.0f;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+            if (lane == 0) rms_s[wave + 4 * j] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(t, (float)a.K), a.eps)));
+        }
+        __syncthreads();
+    }
+
     // ---- staging: activation pieces [3][KG][COLS]; block sums [32][COLS] (INT4: the four k-groups of a block sit in
     // lanes i, i + COLS, i + 2 COLS, i + 3 COLS and are added pairwise, (s0 + s1) + (s2 + s3), identically in all four)
 #pragma unroll
@@ -205,6 +243,10 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
                 const float d = 1.0f + __builtin_amdgcn_exp2f(-v[e] * 1.4426950408889634f);
                 v[e] = v[e] * __builtin_amdgcn_rcpf(d) * (ok ? xa[u][e >> 2][e & 3] : 0.0f);
             }
+        } else if constexpr (XF == 2) {             // rms_norm: (x * (1 / rms)) * w, each rounded
+            const float ir = rms_s[col];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(__fmul_rn(v[e], ir), xa[u][e >> 2][e & 3]);
         }
         u32x4 pc[3];
 #pragma unroll
@@ -309,6 +351,7 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
             for (int i = 0; i < 4; ++i) s[i] += o[i];
         }
         const int n = row0 + 16 * t + (l & 15), m0 = 4 * (l >> 4);
+        float sq[4] = {0.f, 0.f, 0.f, 0.f};
         if (n < a.N) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -319,11 +362,20 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
                         if (a.bias) v = __fadd_rn(v, a.bias[n]);
                         if (a.res) v = __fadd_rn(v, a.res[(size_t)m * a.N + n]);
                         a.y[(size_t)m * a.N + n] = v;
+                        sq[i] = v * v;
                     } else {
                         __hip_atomic_store(&a.part[((size_t)sp * a.M + m) * a.N + n], s[i], __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
+            }
+        }
+        if (a.S == 1 && a.ss) {                     // uniform: the tile's 16 lanes add their squares (lane 0's sum)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) sq[i] += __shfl_xor(sq[i], o);
+                if ((l & 15) == 0 && m0 + i < a.M && row0 + 16 * t < a.N) a.ss[(size_t)(m0 + i) * ((a.N + 15) / 16) + (row0 + 16 * t) / 16] = sq[i];
             }
         }
     }
@@ -338,16 +390,25 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     }
     __syncthreads();
     if (!is_last) return;
+    // the 16 outputs of one 16-column tile are 16 consecutive lanes (16 RT divides the row's count), so the tile's
+    // sum of squares is a 16-lane tree (lane 0's sum)
     for (int i = tid; i < a.M * 16 * RT; i += 256) {
         const int m = i / (16 * RT), n = row0 + i % (16 * RT);
-        if (n >= a.N) continue;
         float v = 0.0f;
-        for (int q = 0; q < a.S; ++q)
-            v += __hip_atomic_load(&a.part[((size_t)q * a.M + m) * a.N + n], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        if (a.bias) v = __fadd_rn(v, a.bias[n]);
-        if (a.res) v = __fadd_rn(v, a.res[(size_t)m * a.N + n]);
-        a.y[(size_t)m * a.N + n] = v;
+        if (n < a.N) {
+            for (int q = 0; q < a.S; ++q)
+                v += __hip_atomic_load(&a.part[((size_t)q * a.M + m) * a.N + n], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            if (a.bias) v = __fadd_rn(v, a.bias[n]);
+            if (a.res) v = __fadd_rn(v, a.res[(size_t)m * a.N + n]);
+            a.y[(size_t)m * a.N + n] = v;
+        }
+        if (a.ss) {                                 // uniform
+            float q2 = v * v;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) q2 += __shfl_xor(q2, o);
+            if ((i & 15) == 0 && n < a.N) a.ss[(size_t)m * ((a.N + 15) / 16) + (n >> 4)] = q2;
+        }
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[rg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -422,10 +483,10 @@ size_t rk_linear_workspace_bytes(int M, int N, int K, int w_type) {
     return p.S == 1 ? 0 : (size_t)p.S * M * N * sizeof(float);
 }
 
-int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const float* aux, long long aux_ld, int M,
-                      int N, int K, const void* w, int w_type, const void* scales, const void* mins,
-                      const float* bias, const float* residual, float* partials, size_t partial_bytes,
-                      uint32_t* counters, int n_counters, void* stream) {
+int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, int x_op, const float* aux,
+                       long long aux_ld, const float* norm_w, float eps, int M, int N, int K, const void* w,
+                       int w_type, const void* scales, const void* mins, const float* bias, const float* residual,
+                       float* partials, size_t partial_bytes, uint32_t* counters, int n_counters, void* stream) {
     if (M == 0 || N == 0) return RK_OK;
     const bool quant = w_type == RK_W_INT8 || w_type == RK_W_INT4;
     if (!y || !x || !w || (quant && !scales) || (w_type == RK_W_INT4 && !mins) || (x_op != RK_X_PLAIN && !aux))
@@ -439,12 +500,20 @@ int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const 
     const bool pv = (K / kQB) % kWaveBlocks == 0 && reinterpret_cast<uintptr_t>(scales) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(mins) % 16 == 0;
     if (x_op != RK_X_PLAIN) {
-        if (x_op != RK_X_SILU_MUL) return fail(RK_ERR_ARG, "rk_linear_rows: input transform %d", x_op);
+        if (x_op != RK_X_SILU_MUL && x_op != RK_X_RMS_NORM)
+            return fail(RK_ERR_ARG, "rk_linear_rows: input transform %d", x_op);
         if (M > 8 || !pv)
             return fail(RK_ERR_UNSUPPORTED, "rk_linear_rows: the fused input transform needs M <= 8 and K %% 256 == 0: "
                         "M %d, K %d", M, K);
-        if (reinterpret_cast<uintptr_t>(aux) % 16 || aux_ld < K || aux_ld % 4)
+        if (x_op == RK_X_SILU_MUL && (reinterpret_cast<uintptr_t>(aux) % 16 || aux_ld < K || aux_ld % 4))
             return fail(RK_ERR_ARG, "rk_linear_rows: up rows must be 16-byte aligned, at a stride >= K of 4n");
+        if (x_op == RK_X_RMS_NORM) {
+            if (!norm_w || reinterpret_cast<uintptr_t>(norm_w) % 16)
+                return fail(RK_ERR_ARG, "rk_linear_rows: the norm weight must be a 16-byte aligned fp32 vector");
+            if (aux_ld < K / 16 || K / 16 > kMaxSsTiles)
+                return fail(RK_ERR_ARG, "rk_linear_rows: %d sums of squares per row (at most %d) at a stride of %lld",
+                            K / 16, kMaxSsTiles, aux_ld);
+        }
     }
     const LinPlan p = lin_plan(M, N, K, w_type, x_op == RK_X_SILU_MUL ? 256 : 512);
     const size_t need = rk_linear_workspace_bytes(M, N, K, w_type);
@@ -458,6 +527,7 @@ int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const 
     a.cnt = counters;
     a.part = partials;
     a.aux = aux; a.x_ld = x_ld; a.aux_ld = aux_ld;
+    a.nw = norm_w; a.ss = ss_out; a.eps = eps;
     a.M = M; a.N = N; a.K = K; a.S = p.S;
     using Fn = void (*)(LinArgs);
     Fn fn = nullptr;
@@ -471,10 +541,20 @@ int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const 
     RK_LIN_PICK(8, 1, false, 0) RK_LIN_PICK(8, 2, false, 0) RK_LIN_PICK(8, 4, false, 0)
     RK_LIN_PICK(16, 1, false, 0) RK_LIN_PICK(16, 2, false, 0) RK_LIN_PICK(16, 4, false, 0)
     RK_LIN_PICK(8, 1, true, 1) RK_LIN_PICK(8, 2, true, 1) RK_LIN_PICK(8, 4, true, 1)
+    RK_LIN_PICK(8, 1, true, 2) RK_LIN_PICK(8, 2, true, 2) RK_LIN_PICK(8, 4, true, 2)
 #undef RK_LIN_PICK
     if (!fn) return fail(RK_ERR_ARG, "rk_linear_rows: no kernel for %d columns, %d row tiles", p.cols, p.rt);
     hipLaunchKernelGGL(fn, dim3((unsigned)(p.groups * p.S)), dim3(256), 0, static_cast<hipStream_t>(stream), a);
     return check_launch("linear_rows");
+}
+
+int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const float* aux, long long aux_ld, int M,
+                      int N, int K, const void* w, int w_type, const void* scales, const void* mins,
+                      const float* bias, const float* residual, float* partials, size_t partial_bytes,
+                      uint32_t* counters, int n_counters, void* stream) {
+    if (x_op == RK_X_RMS_NORM) return fail(RK_ERR_ARG, "rk_linear_rows_ex: input transform %d", x_op);
+    return rk_linear_rows_ex2(y, nullptr, x, x_ld, x_op, aux, aux_ld, nullptr, 0.0f, M, N, K, w, w_type, scales, mins,
+                              bias, residual, partials, partial_bytes, counters, n_counters, stream);
 }
 
 int rk_linear_rows(float* y, const float* x, int M, int N, int K, const void* w, int w_type, const void* scales,

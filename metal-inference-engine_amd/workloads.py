@@ -552,16 +552,26 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
     """One decode step for the batch through the backend protocol, in the order of Qwen3_5Model.decode_batch
     (src/models/qwen3_5.py:228-290) -> logits [B, vocab] fp32. The attention layer's q / k norms, partial RoPE and
     KV write are the one fused attention_prep call, the output gate is fused into paged_attention, and (with a
-    backend that has silu_mul_linear) SwiGLU's silu * up runs inside the down projection; the sequences' lengths
-    are not advanced (a benchmark replays the same step)."""
+    backend that has silu_mul_linear) SwiGLU's silu * up runs inside the down projection, and (with one that has
+    rms_norm_linear) every RMSNorm after the first runs inside the linear that follows it, from the sums of squares
+    the linear before it returned; the sequences' lengths are not advanced (a benchmark replays the same step)."""
     cfg = st.cfg
     B = tokens.shape[0]
     slots, tables, lens, positions = layout
     kv = st.pool.kv
     fused = hasattr(backend, "silu_mul_linear")
+    fused_norm = hasattr(backend, "rms_norm_linear")
+    ss = None                       # sums of squares of h's 16-column tiles, from the linear that wrote h
 
     def norm_linear(h, norm_w, wt):
+        if fused_norm and ss is not None:
+            return backend.rms_norm_linear(h, ss, norm_w, cfg.eps, wt)
         return backend.linear(backend.rms_norm(h, norm_w, cfg.eps), wt)
+
+    def residual_linear(x, wt, h):
+        if fused_norm:
+            return backend.linear_ss(x, wt, residual=h)
+        return backend.linear(x, wt, residual=h), None
 
     h = backend.embedding(w["embed_tokens.weight"], tokens)
     for i in range(cfg.layers):
@@ -573,7 +583,7 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
             q, gate = backend.attention_prep(y, w[a + "q_norm.weight"], w[a + "k_norm.weight"], cfg.eps, positions,
                                              cfg.theta, cfg.rot, (cfg.Hq, cfg.Hkv, cfg.d), kv.k[L], kv.v[L], slots)
             o = backend.paged_attention(q, kv.k[L], kv.v[L], tables, lens, cfg.block_size, gate=gate)
-            h = backend.linear(o.reshape(B, cfg.Hq * cfg.d), w[a + "o_proj.weight"], residual=h)
+            h, ss = residual_linear(o.reshape(B, cfg.Hq * cfg.d), w[a + "o_proj.weight"], h)
         else:
             a = p + "linear_attn."
             y = norm_linear(h, w[p + "input_layernorm.weight"], w[a + "in_proj.weight"])
@@ -581,10 +591,12 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
             o = backend.deltanet_decode_batch(y[:, :C], y[:, C:C + Z], y[:, C + Z:C + Z + H], y[:, C + Z + H:],
                                               st.seqs, L, w[a + "conv1d.weight"], w[a + "A_log"], w[a + "dt_bias"],
                                               w[a + "norm.weight"], cfg.eps, (H, cfg.dk, cfg.dv, H * cfg.dk))
-            h = backend.linear(o, w[a + "out_proj.weight"], residual=h)
+            h, ss = residual_linear(o, w[a + "out_proj.weight"], h)
         gu = norm_linear(h, w[p + "post_attention_layernorm.weight"], w[p + "mlp.gate_up.weight"])
         F = gu.shape[1] // 2
-        if fused:
+        if fused_norm:
+            h, ss = backend.silu_mul_linear_ss(gu[:, :F], gu[:, F:], w[p + "mlp.down_proj.weight"], residual=h)
+        elif fused:
             h = backend.silu_mul_linear(gu[:, :F], gu[:, F:], w[p + "mlp.down_proj.weight"], residual=h)
         else:
             h = backend.linear(backend.silu_mul(gu[:, :F], gu[:, F:]), w[p + "mlp.down_proj.weight"], residual=h)

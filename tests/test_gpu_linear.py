@@ -107,3 +107,54 @@ def test_silu_mul_fused_into_the_linear(backend, kind, N, K):
     yd = yd[:8]
     full = backend.silu_mul_linear(yd[:, :K], yd[:, K:], wd)
     assert torch.equal(backend.silu_mul_linear(yd[3:4, :K], yd[3:4, K:], wd), full[3:4])
+
+
+def tile_sums(y):
+    """Sums of squares of y's 16-column tiles [M, ceil(N / 16)] (the last tile zero-padded)."""
+    M, N = y.shape
+    pad = torch.zeros(M, -(-N // 16) * 16)
+    pad[:, :N] = y
+    return (pad * pad).view(M, -1, 16).sum(-1)
+
+
+@pytest.mark.parametrize("N,K", [(2048, 2048), (2048, 6144), (2064, 1024), (100, 96), (8224, 2048)])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
+def test_linear_with_tile_sums_of_squares(backend, kind, N, K):
+    """rk_linear_rows_ex2 with ss_out: y bit-identical to the plain launch, and the tile sums of squares within 1e-6
+    of the fp64 sums of the same y (S == 1 and S > 1 epilogues; N not a multiple of 16 or 32)."""
+    from native import kernels
+    w, _ = weight(kind, N, K, 3 * N + K)
+    wd = to_dev(w)
+    g = torch.Generator().manual_seed(N)
+    for M in (1, 5, 8, 16):
+        x, r = torch.randn(M, K, generator=g), torch.randn(M, N, generator=g)
+        y, ss = kernels.linear_ss(x.to(DEV), wd, residual=r.to(DEV))
+        assert torch.equal(y.cpu(), kernels.linear_rows(x.to(DEV), wd, residual=r.to(DEV)).cpu())
+        assert ss.shape == (M, -(-N // 16))
+        assert rel_err(ss, tile_sums(y.cpu().double()).float()) < 1e-6
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
+@pytest.mark.parametrize("N,K", [(8224, 2048), (12288, 2048), (6144, 1024), (16384, 256), (248320, 2048)])
+def test_rms_norm_fused_into_the_linear(backend, kind, N, K):
+    """RK_X_RMS_NORM: linear(rms_norm(h)) in one launch from the tile sums of squares of the linear that wrote h,
+    against the oracle's rms_norm then linear (1e-5), for 1, 5 and 8 rows; a row's result does not depend on the
+    batch (bit-identical at M = 1 and M = 8); beyond 8 rows (and for N > 16384, the head) the two-launch form
+    runs."""
+    from native import kernels
+    from oracle import ops_ref
+    w, deq = weight(kind, N, K, N + 7 * K)
+    wp, _ = weight("int4", K, 2048, K)                  # the producer of h
+    wd, wpd = to_dev(w), to_dev(wp)
+    g = torch.Generator().manual_seed(K + 1)
+    nw = (1.0 + 0.1 * torch.randn(K, generator=g)).to(DEV)
+    o8, r8 = torch.randn(8, 2048, generator=g), torch.randn(8, K, generator=g)
+    got_by_m = {}
+    for M in (8, 1, 5, 12):                             # 12: the two-launch form
+        o, r = o8[:M] if M <= 8 else torch.randn(M, 2048, generator=g), r8[:M] if M <= 8 else torch.randn(M, K, generator=g)
+        h, ss = kernels.linear_ss(o.to(DEV), wpd, residual=r.to(DEV))
+        got = kernels.rms_norm_linear(h, ss, nw, 1e-6, wd)
+        want = quant_ref.linear(ops_ref.rms_norm(h.cpu(), nw.cpu(), 1e-6), deq, None, None)
+        assert rel_err(got, want) < TOL
+        got_by_m[M] = got.cpu()
+    assert torch.equal(got_by_m[1][0], got_by_m[8][0])
