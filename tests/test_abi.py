@@ -251,3 +251,25 @@ def test_linear_ex_checked_on_host(lib):
     assert call(xld=2047) == 1 and "stride" in lib.last_error()
     assert call(auxld=100) == 1 and "up rows" in lib.last_error()
     assert call(M=0) == 0
+
+
+def test_linear_ex2_checked_on_host(lib):
+    """rk_linear_rows_ex2's RMSNorm transform: the norm weight, the K and row limits and the sums' stride are checked
+    before any launch; rk_linear_rows_ex does not take the transform."""
+    fake = 4096
+    L = lib.lib
+
+    def call(**kw):
+        a = dict(y=fake, ss=None, x=fake, xld=2048, op=2, aux=fake + 8192, auxld=128, nw=fake, eps=1e-6, M=8, N=2048,
+                 K=2048, w=fake, wt=3, s=fake, m=fake, b=None, r=None, p=fake, pb=1 << 30, c=fake, nc=1024)
+        a.update(kw)
+        return L.rk_linear_rows_ex2(*a.values(), None)
+
+    assert call(nw=None) == 1 and "norm weight" in lib.last_error()
+    assert call(nw=fake + 4) == 1 and "norm weight" in lib.last_error()
+    assert call(auxld=127) == 1 and "sums of squares" in lib.last_error()
+    assert call(K=4096, xld=4096, auxld=256) == 1 and "sums of squares" in lib.last_error()
+    assert call(M=9) == 2 and "M <= 8" in lib.last_error()
+    ex = dict(y=fake, x=fake, xld=2048, op=2, aux=fake, auxld=2048, M=8, N=2048, K=2048, w=fake, wt=3, s=fake, m=fake,
+              b=None, r=None, p=fake, pb=1 << 30, c=fake, nc=1024)
+    assert L.rk_linear_rows_ex(*ex.values(), None) == 1 and "input transform 2" in lib.last_error()
