@@ -1,1 +1,1 @@
-"""Backends of the token-mixing path: the protocol slice (base.py) and the ROCm implementation (rocm.py)."""
+"""The ROCm backend of the token-mixing path (rocm.py)."""

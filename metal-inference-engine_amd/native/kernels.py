@@ -12,6 +12,9 @@ DTYPE_CODES = {torch.float32: RK_F32, torch.bfloat16: RK_BF16}
 KV_DTYPES = (torch.float32, torch.bfloat16)
 
 _workspaces: dict[int, torch.Tensor] = {}
+# Buffers replaced by a larger one are kept until the process ends, never freed: a HIP graph captured before the
+# growth still holds their addresses and writes there on every replay, so the allocator must not hand them out again.
+_retired: list[torch.Tensor] = []
 
 
 def _stream(dev: torch.device) -> int:
@@ -39,7 +42,10 @@ def workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     buf = _workspaces.get(idx)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        if buf is not None:
+            _retired.append(buf)
+        grow = 2 * buf.numel() if buf is not None else 0      # geometric growth bounds the retired total
+        buf = torch.empty(max(nbytes, 1 << 20, grow), dtype=torch.uint8, device=dev)
         _workspaces[idx] = buf
     return buf
 
@@ -642,7 +648,10 @@ def linear_counters(dev: torch.device, n: int) -> torch.Tensor:
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     buf = _linear_cnt.get(idx)
     if buf is None or buf.numel() < n:
-        buf = torch.zeros(max(n, 1 << 14), dtype=torch.int32, device=dev)
+        if buf is not None:
+            _retired.append(buf)                               # see _retired: a captured graph may still use it
+        grow = 2 * buf.numel() if buf is not None else 0
+        buf = torch.zeros(max(n, 1 << 14, grow), dtype=torch.int32, device=dev)
         _linear_cnt[idx] = buf
     return buf
 

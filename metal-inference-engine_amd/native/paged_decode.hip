@@ -36,8 +36,6 @@
 #include "rk_device.h"
 #include "rk_internal.h"
 
-#include <stdlib.h>
-
 namespace rk {
 namespace {
 
@@ -725,14 +723,16 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
         const float rs = M == -INFINITY ? 0.0f : fast_exp2(M - mx);
         float4 nk = make_float4(num.x * rs, num.y * rs, num.z * rs, num.w * rs);
         float dk = den * rs;
+        // a slot not in use is selected away, not multiplied by 0: an empty range never wrote its slot, so the
+        // bytes there are whatever the workspace held before (possibly Inf / NaN)
 #pragma unroll
         for (int j = 0; j < kMergeCh; ++j) {
-            const float sc = use[j] ? fast_exp2(mj[j] - mx) : 0.0f;
-            nk.x = fmaf(sc, v[j].x, nk.x);
-            nk.y = fmaf(sc, v[j].y, nk.y);
-            nk.z = fmaf(sc, v[j].z, nk.z);
-            nk.w = fmaf(sc, v[j].w, nk.w);
-            dk = fmaf(sc, lj[j], dk);
+            const float sc = fast_exp2(mj[j] - mx);
+            nk.x = use[j] ? fmaf(sc, v[j].x, nk.x) : nk.x;
+            nk.y = use[j] ? fmaf(sc, v[j].y, nk.y) : nk.y;
+            nk.z = use[j] ? fmaf(sc, v[j].z, nk.z) : nk.z;
+            nk.w = use[j] ? fmaf(sc, v[j].w, nk.w) : nk.w;
+            dk = use[j] ? fmaf(sc, lj[j], dk) : dk;
         }
         num = nk;
         den = dk;
@@ -826,15 +826,10 @@ MergeFn pick_merge(int D, int GP) {
 
 // Workgroups of the split phase (NG groups of Hkv waves): enough for about one tile per group at the tile count's
 // upper bound, capped at the waves per compute unit that stay resident all at once: 8 for 8-wave workgroups (two
-// per SIMD), 4 for 4-wave ones (their registers allow one per SIMD). RK_PAGED_DECODE_WAVES_PER_CU overrides the cap
-// (tuning).
+// per SIMD), 4 for 4-wave ones (their registers allow one per SIMD).
 int split_groups(int B, int Hkv, int block_size, int max_nb, int GP) {
-    static int per_cu_env = [] {
-        const char* e = getenv("RK_PAGED_DECODE_WAVES_PER_CU");
-        return e ? atoi(e) : 0;
-    }();
     const int wpg = waves_per_group(GP);
-    const int per_cu = per_cu_env > 0 ? per_cu_env : (wpg == 8 ? 8 : 4);
+    const int per_cu = wpg == 8 ? 8 : 4;
     const long long upper = (long long)B * (((long long)max_nb * block_size + kTile - 1) / kTile);
     int cus = device_cus();
     if (cus <= 0) cus = 256;

@@ -21,5 +21,9 @@ Pinning status (what checks each function; see tests/test_oracle.py):
                                float64 brute force at dk = dv = 128 (tests/golden/delta_rule_128.npz);
                                special cases S0 = 0, T < 64 padding, beta = g = 0 leaves S unchanged
   backend_ref.deltanet_decode  float64 brute-force step (conv, norms, gates, delta rule, gated norm)
-  prefill_ref.packed_prefill   float64 brute force per segment; packed == per-segment
+  prefill_ref.packed_prefill   float64 brute force per segment: closed-form writes and gather, query i at p + i, the
+                               gate's closed form; n > 512 across the query chunking; the pool bit-exact after the
+                               writes (tests/test_oracle_compositions.py)
+  decode_ref.hybrid_decode_step  a float64 composition of the model's definitions on a 4-layer stack: logits, states,
+                               conv tails and written KV rows (tests/test_oracle_compositions.py)
 """
