@@ -327,7 +327,7 @@ def bench_chunked_delta(args, backend):
     import workloads as wl
     from native import kernels
     from native.rocm_native import load
-    from state import to_device
+    from native.kernels import to_device
     dev = backend.device
     stream = torch.cuda.current_stream(dev)
     case = wl.c4_chunked_delta()
@@ -393,7 +393,7 @@ def bench_linear_prefill(args, backend):
     import workloads as wl
     from native import kernels
     from native.rocm_native import RK_F32, load
-    from state import to_device
+    from native.kernels import to_device
     dev = backend.device
     stream = torch.cuda.current_stream(dev)
     case = wl.lp_linear_prefill()
@@ -721,7 +721,7 @@ def bench_decode_step(args, backend):
                                             t.mins.cpu() if t.mins is not None else None)
             return t.float().cpu()
         wh = {n: host(w[n]) for n in names}
-        kh, vh = st.pool.kv.k.cpu(), st.pool.kv.v.cpu()
+        kh, vh = st.k.cpu(), st.v.cpu()
         Sh, convh = st.pool.S.cpu(), st.pool.conv.cpu()
         seq_index = torch.tensor([q.seq for q in st.seqs])
         lay = [t.cpu() for t in layout]

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 9
+#define RK_ABI_VERSION 10
 
 /* status codes */
 #define RK_OK 0
@@ -108,12 +108,18 @@ int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float
  *   work [n_work] int32: (segment << 16) | query block (blocks of 32 queries), in the order to schedule them
  *   (longest key range first balances the grid); every block of every segment must appear once.
  *   gate NULL or [N, Hq*D] in gate_dtype (RK_F32 or RK_BF16, read as stored). Group size Hq / Hkv = 4, D in {128, 256},
- *   max_nb * block_size^2 < 2^32. bf16 MFMA operands, fp32 accumulation. */
+ *   max_nb * block_size^2 < 2^32. bf16 MFMA operands, fp32 accumulation.
+ *   window 0 or W >= 1 (causal only): query i also sees only positions above start[s] + i - W (the sliding-window
+ *   prefill of src/models/cohere2.py:155-163; ops.attention's window, src/ops.py:77-81, 97-98); blocks wholly below
+ *   every query's window are never read. causal 0: every query of segment s sees positions 0 .. start[s]+n[s]-1
+ *   (ops.attention with causal=False). k_new = v_new = NULL: nothing is written (the keys are already in the pool);
+ *   this is how Backend.attention with T > 1 (src/backend/base.py:32-35) runs on a contiguous [S, Hkv, D] cache
+ *   viewed as one block of S positions, start = S - T. */
 int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, const void* v_new, int new_dtype,
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
                      int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
-                     void* stream);
+                     int window, int causal, void* stream);
 
 /* ---- P3: chunked gated delta rule (64-token chunks, WY / UT form) for packed prefill of the linear-attention
  * layers. Replaces Backend.gated_delta with T > 1 (TorchBackend.gated_delta -> ops.gated_delta_chunked,

@@ -9,10 +9,11 @@ Method -> kernel:
   paged_attention        rk_paged_decode   (P1; + optional fused sigmoid gate)
   attention, T == 1      rk_paged_decode on the contiguous cache viewed as one block (the reference's
                          attention_decode, src/backend/metal.py:197-210)
+  attention, T > 1       rk_paged_prefill on the same one-block view, no KV write (causal, optional window)
   deltanet_decode[_batch] rk_deltanet_decode (P2; states of one HybridPool in one launch, a standalone state as a
                          pool of one, src/backend/metal.py:232-256)
   paged_prefill_attention rk_paged_prefill (P4; the packed prefill of full_attention, src/models/qwen3_5.py:112-120:
-                         KV write-back, causal attention over prefix + new tokens, fused gate)
+                         KV write-back, causal attention over prefix + new tokens, fused gate; optional window)
   gated_delta[_packed]   rk_gated_delta_chunked (P3; the chunked delta rule of the linear-attention prefill,
                          src/models/qwen3_5.py:157, for one sequence or many packed sequences per launch pair)
   causal_conv1d          rk_causal_conv1d (src/ops.py:127-139)
@@ -87,12 +88,14 @@ class RocmBackend:
         return kernels.paged_decode(q, k_pool, v_pool, tables, lens, block_size, window, gate)
 
     def attention(self, q, k, v, causal=True, window=None):
-        """q [T, Hq, d], k/v [S, Hkv, d] -> [T, Hq, d] fp32. T == 1 (decode on a contiguous cache) runs the paged
-        decode kernel on the cache viewed as a single block."""
+        """Backend.attention (src/backend/base.py:32-35): q [T, Hq, d], k/v [S, Hkv, d] -> [T, Hq, d] fp32; query i
+        sits at position S - T + i; with a window W it sees its last W keys (ops.attention, src/ops.py:65-104).
+        T == 1 (decode on a contiguous cache) runs the paged decode kernel on the cache viewed as a single block;
+        T > 1 (the per-segment prefill of src/models/qwen3_5.py:118 and src/models/cohere2.py:163) runs the prefill
+        attention kernel on the same one-block view, with no KV write."""
         T, Hq, d = q.shape
         if T != 1:
-            raise NotImplementedError("RocmBackend.attention: multi-query prefill attention goes through "
-                                      "paged_prefill_attention")
+            return kernels.attention(q, k, v, causal, window)
         if window is not None and window < 1:
             raise ValueError(f"window must be at least 1, not {window}")
         if window and k.shape[0] > window:
@@ -108,14 +111,16 @@ class RocmBackend:
 
     # ---- P4: packed prefill attention
     def paged_prefill_attention(self, q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
-                                gate=None):
+                                gate=None, window=None):
         """Packed prefill of one attention layer for S segments: writes k_new / v_new [N, Hkv, d] into the pool
         layer at positions start_pos[s] + i of segment s (rows cu_seqlens[s] .. cu_seqlens[s+1]-1, block-table row
         s of tables [S, max_nb]), then causal attention of q [N, Hq, d] over each segment's prefix and new keys
         -> [N, Hq, d] fp32, times sigmoid(gate [N, Hq*d]) when given. The reference runs this per segment as
-        kv.write -> kv.read -> attention(causal) -> gate (src/models/qwen3_5.py:112-120)."""
+        kv.write -> kv.read -> attention(causal) -> gate (src/models/qwen3_5.py:112-120). With a window W each query
+        sees its last W positions (the sliding layers' prefill, src/models/cohere2.py:155-163), and blocks below
+        every query's window are never read."""
         return kernels.paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
-                                     gate)
+                                     gate, window=window)
 
     # ---- P3: chunked gated delta rule
     def gated_delta(self, q, k, v, beta, g, S):

@@ -12,10 +12,12 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB = HERE / "librk_path.so"
+PROBE_LIB = HERE / "librk_probe.so"       # measurement probes (include/rk_probe.h), not on the path
 OBJ_DIR = HERE / "_obj"
 SOURCES = ["rk_abi.cpp", "paged_decode.hip", "kv_cache.hip", "deltanet_step.hip", "paged_prefill.hip",
            "chunked_delta.hip", "deltanet_prefill.hip", "attn_prep.hip",
            "linear.hip", "decode_ops.hip"]
+PROBE_SOURCES = ["probes.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 # packed-fp32 VALU forms are switched off for all device code (see the header of rk_device.h)
@@ -38,19 +40,26 @@ def _compile(src: str, verbose: bool) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source and link librk_path.so (always rebuilds). Returns the library path."""
-    OBJ_DIR.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(lib: Path, objs: list[Path], verbose: bool) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", "-o", str(tmp)] + [str(o) for o in objs] + [f"--offload-arch={ARCH}", "-fPIC"]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError("link failed:\n" + r.stderr)
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {lib.name} failed:\n" + r.stderr)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link librk_path.so and librk_probe.so (always rebuilds). Returns the path
+    library."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    srcs = SOURCES + PROBE_SOURCES
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = dict(zip(srcs, ex.map(lambda s: _compile(s, verbose), srcs)))
+    _link(LIB, [objs[s] for s in SOURCES], verbose)
+    _link(PROBE_LIB, [objs[s] for s in PROBE_SOURCES] + [objs["rk_abi.cpp"]], verbose)
     return LIB
 
 

@@ -17,6 +17,16 @@ _workspaces: dict[int, torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
 
 
+def to_device(t: torch.Tensor, device) -> torch.Tensor:
+    """A small host tensor (offsets, positions, work lists) on `device`, copied without waiting for queued kernels:
+    from a private pinned clone, which keeps the host bytes unchanged until the copy has read them whatever the
+    caller does with its own tensor afterwards."""
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        return t.to(dev)
+    return t.clone().pin_memory().to(dev, non_blocking=True)
+
+
 def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
@@ -185,29 +195,63 @@ def deltanet_decode(qkv, z, b, a, conv_state, S, seq_index, slot: int, conv_w, A
 PREFILL_BLOCK = 32          # queries per work item of rk_paged_prefill
 
 
-def prefill_work(lengths: list[int], starts: list[int]) -> list[int]:
+def prefill_work(lengths: list[int], starts: list[int], window: int | None = None, causal: bool = True) -> list[int]:
     """The work list of rk_paged_prefill: one item (segment << 16 | query block) per block of 32 new queries,
-    longest key range first so the longest items start first."""
+    longest key range first so the longest items start first (a window bounds an item's range to about W + 32
+    keys; without causal masking every item of a segment reads all of its keys)."""
     items = []
     for s, (n, p) in enumerate(zip(lengths, starts)):
         for qb in range(-(-n // PREFILL_BLOCK)):
-            items.append((p + min(n, (qb + 1) * PREFILL_BLOCK), (s << 16) | qb))
+            hi = p + min(n, (qb + 1) * PREFILL_BLOCK) if causal else p + n
+            lo = max(0, p + qb * PREFILL_BLOCK - window + 1) if window else 0
+            items.append((hi - lo, (s << 16) | qb))
     items.sort(key=lambda x: -x[0])
     return [w for _, w in items]
 
 
+def _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu: list[int], st: list[int], gate,
+                    window: int, causal: bool) -> None:
+    """rk_paged_prefill with the host-side segment offsets, start positions and work list in one int32 array."""
+    S = len(st)
+    N, Hq, d = q.shape
+    NB, bs, Hkv, _ = k_pool.shape
+    dev = q.device
+    meta = to_device(torch.tensor(cu + st + prefill_work([b - a for a, b in zip(cu, cu[1:])], st, window, causal),
+                                  dtype=torch.int32), dev)
+    n_work = meta.numel() - (2 * S + 1)
+    load().call("rk_paged_prefill", out.data_ptr(), q.data_ptr(), DTYPE_CODES[q.dtype],
+                k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
+                DTYPE_CODES[k_new.dtype] if k_new is not None else DTYPE_CODES[torch.float32],
+                k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype], tables.data_ptr(), tables.shape[1],
+                meta.data_ptr(), meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq,
+                Hkv, d, bs, NB, gate.data_ptr() if gate is not None else None,
+                DTYPE_CODES[gate.dtype] if gate is not None else DTYPE_CODES[torch.float32], int(window or 0),
+                1 if causal else 0, _stream(dev))
+
+
+def _prefill_shape_check(name: str, Hq: int, Hkv: int, d: int) -> None:
+    if Hkv < 1 or Hq % Hkv or Hq // Hkv != 4:
+        raise NotImplementedError(f"{name}: the prefill attention kernel is built for 4 query heads per kv-head, "
+                                  f"not {Hq} / {Hkv}")
+    if d not in (128, 256):
+        raise NotImplementedError(f"{name}: the prefill attention kernel is built for head_dim 128 or 256, not {d}")
+
+
 def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size: int, gate=None,
-                  out=None) -> torch.Tensor:
+                  out=None, window: int | None = None) -> torch.Tensor:
     """Packed prefill attention (rk_paged_prefill): writes the new K/V rows into one pool layer, then causal GQA
-    attention of every segment's new queries over its prefix + new keys -> [N, Hq, d] fp32 (* sigmoid(gate)).
-    cu_seqlens (S + 1 row offsets) and start_pos (S absolute positions) are host-side lists / CPU tensors, as the
-    packing step produces them; tables [S, max_nb] int32 on the device."""
+    attention of every segment's new queries over its prefix + new keys -> [N, Hq, d] fp32 (* sigmoid(gate)); with a
+    window W each query sees only its last W positions. cu_seqlens (S + 1 row offsets) and start_pos (S absolute
+    positions) are host-side lists / CPU tensors, as the packing step produces them; tables [S, max_nb] int32 on
+    the device."""
     name = "paged_prefill"
     cu = [int(x) for x in cu_seqlens]
     st = [int(x) for x in start_pos]
     S = len(st)
     if len(cu) != S + 1 or cu[0] != 0 or any(b < a for a, b in zip(cu, cu[1:])):
         raise ValueError(f"{name}: cu_seqlens {cu[:8]}... must be S + 1 non-decreasing offsets from 0")
+    if window is not None and window < 1:
+        raise ValueError(f"window must be at least 1, not {window}")
     N, Hq, d = q.shape
     if cu[-1] != N or k_new.shape[0] != N or v_new.shape != k_new.shape:
         raise ValueError(f"{name}: q {tuple(q.shape)}, k_new {tuple(k_new.shape)}, cu_seqlens end {cu[-1]}")
@@ -216,6 +260,7 @@ def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos
     NB, bs, Hkv, dp = k_pool.shape
     if dp != d or bs != block_size or k_new.shape[1:] != (Hkv, d):
         raise ValueError(f"{name}: pool {tuple(k_pool.shape)} vs q {tuple(q.shape)}, k_new {tuple(k_new.shape)}")
+    _prefill_shape_check(name, Hq, Hkv, d)
     if tables.dim() != 2 or tables.shape[0] != S or tables.dtype != torch.int32:
         raise ValueError(f"{name}: tables {tuple(tables.shape)} {tables.dtype} for {S} segments")
     for s in range(S):
@@ -234,16 +279,54 @@ def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos
         out = torch.empty(N, Hq, d, dtype=torch.float32, device=dev)
     if N == 0:
         return out
-    from state import to_device
-    meta = to_device(torch.tensor(cu + st + prefill_work([b - a for a, b in zip(cu, cu[1:])], st),
-                                  dtype=torch.int32), dev)
-    n_work = meta.numel() - (2 * S + 1)
-    load().call("rk_paged_prefill", out.data_ptr(), q.data_ptr(), DTYPE_CODES[q.dtype], k_new.data_ptr(),
-                v_new.data_ptr(), DTYPE_CODES[k_new.dtype], k_pool.data_ptr(), v_pool.data_ptr(),
-                DTYPE_CODES[k_pool.dtype], tables.data_ptr(), tables.shape[1], meta.data_ptr(),
-                meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq, Hkv, d, bs, NB,
-                gate.data_ptr() if gate is not None else None,
-                DTYPE_CODES[gate.dtype] if gate is not None else DTYPE_CODES[torch.float32], _stream(dev))
+    _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu, st, gate, window or 0, True)
+    return out
+
+
+_ONE_BLOCK = 65535          # a contiguous cache up to this many positions is viewed as one pool block
+
+
+def attention(q, k, v, causal: bool = True, window: int | None = None) -> torch.Tensor:
+    """Backend.attention for T >= 1 queries (src/backend/base.py:32-35, ops.attention, src/ops.py:65-104):
+    q [T, Hq, d], k / v [S, Hkv, d] (fp32 or bf16 read as stored, anything else widened) -> [T, Hq, d] fp32; query i
+    sits at position S - T + i. The cache is viewed as a pool of one block holding all S positions (longer caches
+    are copied into blocks of 1024) and run through rk_paged_prefill with no KV write; with a window the keys no
+    query sees are dropped first, as the reference does."""
+    name = "attention"
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
+        raise ValueError(f"{name}: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if window is not None and window < 1:
+        raise ValueError(f"window must be at least 1, not {window}")
+    T, Hq, d = q.shape
+    S, Hkv, dk = k.shape
+    if dk != d:
+        raise ValueError(f"{name}: q head_dim {d}, k head_dim {dk}")
+    if S < T:
+        raise ValueError(f"{name}: {T} queries need at least as many keys, got {S}")
+    _prefill_shape_check(name, Hq, Hkv, d)
+    dev = _need_cuda(name, q, k, v)
+    if window is not None and S > T + window - 1:       # older than the first query's window: no query sees them
+        k, v = k[S - T - window + 1:], v[S - T - window + 1:]
+        S = k.shape[0]
+    if k.dtype != v.dtype or k.dtype not in KV_DTYPES:
+        k, v = k.float(), v.float()
+    q = (q if q.dtype in KV_DTYPES else q.float()).contiguous()
+    out = torch.empty(T, Hq, d, dtype=torch.float32, device=dev)
+    if T == 0:
+        return out
+    if S <= _ONE_BLOCK:
+        bs, nb = S, 1
+        kp, vp = k.contiguous().view(1, S, Hkv, d), v.contiguous().view(1, S, Hkv, d)
+    else:
+        bs = 1024
+        nb = -(-S // bs)
+        kp = torch.zeros(nb * bs, Hkv, d, dtype=k.dtype, device=dev)
+        vp = torch.zeros(nb * bs, Hkv, d, dtype=v.dtype, device=dev)
+        kp[:S], vp[:S] = k, v
+        kp, vp = kp.view(nb, bs, Hkv, d), vp.view(nb, bs, Hkv, d)
+    tables = torch.arange(nb, dtype=torch.int32, device=dev).view(1, nb)
+    _prefill_launch(out, q, None, None, kp, vp, tables, [0, T], [S - T], None,
+                    (window or 0) if causal else 0, causal)
     return out
 
 
@@ -291,7 +374,6 @@ def gated_delta_chunked(q, k, v, beta, g, S, cu_seqlens, seq_index=None, out=Non
     cuc = [0]
     for a, b in zip(cu, cu[1:]):
         cuc.append(cuc[-1] + -(-(b - a) // DELTA_CHUNK))
-    from state import to_device
     meta = to_device(torch.tensor(cu + cuc, dtype=torch.int32), dev)
     lib = load()
     nbytes = lib.lib.rk_gated_delta_workspace_bytes(cuc[-1], H)
@@ -361,7 +443,6 @@ def deltanet_prefill_front(qkv, b, a, conv_state, seq_index, conv_w, A_log, dt_b
         if len(cu) < 2 or cu[0] != 0 or cu[-1] != N or any(hi < lo for lo, hi in zip(cu, cu[1:])):
             raise ValueError(f"{name}: cu_seqlens {cu[:8]}... must be non-decreasing offsets from 0 to {N}")
         n_seqs = len(cu) - 1
-        from state import to_device
         cu_dev = to_device(torch.tensor(cu, dtype=torch.int32), dev)
     if conv_state is not None:
         if conv_state.dtype != torch.float32 or conv_state.dim() != 3 or conv_state.shape[1:] != (K - 1, C) or \

@@ -13,10 +13,18 @@
 //      fp32 accumulation throughout; operands are bf16 (q, k, v as stored; p rounded), so results carry bf16-level
 //      error.
 //   3. The output is divided by the softmax sum, gated and written as fp32 [N, Hq, D].
+// With a window W (causal only), query i also sees only keys above position p[s]+i-W (src/ops.py:77-81, 97-98): a
+// work item starts at the tile holding its first query's first visible key, so whole tiles below every query's
+// window are never read, and the keys below it in that first tile are read as that key (never from blocks outside
+// the window) and masked. Without causal masking every query of a segment sees all its keys (ops.attention with
+// causal=False). Without new rows (k_new null) nothing is written: the keys are already in the pool, which is how
+// Backend.attention's contiguous K / V run here (one block holding all S positions).
 // Bounds: key positions past a segment's length are clamped for addressing (and masked), table entries clamped to
 // the pool, query rows past the segment clamped for loading (and not stored).
 #include "rk_device.h"
 #include "rk_internal.h"
+
+#include <climits>
 
 namespace rk {
 namespace {
@@ -41,6 +49,8 @@ struct PrefillArgs {
     const int32_t* work;        // [n_work] (segment << 16) | query block, longest first
     const void* gate;           // [N, Hq * D] gate_dtype, or null
     int gate_dtype;
+    int window;                 // 0: none; W: keys above position - W (causal only)
+    int causal;                 // 0: every query sees all of its segment's keys
     int q_dtype, new_dtype, pool_dtype;
     int S, n_work, N, Hq, Hkv, G, bs, max_nb, num_blocks;
     float qscale;               // log2(e) / sqrt(D)
@@ -192,15 +202,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int row0 = a.cu[seg] + qblk * kBQ;
     const int nq = min(kBQ, a.cu[seg + 1] - row0);
     const int p0 = a.start[seg] + qblk * kBQ;       // position of the block's first query
-    const int n_keys = p0 + nq;                      // keys 0 .. p0 + nq - 1
-    const int n_tiles = (n_keys + kBKP - 1) / kBKP;
+    // keys kmin .. n_keys - 1: causal, up to the last query (and from the first query's window); otherwise the
+    // whole segment
+    const int n_keys = a.causal ? p0 + nq : a.start[seg] + (a.cu[seg + 1] - a.cu[seg]);
+    const int kmin = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
+    const int t_first = kmin / kBKP;                 // tiles t_first .. t_first + n_tiles - 1
+    const int n_tiles = (n_keys + kBKP - 1) / kBKP - t_first;
+    const int b_first = kmin / a.bs;                 // first block read
     const int32_t* table = a.tables + (long long)seg * a.max_nb;
 
     if (TAB_LDS) {
         const int nb = (n_keys + a.bs - 1) / a.bs;  // <= max_nb <= kTabCache
-        for (int i = tid; i < nb; i += blockDim.x) {
+        for (int i = b_first + tid; i < nb; i += blockDim.x) {
             const int blk = table[i];
-            tab[i] = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+            tab[i - b_first] = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
         }
     }
 
@@ -221,13 +236,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // rows then differ by a constant stride), one per key otherwise
     const bool rows4 = a.bs % 4 == 0;
     const long long rstride = (long long)a.Hkv * D;
-    auto issue = [&](int tile, PoolRow<TP> (&slot)[8]) {
+    auto issue = [&](int t_rel, PoolRow<TP> (&slot)[8]) {
+        const int tile = t_first + t_rel;
         // pos = b * bs + r with b = mulhi(pos, ceil(2^32 / bs)): exact because pos * bs < 2^32 (checked on the host)
         auto row_of = [&](int pos) {
             const int b = (int)__umulhi((uint32_t)pos, a.bs_recip);
             int blk;
             if (TAB_LDS) {
-                blk = tab[b];
+                blk = tab[b - b_first];
             } else {
                 blk = table[b];
                 blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
@@ -237,8 +253,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         auto group = [&](int kq, int dc, const void* base, PoolRow<TP>* rows) {
             const int p4 = tile * kBKP + 4 * kq;
             if (rows4) {
-                // tiles past the end re-read the last key (never used); a clamped group of 4 stays in its block
-                const int pos = p4 + 3 < n_keys ? p4 : (n_keys - 1) / 4 * 4;
+                // tiles past the end re-read the last key (never used); a clamped group of 4 stays in its block;
+                // groups below the window read the group holding its first key (same block: bs % 4 == 0)
+                int pos = p4 + 3 < n_keys ? p4 : (n_keys - 1) / 4 * 4;
+                pos = pos < kmin ? kmin / 4 * 4 : pos;
                 const long long off = (row_of(pos) * a.Hkv + kvh) * D + 8 * dc;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) rows[j].load(base, off + j * rstride);
@@ -247,6 +265,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 for (int j = 0; j < 4; ++j) {
                     int pos = p4 + j;
                     pos = pos < n_keys ? pos : n_keys - 1;
+                    pos = pos < kmin ? kmin : pos;
                     rows[j].load(base, (row_of(pos) * a.Hkv + kvh) * D + 8 * dc);
                 }
             }
@@ -277,15 +296,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // ---- consumer state
     const int head = kvh * G + (producer ? 0 : wave);
     const int col = lane & 31, kg = lane >> 5;      // query column, k-slot group
-    const int qpos = p0 + (col < nq ? col : nq - 1);
+    const int qpos = a.causal ? p0 + (col < nq ? col : nq - 1) : n_keys - 1;
+    const int qlo = a.window > 0 ? qpos - a.window : -1;    // keys at or below qlo are outside the window
+    const int qfirst = a.causal ? p0 : n_keys - 1;           // the smallest qpos of the work item
+    const int qlast = a.causal ? p0 + nq - 1 : n_keys - 1;    // the largest
+    // tiles starting at or below lo_edge hold keys outside some query's window; tiles reaching past qfirst hold keys
+    // after some query: only those are masked
+    const int lo_edge = a.window > 0 ? qlast - a.window : INT_MIN;
     u32x4 qop[NKS];                                  // Q^T operands: q[query col][d = 16 t + 8 kg .. + 8]
     f32x16 o[NDT];
     float m_run = -INFINITY, l_run = 0.0f;
 
     if (TAB_LDS) __syncthreads();                    // the block ids are in LDS
 
-    auto consume = [&](int tile, int stage) {
-        const int k0 = tile * kBKP;
+    auto consume = [&](int t_rel, int stage) {
+        const int k0 = (t_first + t_rel) * kBKP;
         const uint16_t* ks = kst + stage * KBUF;
         const uint16_t* vt = vst + stage * VBUF;
         // ---- S^T = K Q^T for the 32 keys; the K operands of the next two k-steps are requested before this
@@ -312,18 +337,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // maximum m is raised only when a tile's maximum exceeds it by more than kLazy: p = 2^(s - m) then stays
         // <= 2^kLazy (exact in fp32, representable in bf16), and the accumulators are rescaled only when some
         // column's m moves, which after the first tiles is rare.
-        if (k0 + kBKP - 1 > p0) {
+        if (k0 + kBKP - 1 > qfirst || k0 <= lo_edge) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r / 4) + 4 * kg + (r % 4);
-                s[r] = key <= qpos ? s[r] : -INFINITY;
+                s[r] = key <= qpos && key > qlo ? s[r] : -INFINITY;
             }
         }
         float tmax = s[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.qscale;
-        const float m_new = tmax > m_run + kLazy ? tmax : m_run;   // finite: key 0 <= qpos is in the first tile
+        const float m_new = tmax > m_run + kLazy ? tmax : m_run;
+        // -inf only while every key this column has seen was masked (a window starting past the first tile); then
+        // the exponents are taken against 0, so the masked keys give 0 (not NaN) and nothing is rescaled
+        const float mb = m_new == -INFINITY ? 0.0f : m_new;
         float psum = 0.0f;
         u32x4 pop[2];                                // B operands of the 2 key k-steps
 #pragma unroll
@@ -331,7 +359,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             float pv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                pv[e] = fast_exp2(fmaf(s[8 * half + e], a.qscale, -m_new));
+                pv[e] = fast_exp2(fmaf(s[8 * half + e], a.qscale, -mb));
                 psum += pv[e];
             }
             u32x4 w;
@@ -341,7 +369,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         psum += __shfl_xor(psum, 32);
         if (__any(m_new != m_run)) {
-            const float alpha = fast_exp2(m_run - m_new);   // 0 on the first tile (m_run = -inf)
+            const float alpha = fast_exp2(m_run - mb);      // 0 on the first tile (m_run = -inf)
             l_run *= alpha;
 #pragma unroll
             for (int t = 0; t < NDT; ++t) o[t] *= alpha;
@@ -482,10 +510,13 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
                      int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
-                     void* stream) {
+                     int window, int causal, void* stream) {
     if (N == 0) return RK_OK;
-    if (!out || !q || !k_new || !v_new || !k_pool || !v_pool || !tables || !cu_seqlens || !start_pos || !work)
+    if (!out || !q || !k_pool || !v_pool || !tables || !cu_seqlens || !start_pos || !work)
         return fail(RK_ERR_ARG, "rk_paged_prefill: null pointer");
+    if (!k_new != !v_new) return fail(RK_ERR_ARG, "rk_paged_prefill: k_new and v_new must both be given or both null");
+    if (window < 0 || (window > 0 && !causal))
+        return fail(RK_ERR_ARG, "rk_paged_prefill: window %d (>= 0, and only with causal masking)", window);
     if (S < 1 || N < 1 || n_work < 1 || n_work > 65535 * 8 || max_nb < 1 || block_size < 1 || num_blocks < 1)
         return fail(RK_ERR_ARG, "rk_paged_prefill: S %d N %d n_work %d max_nb %d block_size %d", S, N, n_work, max_nb,
                     block_size);
@@ -496,21 +527,23 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     if ((unsigned long long)max_nb * block_size * block_size >= (1ull << 32))
         return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d blocks of %d positions (positions x block size must stay "
                     "below 2^32)", max_nb, block_size);
-    for (int dt : {q_dtype, new_dtype, pool_dtype, gate ? gate_dtype : RK_F32})
+    for (int dt : {q_dtype, k_new ? new_dtype : RK_F32, pool_dtype, gate ? gate_dtype : RK_F32})
         if (dt != RK_F32 && dt != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: dtype %d", dt);
     PrefillArgs a;
     a.out = out; a.q = q; a.k_new = k_new; a.v_new = v_new; a.kp = k_pool; a.vp = v_pool; a.tables = tables;
     a.cu = cu_seqlens; a.start = start_pos; a.work = work; a.gate = gate; a.gate_dtype = gate_dtype;
+    a.window = window; a.causal = causal ? 1 : 0;
     a.q_dtype = q_dtype; a.new_dtype = new_dtype; a.pool_dtype = pool_dtype;
     a.S = S; a.n_work = n_work; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.bs = block_size;
     a.max_nb = max_nb; a.num_blocks = num_blocks;
     a.qscale = kLog2e / sqrtf((float)D);
     a.bs_recip = (uint32_t)(0xffffffffu / (uint32_t)block_size + 1u);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const long long threads = (long long)N * (Hkv * D / 8);
-    hipLaunchKernelGGL(prefill_kv_write, dim3((unsigned)ceil_div((size_t)threads, 256)), dim3(256), 0, s, a, D);
-    int rc = check_launch("prefill_kv_write");
-    if (rc) return rc;
+    if (k_new) {
+        const long long threads = (long long)N * (Hkv * D / 8);
+        hipLaunchKernelGGL(prefill_kv_write, dim3((unsigned)ceil_div((size_t)threads, 256)), dim3(256), 0, s, a, D);
+        if (int rc = check_launch("prefill_kv_write")) return rc;
+    }
     const bool tab_lds = max_nb <= kTabCache;
     const size_t lds = (tab_lds ? kTabCache * 4 : 0) +
                        (size_t)kStages * (kBKP * (D + kKPad) + D * (kBKP + kVPad)) * sizeof(uint16_t);

@@ -1,0 +1,96 @@
+// Measurement probes: what the memory system gives for the access patterns of the two decode kernels, with no
+// arithmetic. They bound what the kernels can reach and are not on the path (no counterpart in the reference).
+//
+//   probe_block_stream: reads whole 16-position KV tiles (both pools) given as a list of pool tile offsets, in the
+//     list's order, with 16-byte loads, and keeps an xor of everything read. With the decode's own tiles in table
+//     order this is the paged decode's K/V traffic (scattered 16 KiB blocks) without the softmax or the merge; with
+//     the same tiles sorted by address it is a near-sequential stream of the same bytes.
+//   probe_state_rmw: reads each selected (sequence, head) state block of the DeltaNet pool, scales it, and writes it
+//     back: the recurrent step's state traffic (one read and one write of 64 KiB per head) without the conv, norms
+//     or delta rule, with `split` workgroups per head.
+#include "rk_device.h"
+#include "rk_internal.h"
+
+namespace rk {
+namespace {
+
+constexpr int kProbeWaves = 8;
+
+// Each wave takes tiles w, w + waves, ... of the list; a tile is 64 * kVec * 16 contiguous bytes at the listed
+// offset in each pool (kVec 16-byte loads per lane and pool, all issued before any is used).
+template <int kVec>
+__global__ __launch_bounds__(64 * kProbeWaves) void probe_block_stream(const char* kp, const char* vp,
+                                                                        const long long* tiles, int n_tiles,
+                                                                        uint32_t* sink) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * kProbeWaves + (threadIdx.x >> 6);
+    const int waves = gridDim.x * kProbeWaves;
+    uint32_t acc = 0;
+    for (int t = wave; t < n_tiles; t += waves) {
+        const long long off = tiles[t] + 16ll * lane;
+        u32x4 x[2 * kVec];
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+            x[j] = *reinterpret_cast<const u32x4*>(kp + off + 1024ll * j);
+            x[kVec + j] = *reinterpret_cast<const u32x4*>(vp + off + 1024ll * j);
+        }
+#pragma unroll
+        for (int j = 0; j < 2 * kVec; ++j) acc ^= x[j][0] ^ x[j][1] ^ x[j][2] ^ x[j][3];
+    }
+    sink[blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
+// One workgroup of 256 threads per (batch row, head, part): part p of `split` covers state rows
+// [p * dk / split, (p + 1) * dk / split) of the head's dk x dv block.
+__global__ __launch_bounds__(256) void probe_state_rmw(float* S, const int32_t* seq_index, int n_linear, int slot,
+                                                       int H, int dk, int dv, int split, float scale) {
+    const int part = blockIdx.x % split;
+    const int h = (blockIdx.x / split) % H;
+    const int b = blockIdx.x / (split * H);
+    const long long head = (((long long)seq_index[b] * n_linear + slot) * H + h) * dk * dv;
+    const int n4 = dk * dv / 4 / split;
+    float4* p = reinterpret_cast<float4*>(S + head) + (long long)part * n4;
+    constexpr int kMax = 16;                    // float4 per thread held at once (64 KiB / 256 threads)
+    float4 x[kMax];
+#pragma unroll
+    for (int i = 0; i < kMax; ++i)
+        if (threadIdx.x + 256 * i < n4) x[i] = p[threadIdx.x + 256 * i];
+#pragma unroll
+    for (int i = 0; i < kMax; ++i)
+        if (threadIdx.x + 256 * i < n4)
+            p[threadIdx.x + 256 * i] = make_float4(x[i].x * scale, x[i].y * scale, x[i].z * scale, x[i].w * scale);
+}
+
+}  // namespace
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" {
+
+int rk_probe_block_stream(const void* k_pool, const void* v_pool, const long long* tile_offsets, int n_tiles,
+                          int tile_bytes, int workgroups, uint32_t* sink, void* stream) {
+    if (!k_pool || !v_pool || !tile_offsets || !sink || n_tiles < 1 || workgroups < 1)
+        return fail(RK_ERR_ARG, "rk_probe_block_stream: null pointer or empty list");
+    typedef void (*Fn)(const char*, const char*, const long long*, int, uint32_t*);
+    Fn fn = tile_bytes == 16384 ? probe_block_stream<16> : tile_bytes == 8192 ? probe_block_stream<8>
+          : tile_bytes == 4096 ? probe_block_stream<4> : nullptr;
+    if (!fn) return fail(RK_ERR_ARG, "rk_probe_block_stream: tile_bytes %d (4096, 8192 or 16384)", tile_bytes);
+    hipLaunchKernelGGL(fn, dim3(workgroups), dim3(64 * kProbeWaves), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const char*>(k_pool), static_cast<const char*>(v_pool), tile_offsets, n_tiles,
+                       sink);
+    return check_launch("probe_block_stream");
+}
+
+int rk_probe_state_rmw(float* S, const int32_t* seq_index, int B, int n_linear, int slot, int H, int dk, int dv,
+                       int split, float scale, void* stream) {
+    if (!S || !seq_index || B < 1 || H < 1 || n_linear < 1 || slot < 0 || slot >= n_linear)
+        return fail(RK_ERR_ARG, "rk_probe_state_rmw: bad arguments");
+    if (split < 1 || (dk * dv / 4) % split || dk * dv / 4 / split > 16 * 256)
+        return fail(RK_ERR_ARG, "rk_probe_state_rmw: split %d of a %d x %d block", split, dk, dv);
+    hipLaunchKernelGGL(probe_state_rmw, dim3(B * H * split), dim3(256), 0, static_cast<hipStream_t>(stream), S,
+                       seq_index, n_linear, slot, H, dk, dv, split, scale);
+    return check_launch("probe_state_rmw");
+}
+
+}  // extern "C"

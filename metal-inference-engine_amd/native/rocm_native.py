@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 RK_F32, RK_BF16 = 0, 1
 RK_W_BF16, RK_W_INT8, RK_W_INT4 = 1, 2, 3
@@ -33,7 +33,7 @@ SIGNATURES = {
     "rk_kv_gather": (c_int, [P, P, P, P, c_int, P] + [c_int] * 7 + [P]),
     "rk_deltanet_decode": (c_int, [P] * 5 + [c_longlong] * 3 + [P] * 7 + [c_int] * 7 + [c_float, P]),
     "rk_paged_prefill": (c_int, [P, P, c_int, P, P, c_int, P, P, c_int, P, c_int, P, P, P] + [c_int] * 8
-                         + [P, c_int, P]),
+                         + [P, c_int, c_int, c_int, P]),
     "rk_gated_delta_workspace_bytes": (c_size_t, [c_int, c_int]),
     "rk_gated_delta_chunked": (c_int, [P, P, c_longlong, P, P, P, c_int, P, P, P, P, P] + [c_int] * 5
                                + [P, c_size_t, P]),
@@ -57,6 +57,14 @@ SIGNATURES = {
 }
 
 
+PROBE_LIB_PATH = HERE / "librk_probe.so"
+# the measurement probes of include/rk_probe.h (their library also exports rk_last_error)
+PROBE_SIGNATURES = {
+    "rk_probe_block_stream": (c_int, [P, P, P, c_int, c_int, c_int, P, P]),
+    "rk_probe_state_rmw": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P]),
+}
+
+
 class RocmKernelError(RuntimeError):
     """A C-ABI call returned a nonzero status."""
 
@@ -64,12 +72,13 @@ class RocmKernelError(RuntimeError):
 class NativeRocm:
     """The loaded library with typed entry points. call(name, *args) raises RocmKernelError on a nonzero status."""
 
-    def __init__(self, path: Path = LIB_PATH):
+    def __init__(self, path: Path = LIB_PATH, signatures: dict = SIGNATURES):
         if not Path(path).exists():
             raise FileNotFoundError(f"{path} is missing: build it with `python metal-inference-engine_amd/native/build.py` "
                                     "(or __graft_entry__.build())")
         lib = ctypes.CDLL(str(path))
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in {**signatures, "rk_last_error": SIGNATURES["rk_last_error"],
+                                  "rk_abi_version": SIGNATURES["rk_abi_version"]}.items():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
@@ -97,3 +106,14 @@ def load() -> NativeRocm:
     if _lib is None:
         _lib = NativeRocm()
     return _lib
+
+
+_probes: NativeRocm | None = None
+
+
+def load_probes() -> NativeRocm:
+    """The measurement-probe library (librk_probe.so), loaded on first use."""
+    global _probes
+    if _probes is None:
+        _probes = NativeRocm(PROBE_LIB_PATH, PROBE_SIGNATURES)
+    return _probes

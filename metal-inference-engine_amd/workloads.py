@@ -111,33 +111,75 @@ def c3_paged_decode(seed: int = 3, batch: int = 64) -> PagedDecodeCase:
     return case
 
 
+# ---------------------------------------------------------------- layouts the kernels read
+# The engine keeps its KV and recurrent state in fixed layouts (src/state.py:11-17, 106-129, 196-262, 420-460), and
+# the kernels read those buffers in place. The builders below produce the same layouts directly from a list of
+# lengths, for the benchmark workloads and the tests; the engine's own bookkeeping (which block a sequence gets
+# next, when a slot is freed) is not part of the token-mixing path and is not restated here.
+
+def kv_pool(shape: tuple, device="cpu", dtype=torch.float32) -> tuple[torch.Tensor, torch.Tensor]:
+    """K and V pools of `shape` ([layers, blocks, block_size, Hkv, d]) as the two halves of one zero-filled
+    [2, *shape] buffer, the engine's pool layout."""
+    both = torch.zeros(2, *shape, device=device, dtype=dtype)
+    return both[0], both[1]
+
+
+def scattered_tables(lens: list[int], num_blocks: int, block_size: int, gen: torch.Generator) -> torch.Tensor:
+    """Block tables [B, max_nb] int32 (0-padded) for sequences of `lens` positions whose blocks are consecutive
+    slices of a seeded permutation of the pool: every sequence's blocks are scattered over the pool."""
+    nbs = [math.ceil(n / block_size) for n in lens]
+    if sum(nbs) > num_blocks:
+        raise ValueError(f"{sum(nbs)} blocks needed, pool has {num_blocks}")
+    return _tables_from_perm(torch.randperm(num_blocks, generator=gen).tolist(), nbs)
+
+
+def ring_size(window: int, block_size: int, max_chunk: int) -> int:
+    """Units in a sliding layer's ring: every block one forward of at most max_chunk tokens reads or writes
+    (the first query's window through the last new token) fits, so logical block b can live in slot b % ring."""
+    return math.ceil((window + max_chunk + block_size - 2) / block_size)
+
+
+def ring_tables(lens: list[int], window: int, block_size: int, ring: int, gen: torch.Generator):
+    """Decode tables of a sliding-window layer whose sequences keep their blocks in rings: sequence i owns
+    min(ring, blocks) units (a seeded scattered choice), logical block b sits in ring slot b % ring, and the table
+    (by absolute block, up to the block of position len - 1) names that unit for the blocks of the window
+    [len - W, len) and unit 0 for every block below it, which the kernels never read; unit 0 belongs to no ring.
+    -> (tables [B, width] int32, number of units, [the units of each ring])."""
+    held = [min(ring, math.ceil(n / block_size)) for n in lens]
+    perm = (torch.randperm(sum(held), generator=gen) + 1).tolist()
+    rings, at = [], 0
+    for h in held:
+        rings.append(perm[at:at + h])
+        at += h
+    width = max(math.ceil(n / block_size) for n in lens)
+    rows = []
+    for n, units in zip(lens, rings):
+        nb = math.ceil(n / block_size)
+        first = max(0, n - window) // block_size
+        rows.append([units[b % ring] if b >= first else 0 for b in range(nb)] + [0] * (width - nb))
+    return torch.tensor(rows, dtype=torch.int32), sum(held) + 1, rings
+
+
 WD_WINDOW, WD_HQ, WD_HKV, WD_DIM = 4096, 16, 4, 128
 
 
 def wd_windowed_decode(seed: int = 7, batch: int = 64) -> PagedDecodeCase:
-    """Sliding-window decode through the grouped pool (Tiny Aya's sliding layers: 16 query / 4 kv heads x 128, a
-    4096-token window, bf16 KV): config 3's batch shape (lengths U[128, 8192]), each sequence's ring of
-    R = ceil((W + 512 + 14) / 16) units written through for all its blocks (so longer sequences have wrapped), the
-    decode step's tables from GroupedKVPool.batch_layout. The pool holds the rings only (one sliding layer group)."""
-    from state import GroupedKVPool
+    """Sliding-window decode through ring tables (Tiny Aya's sliding layers: 16 query / 4 kv heads x 128, a
+    4096-token window, bf16 KV): config 3's batch shape (lengths U[128, 8192]), each sequence's blocks in a ring
+    of ceil((W + 512 + 14) / 16) units (so longer sequences have wrapped), the decode step's tables by absolute
+    block. The pool holds the rings only (one sliding layer)."""
     lens = c3_lens(seed, batch)
     gen = torch.Generator().manual_seed(seed)
-    probe = GroupedKVPool([WD_WINDOW], WD_HKV, WD_DIM, num_blocks=1, block_size=BLOCK, dtype=torch.bfloat16)
-    units = sum(probe.blocks_for(n) for n in lens)
-    pool = GroupedKVPool([WD_WINDOW], WD_HKV, WD_DIM, num_blocks=units, block_size=BLOCK, dtype=torch.bfloat16)
-    seqs = [pool.new_sequence() for _ in lens]
-    for s, n in zip(seqs, lens):
-        s.reserve(n)
-        for b in range(math.ceil(n / BLOCK)):         # every block of the history written through the ring
-            s.unit(0, b, write=True)
-        s.length = n - 1
-    _, _, tables, lens_t = pool.batch_layout(seqs, [n - 1 for n in lens])
-    pool.k[0].copy_(torch.randn(pool.k[0].shape, generator=gen))
-    pool.v[0].copy_(torch.randn(pool.v[0].shape, generator=gen))
+    ring = ring_size(WD_WINDOW, BLOCK, 512)
+    tables, units, _ = ring_tables(lens, WD_WINDOW, BLOCK, ring, gen)
+    k, v = kv_pool((units, BLOCK, WD_HKV, WD_DIM), dtype=torch.bfloat16)
+    k.copy_(torch.randn(k.shape, generator=gen))
+    v.copy_(torch.randn(v.shape, generator=gen))
     q = torch.randn(batch, WD_HQ, WD_DIM, generator=gen)
     gate = torch.randn(batch, WD_HQ * WD_DIM, generator=gen)
-    return PagedDecodeCase(q, gate, pool.k[0], pool.v[0], tables[0], lens_t, BLOCK, WD_WINDOW,
-                           {"config": "wd", "lens": lens, "units": units, "ring": pool.ring})
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    return PagedDecodeCase(q, gate, k, v, tables, lens_t, BLOCK, WD_WINDOW,
+                           {"config": "wd", "lens": lens, "units": units, "ring": ring})
 
 
 @dataclass
@@ -507,29 +549,59 @@ def random_device_weights(cfg: HybridConfig, scheme: str, dev, seed: int = 0) ->
     return out
 
 
+class StateSlots:
+    """Gated DeltaNet state of max_seqs sequences in the engine's pool layout (src/state.py:428-429):
+    S [max_seqs, n_linear, H, dk, dv] and conv [max_seqs, n_linear, K-1, C], fp32. views(rows) hands out one object
+    per sequence with the attributes the backend reads from the engine's states (pool, seq, S, conv_tail), and
+    seq_index(states) the rows of a batch as a device int32 tensor, cached per batch composition."""
+
+    def __init__(self, max_seqs: int, n_linear: int, H: int, dk: int, dv: int, conv_dim: int, conv_k: int,
+                 device="cpu"):
+        self.S = torch.zeros(max_seqs, n_linear, H, dk, dv, device=device, dtype=torch.float32)
+        self.conv = torch.zeros(max_seqs, n_linear, conv_k - 1, conv_dim, device=device, dtype=torch.float32)
+        self._index: dict[tuple, torch.Tensor] = {}
+
+    def views(self, rows) -> list:
+        return [SlotView(self, int(r)) for r in rows]
+
+    def seq_index(self, states) -> torch.Tensor:
+        key = tuple(st.seq for st in states)
+        if key not in self._index:
+            from native.kernels import to_device
+            self._index[key] = to_device(torch.tensor(key, dtype=torch.int32), self.S.device)
+        return self._index[key]
+
+
+class SlotView:
+    """One sequence's row of a StateSlots."""
+
+    def __init__(self, pool: StateSlots, seq: int):
+        self.pool, self.seq = pool, seq
+        self.S, self.conv_tail = pool.S[seq], pool.conv[seq]
+
+
 class HybridDecodeState:
-    """The sequences of one decode batch in the reference's pools: a PagedKVPool layer per attention layer (bf16)
-    and a HybridPool slot per sequence (S and conv tails of every DeltaNet layer), with histories of `lens`
-    positions already written (seeded random K / V, S ~ N(0, 0.02^2), tails ~ N(0, 1))."""
+    """The sequences of one decode batch in the engine's layouts: a KV pool layer per attention layer (bf16, blocks
+    scattered over the pool) and a DeltaNet state row per sequence (S and conv tails of every DeltaNet layer), with
+    histories of `lens` positions already written (seeded random K / V, S ~ N(0, 0.02^2), tails ~ N(0, 1)). The
+    blocks for one more position are in the tables."""
 
     def __init__(self, cfg: HybridConfig, lens: list[int], device, seed: int = 0, kv_dtype=torch.bfloat16):
-        from state import HybridPool, PagedKVPool
         self.cfg = cfg
+        self.lens = list(lens)
         n_full = sum(cfg.is_full(i) for i in range(cfg.layers))
         n_linear = cfg.layers - n_full
         bs = cfg.block_size
-        num_blocks = sum(math.ceil((L + 1) / bs) for L in lens) + 1
-        kv = PagedKVPool(n_full, cfg.Hkv, cfg.d, num_blocks, bs, device=device, dtype=kv_dtype)
-        self.pool = HybridPool(kv, len(lens), n_linear, cfg.H, cfg.dk, cfg.dv, cfg.conv_dim, cfg.conv_k, device)
-        self.seqs = [self.pool.new_sequence() for _ in lens]
         gen = torch.Generator().manual_seed(seed)
-        for st, L in zip(self.seqs, lens):
-            st.reserve(L + 1)
-            st.kv.length = L
-        kv.k.copy_(torch.randn(kv.k.shape, generator=gen).to(kv_dtype))
-        kv.v.copy_(torch.randn(kv.v.shape, generator=gen).to(kv_dtype))
+        num_blocks = sum(math.ceil((L + 1) / bs) for L in lens) + 1
+        self.tables = scattered_tables([L + 1 for L in lens], num_blocks, bs, gen)
+        self.k, self.v = kv_pool((n_full, num_blocks, bs, cfg.Hkv, cfg.d), device, kv_dtype)
+        self.k.copy_(torch.randn(self.k.shape, generator=gen).to(kv_dtype))
+        self.v.copy_(torch.randn(self.v.shape, generator=gen).to(kv_dtype))
+        self.pool = StateSlots(len(lens), n_linear, cfg.H, cfg.dk, cfg.dv, cfg.conv_dim, cfg.conv_k, device)
         self.pool.S.copy_(0.02 * torch.randn(self.pool.S.shape, generator=gen))
         self.pool.conv.copy_(torch.randn(self.pool.conv.shape, generator=gen))
+        self.seqs = self.pool.views(range(len(lens)))
         # layer slots: attention layers index the KV pool, DeltaNet layers the state pool (the model's self.slot)
         self.slot, nf, nl = [], 0, 0
         for i in range(cfg.layers):
@@ -537,15 +609,15 @@ class HybridDecodeState:
             nf, nl = nf + cfg.is_full(i), nl + (not cfg.is_full(i))
 
     def layout(self):
-        """One step's KV layout (src/models/qwen3_5.py:237-245): write slots, tables, lengths after the step, and
-        the positions of the new tokens."""
-        from state import to_device
-        starts = [st.length for st in self.seqs]
-        kvs = [st.kv for st in self.seqs]
-        blocks, offsets, tables, lens = self.pool.kv.batch_layout(kvs, starts)
-        slots = blocks * self.cfg.block_size + offsets
-        positions = to_device(torch.tensor(starts, dtype=torch.int32), self.pool.S.device)
-        return slots, tables, lens, positions
+        """One step's KV layout (src/models/qwen3_5.py:237-245): the pool row each new token is written to
+        (block * block_size + offset, int64), the tables, the lengths after the step and the new tokens'
+        positions, as device tensors."""
+        from native.kernels import to_device
+        bs, dev = self.cfg.block_size, self.k.device
+        slots = torch.tensor([int(self.tables[i, L // bs]) * bs + L % bs for i, L in enumerate(self.lens)])
+        lens = torch.tensor([L + 1 for L in self.lens], dtype=torch.int32)
+        positions = torch.tensor(self.lens, dtype=torch.int32)
+        return tuple(to_device(t, dev) for t in (slots, self.tables, lens, positions))
 
 
 def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Tensor, layout) -> torch.Tensor:
@@ -558,7 +630,6 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
     cfg = st.cfg
     B = tokens.shape[0]
     slots, tables, lens, positions = layout
-    kv = st.pool.kv
     fused = hasattr(backend, "silu_mul_linear")
     fused_norm = hasattr(backend, "rms_norm_linear")
     ss = None                       # sums of squares of h's 16-column tiles, from the linear that wrote h
@@ -581,8 +652,8 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
             a = p + "self_attn."
             y = norm_linear(h, w[p + "input_layernorm.weight"], w[a + "qkvg.weight"])
             q, gate = backend.attention_prep(y, w[a + "q_norm.weight"], w[a + "k_norm.weight"], cfg.eps, positions,
-                                             cfg.theta, cfg.rot, (cfg.Hq, cfg.Hkv, cfg.d), kv.k[L], kv.v[L], slots)
-            o = backend.paged_attention(q, kv.k[L], kv.v[L], tables, lens, cfg.block_size, gate=gate)
+                                             cfg.theta, cfg.rot, (cfg.Hq, cfg.Hkv, cfg.d), st.k[L], st.v[L], slots)
+            o = backend.paged_attention(q, st.k[L], st.v[L], tables, lens, cfg.block_size, gate=gate)
             h, ss = residual_linear(o.reshape(B, cfg.Hq * cfg.d), w[a + "o_proj.weight"], h)
         else:
             a = p + "linear_attn."

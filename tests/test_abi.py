@@ -11,11 +11,12 @@ from native import rocm_native
 from native.rocm_native import SIGNATURES, NativeRocm
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "rk_path.h"
+PROBE_HEADER = HEADER.with_name("rk_probe.h")
 
 
-def declarations() -> dict[str, list[str]]:
+def declarations(header: Path = HEADER) -> dict[str, list[str]]:
     """name -> list of parameter declarations, for every function prototype in the header."""
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     out = {}
     for m in re.finditer(r"^[\w\s\*]*?\b(rk_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
         params = [p.strip() for p in m.group(2).replace("\n", " ").split(",") if p.strip() and p.strip() != "void"]
@@ -56,6 +57,18 @@ def test_every_declared_symbol_is_exported(lib):
     for name in declarations():
         assert hasattr(lib.lib, name), name
     assert lib.lib.rk_abi_version() == rocm_native.ABI_VERSION
+
+
+def test_probe_library_matches_its_header():
+    decl = declarations(PROBE_HEADER)
+    assert set(decl) == set(rocm_native.PROBE_SIGNATURES)
+    for name, (_, argtypes) in rocm_native.PROBE_SIGNATURES.items():
+        assert [kind(p) for p in decl[name]] == [CTYPE_KIND[a] for a in argtypes], name
+    probes = rocm_native.load_probes()
+    for name in decl:
+        assert hasattr(probes.lib, name), name
+    rc = probes.lib.rk_probe_block_stream(None, None, None, 0, 16384, 1, None, None)
+    assert rc == 1 and b"rk_probe_block_stream" in probes.lib.rk_last_error()
 
 
 def test_null_pointer_is_an_argument_error(lib):

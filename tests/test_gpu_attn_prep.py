@@ -93,28 +93,30 @@ def test_decode_attention_layer_end_to_end(backend):
     """prep (norms, RoPE, KV write) + paged decode with the fused gate == the reference's decode steps
     (qwen3_5.py:251-271: norms, rope, write_batch, paged_attention, * sigmoid(gate)) on a bf16 pool."""
     from oracle import backend_ref as br
-    from state import PagedKVPool
+    import workloads as wl
     Hq, Hkv, d, rot, theta, B, bs = 8, 2, 256, 64, 1e7, 16, 16
     g_ = torch.Generator().manual_seed(9)
-    pool = PagedKVPool(1, Hkv, d, 128, bs, device="cpu", dtype=torch.bfloat16)
-    seqs = [pool.new_sequence() for _ in range(B)]
     lens = torch.randint(1, 200, (B,), generator=g_).tolist()
-    for s, n in zip(seqs, lens):                                      # history of n - 1 tokens, then the new one
-        s.reserve(n)
-        if n > 1:
-            s.write(0, 0, torch.randn(n - 1, Hkv, d, generator=g_), torch.randn(n - 1, Hkv, d, generator=g_))
+    tables = wl.scattered_tables(lens, 128, bs, g_)
+    kh, vh = wl.kv_pool((1, 128, bs, Hkv, d), "cpu", torch.bfloat16)
+    for i, n in enumerate(lens):                                     # history of n - 1 tokens, then the new one
+        for p in range(n - 1):
+            kh[0, int(tables[i, p // bs]), p % bs] = torch.randn(Hkv, d, generator=g_).to(torch.bfloat16)
+            vh[0, int(tables[i, p // bs]), p % bs] = torch.randn(Hkv, d, generator=g_).to(torch.bfloat16)
     starts = [n - 1 for n in lens]
-    blocks, offsets, tables, lens_t = pool.batch_layout(seqs, starts)
+    blocks = torch.tensor([int(tables[i, p // bs]) for i, p in enumerate(starts)])
+    offsets = torch.tensor([p % bs for p in starts])
+    lens_t = torch.tensor(lens, dtype=torch.int32)
     y, qw, kw, _ = layer(10, B, Hq, Hkv, d)
     pos = torch.tensor(starts, dtype=torch.int32)
     # oracle on CPU copies of the pool
-    k_ref_pool, v_ref_pool = pool.k[0].clone(), pool.v[0].clone()
+    k_ref_pool, v_ref_pool = kh[0].clone(), vh[0].clone()
     q_ref, k_ref, v_ref, gate = br.attention_prep(y, qw, kw, 1e-6, pos, theta, rot, (Hq, Hkv, d))
     k_ref_pool[blocks, offsets] = k_ref.to(torch.bfloat16)
     v_ref_pool[blocks, offsets] = v_ref.to(torch.bfloat16)
     o_ref = br.gate(br.paged_attention(q_ref, k_ref_pool, v_ref_pool, tables, lens_t, bs).reshape(B, Hq * d), gate)
     # device
-    kp, vp = pool.k[0].to(DEV), pool.v[0].to(DEV)
+    kp, vp = kh[0].to(DEV), vh[0].to(DEV)
     slots = (blocks * bs + offsets).to(DEV)
     q, g_dev = backend.attention_prep(y.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6, pos.to(DEV), theta, rot,
                                       (Hq, Hkv, d), kp, vp, slots)

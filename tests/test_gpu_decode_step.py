@@ -52,8 +52,7 @@ def test_hybrid_decode_step_matches_oracle(scheme):
         assert wd["embed_tokens.weight"].scheme == "int8" and wd["layers.0.mlp.gate_up.weight"].scheme == "int4"
     lens = [5, 40, 17, 100]
     st = wl.HybridDecodeState(cfg, lens, DEV, seed=22)
-    kv = st.pool.kv
-    kh, vh = kv.k.cpu(), kv.v.cpu()
+    kh, vh = st.k.cpu(), st.v.cpu()
     Sh, convh = st.pool.S.cpu(), st.pool.conv.cpu()
     seq_index = torch.tensor([s.seq for s in st.seqs])
     layout = st.layout()
@@ -66,8 +65,8 @@ def test_hybrid_decode_step_matches_oracle(scheme):
     assert rel_err(got, want) < TOL
     assert rel_err(st.pool.S, Sh) < TOL and rel_err(st.pool.conv, convh) < TOL
     rows = slots.long()
-    for L in range(kv.k.shape[0]):
-        for pool, ref in ((kv.k, kh), (kv.v, vh)):
+    for L in range(st.k.shape[0]):
+        for pool, ref in ((st.k, kh), (st.v, vh)):
             g = pool[L].view(-1, cfg.Hkv, cfg.d)[rows.to(DEV)].float().cpu()
             r = ref[L].view(-1, cfg.Hkv, cfg.d)[rows].float()
             ulp = r.abs().clamp_min(1e-30) * 2.0 ** -7

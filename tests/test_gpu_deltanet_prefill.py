@@ -14,7 +14,7 @@ import torch
 
 from helpers import SlotState, rel_err
 from oracle import backend_ref, ops_ref
-from state import HybridPool, PagedKVPool
+import workloads as wl
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -90,12 +90,10 @@ LENGTHS = [5, 0, 1, 2, 64, 130, 3]
 
 
 def pool_with_states(g_, n):
-    pool = HybridPool(PagedKVPool(1, 2, 64, 8, 16, device=DEV), n + 3, 2, H, DK, DV, C, K, device=DEV)
+    pool = wl.StateSlots(n + 3, 2, H, DK, DV, C, K, device=DEV)
     pool.S.copy_(0.05 * torch.randn(pool.S.shape, generator=g_))
     pool.conv.copy_(torch.randn(pool.conv.shape, generator=g_))
-    for _ in range(2):
-        pool.new_sequence()                                           # slots the batch does not use
-    return pool, [pool.new_sequence() for _ in range(n)]
+    return pool, pool.views(range(2, n + 2))                          # rows 0, 1 and n + 2: not in the batch
 
 
 # the kernel streams runs of 32 packed tokens: runs that cross several (and empty) segments, and runs that start
@@ -202,12 +200,10 @@ def test_packing_is_bit_identical_to_single_segments(backend):
     y = projection(300, torch.bfloat16, g_).to(DEV)
     args = (lw["conv_w"].to(DEV), lw["A_log"].to(DEV), lw["dt_bias"].to(DEV), lw["norm_w"].to(DEV), 1e-6, DIMS)
     pool, states = pool_with_states(g_, 4)
-    pool2 = HybridPool(PagedKVPool(1, 2, 64, 8, 16, device=DEV), pool.S.shape[0], 2, H, DK, DV, C, K, device=DEV)
+    pool2 = wl.StateSlots(pool.S.shape[0], 2, H, DK, DV, C, K, device=DEV)
     pool2.S.copy_(pool.S)
     pool2.conv.copy_(pool.conv)
-    for _ in range(2):
-        pool2.new_sequence()
-    states2 = [pool2.new_sequence() for _ in range(4)]
+    states2 = pool2.views(range(2, 6))
     packed = backend.deltanet_prefill(*cols(y), states, 1, cu, *args)
     alone = torch.cat([backend.deltanet_prefill(*(t[lo:hi] for t in cols(y)), [st], 1, [0, hi - lo], *args)
                        for st, lo, hi in zip(states2, cu, cu[1:]) if hi > lo])

@@ -11,7 +11,6 @@ import torch
 import workloads as wl
 from helpers import SlotState, rel_err
 from oracle import backend_ref
-from state import HybridPool, PagedKVPool
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -76,8 +75,8 @@ def test_pool_states_one_launch(backend):
     """States of one HybridPool decode together; mixed standalone states run one by one; both match the oracle."""
     gen = torch.Generator().manual_seed(5)
     H, dk, dv, KD, C = 16, 128, 128, 2048, 6144
-    pool = HybridPool(PagedKVPool(1, 2, 64, 8, 16, device=DEV), 4, 2, H, dk, dv, C, 4, device=DEV)
-    states = [pool.new_sequence() for _ in range(3)]
+    pool = wl.StateSlots(4, 2, H, dk, dv, C, 4, device=DEV)
+    states = pool.views(range(3))
     pool.S.normal_(0, 0.02, generator=torch.Generator(device=DEV).manual_seed(1))
     pool.conv.normal_(0, 1, generator=torch.Generator(device=DEV).manual_seed(2))
     refs = [SlotState(st.S.cpu().clone(), st.conv_tail.cpu().clone()) for st in states]

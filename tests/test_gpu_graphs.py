@@ -51,3 +51,35 @@ def test_decode_launch_chain_replays_bit_identical():
         torch.cuda.synchronize()
         for got, ref in zip(eager, want):
             assert torch.equal(got, ref)
+
+
+def test_replay_after_the_workspace_grew():
+    """A graph captured while the shared workspace was small keeps writing to that buffer on every replay; when an
+    eager call needs a larger one, the old buffer must stay allocated (never handed out again), and replays and
+    eager calls must both keep giving the captured bits."""
+    from native import kernels
+    c = wl.c1_paged_decode().to(DEV)
+
+    def decode():
+        return kernels.paged_decode(c.q, c.k_pool, c.v_pool, c.tables, c.lens, c.block_size, gate=c.gate)
+
+    want = decode().clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        decode()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = decode()
+    old = kernels.workspace(c.q.device, 1)
+    grown = kernels.workspace(c.q.device, old.numel() * 4)          # an eager call needing more: a new buffer
+    assert grown.data_ptr() != old.data_ptr()
+    junk = [torch.full((old.numel() // 4,), float("nan"), device=DEV) for _ in range(4)]   # allocations after it
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep}"
+        assert all(torch.isnan(j).all() for j in junk)              # the replay wrote nothing into them
+        assert torch.equal(decode(), want)                          # eager, on the grown buffer

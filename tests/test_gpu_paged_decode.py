@@ -129,3 +129,17 @@ def test_other_kv_dtypes_refused(backend, kd, vd):
     case = wl.paged_decode_case(REF_LENS, 32, 8, 2, 256, 16, torch.float32, seed=16).to(DEV)
     with pytest.raises(TypeError):
         backend.paged_attention(case.q, case.k_pool.to(kd), case.v_pool.to(vd), case.tables, case.lens, 16)
+
+
+def test_stale_workspace_is_never_read(backend):
+    """With more split workgroups than tiles (REF_LENS: 25 tiles), empty ranges write no partial; the merge must not
+    read their slots. The workspace is filled with NaN first: the output must still match the oracle."""
+    from native import kernels
+    case = wl.paged_decode_case(REF_LENS, 32, 8, 2, 256, 16, torch.bfloat16, seed=13)
+    c = case.to(DEV)
+    lib = backend.lib
+    need = lib.lib.rk_paged_decode_workspace_bytes(len(REF_LENS), 8, 2, 256, 16, c.tables.shape[1])
+    kernels.workspace(c.q.device, need).view(torch.float32).fill_(float("nan"))
+    got = gpu(backend, case, gate=True)
+    assert torch.isfinite(got).all()
+    assert rel_err(got, oracle(case, gate=True)) < 1e-5

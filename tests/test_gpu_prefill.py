@@ -74,8 +74,17 @@ def test_config5_full_size(backend):
 
 
 def test_bad_group_size_refused(backend):
+    """Group sizes other than 4 have no kernel instance: the wrapper refuses before launching, and so does the C
+    entry point if called directly."""
     case = wl.prefill_case([8], [0], 8, 1, 128, seed=10).to(DEV)
-    from native.rocm_native import RocmKernelError
-    with pytest.raises(RocmKernelError):
+    with pytest.raises(NotImplementedError):
         backend.paged_prefill_attention(case.q, case.k_new, case.v_new, case.k_pool, case.v_pool, case.tables,
                                         case.cu_seqlens, case.starts, 16)
+    from native.rocm_native import RocmKernelError
+    meta = torch.tensor([0, 8, 0, 0], dtype=torch.int32, device=DEV)
+    out = torch.empty(8, 8, 128, device=DEV)
+    with pytest.raises(RocmKernelError):
+        backend.lib.call("rk_paged_prefill", out.data_ptr(), case.q.data_ptr(), 1, case.k_new.data_ptr(),
+                         case.v_new.data_ptr(), 1, case.k_pool.data_ptr(), case.v_pool.data_ptr(), 1,
+                         case.tables.data_ptr(), case.tables.shape[1], meta.data_ptr(), meta.data_ptr() + 8,
+                         meta.data_ptr() + 12, 1, 1, 8, 8, 1, 128, 16, case.k_pool.shape[0], None, 0, 0, 1, None)

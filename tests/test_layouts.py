@@ -1,0 +1,48 @@
+"""The layout builders the workloads and GPU tests use (workloads.py), on the CPU: scattered tables cover each
+sequence with distinct blocks of the pool; ring tables name, for every block of a window, the ring unit a
+block-by-block write of the whole history left that block in (simulated here with a dict of unit -> block), and
+unit 0 below the window."""
+import math
+
+import pytest
+import torch
+
+import workloads as wl
+
+
+def test_scattered_tables_are_distinct_and_padded():
+    gen = torch.Generator().manual_seed(0)
+    lens = [1, 16, 17, 300, 0 + 5]
+    t = wl.scattered_tables(lens, 40, 16, gen)
+    used = []
+    for row, n in zip(t.tolist(), lens):
+        nb = math.ceil(n / 16)
+        used += row[:nb]
+        assert all(x == 0 for x in row[nb:])
+    assert len(set(used)) == len(used) and all(0 <= x < 40 for x in used)
+    with pytest.raises(ValueError):
+        wl.scattered_tables([16 * 41], 40, 16, gen)
+
+
+@pytest.mark.parametrize("W,bs,chunk", [(37, 4, 16), (100, 16, 16), (4096, 16, 512), (5, 1, 3)])
+def test_ring_tables_name_the_unit_holding_each_window_block(W, bs, chunk):
+    gen = torch.Generator().manual_seed(W)
+    lens = [1, 2, W - 1, W, W + 1, 2 * W + 5, 3 * W + 33, 7 * W + 1]
+    ring = wl.ring_size(W, bs, chunk)
+    tables, units, rings = wl.ring_tables(lens, W, bs, ring, gen)
+    owned = [u for r in rings for u in r]
+    assert 0 not in owned and len(set(owned)) == len(owned) and max(owned) < units
+    for i, n in enumerate(lens):
+        holds = {}                                        # unit -> logical block it holds after the writes
+        for b in range(math.ceil(n / bs)):
+            holds[rings[i][b % ring]] = b
+        first = max(0, n - W) // bs
+        row = tables[i].tolist()
+        for b in range(math.ceil(n / bs)):
+            if b < first:
+                assert row[b] == 0
+            else:
+                assert holds[row[b]] == b                 # the window's block is still in the ring
+        # a chunk of up to `chunk` tokens after the window still fits (the ring-size rule)
+        span = math.ceil((n + chunk) / bs) - max(0, n - W + 1) // bs
+        assert span <= ring
