@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 10
+#define RK_ABI_VERSION 11
 
 /* status codes */
 #define RK_OK 0
@@ -61,6 +61,18 @@ int rk_paged_decode(float* out, const float* q, const void* k_pool, const void* 
                     const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
                     int max_nb, int num_blocks, int window, const float* gate, long long gate_ld, void* workspace,
                     size_t workspace_bytes, void* stream);
+/* rk_paged_decode without a workspace argument and without any device allocation: the split-K partials go to a
+ * fixed scratch array of rk_paged_decode_noalloc_max_bytes() (16 MiB) that the library holds on every GPU it runs on
+ * until the process ends. No counterpart in the reference: for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid hipMalloc). Shapes whose partials exceed the scratch are refused with
+ * RK_ERR_WORKSPACE before any launch (batch 64 at 2 kv-heads x 256 needs 2.6 MB; the limit binds only beyond
+ * several hundred sequences). All calls on one GPU share its scratch: calls that overlap on that GPU (different
+ * streams, no ordering between them) race and must not be issued; stream-ordered calls are safe. */
+size_t rk_paged_decode_noalloc_max_bytes(void);
+int rk_paged_decode_noalloc(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                            const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
+                            int max_nb, int num_blocks, int window, const float* gate, long long gate_ld,
+                            void* stream);
 /* The two launches of rk_paged_decode, separately (phase 0: split-K partials into the workspace; phase 1: merge,
  * gate, write out). Used to time the dominant phase on its own; rk_paged_decode == phase 0 then phase 1. */
 int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,

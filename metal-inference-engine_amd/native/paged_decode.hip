@@ -36,7 +36,16 @@
 #include "rk_device.h"
 #include "rk_internal.h"
 
+#include <mutex>
+
 namespace rk {
+
+// Split-K partials of the allocation-free entry point (rk_paged_decode_noalloc): a file-scope device array, one
+// copy per GPU, held until the process ends. Host code never passes the array's name to a kernel (on the host it
+// is only a stand-in for the symbol); each device's address comes from hipGetSymbolAddress with that device current.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
 namespace {
 
 constexpr int kMaxBatch = 1024;
@@ -916,6 +925,43 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     }
     hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
     return check_launch("paged_decode_merge");
+}
+
+size_t rk_paged_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int rk_paged_decode_noalloc(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                            const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
+                            int max_nb, int num_blocks, int window, const float* gate, long long gate_ld,
+                            void* stream) {
+    static std::mutex mu;
+    static void* addr[64] = {};                // per device: the address of `scratch` in that device's memory
+    int rc = validate(out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                      num_blocks, window);
+    if (rc) return rc;
+    const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
+    const size_t need = workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb, GP));
+    if (need > kScratchBytes)
+        return fail(RK_ERR_WORKSPACE, "rk_paged_decode_noalloc: %zu bytes of partials for batch %d x %d kv-heads x "
+                    "head_dim %d exceed its fixed %zu-byte scratch (use rk_paged_decode with a workspace)", need, B,
+                    Hkv, D, kScratchBytes);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(RK_ERR_HIP, "rk_paged_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= 64) return fail(RK_ERR_UNSUPPORTED, "rk_paged_decode_noalloc: device %d >= 64", dev);
+    void* ptr = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!addr[dev]) {
+            e = hipGetSymbolAddress(&addr[dev], HIP_SYMBOL(scratch));
+            if (e != hipSuccess) {
+                addr[dev] = nullptr;
+                return fail(RK_ERR_HIP, "rk_paged_decode_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+            }
+        }
+        ptr = addr[dev];
+    }
+    return rk_paged_decode(out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                           num_blocks, window, gate, gate_ld, ptr, kScratchBytes, stream);
 }
 
 int rk_paged_decode(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
