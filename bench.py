@@ -1,9 +1,12 @@
 #!/usr/bin/env python3
 """Benchmark of the token-mixing hot path on one MI355X.
 
-Default workload (the BASELINE metric): config 3 — paged GQA decode attention, batch 64, bf16 KV pool, lengths
+Default run: the BASELINE metric on config 3 — paged GQA decode attention, batch 64, bf16 KV pool, lengths
 U[128, 8192], 8/2 heads x 256, block 16, sigmoid output gate fused. One step = one RocmBackend.paged_attention call
-over the whole batch (split-K kernel + merge/gate kernel), inputs already resident in HBM. Prints ONE JSON line.
+over the whole batch (split-K kernel + merge/gate kernel), inputs already resident in HBM. Prints ONE JSON line, whose
+"configs" holds the same record (value, roofline, cpu_baseline) for configs 1, 2, 4 and 5, and whose
+"access_pattern_ceiling" entries (config 3 here, config 2 under configs) give what the memory system delivers for
+each decode kernel's own access pattern with no arithmetic (librk_probe.so).
 
   value           decode-attention tokens/s = batch / step time (one attention-layer call per decode token)
   roofline        the split-K kernel (the dominant launch): its algorithmic bytes (every visible K/V byte once, q,
@@ -167,6 +170,7 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
             raise RuntimeError(lib.last_error())
 
     split_ms = time_region(split, args.steps, args.warmup, stream)
+    ceiling = block_stream_ceiling(case, sets, args, stream) if getattr(args, "ceiling", False) else None
     kv = case.kv_bytes()
     split_bytes = kv + B * Hq * d * 4 + 4 * case.table_entries() + 4 * B
     achieved = split_bytes / (split_ms * 1e-3) / 1e9
@@ -204,7 +208,52 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(f"paged_decode_split/{workload_name}"),
                      "kernel": "paged_decode_split", "bytes_per_launch": split_bytes, "avg_ms": split_ms},
         "cpu_baseline": cpu,
+        **({"access_pattern_ceiling": ceiling} if ceiling else {}),
     }
+
+
+def block_stream_ceiling(case, sets, args, stream) -> dict:
+    """What HBM delivers for this batch's K / V tiles with no arithmetic (rk_probe_block_stream over the same
+    device pools): the tiles in table order (the decode's scattered 16 KiB blocks) and sorted by address (a
+    near-sequential stream of the same bytes), best of three grid sizes each."""
+    import torch
+    from native.rocm_native import load_probes
+    probes = load_probes()
+    NB, bs, Hkv, d = case.k_pool.shape
+    esz = case.k_pool.element_size()
+    if (bs * Hkv * d * esz) not in (4096, 8192, 16384):
+        return None
+    tile_bytes = bs * Hkv * d * esz
+    offs = [int(case.tables[i, b]) * tile_bytes for i, n in enumerate(case.lens.tolist())
+            for b in range(((n - case.window) // bs if case.window and n > case.window else 0), -(-n // bs))]
+    dev = sets[0].q.device
+    lists = {"table_order": torch.tensor(offs, dtype=torch.int64, device=dev),
+             "address_order": torch.tensor(sorted(offs), dtype=torch.int64, device=dev)}
+    sink = torch.empty(1024 * 512, dtype=torch.int32, device=dev)
+    moved = 2 * tile_bytes * len(offs)
+    out = {"kernel": "probe_block_stream", "tiles": len(offs), "bytes_per_launch": moved,
+           "kv_bytes_visible": case.kv_bytes()}
+    # persistent grids of 256 / 512 / 1024 workgroups (8 waves each), and one-shot workgroups over runs of
+    # 8 / 16 / 32 consecutive tiles; the fastest of each kind is kept
+    shapes = [("persistent", w, 0) for w in (256, 512, 1024)] + [("one_shot", 0, n) for n in (8, 16, 32)]
+    for name, lst in lists.items():
+        res = {}
+        for kind, wgs, per in shapes:
+            j = [0]
+
+            def run():
+                c = sets[j[0] % len(sets)]
+                j[0] += 1
+                probes.call("rk_probe_block_stream", c.k_pool.data_ptr(), c.v_pool.data_ptr(), lst.data_ptr(),
+                            len(offs), tile_bytes, wgs, per, sink.data_ptr(), stream.cuda_stream)
+            ms = time_region(run, args.steps, args.warmup, stream)
+            log(f"[bench] ceiling ({name}, {kind}, {wgs or per}): {ms * 1e3:.1f} us")
+            if kind not in res or ms < res[kind]["avg_ms"]:
+                gbs = moved / (ms * 1e-3) / 1e9
+                res[kind] = {"avg_ms": ms, "workgroups" if wgs else "tiles_per_workgroup": wgs or per, "gbs": gbs,
+                             "frac": gbs / HBM_PEAK_GBS}
+        out[name] = res
+    return out
 
 
 class SlotState:
@@ -244,6 +293,25 @@ def bench_deltanet(args, backend):
     nbytes = case.algorithmic_bytes()
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] c2: {ms * 1e3:.2f} us per step, {gbs:.0f} GB/s algorithmic")
+    ceiling = None
+    if getattr(args, "ceiling", False):
+        # the step's state traffic alone (read, scale, write back each head's 64 KiB block), same rotation
+        from native.rocm_native import load_probes
+        probes = load_probes()
+        H, dk, dv, _ = case.dims
+        state_bytes = 2 * B * H * dk * dv * 4
+        ceiling = {"kernel": "probe_state_rmw", "bytes_per_launch": state_bytes}
+        for split in (1, 2, 4, 8, 16):
+            def rmw():
+                seqs, slot = combos[k[0] % len(combos)]
+                k[0] += 1
+                probes.call("rk_probe_state_rmw", c.S.data_ptr(), seqs.data_ptr(), B, n_linear, slot, H, dk, dv,
+                            split, 1.0, torch.cuda.current_stream(dev).cuda_stream)   # the capture stream
+            t = graph_time(rmw, args.steps, stream)
+            ceiling[f"split_{split}"] = {"workgroups": B * H * split, "avg_ms": t,
+                                         "gbs": state_bytes / (t * 1e-3) / 1e9,
+                                         "frac_of_step_bytes": nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS}
+            log(f"[bench] c2 state ceiling, {split} workgroups per head: {t * 1e3:.2f} us")
     cpu = None
     if not args.no_cpu:
         torch.set_num_threads(cpu_threads())
@@ -266,6 +334,7 @@ def bench_deltanet(args, backend):
                      "traffic": traffic_for("deltanet_step/c2"), "kernel": "deltanet_step_kernel",
                      "bytes_per_launch": nbytes, "avg_ms": ms},
         "cpu_baseline": cpu,
+        **({"access_pattern_ceiling": ceiling} if ceiling else {}),
     }
 
 
@@ -762,11 +831,16 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd", "mv", "ds"])
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd", "mv", "ds"],
+                    help="all (default): the config-3 headline record with configs 1, 2, 4, 5 as sub-records and "
+                         "the measured access-pattern ceilings")
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches only (for counter collection)")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the access-pattern probes")
     args = ap.parse_args()
+    args.ceiling = not args.no_ceiling
     global USE_GRAPHS
     USE_GRAPHS = not args.no_graph
     if args.gpus != 1:
@@ -781,21 +855,47 @@ def main() -> int:
     import workloads as wl
     from backend.rocm import RocmBackend
     backend = RocmBackend("cuda:0")
-    if args.workload == "c3":
+
+    def c3():
         case = wl.c3_paged_decode()
         lens = case.lens
         config = {"workload": "config 3: paged GQA decode, batch 64, bf16 KV, fp32 accumulate, 8/2 heads x 256, "
                               "block 16, lengths U[128, 8192], pool 1.25 x positions, sigmoid gate",
                   "batch": 64, "total_positions": int(lens.sum()), "num_blocks": int(case.k_pool.shape[0]),
                   "kv_bytes": case.kv_bytes()}
-        rec = bench_paged_decode(case, args, backend, "c3", config)
-    elif args.workload == "c1":
+        return bench_paged_decode(case, args, backend, "c3", config)
+
+    def c1():
         case = wl.c1_paged_decode()
+        sets = args.sets
         args.sets = max(args.sets, 64)                 # 64 x 8 MiB pools > the 256 MB Infinity Cache
+        ceiling, args.ceiling = args.ceiling, False
         rec = bench_paged_decode(case, args, backend, "c1",
                                  {"workload": "config 1: paged GQA decode, batch 1, fp32 KV, 512 positions"})
+        args.sets, args.ceiling = sets, ceiling
         rec["metric"] = "decode attn tokens/s @ batch 1 (config 1 latency case), 1 GPU"
         rec["dtype"] = "f32"
+        return rec
+
+    if args.workload == "all":
+        global CPU_SAMPLE_S
+        rec = c3()
+        torch.cuda.empty_cache()
+        CPU_SAMPLE_S = 5.0                             # the sub-records' CPU samples: about 5 s each
+        keep = ("metric", "value", "unit", "ms_per_step", "dtype", "config", "roofline", "cpu_baseline",
+                "access_pattern_ceiling", "eager_ms_per_step")
+        subs = {}
+        for name, fn in (("c1", c1), ("c2", lambda: bench_deltanet(args, backend)),
+                         ("c4", lambda: bench_chunked_delta(args, backend)),
+                         ("c5", lambda: bench_prefill(args, backend))):
+            sub = fn()
+            subs[name] = {k: v for k, v in sub.items() if k in keep}
+            torch.cuda.empty_cache()
+        rec["configs"] = subs
+    elif args.workload == "c3":
+        rec = c3()
+    elif args.workload == "c1":
+        rec = c1()
     elif args.workload == "wd":
         case = wl.wd_windowed_decode()
         rec = bench_paged_decode(case, args, backend, "wd",

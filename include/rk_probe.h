@@ -14,11 +14,13 @@ extern "C" {
 #endif
 
 /* Reads tile_bytes (4096, 8192 or 16384) contiguous bytes at each byte offset tile_offsets[i] (16-byte aligned) of
- * both k_pool and v_pool, in list order, spread over `workgroups` workgroups of 8 waves; xors of the data go to
- * sink [workgroups * 512] uint32. With the paged decode's tiles (16 positions x Hkv x D of one block) in table order
- * it is that kernel's K / V traffic alone. */
+ * both k_pool and v_pool. tiles_per_group 0: `workgroups` persistent workgroups of 8 waves, wave i taking entries
+ * i, i + waves, ...; xors of the data go to sink [workgroups * 512] uint32. tiles_per_group n > 0: ceil(n_tiles / n)
+ * one-shot workgroups of 8 waves over consecutive runs of n entries (sink [512], written only on an improbable
+ * value). With the paged decode's tiles (16 positions x Hkv x D of one block) in table order it is that kernel's
+ * K / V traffic alone. */
 int rk_probe_block_stream(const void* k_pool, const void* v_pool, const long long* tile_offsets, int n_tiles,
-                          int tile_bytes, int workgroups, uint32_t* sink, void* stream);
+                          int tile_bytes, int workgroups, int tiles_per_group, uint32_t* sink, void* stream);
 
 /* For each of the B rows seq_index[b] of the DeltaNet state pool S [seqs, n_linear, H, dk, dv] fp32 and each head,
  * reads the [dk, dv] block at layer `slot`, multiplies it by `scale` and writes it back, with `split` workgroups of

@@ -4,7 +4,8 @@
 //   probe_block_stream: reads whole 16-position KV tiles (both pools) given as a list of pool tile offsets, in the
 //     list's order, with 16-byte loads, and keeps an xor of everything read. With the decode's own tiles in table
 //     order this is the paged decode's K/V traffic (scattered 16 KiB blocks) without the softmax or the merge; with
-//     the same tiles sorted by address it is a near-sequential stream of the same bytes.
+//     the same tiles sorted by address it is a near-sequential stream of the same bytes. Either as persistent waves
+//     striding over the list, or as one-shot workgroups over consecutive runs of it.
 //   probe_state_rmw: reads each selected (sequence, head) state block of the DeltaNet pool, scales it, and writes it
 //     back: the recurrent step's state traffic (one read and one write of 64 KiB per head) without the conv, norms
 //     or delta rule, with `split` workgroups per head.
@@ -40,6 +41,31 @@ __global__ __launch_bounds__(64 * kProbeWaves) void probe_block_stream(const cha
     sink[blockIdx.x * blockDim.x + threadIdx.x] = acc;
 }
 
+// One-shot workgroups: workgroup w reads list entries [w * per_group, (w + 1) * per_group), its waves taking
+// consecutive entries in turn (one tile per wave in flight), and exits; the hardware dispatcher hands the next
+// workgroup to whichever compute unit frees a slot first.
+template <int kVec>
+__global__ __launch_bounds__(64 * kProbeWaves) void probe_block_oneshot(const char* kp, const char* vp,
+                                                                         const long long* tiles, int n_tiles,
+                                                                         int per_group, uint32_t* sink) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * per_group, t1 = min(n_tiles, t0 + per_group);
+    uint32_t acc = 0;
+    for (int t = t0 + wave; t < t1; t += kProbeWaves) {
+        const long long off = tiles[t] + 16ll * lane;
+        u32x4 x[2 * kVec];
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+            x[j] = *reinterpret_cast<const u32x4*>(kp + off + 1024ll * j);
+            x[kVec + j] = *reinterpret_cast<const u32x4*>(vp + off + 1024ll * j);
+        }
+#pragma unroll
+        for (int j = 0; j < 2 * kVec; ++j) acc ^= x[j][0] ^ x[j][1] ^ x[j][2] ^ x[j][3];
+    }
+    if (acc == 0x9e3779b9u) sink[threadIdx.x] = acc;     // keeps the loads; practically never stores
+}
+
 // One workgroup of 256 threads per (batch row, head, part): part p of `split` covers state rows
 // [p * dk / split, (p + 1) * dk / split) of the head's dk x dv block.
 __global__ __launch_bounds__(256) void probe_state_rmw(float* S, const int32_t* seq_index, int n_linear, int slot,
@@ -69,16 +95,27 @@ using namespace rk;
 extern "C" {
 
 int rk_probe_block_stream(const void* k_pool, const void* v_pool, const long long* tile_offsets, int n_tiles,
-                          int tile_bytes, int workgroups, uint32_t* sink, void* stream) {
-    if (!k_pool || !v_pool || !tile_offsets || !sink || n_tiles < 1 || workgroups < 1)
+                          int tile_bytes, int workgroups, int tiles_per_group, uint32_t* sink, void* stream) {
+    if (!k_pool || !v_pool || !tile_offsets || !sink || n_tiles < 1 || (tiles_per_group <= 0 && workgroups < 1))
         return fail(RK_ERR_ARG, "rk_probe_block_stream: null pointer or empty list");
+    if (tile_bytes != 16384 && tile_bytes != 8192 && tile_bytes != 4096)
+        return fail(RK_ERR_ARG, "rk_probe_block_stream: tile_bytes %d (4096, 8192 or 16384)", tile_bytes);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const char* kp = static_cast<const char*>(k_pool);
+    const char* vp = static_cast<const char*>(v_pool);
+    if (tiles_per_group > 0) {
+        typedef void (*Fn)(const char*, const char*, const long long*, int, int, uint32_t*);
+        Fn fn = tile_bytes == 16384 ? probe_block_oneshot<16> : tile_bytes == 8192 ? probe_block_oneshot<8>
+                                                                                   : probe_block_oneshot<4>;
+        const int grid = (n_tiles + tiles_per_group - 1) / tiles_per_group;
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kProbeWaves), 0, s, kp, vp, tile_offsets, n_tiles,
+                           tiles_per_group, sink);
+        return check_launch("probe_block_oneshot");
+    }
     typedef void (*Fn)(const char*, const char*, const long long*, int, uint32_t*);
     Fn fn = tile_bytes == 16384 ? probe_block_stream<16> : tile_bytes == 8192 ? probe_block_stream<8>
-          : tile_bytes == 4096 ? probe_block_stream<4> : nullptr;
-    if (!fn) return fail(RK_ERR_ARG, "rk_probe_block_stream: tile_bytes %d (4096, 8192 or 16384)", tile_bytes);
-    hipLaunchKernelGGL(fn, dim3(workgroups), dim3(64 * kProbeWaves), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const char*>(k_pool), static_cast<const char*>(v_pool), tile_offsets, n_tiles,
-                       sink);
+                                                                              : probe_block_stream<4>;
+    hipLaunchKernelGGL(fn, dim3(workgroups), dim3(64 * kProbeWaves), 0, s, kp, vp, tile_offsets, n_tiles, sink);
     return check_launch("probe_block_stream");
 }
 

@@ -62,7 +62,7 @@ SIGNATURES = {
 PROBE_LIB_PATH = HERE / "librk_probe.so"
 # the measurement probes of include/rk_probe.h (their library also exports rk_last_error)
 PROBE_SIGNATURES = {
-    "rk_probe_block_stream": (c_int, [P, P, P, c_int, c_int, c_int, P, P]),
+    "rk_probe_block_stream": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, P]),
     "rk_probe_state_rmw": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P]),
 }
 

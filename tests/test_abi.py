@@ -67,7 +67,7 @@ def test_probe_library_matches_its_header():
     probes = rocm_native.load_probes()
     for name in decl:
         assert hasattr(probes.lib, name), name
-    rc = probes.lib.rk_probe_block_stream(None, None, None, 0, 16384, 1, None, None)
+    rc = probes.lib.rk_probe_block_stream(None, None, None, 0, 16384, 1, 0, None, None)
     assert rc == 1 and b"rk_probe_block_stream" in probes.lib.rk_last_error()
 
 
