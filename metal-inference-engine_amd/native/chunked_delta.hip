@@ -423,6 +423,11 @@ __device__ __forceinline__ void scan_wave(const DeltaArgs& p, char* lds, int s, 
             a.k[k].load(Kg + off + 32 * k);
             a.q[k].load(Qg + off + 32 * k);
         }
+    };
+    // the values and coefficients of row tile W
+    auto load_ahead_v = [&](int c, Ahead& a) {
+        const int nt = min(kC, Tn - c * kC);
+        const int tc = T0 + c * kC;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tv = min(16 * W + 4 * q + i, nt - 1);
@@ -435,14 +440,18 @@ __device__ __forceinline__ void scan_wave(const DeltaArgs& p, char* lds, int s, 
         a.eg = cf[2 * kC + 16 * W + r];
         a.egr = cf[3 * kC + 16 * W + r];
         a.glast = cf[2 * kC + kC - 1];
+    };
+    // the T and P pieces of row tile W (the larger part of the look-ahead bytes), requested separately so that
+    // their issue overlaps the X / QS products instead of preceding them
+    auto load_ahead_tp = [&](int c, Ahead& a, int which) {   // which: 0 = T pieces, 1 = P pieces
         const uint16_t* ws16 = reinterpret_cast<const uint16_t*>(p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats);
 #pragma unroll
         for (int k = 0; k < KS; ++k)
 #pragma unroll
             for (int pi = 0; pi < kTP; ++pi) {
                 const int e = rt_base(W) + r * rt_width(W) + 32 * k + 8 * q + pi * kPieceElems;
-                a.ta[k][pi] = *reinterpret_cast<const u32x4*>(ws16 + kTOff + e);
-                a.pa[k][pi] = *reinterpret_cast<const u32x4*>(ws16 + kPOff + e);
+                if (which == 0) a.ta[k][pi] = *reinterpret_cast<const u32x4*>(ws16 + kTOff + e);
+                else a.pa[k][pi] = *reinterpret_cast<const u32x4*>(ws16 + kPOff + e);
             }
     };
     // An empty asm that takes every register of `a` as input and output: the loads behind them complete at this
@@ -472,6 +481,9 @@ __device__ __forceinline__ void scan_wave(const DeltaArgs& p, char* lds, int s, 
     };
     Ahead cur;
     load_ahead(0, cur);
+    load_ahead_v(0, cur);
+    load_ahead_tp(0, cur, 0);
+    load_ahead_tp(0, cur, 1);
     // the first chunk's data and the initial state complete before the loop, so no wait for them lands inside it
     resident(cur);
 #pragma unroll
@@ -487,6 +499,7 @@ __device__ __forceinline__ void scan_wave(const DeltaArgs& p, char* lds, int s, 
         // everything chunk c+1 reads from global memory is requested now and first used at the end of this chunk
         // (before this chunk's output stores are issued, so that wait never includes store completions)
         load_ahead(c + 1 < nch ? c + 1 : c, nxt);
+        load_ahead_v(c + 1 < nch ? c + 1 : c, nxt);
 
         // ---- A1: state pieces -> LDS [piece][column][dk]
 #pragma unroll
@@ -508,6 +521,12 @@ __device__ __forceinline__ void scan_wave(const DeltaArgs& p, char* lds, int s, 
         for (int ct = 0; ct < kCT; ++ct) x[ct] = qs[ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
+            if (k == 1 || k == 3) {
+                __builtin_amdgcn_sched_barrier(0);
+                load_ahead_tp(c + 1 < nch ? c + 1 : c, nxt, k == 1 ? 0 : 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+
             u32x4 ok[KP], oq[KP];
             cur.k[k].pieces(ok);
             cur.q[k].pieces(oq);
