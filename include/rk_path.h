@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 11
+#define RK_ABI_VERSION 12
 
 /* status codes */
 #define RK_OK 0
@@ -93,6 +93,31 @@ int rk_kv_write(void* k_pool, void* v_pool, int pool_dtype, const int64_t* slots
                 void* stream);
 int rk_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool, int dtype, const int32_t* table,
                  int table_len, int lo, int end, int Hkv, int D, int block_size, int num_blocks, void* stream);
+
+/* ---- paged KV bookkeeping on the device: the block allocator and block tables (BlockAllocator, PagedSequence,
+ * PagedKVPool.batch_layout, src/state.py:78-103, 119-157, 182-186) kept in device memory, so a step's layout needs no
+ * host work and no host-to-device copy. tables [max_seqs, max_blocks] int32 (row = sequence slot), lens [max_seqs]
+ * int32 (positions written), stack [num_blocks] int32 (free blocks), meta [2] int32: meta[0] = free blocks,
+ * meta[1] = status (0 ok; 1 out of blocks; 2 a sequence would outgrow max_blocks; 3 a release would overfill the
+ * stack; 4 a row outside [0, max_seqs)). A step that fails changes nothing but the status (all or nothing, as
+ * PagedSequence._ensure), writes slots of -1 (skipped by rk_kv_write) and the old lengths.
+ *   rk_pages_init: empty tables, stack handing out block 0 first (BlockAllocator.__init__).
+ *   rk_pages_advance: batch entry b grows sequence rows[b] (distinct rows, B <= 1024) by n_new positions, taking
+ *     blocks in batch order; slots [B * n_new] int64 = block * block_size + offset of each new position (the rows
+ *     rk_kv_write / rk_attn_prep write; NULL to skip), out_lens [B] = lengths after the step (NULL to skip).
+ *   rk_pages_release: rows[r] (R <= 1024) return their blocks (reverse table order, as BlockAllocator.free) and
+ *     become empty.
+ *   rk_pages_gather: out [B, width] int32 = the tables of rows[b], entries past the blocks held set to 0 (the
+ *     0-padded tables of batch_layout, src/state.py:124-128). */
+int rk_pages_init(int32_t* tables, int32_t* lens, int32_t* stack, int32_t* meta, int max_seqs, int max_blocks,
+                  int num_blocks, void* stream);
+int rk_pages_advance(int32_t* tables, int32_t* lens, int32_t* stack, int32_t* meta, int max_seqs, int max_blocks,
+                     int num_blocks, int block_size, const int32_t* rows, int B, int n_new, int64_t* slots,
+                     int32_t* out_lens, void* stream);
+int rk_pages_release(int32_t* tables, int32_t* lens, int32_t* stack, int32_t* meta, int max_seqs, int max_blocks,
+                     int num_blocks, int block_size, const int32_t* rows, int R, void* stream);
+int rk_pages_gather(const int32_t* tables, const int32_t* lens, int max_seqs, int max_blocks, int block_size,
+                    const int32_t* rows, int B, int width, int32_t* out, void* stream);
 
 /* ---- P2: fused Gated DeltaNet decode step for B sequences (conv + SiLU, l2norm, beta/decay, delta rule, gated
  * RMSNorm). Replaces MetalBackend.deltanet_decode_batch + conv_step + gdn_decode (src/backend/metal.py:232-256;

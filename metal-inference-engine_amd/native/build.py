@@ -14,7 +14,7 @@ HERE = Path(__file__).resolve().parent
 LIB = HERE / "librk_path.so"
 PROBE_LIB = HERE / "librk_probe.so"       # measurement probes (include/rk_probe.h), not on the path
 OBJ_DIR = HERE / "_obj"
-SOURCES = ["rk_abi.cpp", "paged_decode.hip", "kv_cache.hip", "deltanet_step.hip", "paged_prefill.hip",
+SOURCES = ["rk_abi.cpp", "paged_decode.hip", "kv_cache.hip", "page_table.hip", "deltanet_step.hip", "paged_prefill.hip",
            "chunked_delta.hip", "deltanet_prefill.hip", "attn_prep.hip",
            "linear.hip", "decode_ops.hip"]
 PROBE_SOURCES = ["probes.hip"]

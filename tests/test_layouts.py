@@ -46,3 +46,31 @@ def test_ring_tables_name_the_unit_holding_each_window_block(W, bs, chunk):
         # a chunk of up to `chunk` tokens after the window still fits (the ring-size rule)
         span = math.ceil((n + chunk) / bs) - max(0, n - W + 1) // bs
         assert span <= ring
+
+
+# ---------------------------------------------------------------- the CPU model of the device page table
+
+def test_pages_model_known_answers():
+    """The reference allocator's documented behaviour (src/state.py:78-103): a fresh pool hands out block 0 first,
+    in ascending order; freed blocks come back in the order the table held them; growth takes only missing blocks."""
+    from oracle.pages_ref import PagesModel
+    m = PagesModel(num_blocks=10, max_seqs=4, max_blocks=5, block_size=4)
+    assert m.advance([0], 9) == ([0, 1, 2, 3, 4, 5, 6, 7, 8], [9])          # blocks 0, 1, 2
+    assert m.tables[0] == [0, 1, 2]
+    assert m.advance([1, 0], 1) == ([12, 9], [1, 10])                       # seq 1 takes block 3; seq 0 fits in 2
+    assert m.tables[1] == [3]
+    m.release([0])
+    assert m.advance([2], 6) == ([0, 1, 2, 3, 4, 5], [6])                    # blocks 0, 1 again, in table order
+    assert m.tables[2] == [0, 1] and len(m.free) == 10 - 3                  # blocks 3 (seq 1), 0, 1 (seq 2)
+
+
+def test_pages_model_all_or_nothing():
+    from oracle.pages_ref import PagesModel
+    m = PagesModel(num_blocks=3, max_seqs=3, max_blocks=8, block_size=2)
+    assert m.advance([0], 4) is not None                                     # 2 blocks taken, 1 free
+    before = ([list(t) for t in m.tables], list(m.lens), list(m.free))
+    assert m.advance([1, 2], 1) is None and m.status == 1                    # needs 2, 1 free: nothing moves
+    assert ([list(t) for t in m.tables], list(m.lens), list(m.free)) == before
+    m.status = 0
+    assert m.advance([0], 100) is None and m.status == 2                     # past max_blocks
+    assert m.advance([5], 1) is None and m.status == 4                       # no such row
