@@ -282,7 +282,8 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
  * ops.rms_norm, ops.layer_norm, ops.rope, ops.silu_mul, src/ops.py:7-54, 107-110). fp32 outputs, contiguous.
  *
  * rk_rms_norm: out [rows, D] = (x / sqrt(mean(x^2) + eps)) * w; x rows at x + r * x_ld (RK_F32 / RK_BF16),
- *   w [D] (RK_F32 / RK_BF16); D a multiple of 4, at most 4096; x, w, out aligned to 4 elements.
+ *   w [D] (RK_F32 / RK_BF16); any D >= 1 and x_ld >= D (rows of up to 4096 values, a multiple of 4, with x, w,
+ *   out aligned to 4 elements stay in registers, one wave per row; other rows take a workgroup each).
  * rk_layer_norm: out = w * ((x - mean) * (1 / sqrt(var + eps))), no bias; arguments as rk_rms_norm.
  * rk_rope: out [T, H, d] = x rotated by positions[t] * inv_freq[i] over the pairs (i, i + d/2) (HF rotate_half);
  *   inv_freq [d/2] fp32 as the reference computes it on the host (ops.rope_inv_freq).

@@ -12,7 +12,8 @@
 // Means are sums of rounded terms in a different order than torch's (a wave tree), within the 1e-5 bar; the square
 // root and divisions are correctly rounded, cos / sin / exp are the device library's.
 // Norms: one wave per row, lane l holding 4-float chunks l, l + 64, ... of it (rows of up to 64 * 4 * MAXV
-// values stay in registers: one read of x, one write of out). RoPE and silu_mul: one thread per element pair /
+// values stay in registers: one read of x, one write of out); any other row (longer than 4096, a length not a
+// multiple of 4, or unaligned) takes a workgroup of its own and reads its row two or three times. RoPE and silu_mul: one thread per element pair /
 // four elements.
 #include "rk_device.h"
 #include "rk_internal.h"
@@ -90,6 +91,56 @@ __global__ __launch_bounds__(256) void row_norm_kernel(float* __restrict__ out, 
     }
 }
 
+// Rows the register kernel does not take (D above 4096, D not a multiple of 4, or unaligned rows): one workgroup of
+// 256 threads per row, thread t holding elements t, t + 256, ... of it; the sums go through a wave tree and LDS.
+// RMSNorm reads the row twice (sum of squares, then the output), LayerNorm three times (mean, centred squares,
+// output); a row of a few thousand values stays in L2 between the passes.
+__device__ __forceinline__ float ld1(const void* p, long long off, int dt) {
+    return dt == RK_BF16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(p)[off]) : static_cast<const float*>(p)[off];
+}
+
+__device__ __forceinline__ float block256_sum(float x, float* red) {
+    x = wave_sum(x);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = x;
+    __syncthreads();
+    const float t = __fadd_rn(__fadd_rn(red[0], red[1]), __fadd_rn(red[2], red[3]));
+    __syncthreads();                                // red is reused by the next reduction
+    return t;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void row_norm_wide_kernel(float* __restrict__ out, const void* __restrict__ x,
+                                                            int x_dtype, long long ld, const void* __restrict__ w,
+                                                            int w_dtype, int D, float eps) {
+    __shared__ float red[4];
+    const long long row = blockIdx.x;
+    const long long xo = row * ld;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float v = ld1(x, xo + i, x_dtype);
+        s = KIND == 0 ? __fadd_rn(s, __fmul_rn(v, v)) : __fadd_rn(s, v);
+    }
+    s = block256_sum(s, red);
+    float scale, mean = 0.0f;
+    if constexpr (KIND == 0) {
+        scale = sqrtf(__fadd_rn(__fdiv_rn(s, (float)D), eps));
+    } else {
+        mean = __fdiv_rn(s, (float)D);
+        float q = 0.0f;
+        for (int i = threadIdx.x; i < D; i += 256) {
+            const float c = __fsub_rn(ld1(x, xo + i, x_dtype), mean);
+            q = __fadd_rn(q, __fmul_rn(c, c));
+        }
+        q = block256_sum(q, red);
+        scale = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(q, (float)D), eps)));
+    }
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float v = ld1(x, xo + i, x_dtype), wv = ld1(w, i, w_dtype);
+        out[row * D + i] = KIND == 0 ? __fmul_rn(__fdiv_rn(v, scale), wv) : __fmul_rn(wv, __fmul_rn(__fsub_rn(v, mean), scale));
+    }
+}
+
 // RoPE over whole heads: thread (t, h, i < d/2) rotates the pair (i, i + d/2) of x[t, h].
 __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ out, const float* __restrict__ x,
                                                    const int32_t* __restrict__ pos,
@@ -143,13 +194,18 @@ int launch_norm(float* out, const void* x, int x_dtype, long long ld, const void
     if (!out || !x || !w) return fail(RK_ERR_ARG, "%s: null pointer", name);
     if ((x_dtype != RK_F32 && x_dtype != RK_BF16) || (w_dtype != RK_F32 && w_dtype != RK_BF16))
         return fail(RK_ERR_UNSUPPORTED, "%s: dtypes x %d, w %d", name, x_dtype, w_dtype);
-    if (rows < 0 || D < 4 || D % 4 || D > kMaxNormD || ld < D || ld % 4)
-        return fail(RK_ERR_ARG, "%s: rows %d, D %d (4 .. %d, a multiple of 4), row stride %lld", name, rows, D,
-                    kMaxNormD, ld);
+    if (rows < 0 || D < 1 || ld < D)
+        return fail(RK_ERR_ARG, "%s: rows %d, D %d, row stride %lld", name, rows, D, ld);
     const size_t xa = x_dtype == RK_BF16 ? 8 : 16, wa = w_dtype == RK_BF16 ? 8 : 16;
-    if (reinterpret_cast<uintptr_t>(x) % xa || reinterpret_cast<uintptr_t>(w) % wa ||
-        reinterpret_cast<uintptr_t>(out) % 16)
-        return fail(RK_ERR_ARG, "%s: x, w and out must be aligned to 4 elements", name);
+    const bool in_registers = D % 4 == 0 && D <= kMaxNormD && ld % 4 == 0 &&
+                              reinterpret_cast<uintptr_t>(x) % xa == 0 && reinterpret_cast<uintptr_t>(w) % wa == 0 &&
+                              reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    if (!in_registers) {
+        if ((unsigned long long)rows > 0x7fffffffull) return fail(RK_ERR_ARG, "%s: %d rows", name, rows);
+        hipLaunchKernelGGL(row_norm_wide_kernel<KIND>, dim3((unsigned)rows), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), out, x, x_dtype, ld, w, w_dtype, D, eps);
+        return check_launch(name);
+    }
     using Fn = void (*)(float*, const void*, int, long long, const void*, int, int, int, float);
     const int nv = (D / 4 + 63) / 64;
     const Fn fn = nv <= 1 ? row_norm_kernel<KIND, 1> : nv <= 2 ? row_norm_kernel<KIND, 2>

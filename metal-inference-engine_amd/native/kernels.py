@@ -784,26 +784,23 @@ def linear(x, w, bias=None, residual=None) -> torch.Tensor:
     return y + residual.float() if residual is not None else y
 
 
-NORM_MAX_D = 4096           # rk_rms_norm / rk_layer_norm keep a row in registers: up to 4096 values
-
-
 def _norm(entry: str, x, w, eps: float) -> torch.Tensor:
+    """Rows of any length D: up to 4096 values (a multiple of 4, aligned) stay in registers, one wave per row; any
+    other row takes a workgroup of its own (rk_rms_norm / rk_layer_norm choose)."""
     name = entry[3:]
     D = x.shape[-1]
-    if w.numel() != D or D % 4 or D > NORM_MAX_D:
-        raise ValueError(f"{name}: x {tuple(x.shape)}, w {tuple(w.shape)} (D a multiple of 4, at most {NORM_MAX_D})")
+    if w.numel() != D or D < 1:
+        raise ValueError(f"{name}: x {tuple(x.shape)}, w {tuple(w.shape)}")
     dev = _need_cuda(name, x)
     shape = x.shape
     if x.dtype not in KV_DTYPES:
         x = x.float()
     x = x.reshape(-1, D)
-    if x.stride(1) != 1 or x.stride(0) % 4 or x.data_ptr() % (4 * x.element_size()):
-        x = x.contiguous() if not x.is_contiguous() else x.clone()
+    if x.stride(1) != 1:
+        x = x.contiguous()
     if w.dtype not in KV_DTYPES:
         w = w.float()
     w = w.to(dev).contiguous()
-    if w.data_ptr() % (4 * w.element_size()):
-        w = w.clone()
     rows = x.shape[0]
     out = torch.empty(rows, D, dtype=torch.float32, device=dev)
     load().call(entry, out.data_ptr(), x.data_ptr(), DTYPE_CODES[x.dtype], x.stride(0), w.data_ptr(),

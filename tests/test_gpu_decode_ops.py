@@ -3,9 +3,10 @@ layer_norm / rope / silu_mul / swiglu / prepare) with the oracle's restatement o
 (oracle/ops_ref.py: src/ops.py:7-54, 107-110), and a whole MLP block and attention-input block of a decode step
 composed from backend calls against the same composition on the oracle.
 
-Bar: fp32 outputs within 1e-5 relative (max |diff| / max |ref|). Edge cases: D from 4 to 4096 (one chunk per lane to
-sixteen; D not a multiple of 256), bf16 inputs and weights read as stored, strided rows, large positions, F not a
-multiple of 4 (the scalar path), the two halves of one projection read in place."""
+Bar: fp32 outputs within 1e-5 relative (max |diff| / max |ref|). Edge cases: D from 1 to 12290 (one chunk per lane to
+sixteen; D not a multiple of 256 or of 4; rows past 4096 values), bf16 inputs and weights read as stored, strided and
+unaligned rows, large positions, F not a multiple of 4 (the scalar path), the two halves of one projection read in
+place."""
 import pytest
 import torch
 
@@ -41,6 +42,24 @@ def test_row_norms(backend, kind, D):
     wide = torch.randn(37, 2 * D + 8, generator=g)
     view = wide.to(DEV)[:, 4:4 + D]
     assert rel_err(fn(view, w.to(DEV), 1e-6), ref(wide[:, 4:4 + D], w, 1e-6)) < TOL
+
+
+@pytest.mark.parametrize("D", [1, 5, 4097, 4100, 8192, 12290])
+@pytest.mark.parametrize("kind", ["rms", "layer"])
+def test_row_norms_of_any_length(backend, kind, D):
+    """Rows the register kernel does not take (longer than 4096, a length not a multiple of 4, unaligned): the
+    reference's ops have no limit on D (src/ops.py:7-24)."""
+    g = torch.Generator().manual_seed(100 + D)
+    x = torch.randn(9, D, generator=g) * 3 - 0.25
+    w = torch.randn(D, generator=g)
+    ref = ops_ref.rms_norm if kind == "rms" else ops_ref.layer_norm
+    fn = backend.rms_norm if kind == "rms" else backend.layer_norm
+    assert rel_err(fn(x.to(DEV), w.to(DEV), 1e-6), ref(x, w, 1e-6)) < TOL
+    xb, wb = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    assert rel_err(fn(xb.to(DEV), wb.to(DEV), 1e-5), ref(xb, wb, 1e-5)) < TOL
+    wide = torch.randn(9, 2 * D + 3, generator=g)   # rows strided by an odd number of elements, start unaligned
+    view = wide.to(DEV)[:, 1:1 + D]
+    assert rel_err(fn(view, w.to(DEV), 1e-6), ref(wide[:, 1:1 + D], w, 1e-6)) < TOL
 
 
 def test_row_norm_of_constant_rows(backend):
