@@ -338,13 +338,16 @@ def bench_deltanet(args, backend):
     }
 
 
-def bench_prefill(args, backend):
+def bench_prefill(args, backend, chunk: bool = False):
+    """Config 5 (chunk False), or one 512-token chunk over a 32,768-token history (chunk True: the grid without
+    split key ranges would fill 32 of 256 CUs)."""
     import torch
     import workloads as wl
     from native import kernels
     dev = backend.device
     stream = torch.cuda.current_stream(dev)
-    case = wl.c5_prefill()
+    case = wl.chunk_prefill() if chunk else wl.c5_prefill()
+    tag = "ck" if chunk else "c5"
     c = case.to(dev)
     torch.cuda.synchronize()
 
@@ -356,14 +359,16 @@ def bench_prefill(args, backend):
     flops = case.flops()
     tflops = flops / (ms * 1e-3) / 1e12
     N = case.q.shape[0]
-    log(f"[bench] c5: {ms * 1e3:.1f} us per packed prefill, {tflops:.1f} TFLOP/s")
+    log(f"[bench] {tag}: {ms * 1e3:.1f} us per packed prefill, {tflops:.1f} TFLOP/s")
     cpu = None
     if not args.no_cpu:
         from oracle import prefill_ref
         torch.set_num_threads(cpu_threads())
-        # sample: the shortest segment, scaled to the whole batch by flops
+        # sample: the shortest segment (of the chunk: its first 64 tokens), scaled to the whole batch by flops
         s = min(range(len(case.starts)), key=lambda i: case.lengths()[i] * (case.starts[i] + case.lengths()[i]))
         lo, hi = case.cu_seqlens[s], case.cu_seqlens[s + 1]
+        if chunk:
+            hi = lo + 64
         one = wl.PrefillCase(case.q[lo:hi], case.k_new[lo:hi], case.v_new[lo:hi], case.gate[lo:hi],
                              case.k_pool.clone(), case.v_pool.clone(), case.tables[s:s + 1], [0, hi - lo],
                              [case.starts[s]], case.block_size)
@@ -376,6 +381,22 @@ def bench_prefill(args, backend):
                "sample": f"segment {s} alone ({hi - lo} new tokens on a {case.starts[s]}-token prefix): median of "
                          f"{calls} calls ({total:.1f} s in all), {t:.3f} s per call, scaled to the whole pack by "
                          f"flops"}
+    work, n_slots = kernels.prefill_work(case.lengths(), case.starts, None, True, kernels.PREFILL_SPLIT_TILES,
+                                         case.k_pool.shape[2], kernels.device_cus(dev))
+    if chunk:
+        return {
+            "metric": "chunked-prefill attention tokens/s (512 new on 32,768 cached) + TFLOP/s, 1 GPU",
+            "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded)",
+            "config": {"workload": "one 512-token chunk after 32,768 cached positions, 8/2 heads x 256, block 16, "
+                                   "causal, gate, KV write-back", "new_tokens": N, "flops": flops,
+                       "work_entries": len(work) // 5, "split_pieces": n_slots},
+            "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": tflops / 2500.0, "traffic": None,
+                         "kernel": "prefill_attention (+ prefill_kv_write)", "avg_ms": ms},
+            "cpu_baseline": cpu,
+        }
     return {
         "metric": "packed prefill attention tokens/s (config 5) + TFLOP/s (% of bf16 MFMA peak), 1 GPU",
         "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -832,7 +853,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c4", "c5", "lp", "ap", "wd", "mv", "ds"],
+                    choices=["all", "c1", "c2", "c3", "c4", "c5", "ck", "lp", "ap", "wd", "mv", "ds"],
                     help="all (default): the config-3 headline record with configs 1, 2, 4, 5 as sub-records and "
                          "the measured access-pattern ceilings")
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
@@ -908,6 +929,8 @@ def main() -> int:
         rec["metric"] = "sliding-window decode attn tokens/s @ batch 64 (grouped pool rings) + achieved HBM GB/s, 1 GPU"
     elif args.workload == "c5":
         rec = bench_prefill(args, backend)
+    elif args.workload == "ck":
+        rec = bench_prefill(args, backend, chunk=True)
     elif args.workload == "c4":
         rec = bench_chunked_delta(args, backend)
     elif args.workload == "lp":

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 12
+#define RK_ABI_VERSION 13
 
 /* status codes */
 #define RK_OK 0
@@ -142,8 +142,16 @@ int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float
  *   tables [S, max_nb] (blocks for positions < start[s] + n[s] must be allocated).
  *   The new rows are written into k_pool / v_pool (pool_dtype; fp32 -> bf16 rounds to nearest even) before any
  *   attention reads, then query i of segment s attends causally to positions 0 .. start[s] + i.
- *   work [n_work] int32: (segment << 16) | query block (blocks of 32 queries), in the order to schedule them
- *   (longest key range first balances the grid); every block of every segment must appear once.
+ *   work [n_work][5] int32, in the order to schedule them (longest first balances the grid): {(segment << 16) |
+ *   query block (blocks of 32 queries), first key tile, end key tile (tiles of 32 positions; the entry covers the
+ *   block's keys within [first * 32, end * 32)), first partial slot or -1, (piece << 16) | pieces}. An entry with
+ *   slot -1 is a whole block (every block of every segment appears once, as one whole entry or as all the pieces
+ *   of one split). A block split into `pieces` entries over disjoint consecutive tile ranges uses the partial slots
+ *   first .. first + pieces - 1 (unique, < n_slots): each piece writes its (o, m, l) there and the last to finish
+ *   combines them in piece order, so the output does not depend on the finishing order.
+ *   n_slots 0: no splits (partials, counters may be NULL); else partials of rk_paged_prefill_workspace_bytes(n_slots,
+ *   Hkv, D) bytes (no zeroing needed) and counters of n_slots * Hkv * 4 uint32, zero before the call; every call
+ *   leaves them at zero.
  *   gate NULL or [N, Hq*D] in gate_dtype (RK_F32 or RK_BF16, read as stored). Group size Hq / Hkv = 4, D in {128, 256},
  *   max_nb * block_size^2 < 2^32. bf16 MFMA operands, fp32 accumulation.
  *   window 0 or W >= 1 (causal only): query i also sees only positions above start[s] + i - W (the sliding-window
@@ -156,7 +164,11 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
                      int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
-                     int window, int causal, void* stream);
+                     int window, int causal, int n_slots, float* partials, size_t partial_bytes, uint32_t* counters,
+                     void* stream);
+
+/* Bytes of rk_paged_prefill's partial records for n_slots split pieces (kv-heads Hkv, head_dim D). */
+size_t rk_paged_prefill_workspace_bytes(int n_slots, int Hkv, int D);
 
 /* ---- P3: chunked gated delta rule (64-token chunks, WY / UT form) for packed prefill of the linear-attention
  * layers. Replaces Backend.gated_delta with T > 1 (TorchBackend.gated_delta -> ops.gated_delta_chunked,

@@ -60,6 +60,17 @@ def workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+_cus: dict[int, int] = {}
+
+
+def device_cus(dev: torch.device) -> int:
+    """The device's compute units (256 on an MI355X), read once per device."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _cus:
+        _cus[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _cus[idx]
+
+
 def paged_decode(q, k_pool, v_pool, tables, lens, block_size: int, window: int | None = None, gate=None,
                  out=None, phase: int | None = None) -> torch.Tensor:
     """Batched decode attention over one layer of a paged pool (rk_paged_decode). q [B, Hq, d] -> [B, Hq, d] fp32.
@@ -193,40 +204,83 @@ def deltanet_decode(qkv, z, b, a, conv_state, S, seq_index, slot: int, conv_w, A
 
 
 PREFILL_BLOCK = 32          # queries per work item of rk_paged_prefill
+PREFILL_TILE = 32           # key positions per tile of rk_paged_prefill
+PREFILL_SPLIT_TILES = None  # None: split only when the blocks x KV heads leave CUs idle; an int forces a split size
+PREFILL_MIN_SPLIT = 32      # the smallest automatic piece, in tiles (1024 keys: the merge stays a small fraction)
 
 
-def prefill_work(lengths: list[int], starts: list[int], window: int | None = None, causal: bool = True) -> list[int]:
-    """The work list of rk_paged_prefill: one item (segment << 16 | query block) per block of 32 new queries,
-    longest key range first so the longest items start first (a window bounds an item's range to about W + 32
-    keys; without causal masking every item of a segment reads all of its keys)."""
-    items = []
+def prefill_split_tiles(spans: list[int], heads: int, n_cu: int) -> int:
+    """The automatic split size of rk_paged_prefill's work list, from the key span (in tiles) of each 32-query
+    block: 0 (no split) when the blocks times the KV heads already give every CU a workgroup, else the size that
+    cuts the total into about one workgroup per CU, at least PREFILL_MIN_SPLIT tiles. A split block costs a partial
+    record per piece and a merge, which only pays where CUs would otherwise idle (one long chunk over a long
+    prefix: a 512-query chunk is 16 blocks, 32 workgroups with 2 KV heads, on 256 CUs)."""
+    if not spans or len(spans) * heads >= n_cu:
+        return 0
+    per_cu = -(-sum(spans) * heads // n_cu)
+    return max(PREFILL_MIN_SPLIT, per_cu)
+
+
+def prefill_work(lengths: list[int], starts: list[int], window: int | None = None, causal: bool = True,
+                 split_tiles: int | None = PREFILL_SPLIT_TILES, heads: int = 1,
+                 n_cu: int = 256) -> tuple[list[int], int]:
+    """The work list of rk_paged_prefill -> (entries, partial slots used). One entry of 5 int32 per block of 32 new
+    queries, {(segment << 16) | block, first tile, end tile, first slot or -1, (piece << 16) | pieces}; a block whose
+    key range spans more than split_tiles tiles of 32 positions is split at absolute multiples of split_tiles into
+    pieces (consecutive partial slots), which the kernel combines in piece order. split_tiles None takes
+    prefill_split_tiles over the blocks (heads = KV heads, n_cu = the device's CUs); 0 never splits. For a given
+    split size, where a block is cut depends only on the block, so a segment packed with others gives the same
+    bits as the segment alone under the same split size. Entries go longest first, so the longest start first (a
+    window bounds a block's range to about W + 32 keys; without causal masking every block of a segment reads all
+    of its keys)."""
+    blocks = []
     for s, (n, p) in enumerate(zip(lengths, starts)):
         for qb in range(-(-n // PREFILL_BLOCK)):
             hi = p + min(n, (qb + 1) * PREFILL_BLOCK) if causal else p + n
             lo = max(0, p + qb * PREFILL_BLOCK - window + 1) if window else 0
-            items.append((hi - lo, (s << 16) | qb))
-    items.sort(key=lambda x: -x[0])
-    return [w for _, w in items]
+            blocks.append(((s << 16) | qb, lo // PREFILL_TILE, -(-hi // PREFILL_TILE)))
+    if split_tiles is None:
+        split_tiles = prefill_split_tiles([t1 - t0 for _, t0, t1 in blocks], heads, n_cu)
+    entries, n_slots = [], 0
+    for word, t0, t1 in blocks:
+        if split_tiles <= 0 or t1 - t0 <= split_tiles:
+            entries.append((t1 - t0, [word, t0, t1, -1, 1]))
+            continue
+        cuts = [t0] + list(range((t0 // split_tiles + 1) * split_tiles, t1, split_tiles)) + [t1]
+        pieces = len(cuts) - 1
+        for i in range(pieces):
+            entries.append((cuts[i + 1] - cuts[i], [word, cuts[i], cuts[i + 1], n_slots, (i << 16) | pieces]))
+        n_slots += pieces
+    entries.sort(key=lambda x: -x[0])
+    return [v for _, e in entries for v in e], n_slots
 
 
 def _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu: list[int], st: list[int], gate,
                     window: int, causal: bool) -> None:
-    """rk_paged_prefill with the host-side segment offsets, start positions and work list in one int32 array."""
+    """rk_paged_prefill with the host-side segment offsets, start positions and work list in one int32 array, and
+    the partial records / arrival counters of split blocks from the device's shared workspace."""
     S = len(st)
     N, Hq, d = q.shape
     NB, bs, Hkv, _ = k_pool.shape
     dev = q.device
-    meta = to_device(torch.tensor(cu + st + prefill_work([b - a for a, b in zip(cu, cu[1:])], st, window, causal),
-                                  dtype=torch.int32), dev)
-    n_work = meta.numel() - (2 * S + 1)
-    load().call("rk_paged_prefill", out.data_ptr(), q.data_ptr(), DTYPE_CODES[q.dtype],
-                k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
-                DTYPE_CODES[k_new.dtype] if k_new is not None else DTYPE_CODES[torch.float32],
-                k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype], tables.data_ptr(), tables.shape[1],
-                meta.data_ptr(), meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq,
-                Hkv, d, bs, NB, gate.data_ptr() if gate is not None else None,
-                DTYPE_CODES[gate.dtype] if gate is not None else DTYPE_CODES[torch.float32], int(window or 0),
-                1 if causal else 0, _stream(dev))
+    work, n_slots = prefill_work([b - a for a, b in zip(cu, cu[1:])], st, window, causal, PREFILL_SPLIT_TILES,
+                                 Hkv, device_cus(dev))
+    meta = to_device(torch.tensor(cu + st + work, dtype=torch.int32), dev)
+    n_work = len(work) // 5
+    lib = load()
+    part_ptr, part_bytes, cnt_ptr = None, 0, None
+    if n_slots:
+        part_bytes = lib.lib.rk_paged_prefill_workspace_bytes(n_slots, Hkv, d)
+        part_ptr = workspace(dev, part_bytes).data_ptr()
+        cnt_ptr = linear_counters(dev, n_slots * Hkv * 4).data_ptr()
+    lib.call("rk_paged_prefill", out.data_ptr(), q.data_ptr(), DTYPE_CODES[q.dtype],
+             k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
+             DTYPE_CODES[k_new.dtype] if k_new is not None else DTYPE_CODES[torch.float32],
+             k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype], tables.data_ptr(), tables.shape[1],
+             meta.data_ptr(), meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq,
+             Hkv, d, bs, NB, gate.data_ptr() if gate is not None else None,
+             DTYPE_CODES[gate.dtype] if gate is not None else DTYPE_CODES[torch.float32], int(window or 0),
+             1 if causal else 0, n_slots, part_ptr, part_bytes, cnt_ptr, _stream(dev))
 
 
 def _prefill_shape_check(name: str, Hq: int, Hkv: int, d: int) -> None:
@@ -724,8 +778,9 @@ _linear_cnt: dict[int, torch.Tensor] = {}
 
 
 def linear_counters(dev: torch.device, n: int) -> torch.Tensor:
-    """rk_linear_rows's per-row-block arrival counters on dev: zero-filled when (re)allocated, and every call leaves
-    them at zero, so one buffer serves all stream-ordered calls."""
+    """The arrival counters of rk_linear_rows (per row block) and rk_paged_prefill (per split block, kv-head and
+    head) on dev: zero-filled when (re)allocated, and every call of either leaves them at zero, so one buffer serves
+    all stream-ordered calls."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     buf = _linear_cnt.get(idx)
     if buf is None or buf.numel() < n:

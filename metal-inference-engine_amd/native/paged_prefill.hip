@@ -32,6 +32,8 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBQ = 32;    // queries per wave
+constexpr int kMaxGroup = 4;  // query heads per kv-head (the only group size built)
+constexpr int kWorkInts = 5;  // int32 per work entry
 constexpr int kKPad = 8;   // bf16 padding of a K row in LDS (16 bytes)
 constexpr int kVPad = 4;   // bf16 padding of a V^T row in LDS: rows of 18 dwords (= 2 mod 4) put 16
                            // consecutive rows' 8-byte pieces on distinct bank pairs
@@ -46,13 +48,16 @@ struct PrefillArgs {
     const int32_t* tables;      // [S, max_nb]
     const int32_t* cu;          // [S + 1] new-row offsets
     const int32_t* start;       // [S] absolute position of each segment's first new token
-    const int32_t* work;        // [n_work] (segment << 16) | query block, longest first
+    const int32_t* work;        // [n_work][kWorkInts]: (segment << 16) | query block, first and end key tile, first
+                                // partial slot (-1: the whole item), (piece << 16) | pieces; longest first
+    float* part;                // split items: per (slot, kv-head, head) the piece's (o, m, l) record
+    uint32_t* cnt;              // split items: per (first slot, kv-head, head) arrival counter, zero between calls
     const void* gate;           // [N, Hq * D] gate_dtype, or null
     int gate_dtype;
     int window;                 // 0: none; W: keys above position - W (causal only)
     int causal;                 // 0: every query sees all of its segment's keys
     int q_dtype, new_dtype, pool_dtype;
-    int S, n_work, N, Hq, Hkv, G, bs, max_nb, num_blocks;
+    int S, n_work, N, Hq, Hkv, G, bs, max_nb, num_blocks, n_slots;
     float qscale;               // log2(e) / sqrt(D)
     uint32_t bs_recip;          // ceil(2^32 / bs): pos / bs = mulhi(pos, bs_recip) for pos * bs < 2^32
 };
@@ -197,7 +202,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int G = a.G;
     const bool producer = wave >= G;
     const int kvh = blockIdx.y;
-    const int item = a.work[blockIdx.x];
+    const int32_t* we = a.work + (long long)kWorkInts * blockIdx.x;
+    const int item = we[0];
     const int seg = item >> 16, qblk = item & 0xffff;
     const int row0 = a.cu[seg] + qblk * kBQ;
     const int nq = min(kBQ, a.cu[seg + 1] - row0);
@@ -206,8 +212,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // whole segment
     const int n_keys = a.causal ? p0 + nq : a.start[seg] + (a.cu[seg + 1] - a.cu[seg]);
     const int kmin = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
-    const int t_first = kmin / kBKP;                 // tiles t_first .. t_first + n_tiles - 1
-    const int n_tiles = (n_keys + kBKP - 1) / kBKP - t_first;
+    // this work entry's key tiles: the item's (kmin / 32 .. the tile holding key n_keys - 1) within the entry's range
+    const int t_first = max(kmin / kBKP, we[1]);     // tiles t_first .. t_first + n_tiles - 1
+    const int n_tiles = min((n_keys + kBKP - 1) / kBKP, we[2]) - t_first;
     const int b_first = kmin / a.bs;                 // first block read
     const int32_t* table = a.tables + (long long)seg * a.max_nb;
 
@@ -460,6 +467,75 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         lds_barrier();
     }
 
+    // A piece of a split item stores its (o, m, l) for its head, then counts itself in; the last of the item's
+    // pieces to finish reads all of them back in piece order and combines them: m = max m_p,
+    // l = sum 2^(m_p - m) l_p, o = sum 2^(m_p - m) o_p, so the result depends only on the pieces, not on which
+    // finishes last. It then leaves the counter at zero and goes on to the normal output below.
+    // The records go through a buffer resource of exactly one record with the sc1 cache policy (the bit that
+    // agent-scope atomic loads and stores carry: coherent across the device's L2s), as 16-byte transfers issued
+    // back to back, with one wait per piece; the stores complete (vmcnt 0) before the wave counts itself in.
+    const int piece = we[4] >> 16, pieces = we[4] & 0xffff;
+    const int first = we[3] >= 0 && piece < pieces && we[3] + pieces <= a.n_slots ? we[3] : -1;   // slots in range
+    if (first >= 0) {
+        constexpr int REC = kBQ * D + 2 * kBQ;
+        constexpr int kSc1 = 16;                     // cache-policy operand: sc1
+        auto rsrc_of = [&](int pc) {
+            const unsigned long long u = reinterpret_cast<unsigned long long>(
+                a.part + (((long long)(first + pc) * a.Hkv + kvh) * kMaxGroup + wave) * REC);
+            const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
+            const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+            return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo),
+                                                     (short)0, REC * 4, 0x00020000);
+        };
+        auto o_off = [&](int dt, int q) { return 4 * (col * D + 32 * dt + 8 * q + 4 * kg); };
+        const int m_off = 4 * (kBQ * D + col), l_off = 4 * (kBQ * D + kBQ + col);
+        {
+            const auto rs = rsrc_of(piece);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, f32x4{o[dt][4 * q], o[dt][4 * q + 1], o[dt][4 * q + 2],
+                                                        o[dt][4 * q + 3]}),
+                        rs, o_off(dt, q), 0, kSc1);
+            if (kg == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), rs, m_off, 0, kSc1);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), rs, l_off, 0, kSc1);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): this wave's stores have completed
+        uint32_t* counter = a.cnt + ((long long)first * a.Hkv + kvh) * kMaxGroup + wave;
+        uint32_t before = 0;
+        if (lane == 0) before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        before = __shfl(before, 0);
+        if (before != (uint32_t)(pieces - 1)) return;
+        float mx = -INFINITY;
+#pragma unroll 4
+        for (int pc = 0; pc < pieces; ++pc)
+            mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_of(pc), m_off, 0, kSc1)));
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x16{};
+        l_run = 0.0f;
+        for (int pc = 0; pc < pieces; ++pc) {
+            const auto rs = rsrc_of(pc);
+            u32x4 v[NDT][4];
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[dt][q] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off(dt, q), 0, kSc1);
+            const float mp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, m_off, 0, kSc1));
+            const float lp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, l_off, 0, kSc1));
+            const float sc = mp == -INFINITY ? 0.0f : fast_exp2(mp - mx);     // a piece with no key for this row
+            l_run = fmaf(sc, lp, l_run);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][r] = fmaf(sc, __uint_as_float(v[dt][r / 4][r % 4]), o[dt][r]);
+        }
+        if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // The gate values of a 32-dim block are requested together (one branch per block, not per element: a
     // branch per element would make every gate load a round trip of its own).
     if (col < nq) {
@@ -506,12 +582,23 @@ using namespace rk;
 
 extern "C" {
 
+size_t rk_paged_prefill_workspace_bytes(int n_slots, int Hkv, int D) {
+    if (n_slots <= 0 || Hkv <= 0 || D <= 0) return 0;
+    return (size_t)n_slots * Hkv * kMaxGroup * (kBQ * (size_t)D + 2 * kBQ) * sizeof(float);
+}
+
 int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, const void* v_new, int new_dtype,
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
                      int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
-                     int window, int causal, void* stream) {
+                     int window, int causal, int n_slots, float* partials, size_t partial_bytes, uint32_t* counters,
+                     void* stream) {
     if (N == 0) return RK_OK;
+    if (n_slots < 0 || (n_slots > 0 && (!partials || !counters)))
+        return fail(RK_ERR_ARG, "rk_paged_prefill: %d partial slots need partials and counters", n_slots);
+    if (n_slots > 0 && partial_bytes < rk_paged_prefill_workspace_bytes(n_slots, Hkv, D))
+        return fail(RK_ERR_WORKSPACE, "rk_paged_prefill: %zu partial bytes for %d slots (need %zu)", partial_bytes,
+                    n_slots, rk_paged_prefill_workspace_bytes(n_slots, Hkv, D));
     if (!out || !q || !k_pool || !v_pool || !tables || !cu_seqlens || !start_pos || !work)
         return fail(RK_ERR_ARG, "rk_paged_prefill: null pointer");
     if (!k_new != !v_new) return fail(RK_ERR_ARG, "rk_paged_prefill: k_new and v_new must both be given or both null");
@@ -536,6 +623,7 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     a.q_dtype = q_dtype; a.new_dtype = new_dtype; a.pool_dtype = pool_dtype;
     a.S = S; a.n_work = n_work; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.bs = block_size;
     a.max_nb = max_nb; a.num_blocks = num_blocks;
+    a.part = partials; a.cnt = counters; a.n_slots = n_slots;
     a.qscale = kLog2e / sqrtf((float)D);
     a.bs_recip = (uint32_t)(0xffffffffu / (uint32_t)block_size + 1u);
     hipStream_t s = static_cast<hipStream_t>(stream);

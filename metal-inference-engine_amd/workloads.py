@@ -309,6 +309,13 @@ def c5_prefill(seed: int = 5) -> PrefillCase:
     return prefill_case(lengths, starts, seed=seed + 1000)
 
 
+def chunk_prefill(seed: int = 6) -> PrefillCase:
+    """One chunk of a chunked prefill over a long history: 512 new tokens after 32,768 cached positions, config 5's
+    heads (8/2 x 256), block 16, bf16 everything, sigmoid gate. 16 query blocks x 2 KV heads: the case the split
+    key ranges of the prefill work list are for."""
+    return prefill_case([512], [32768], seed=seed)
+
+
 @dataclass
 class ChunkedDeltaCase:
     """Packed prefill of one linear-attention layer's delta rule: sequence i is rows cu_seqlens[i] ..

@@ -1,7 +1,8 @@
 """The layout builders the workloads and GPU tests use (workloads.py), on the CPU: scattered tables cover each
 sequence with distinct blocks of the pool; ring tables name, for every block of a window, the ring unit a
 block-by-block write of the whole history left that block in (simulated here with a dict of unit -> block), and
-unit 0 below the window."""
+unit 0 below the window; the prefill attention's work list covers every query block once, whole or as pieces cut at
+absolute tile multiples."""
 import math
 
 import pytest
@@ -74,3 +75,56 @@ def test_pages_model_all_or_nothing():
     m.status = 0
     assert m.advance([0], 100) is None and m.status == 2                     # past max_blocks
     assert m.advance([5], 1) is None and m.status == 4                       # no such row
+
+
+@pytest.mark.parametrize("split", [0, 1, 2, 5, 320])
+@pytest.mark.parametrize("window,causal", [(None, True), (40, True), (None, False)])
+def test_prefill_work_covers_every_block_once(split, window, causal):
+    """rk_paged_prefill's work list: every (segment, block) appears as one whole entry or as pieces over consecutive
+    disjoint tile ranges that together are exactly the block's range, cut at absolute multiples of `split`; the
+    pieces of a block use consecutive slots; entries go longest first."""
+    from native import kernels
+    lengths, starts = [70, 129, 3, 40, 1], [50, 900, 500, 0, 7]
+    work, n_slots = kernels.prefill_work(lengths, starts, window, causal, split)
+    entries = [work[i:i + 5] for i in range(0, len(work), 5)]
+    sizes = [e[2] - e[1] for e in entries]
+    assert sizes == sorted(sizes, reverse=True) and min(sizes) >= 1
+    by_block, slots = {}, []
+    for word, t0, t1, first, pp in entries:
+        by_block.setdefault(word, []).append((t0, t1, first, pp >> 16, pp & 0xffff))
+    for s, (n, p) in enumerate(zip(lengths, starts)):
+        for qb in range(-(-n // 32)):
+            hi = p + min(n, 32 * (qb + 1)) if causal else p + n
+            lo = max(0, p + 32 * qb - window + 1) if window else 0
+            got = sorted(by_block.pop((s << 16) | qb))
+            assert got[0][0] == lo // 32 and got[-1][1] == -(-hi // 32)
+            if len(got) == 1:
+                assert got[0][2] == -1 and got[0][4] == 1
+                continue
+            assert all(a[1] == b[0] for a, b in zip(got, got[1:]))          # consecutive, disjoint
+            assert all(c[0] % split == 0 for c in got[1:])                  # cut at absolute multiples
+            first = got[0][2]
+            assert [(c[2], c[3], c[4]) for c in got] == [(first, i, len(got)) for i in range(len(got))]
+            slots.extend(range(first, first + len(got)))
+    assert not by_block
+    assert sorted(slots) == list(range(n_slots))
+
+
+def test_prefill_auto_split():
+    """The automatic split size: none while the 32-query blocks times the KV heads give every CU a workgroup (a
+    packed batch like config 5); for one chunk over a long prefix, pieces that bring the workgroups to about one
+    per CU, never smaller than the minimum piece."""
+    from native import kernels
+    assert kernels.prefill_split_tiles([500] * 128, 2, 256) == 0           # 256 workgroups already
+    assert kernels.prefill_split_tiles([], 2, 256) == 0
+    assert kernels.prefill_split_tiles([10] * 4, 2, 256) == kernels.PREFILL_MIN_SPLIT
+    spans = [1024 + i for i in range(16)]                                   # 512 queries after a 32K prefix
+    size = kernels.prefill_split_tiles(spans, 2, 256)
+    assert size == -(-sum(spans) * 2 // 256)
+    work, n_slots = kernels.prefill_work([512], [32768], None, True, None, 2, 256)
+    n = len(work) // 5
+    assert 256 <= 2 * n <= 2 * 256 + 2 * 16 and n_slots == n               # every block split, ~1 piece per CU
+    gen = torch.Generator().manual_seed(5)                                  # config 5's draw
+    lengths = torch.randint(64, 2049, (8,), generator=gen).tolist()
+    starts = torch.randint(0, 16385, (8,), generator=gen).tolist()
+    assert kernels.prefill_work(lengths, starts, None, True, None, 2, 256)[1] == 0   # config 5: not split
