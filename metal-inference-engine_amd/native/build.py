@@ -15,7 +15,7 @@ LIB = HERE / "librk_path.so"
 PROBE_LIB = HERE / "librk_probe.so"       # measurement probes (include/rk_probe.h), not on the path
 OBJ_DIR = HERE / "_obj"
 SOURCES = ["rk_abi.cpp", "paged_decode.hip", "kv_cache.hip", "page_table.hip", "deltanet_step.hip", "paged_prefill.hip",
-           "chunked_delta.hip", "deltanet_prefill.hip", "attn_prep.hip",
+           "chunked_delta.hip", "chunked_delta_cols.hip", "deltanet_prefill.hip", "attn_prep.hip",
            "linear.hip", "decode_ops.hip"]
 PROBE_SOURCES = ["probes.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -25,9 +25,13 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+# per-source additions: the bf16 delta scan splits and scales its MFMA results every chunk, so they stay in VGPRs
+SOURCE_FLAGS = {"chunked_delta_cols.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str, verbose: bool) -> Path:
     obj = OBJ_DIR / (Path(src).stem + ".o")
-    cmd = [HIPCC, "-x", "hip", "-c", str(HERE / src), "-o", str(obj)] + FLAGS
+    cmd = [HIPCC, "-x", "hip", "-c", str(HERE / src), "-o", str(obj)] + FLAGS + SOURCE_FLAGS.get(src, [])
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

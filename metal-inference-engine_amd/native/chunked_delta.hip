@@ -11,19 +11,21 @@
 //   S <- e^{G_last} S + K^T diag(e^{G_last - G}) vn                           (:190)
 // Rows past a sequence's end are zero (k = v = beta = g = 0), which leaves S untouched, as the reference's padding.
 //
-// Two kernels:
+// Kernels:
 //   delta_chunk_prep  one workgroup per (chunk, head), all chunks in parallel: beta, G (summed in fp64 and rounded
 //                     once, as torch's CPU cumsum of fp32 accumulates in double), exp(G), exp(G_last - G); K K^T and
 //                     Q K^T on MFMA from K rows staged in LDS; P = Q K^T * D; T by blocked inversion of the unit lower
 //                     triangular matrix (16 x 16 diagonal blocks by substitution, off-diagonal blocks by fp32 MFMA
 //                     products in three levels). T and P go to the workspace already split into bf16 pieces, in the
-//                     operand order the scan loads, so the 8 scan workgroups of a head share them instead of each
+//                     operand order the scan loads, so the scan workgroups of a head share them instead of each
 //                     recomputing them.
-//   delta_chunk_scan  one workgroup per (sequence, head, 32-column slice of S): the columns of S evolve
+//   delta_chunk_scan_cols (bf16 inputs, chunked_delta_cols.hip)  one workgroup per (sequence, head, 32-column slice
+//                     of S), one wave per 16 columns over all 64 tokens of a chunk: no exchange between waves at all.
+//   delta_chunk_scan  (fp32 inputs) one workgroup per (sequence, head, 32-column slice of S): the columns of S evolve
 //                     independently, so the serial pass over a sequence's chunks runs 4 workgroups wide per head.
 //                     Wave w owns token rows 16w..16w+15 of the chunk and state rows 32w..32w+31 (two 16-column
-//                     tiles sharing every A operand: the K / Q / T / P bytes a CU pulls from L2 per chunk, which
-//                     bound this kernel, are spread over 32 columns); the three
+//                     tiles sharing every A operand: the K / Q / T / P bytes a CU pulls from L2 per chunk are spread
+//                     over 32 columns); the three
 //                     exchanges per chunk (state pieces, Y, vn) go through LDS behind LDS-only barriers. Everything
 //                     chunk c+1 reads from global memory (K, Q, V rows, coefficients, T and P pieces) is requested at
 //                     the start of chunk c, so memory latency hides behind a whole chunk of work.
@@ -32,151 +34,13 @@
 // exact operands. Products are therefore exact to ~2^-20 relative and accumulate in fp32: fp32-level results.
 #include <type_traits>
 
-#include "rk_device.h"
+#include "chunked_delta.h"
 #include "rk_internal.h"
 
 namespace rk {
 namespace {
 
-constexpr int kC = 64;                       // tokens per chunk
-constexpr int kDk = 128, kDv = 128;
-constexpr int kCT = 2;                       // 16-column tiles of the state per scan wave
-constexpr int kCols = 16 * kCT;              // state columns per scan workgroup
-constexpr int kSlices = kDv / kCols;         // 4
-constexpr int kNS = 3;                       // bf16 pieces of an fp32 operand that changes with the state
-// bf16 pieces of the stored T and P entries: 3 = exact (truncation); 2 = round to nearest (2^-17), which saves a
-// third of the workspace traffic (6% of the call at config 4) but raises the output error ~10x, to ~5e-6
-constexpr int kTP = 3;
-constexpr int kCoefRows = 4;                 // beta, G, exp(G), exp(G_last - G)
-// per (chunk, head): T and P as kTP bf16 pieces of 3072 elements each, then the coefficient rows
-constexpr int kChunkFloats = 2 * kTP * 3072 / 2 + kCoefRows * kC;
-constexpr int kPieceRow = kC + 8;            // bf16 row stride of the [piece][column][token] exchange arrays
-constexpr int kStateRow = kDk + 8;           // bf16 row stride of the [piece][column][dk] state pieces
-
-struct DeltaArgs {
-    float* out;                 // [N, H, dv] fp32
-    float* S;                   // state of sequence i at S + idx(i) * s_stride, [H, dk, dv] fp32, in place
-    const void* q;              // [N, H, dk] bf16 or fp32 (q already scaled)
-    const void* k;              // [N, H, dk]
-    const void* v;              // [N, H, dv]
-    const float* beta;          // [N, H]
-    const float* g;             // [N, H] log-decay (<= 0)
-    const int32_t* cu;          // [n_seqs + 1] token offsets
-    const int32_t* cu_chunks;   // [n_seqs + 1] chunk offsets (ceil(len / 64) per sequence)
-    const int32_t* seq_index;   // [n_seqs] state index of each sequence, or null for 0 .. n_seqs-1
-    float* ws;                  // [total_chunks, H] records of kChunkFloats floats
-    long long s_stride;
-    int n_seqs, H, n_pairs;
-};
-
-// ---- operands: 8 consecutive elements of one row per lane, as bf16 pieces
-__device__ __forceinline__ uint32_t mask_if(bool keep) { return keep ? 0xffffffffu : 0u; }
-__device__ __forceinline__ float to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
-__device__ __forceinline__ float to_f32(uint32_t x) { return __uint_as_float(x << 16); }   // bf16 bits, zero-extended
-__device__ __forceinline__ float to_f32(float x) { return x; }
-
-template <typename In> struct Row8;
-template <> struct Row8<uint16_t> {            // bf16 input: one exact piece
-    static constexpr int KP = 1;
-    u32x4 v;
-    __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const u32x4*>(p); }
-    __device__ __forceinline__ void keep(uint32_t m) { v &= (u32x4){m, m, m, m}; }
-    __device__ __forceinline__ void pieces(u32x4 (&o)[1]) const { o[0] = v; }
-    __device__ __forceinline__ uint16_t raw(int e) const { return (uint16_t)(v[e >> 1] >> (16 * (e & 1))); }
-};
-template <> struct Row8<float> {               // fp32 input: three pieces
-    static constexpr int KP = kNS;
-    f32x4 a, b;
-    __device__ __forceinline__ void load(const float* p) {
-        a = *reinterpret_cast<const f32x4*>(p);
-        b = *reinterpret_cast<const f32x4*>(p + 4);
-    }
-    __device__ __forceinline__ void keep(uint32_t m) {
-        for (int e = 0; e < 4; ++e) {
-            a[e] = __uint_as_float(__float_as_uint(a[e]) & m);
-            b[e] = __uint_as_float(__float_as_uint(b[e]) & m);
-        }
-    }
-    __device__ __forceinline__ float raw(int e) const { return e < 4 ? a[e] : b[e - 4]; }
-    __device__ __forceinline__ void pieces(u32x4 (&o)[kNS]) const;
-};
-
-// Exact split of 8 fp32 values into kNS bf16 pieces, packed as MFMA operands (element e in slot e).
-__device__ __forceinline__ void split8(const float (&x)[8], u32x4 (&o)[kNS]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const Split3 s0 = split3(x[2 * j]), s1 = split3(x[2 * j + 1]);
-        o[0][j] = pack_hi2(s0.hi, s1.hi);
-        o[1][j] = pack_hi2(s0.mid, s1.mid);
-        o[2][j] = pack_hi2(s0.lo, s1.lo);
-    }
-}
-// Two-piece split of 4 fp32 values, rounding to nearest at both steps: x = hi + lo + e with |e| <= 2^-17 |x|.
-__device__ __forceinline__ void split4_rn(const float (&x)[4], u32x2 (&o)[kTP]) {
-    uint32_t hi[4], lo[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        hi[e] = f32_to_bf16_rne(x[e]);
-        lo[e] = f32_to_bf16_rne(x[e] - __uint_as_float(hi[e] << 16));
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        o[0][j] = hi[2 * j] | (hi[2 * j + 1] << 16);
-        o[1][j] = lo[2 * j] | (lo[2 * j + 1] << 16);
-    }
-}
-// Split of 4 fp32 values: kNS pieces of 4 bf16 each (2 dwords).
-__device__ __forceinline__ void split4(const float (&x)[4], u32x2 (&o)[kNS]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const Split3 s0 = split3(x[2 * j]), s1 = split3(x[2 * j + 1]);
-        o[0][j] = pack_hi2(s0.hi, s1.hi);
-        o[1][j] = pack_hi2(s0.mid, s1.mid);
-        o[2][j] = pack_hi2(s0.lo, s1.lo);
-    }
-}
-
-__device__ __forceinline__ void Row8<float>::pieces(u32x4 (&o)[kNS]) const {
-    const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-    split8(x, o);
-}
-
-// Sum of the piece products a_i * b_j with i + j < kNS (smallest terms first).
-template <int PA, int PB>
-__device__ __forceinline__ f32x4 mma(const u32x4 (&a)[PA], const u32x4 (&b)[PB], f32x4 c) {
-#pragma unroll
-    for (int d = kNS - 1; d >= 0; --d)
-#pragma unroll
-        for (int i = 0; i < PA; ++i) {
-            const int j = d - i;
-            if (j >= 0 && j < PB) c = mfma16x16x32(a[i], b[j], c);
-        }
-    return c;
-}
-
-__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// Sequence owning global chunk gc: the last s with cu_chunks[s] <= gc (empty sequences own no chunk).
-__device__ __forceinline__ int seq_of_chunk(const DeltaArgs& p, int gc) {
-    int lo = 0, hi = p.n_seqs;
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (p.cu_chunks[mid] <= gc) lo = mid; else hi = mid;
-    }
-    return lo;
-}
-
-// Per-chunk workspace record (floats): T and P as kNS bf16 pieces each, in the operand order the scan reads, then the
-// coefficient rows. Row tile a (rows 16a .. 16a+15) keeps columns 0 .. rt_width(a)-1, the 32-token k-steps that reach
-// its diagonal: 32, 32, 64, 64 columns (3072 elements per piece).
-__host__ __device__ constexpr int rt_width(int a) { return a < 2 ? 32 : 64; }
-__host__ __device__ constexpr int rt_base(int a) { return a == 0 ? 0 : (a == 1 ? 512 : (a == 2 ? 1024 : 2048)); }
-constexpr int kPieceElems = 3072;                                  // bf16 elements of one piece of T or P
-constexpr int kTOff = 0;                                           // T pieces   (uint16 offset)
-constexpr int kPOff = kTP * kPieceElems;                           // P pieces   (uint16 offset)
-constexpr int kCoefOff = kTP * kPieceElems;                        // coefficients (float offset: after 2 x kTP pieces)
+using namespace delta;
 
 // =====================================================================================================================
 // Phase 1: per-chunk coefficients, T and P
@@ -256,6 +120,8 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     uint16_t* ws16 = reinterpret_cast<uint16_t*>(p.ws + ((size_t)gc * H + h) * kChunkFloats);
     const float Gt = __shfl(G, 16 * w + r), bt = __shfl(bl, 16 * w + r);
     const int t = 16 * w + r;
+    constexpr bool kLane = sizeof(In) == 2;
+    float pe[4];                          // lane order: P of the even block of the current k-step
     for (int b = 0; b < 2 * ((w >> 1) + 1); ++b) {
         float pv[4] = {0.f, 0.f, 0.f, 0.f};
         if (b <= w) {
@@ -288,7 +154,25 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
                 pv[i] = pq[i] * d;
             }
         }
-        store_pieces4(ws16 + kPOff + rt_base(w) + r * rt_width(w) + 16 * b + 4 * q, pv);
+        if constexpr (kLane) {
+            // block b of P^T leaves row 16w + r, columns 16b + 4q + i in this lane: slots e and e + 4 of the lane's
+            // k-step (b >> 1) operand
+            static_assert(kTP == kNS, "lane-order pieces are exact three-piece splits");
+            if ((b & 1) == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pe[i] = pv[i];
+            } else {
+                const float x[8] = {pe[0], pe[1], pe[2], pe[3], pv[0], pv[1], pv[2], pv[3]};
+                u32x4 pc[kNS];
+                split8(x, pc);
+                const int blk = pair_of(w, b >> 1);
+#pragma unroll
+                for (int pi = 0; pi < kNS; ++pi)
+                    *reinterpret_cast<u32x4*>(ws16 + kPOff + 512 * (6 * pi + blk) + 8 * lane) = pc[pi];
+            }
+        } else {
+            store_pieces4(ws16 + kPOff + rt_base(w) + r * rt_width(w) + 16 * b + 4 * q, pv);
+        }
     }
     lds_barrier();                         // sK is dead from here: its space holds T
 
@@ -331,6 +215,24 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     }
 
     // T pieces, row-tile blocks as for P; entries above the diagonal are zero
+    if constexpr (kLane) {
+        for (int idx = threadIdx.x; idx < 6 * 64; idx += 256) {
+            const int blk = idx >> 6, L = idx & 63;
+            const int a = blk < 2 ? blk : 2 + ((blk - 2) >> 1), k = blk < 2 ? 0 : ((blk - 2) & 1);
+            const int row = 16 * a + (L & 15);
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int col = 32 * k + perm_k(8 * (L >> 4) + e);
+                x[e] = col <= row ? sT[row][col] : 0.f;
+            }
+            u32x4 pc[kNS];
+            split8(x, pc);
+#pragma unroll
+            for (int pi = 0; pi < kNS; ++pi)
+                *reinterpret_cast<u32x4*>(ws16 + kTOff + 512 * (6 * pi + blk) + 8 * L) = pc[pi];
+        }
+    } else
 #pragma unroll
     for (int it = 0; it < kPieceElems / 4 / 256; ++it) {
         const int off = 4 * (threadIdx.x + 256 * it);
@@ -688,11 +590,15 @@ int launch(const DeltaArgs& a, int total_chunks, hipStream_t stream) {
         hipLaunchKernelGGL(delta_chunk_prep<In>, dim3(total_chunks, a.H), dim3(256), 0, stream, a);
         if (int rc = check_launch("delta_chunk_prep")) return rc;
     }
-    const size_t lds = ScanLayout<In>::bytes;
-    if (int rc = allow_dynamic_lds((const void*)delta_chunk_scan<In>, lds)) return rc;
     const int groups = (a.n_pairs + 7) / 8;
-    hipLaunchKernelGGL(delta_chunk_scan<In>, dim3(groups * 8 * kSlices), dim3(256), lds, stream, a);
-    return check_launch("delta_chunk_scan");
+    if constexpr (sizeof(In) == 2) {
+        return launch_scan_cols(a, groups * 8 * kSlices, stream);
+    } else {
+        const size_t lds = ScanLayout<In>::bytes;
+        if (int rc = allow_dynamic_lds((const void*)delta_chunk_scan<In>, lds)) return rc;
+        hipLaunchKernelGGL(delta_chunk_scan<In>, dim3(groups * 8 * kSlices), dim3(256), lds, stream, a);
+        return check_launch("delta_chunk_scan");
+    }
 }
 
 }  // namespace

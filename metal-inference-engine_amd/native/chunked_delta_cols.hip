@@ -1,0 +1,336 @@
+// P3, bf16 inputs: the serial pass over a sequence's chunks with one wave per 16 state columns over all 64 tokens
+// of a chunk (delta_chunk_scan_cols). Same maths and precision as chunked_delta.hip, which builds its operands
+// (delta_chunk_prep, lane order) and holds the C ABI. Built on its own so that the compiler keeps MFMA results in
+// VGPRs here (the piece splits and scalings read them every chunk) without changing the other kernels' allocation.
+#include "chunked_delta.h"
+#include "rk_internal.h"
+
+namespace rk {
+namespace delta {
+namespace {
+
+// =====================================================================================================================
+// Phase 2 for bf16 inputs: one wave per 16 state columns over all 64 tokens of a chunk
+// =====================================================================================================================
+// The columns of S evolve independently, so a wave that owns 16 columns for all 64 tokens needs nothing from any
+// other wave: X = K S, (Q S)^T, vn = T Y, o^T = (Q S)^T diag(e^G) + vn^T P^T and the update K^T vn' keep the wave's 16
+// columns in one MFMA dimension and 64 tokens (or 128 state rows) in the other. Every operand that is a product of
+// the chunk (the state, Y, vn) is an accumulator pair of the product before, read in the k order perm_k (see
+// pair_of), so no value moves between lanes. K rows, Q rows, T, P (and K^T, by transposed reads of the K rows) come
+// from an LDS stage shared by the workgroup: waves 0 and 1 compute (32 columns), waves 2 and 3 fill the stage of
+// chunk c+1 by global_load_lds_dwordx4 (1 KB per instruction, no registers) while chunk c is computed; one barrier
+// per chunk hands the two stages over. The output of a chunk (o^T: 16-byte rows of 4 columns per lane) is stored at
+// the start of the next chunk, so the wait before a barrier never waits for fresh stores.
+struct ColStage {
+    static constexpr int kK = 0;                        // K rows [64][128] bf16, 16-byte units swizzled by swz()
+    static constexpr int kQ = kK + kC * 256;            // Q rows, the same
+    static constexpr int kT = kQ + kC * 256;            // T pieces, 18 blocks of 1 KB in lane order
+    static constexpr int kP = kT + 18 * 1024;           // P pieces, the same
+    static constexpr int kV = kP + 18 * 1024;           // V [64 tokens][32 columns] bf16 of the workgroup's columns
+    static constexpr int kCf = kV + kC * 64;            // beta, G, exp(G), exp(G_last - G): 4 x 64 floats
+    static constexpr int bytes = kCf + kCoefRows * kC * 4;
+};
+static_assert(2 * ColStage::bytes <= 160 * 1024, "two stages fit the LDS");
+
+// 16-byte unit of K / Q row `row` at which logical unit u is stored: u ^ swz(row). With it the 16 rows of a row-operand
+// read (one unit each) and the 8 rows x 32 bytes of a transposed read fall on distinct 16-byte slots of the 256-byte
+// bank line.
+__device__ __forceinline__ int swz(int row) { return 2 * (row & 7) + ((row >> 3) & 1); }
+
+__device__ __forceinline__ void load_to_lds(const void* src, char* dst) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+// Transposed 8-byte LDS read: within each 16 lanes, lane a + 4 j supplies 4 consecutive bf16 and lane 4 a + b
+// receives element b of the 4 lanes a, a + 4, a + 8, a + 12.
+__device__ __forceinline__ u32x2 read_tr16(const char* p) {
+    const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p);
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// Row operand of row `row` (token) of a K / Q stage, 32-dim step kd, in the k order perm_k: dims 32 kd + 4q .. +3 and
+// 32 kd + 16 + 4q .. +3.
+__device__ __forceinline__ u32x4 row_operand(const char* base, int row, int kd, int q) {
+    const char* rp = base + row * 256 + 8 * (q & 1);
+    const int s = swz(row);
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(rp + 16 * ((4 * kd + (q >> 1)) ^ s));
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16 * ((4 * kd + 2 + (q >> 1)) ^ s));
+    return (u32x4){lo[0], lo[1], hi[0], hi[1]};
+}
+
+// K^T operand: rows 16 a2 + r (dims) of K^T, tokens 32k + perm_k(8q + e), by two transposed reads of the K rows.
+__device__ __forceinline__ u32x4 kt_operand(const char* base, int a2, int k, int lane) {
+    const int q = lane >> 4, m = lane & 15;
+    const int row0 = 32 * k + 4 * q + (m >> 2), row1 = row0 + 16;
+    const int u = 2 * a2 + ((m & 3) >> 1), off = 8 * (m & 1);
+    const u32x2 lo = read_tr16(base + row0 * 256 + 16 * (u ^ swz(row0)) + off);
+    const u32x2 hi = read_tr16(base + row1 * 256 + 16 * (u ^ swz(row1)) + off);
+    return (u32x4){lo[0], lo[1], hi[0], hi[1]};
+}
+
+// the 8 fp32 values of an accumulator pair as kNS bf16 pieces in the k order perm_k
+__device__ __forceinline__ void pair_pieces(f32x4 lo, f32x4 hi, u32x4 (&o)[kNS]) {
+    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    split8(x, o);
+}
+
+__global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
+    __shared__ __align__(16) char stage0[ColStage::bytes];
+    __shared__ __align__(16) char stage1[ColStage::bytes];
+    // all slices of one (sequence, head) get ids congruent mod 8: one XCD, one L2 for their common operand reads
+    const int id = blockIdx.x;
+    const int slice = (id >> 3) % kSlices;
+    const int pair = (id / (8 * kSlices)) * 8 + (id & 7);
+    if (pair >= p.n_pairs) return;
+    const int s = pair / p.H, h = pair % p.H, H = p.H;
+    const int lane = threadIdx.x & 63, ct = threadIdx.x >> 6, q = lane >> 4, r = lane & 15;
+    const int T0 = p.cu[s], Tn = p.cu[s + 1] - T0;
+    const int gc0 = p.cu_chunks[s];
+    // chunks of this sequence; never more than its workspace records (both offsets arrays come from the caller)
+    const int nch = min((Tn + kC - 1) / kC, p.cu_chunks[s + 1] - gc0);
+    if (nch <= 0) return;                 // empty sequence: state unchanged, no barrier is reached by either wave
+    const int col0 = slice * kCols;
+    const int col = col0 + 16 * (ct & 1) + r;
+    float* Sg = p.S + (long long)(p.seq_index ? p.seq_index[s] : s) * p.s_stride + (long long)h * kDk * kDv + col;
+    const uint16_t* Kg = static_cast<const uint16_t*>(p.k);
+    const uint16_t* Qg = static_cast<const uint16_t*>(p.q);
+    const uint16_t* Vg = static_cast<const uint16_t*>(p.v);
+
+    // This wave's share of the direct loads of chunk c's stage: the K, Q, T, P and V groups j with j % 2 == wave
+    // (the coefficient rows: wave 0), in three parts issued at different points of the previous chunk. Per-lane byte
+    // offsets of full chunks are fixed for the kernel; a chunk that ends early repeats its last row instead (rows past
+    // the sequence's end have beta 0, so they leave S and the rows before them untouched).
+    const int wv = __builtin_amdgcn_readfirstlane(ct & 1);
+    uint32_t kq_off[8], v_off[2];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+        const int row = 4 * (2 * jj + wv) + (lane >> 4), u = lane & 15;
+        kq_off[jj] = 2u * (uint32_t)(row * H * kDk + 8 * (u ^ swz(row)));
+    }
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const int tok = 16 * (2 * jj + wv) + (lane >> 2);
+        v_off[jj] = 2u * (uint32_t)(tok * H * kDv + col0 + 8 * (lane & 3));
+    }
+    // The i-th direct load of this wave for chunk c (full chunks): 0-7 K rows, 8-16 T, 17-24 Q, 25-33 P, 34-35 V,
+    // 36 the coefficient rows (wave 0 only).
+    auto load_one = [&](int c, char* stage, int i) __attribute__((always_inline)) {
+        const long long row0 = (long long)(T0 + c * kC) * H + h;
+        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats);
+        if (i < 8 || (i >= 17 && i < 25)) {
+            const int jj = i < 8 ? i : i - 17;
+            const char* base = reinterpret_cast<const char*>((i < 8 ? Kg : Qg) + row0 * kDk);
+            load_to_lds(base + kq_off[jj], stage + (i < 8 ? ColStage::kK : ColStage::kQ) + 1024 * wv + 2048 * jj);
+        } else if (i < 34) {
+            const bool t = i < 17;
+            const int jj = t ? i - 8 : i - 25;
+            load_to_lds(rec + 2 * (t ? kTOff : kPOff) + 1024 * wv + 2048 * jj + 16 * lane,
+                        stage + (t ? ColStage::kT : ColStage::kP) + 1024 * wv + 2048 * jj);
+        } else if (i < 36) {
+            const int jj = i - 34;
+            load_to_lds(reinterpret_cast<const char*>(Vg + row0 * kDv) + v_off[jj],
+                        stage + ColStage::kV + 1024 * wv + 2048 * jj);
+        } else if (wv == 0) {
+            load_to_lds(rec + 4 * kCoefOff + 16 * lane, stage + ColStage::kCf);
+        }
+    };
+    constexpr int kLoads = 37;
+    // All of chunk c's direct loads at once, rows past the sequence's end repeating its last row (used for the first
+    // chunk and for a chunk that ends early).
+    auto stage_loads = [&](int c, char* stage) __attribute__((always_inline)) {
+        const int nt = min(kC, Tn - c * kC);
+        if (nt == kC) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) load_one(c, stage, i);
+            return;
+        }
+        const long long row0 = (long long)(T0 + c * kC) * H + h;
+        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats);
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+            const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
+            char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ) + 1024 * wv;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const int row = 4 * (2 * jj + wv) + (lane >> 4), u = lane & 15;
+                load_to_lds(base + 2 * ((long long)min(row, nt - 1) * H * kDk + 8 * (u ^ swz(row))), dst + 2048 * jj);
+            }
+            const char* blocks = rec + 2 * (part == 0 ? kTOff : kPOff) + 1024 * wv + 16 * lane;
+            char* bdst = stage + (part == 0 ? ColStage::kT : ColStage::kP) + 1024 * wv;
+#pragma unroll
+            for (int jj = 0; jj < 9; ++jj) load_to_lds(blocks + 2048 * jj, bdst + 2048 * jj);
+        }
+        const char* vbase = reinterpret_cast<const char*>(Vg + row0 * kDv);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int tok = 16 * (2 * jj + wv) + (lane >> 2);
+            load_to_lds(vbase + 2 * ((long long)min(tok, nt - 1) * H * kDv + col0 + 8 * (lane & 3)),
+                        stage + ColStage::kV + 1024 * wv + 2048 * jj);
+        }
+        if (wv == 0) load_to_lds(rec + 4 * kCoefOff + 16 * lane, stage + ColStage::kCf);
+    };
+
+    // Waves 2 and 3 only load: every stage's direct loads are theirs (a direct load holds its issuing wave for ~90
+    // cycles, which on the two computing waves would add up to a third of a chunk). All four waves meet at the one
+    // barrier per chunk: after it, stage c is complete and stage c-1 is free for chunk c+1.
+    if (ct >= 2) {
+        stage_loads(0, stage0);
+        __syncthreads();
+        for (int c = 0; c < nch; c += 2) {
+            if (c + 1 < nch) stage_loads(c + 1, stage1);
+            __syncthreads();
+            if (c + 1 < nch) {
+                if (c + 2 < nch) stage_loads(c + 2, stage0);
+                __syncthreads();
+            }
+        }
+        return;
+    }
+
+    // state rows 16 a2 + 4q + i, column `col` (accumulator layout of the update)
+    f32x4 st[8];
+#pragma unroll
+    for (int a2 = 0; a2 < 8; ++a2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[a2][i] = Sg[(long long)(16 * a2 + 4 * q + i) * kDv];
+    __syncthreads();                                      // waits for this wave's loads; then both waves' are in LDS
+
+    // o^T of the previous chunk, stored one chunk late: lane (q, r) of tile a holds token 16a + r, columns
+    // 16 (wave & 1) + 4q .. +3
+    f32x4 o[4];
+    auto store_out = [&](int c) __attribute__((always_inline)) {
+        const int nt = min(kC, Tn - c * kC);
+        float* orow = p.out + ((long long)(T0 + c * kC + r) * H + h) * kDv + col0 + 16 * (ct & 1) + 4 * q;
+        if (nt == kC) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) *reinterpret_cast<f32x4*>(orow + (long long)16 * a * H * kDv) = o[a];
+        } else {
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                if (16 * a + r < nt) *reinterpret_cast<f32x4*>(orow + (long long)16 * a * H * kDv) = o[a];
+        }
+    };
+
+    // one chunk on stage `cur` (chunk c), filling stage `nxt` with chunk c+1
+    auto step = [&](int c, const char* cur, char* nxt) __attribute__((always_inline)) {
+        (void)nxt;
+        if (c > 0) store_out(c - 1);
+        // this chunk's coefficients and values, read before they are needed
+        const float* cf = reinterpret_cast<const float*>(cur + ColStage::kCf);
+        const uint16_t* vs = reinterpret_cast<const uint16_t*>(cur + ColStage::kV);
+        f32x4 be[4], eg[4], er[4];
+        float vv[4][4], egt[4];             // egt: exp(G) of token 16a + r (the rows of o^T's lane)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            be[a] = *reinterpret_cast<const f32x4*>(cf + 16 * a + 4 * q);
+            eg[a] = *reinterpret_cast<const f32x4*>(cf + 2 * kC + 16 * a + 4 * q);
+            egt[a] = cf[2 * kC + 16 * a + r];
+            er[a] = *reinterpret_cast<const f32x4*>(cf + 3 * kC + 16 * a + 4 * q);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[a][i] = to_f32(vs[(16 * a + 4 * q + i) * kCols + 16 * ct + r]);
+        }
+        const float glast = cf[2 * kC + kC - 1];
+
+        // ---- X = K S (B: the state, in perm_k order of its rows) and (Q S)^T (A: the same state pieces)
+        f32x4 x[4], qs[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) x[a] = qs[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kd = 0; kd < 4; ++kd) {
+            u32x4 sb[kNS];
+            pair_pieces(st[2 * kd], st[2 * kd + 1], sb);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const u32x4 ka[1] = {row_operand(cur + ColStage::kK, 16 * a + r, kd, q)};
+                x[a] = mma(ka, sb, x[a]);
+                const u32x4 qb[1] = {row_operand(cur + ColStage::kQ, 16 * a + r, kd, q)};
+                qs[a] = mma(sb, qb, qs[a]);
+            }
+        }
+
+        // ---- Y = beta (V - e^G X), then vn = T Y
+        u32x4 yb[2][kNS];
+        {
+            f32x4 y[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[a][i] = be[a][i] * (vv[a][i] - eg[a][i] * x[a][i]);
+            pair_pieces(y[0], y[1], yb[0]);
+            pair_pieces(y[2], y[3], yb[1]);
+        }
+        f32x4 vn[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            vn[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k <= (a >> 1); ++k) {
+                u32x4 ta[kTP];
+#pragma unroll
+                for (int pi = 0; pi < kTP; ++pi)
+                    ta[pi] = *reinterpret_cast<const u32x4*>(cur + ColStage::kT + 1024 * (6 * pi + pair_of(a, k)) +
+                                                             16 * lane);
+                vn[a] = mma(ta, yb[k], vn[a]);
+            }
+        }
+
+        // ---- o^T = (Q S)^T diag(e^G) + vn^T P^T; S = e^{G_last} S + K^T (e^{G_last - G} vn)
+        u32x4 vb[2][kNS], vq[2][kNS];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            pair_pieces(vn[2 * k], vn[2 * k + 1], vb[k]);
+            f32x4 w0, w1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w0[i] = er[2 * k][i] * vn[2 * k][i];
+                w1[i] = er[2 * k + 1][i] * vn[2 * k + 1][i];
+            }
+            pair_pieces(w0, w1, vq[k]);
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[a][i] = egt[a] * qs[a][i];
+#pragma unroll
+            for (int k = 0; k <= (a >> 1); ++k) {
+                u32x4 pb[kTP];
+#pragma unroll
+                for (int pi = 0; pi < kTP; ++pi)
+                    pb[pi] = *reinterpret_cast<const u32x4*>(cur + ColStage::kP + 1024 * (6 * pi + pair_of(a, k)) +
+                                                             16 * lane);
+                o[a] = mma(vb[k], pb, o[a]);
+            }
+        }
+#pragma unroll
+        for (int a2 = 0; a2 < 8; ++a2)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if (k == 0)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) st[a2][i] *= glast;
+                const u32x4 kt[1] = {kt_operand(cur + ColStage::kK, a2, k, lane)};
+                st[a2] = mma(kt, vq[k], st[a2]);
+            }
+        // the loading waves have completed stage c+1 and this wave is done with stage `cur`, which they refill next
+        __syncthreads();
+    };
+    for (int c = 0; c < nch; c += 2) {
+        step(c, stage0, stage1);
+        if (c + 1 < nch) step(c + 1, stage1, stage0);
+    }
+    store_out(nch - 1);
+#pragma unroll
+    for (int a2 = 0; a2 < 8; ++a2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Sg[(long long)(16 * a2 + 4 * q + i) * kDv] = st[a2][i];
+}
+
+}  // namespace
+
+int launch_scan_cols(const DeltaArgs& a, int grid, hipStream_t stream) {
+    hipLaunchKernelGGL(delta_chunk_scan_cols, dim3(grid), dim3(256), 0, stream, a);
+    return check_launch("delta_chunk_scan_cols");
+}
+
+}  // namespace delta
+}  // namespace rk
