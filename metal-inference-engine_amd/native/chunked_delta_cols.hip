@@ -21,21 +21,32 @@ namespace {
 // chunk c+1 by global_load_lds_dwordx4 (1 KB per instruction, no registers) while chunk c is computed; one barrier
 // per chunk hands the two stages over. The output of a chunk (o^T: 16-byte rows of 4 columns per lane) is stored at
 // the start of the next chunk, so the wait before a barrier never waits for fresh stores.
+// K and Q rows: 16 groups of 4 rows (one 1 KB direct load each); the K and Q groups g share a 2 KB pair at
+// pair_base(g), each at an offset kq_group_off(g) (see kq_unit).
+__host__ __device__ constexpr int pair_base(int g) { return 2048 * g + 256 * (g >> 1); }
+__host__ __device__ constexpr int kq_group_off(int g) { return (g & 1 ? 32 : 0) + (g & 2 ? 16 : 0); }
 struct ColStage {
-    static constexpr int kK = 0;                        // K rows [64][128] bf16, 16-byte units swizzled by swz()
-    static constexpr int kQ = kK + kC * 256;            // Q rows, the same
-    static constexpr int kT = kQ + kC * 256;            // T pieces, 18 blocks of 1 KB in lane order
+    static constexpr int kK = 0;                        // K rows, group g at kK + pair_base(g) + kq_group_off(g)
+    static constexpr int kQ = kK + 1024;                // Q rows, the same
+    static constexpr int kT = 34816;                    // T pieces, 18 blocks of 1 KB in lane order
     static constexpr int kP = kT + 18 * 1024;           // P pieces, the same
     static constexpr int kV = kP + 18 * 1024;           // V [64 tokens][32 columns] bf16 of the workgroup's columns
     static constexpr int kCf = kV + kC * 64;            // beta, G, exp(G), exp(G_last - G): 4 x 64 floats
     static constexpr int bytes = kCf + kCoefRows * kC * 4;
 };
 static_assert(2 * ColStage::bytes <= 160 * 1024, "two stages fit the LDS");
+static_assert(pair_base(15) + 2048 + kq_group_off(15) <= ColStage::kT, "the K / Q pairs end before T");
 
-// 16-byte unit of K / Q row `row` at which logical unit u is stored: u ^ swz(row). With it the 16 rows of a row-operand
-// read (one unit each) and the 8 rows x 32 bytes of a transposed read fall on distinct 16-byte slots of the 256-byte
-// bank line.
-__device__ __forceinline__ int swz(int row) { return 2 * (row & 7) + ((row >> 3) & 1); }
+// Byte offset, from kK or kQ, of the 16-byte unit u (dims 8u .. 8u+7) of K / Q row `row`: row t = row & 3 of group
+// row >> 2 stores unit u at slot u ^ 4t. So:
+//  - a row operand's two 8-byte halves (units 4kd + j and 4kd + 2 + j, j < 2; 4t never has bit 1) are always 32
+//    bytes apart, one ds_read2_b64 into the operand's four registers;
+//  - the 16 rows of a row-operand read sit on 16 distinct 16-byte slots of the 256-byte bank line (slot 4t^u within a
+//    group, the groups 0 / 2 / 1 / 3 slots apart), and so do the 8 rows x 32 bytes of a transposed read.
+__device__ __forceinline__ int kq_unit(int row, int u) {
+    const int g = row >> 2, t = row & 3;
+    return pair_base(g) + kq_group_off(g) + 256 * t + 16 * (u ^ (4 * t));
+}
 
 __device__ __forceinline__ void load_to_lds(const void* src, char* dst) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
@@ -51,20 +62,20 @@ __device__ __forceinline__ u32x2 read_tr16(const char* p) {
 // Row operand of row `row` (token) of a K / Q stage, 32-dim step kd, in the k order perm_k: dims 32 kd + 4q .. +3 and
 // 32 kd + 16 + 4q .. +3.
 __device__ __forceinline__ u32x4 row_operand(const char* base, int row, int kd, int q) {
-    const char* rp = base + row * 256 + 8 * (q & 1);
-    const int s = swz(row);
-    const u32x2 lo = *reinterpret_cast<const u32x2*>(rp + 16 * ((4 * kd + (q >> 1)) ^ s));
-    const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 16 * ((4 * kd + 2 + (q >> 1)) ^ s));
+    const char* rp = base + kq_unit(row, 4 * kd + (q >> 1)) + 8 * (q & 1);
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(rp);
+    const u32x2 hi = *reinterpret_cast<const u32x2*>(rp + 32);
     return (u32x4){lo[0], lo[1], hi[0], hi[1]};
 }
 
 // K^T operand: rows 16 a2 + r (dims) of K^T, tokens 32k + perm_k(8q + e), by two transposed reads of the K rows.
 __device__ __forceinline__ u32x4 kt_operand(const char* base, int a2, int k, int lane) {
     const int q = lane >> 4, m = lane & 15;
-    const int row0 = 32 * k + 4 * q + (m >> 2), row1 = row0 + 16;
-    const int u = 2 * a2 + ((m & 3) >> 1), off = 8 * (m & 1);
-    const u32x2 lo = read_tr16(base + row0 * 256 + 16 * (u ^ swz(row0)) + off);
-    const u32x2 hi = read_tr16(base + row1 * 256 + 16 * (u ^ swz(row1)) + off);
+    const int row0 = 32 * k + 4 * q + (m >> 2);
+    const int u = 2 * a2 + ((m & 3) >> 1);
+    const char* p0 = base + kq_unit(row0, u) + 8 * (m & 1);
+    const u32x2 lo = read_tr16(p0);
+    const u32x2 hi = read_tr16(p0 + pair_base(4) - pair_base(0));       // row0 + 16: group + 4, same slot
     return (u32x4){lo[0], lo[1], hi[0], hi[1]};
 }
 
@@ -105,7 +116,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
         const int row = 4 * (2 * jj + wv) + (lane >> 4), u = lane & 15;
-        kq_off[jj] = 2u * (uint32_t)(row * H * kDk + 8 * (u ^ swz(row)));
+        kq_off[jj] = 2u * (uint32_t)(row * H * kDk + 8 * (u ^ (4 * (row & 3))));
     }
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
@@ -120,7 +131,8 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
         if (i < 8 || (i >= 17 && i < 25)) {
             const int jj = i < 8 ? i : i - 17;
             const char* base = reinterpret_cast<const char*>((i < 8 ? Kg : Qg) + row0 * kDk);
-            load_to_lds(base + kq_off[jj], stage + (i < 8 ? ColStage::kK : ColStage::kQ) + 1024 * wv + 2048 * jj);
+            const int g = 2 * jj + wv;
+            load_to_lds(base + kq_off[jj], stage + (i < 8 ? ColStage::kK : ColStage::kQ) + pair_base(g) + kq_group_off(g));
         } else if (i < 34) {
             const bool t = i < 17;
             const int jj = t ? i - 8 : i - 25;
@@ -149,11 +161,12 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
 #pragma unroll
         for (int part = 0; part < 2; ++part) {
             const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
-            char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ) + 1024 * wv;
+            char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ);
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj) {
-                const int row = 4 * (2 * jj + wv) + (lane >> 4), u = lane & 15;
-                load_to_lds(base + 2 * ((long long)min(row, nt - 1) * H * kDk + 8 * (u ^ swz(row))), dst + 2048 * jj);
+                const int g = 2 * jj + wv, row = 4 * g + (lane >> 4), u = lane & 15;
+                load_to_lds(base + 2 * ((long long)min(row, nt - 1) * H * kDk + 8 * (u ^ (4 * (row & 3)))),
+                            dst + pair_base(g) + kq_group_off(g));
             }
             const char* blocks = rec + 2 * (part == 0 ? kTOff : kPOff) + 1024 * wv + 16 * lane;
             char* bdst = stage + (part == 0 ? ColStage::kT : ColStage::kP) + 1024 * wv;

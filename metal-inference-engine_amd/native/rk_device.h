@@ -50,7 +50,9 @@ __device__ __forceinline__ uint32_t pack_hi2(uint32_t e0, uint32_t e1) {
 
 // Exact three-way split of an fp32 value into bf16-representable parts x = hi + mid + lo (truncation at every
 // step: hi keeps sign, exponent and the top 7 mantissa bits; the remainder has at most 16 significant bits, so its
-// truncated top part and the final rest are exact in bf16). Returned as fp32 bit patterns whose low halves are 0.
+// truncated top part and the final rest are exact in bf16). Returned as fp32 bit patterns: hi and mid with low halves
+// 0; lo is the final rest as is, whose low half is 0 as well (it is exact in bf16), and which is only ever packed
+// by its top half (pack_hi2), so no mask is spent on it.
 struct Split3 {
     uint32_t hi, mid, lo;
 };
@@ -59,8 +61,7 @@ __device__ __forceinline__ Split3 split3(float x) {
     float r1 = x - __uint_as_float(hb);
     uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
     float r2 = r1 - __uint_as_float(mb);
-    uint32_t lb = __float_as_uint(r2) & 0xffff0000u;
-    return {hb, mb, lb};
+    return {hb, mb, __float_as_uint(r2)};
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
