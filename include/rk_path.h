@@ -99,14 +99,15 @@ int rk_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_poo
  * host work and no host-to-device copy. tables [max_seqs, max_blocks] int32 (row = sequence slot), lens [max_seqs]
  * int32 (positions written), stack [num_blocks] int32 (free blocks), meta [2] int32: meta[0] = free blocks,
  * meta[1] = status (0 ok; 1 out of blocks; 2 a sequence would outgrow max_blocks; 3 a release would overfill the
- * stack; 4 a row outside [0, max_seqs)). A step that fails changes nothing but the status (all or nothing, as
+ * stack; 4 a row outside [0, max_seqs); 5 a row named twice in one call: a double allocation or a double free,
+ * which BlockAllocator.free refuses, src/state.py:94-99). A step that fails changes nothing but the status (all or nothing, as
  * PagedSequence._ensure), writes slots of -1 (skipped by rk_kv_write) and the old lengths.
  *   rk_pages_init: empty tables, stack handing out block 0 first (BlockAllocator.__init__).
  *   rk_pages_advance: batch entry b grows sequence rows[b] (distinct rows, B <= 1024) by n_new positions, taking
  *     blocks in batch order; slots [B * n_new] int64 = block * block_size + offset of each new position (the rows
  *     rk_kv_write / rk_attn_prep write; NULL to skip), out_lens [B] = lengths after the step (NULL to skip).
- *   rk_pages_release: rows[r] (R <= 1024) return their blocks (reverse table order, as BlockAllocator.free) and
- *     become empty.
+ *   rk_pages_release: rows[r] (distinct rows, R <= 1024) return their blocks (reverse table order, as
+ *     BlockAllocator.free) and become empty.
  *   rk_pages_gather: out [B, width] int32 = the tables of rows[b], entries past the blocks held set to 0 (the
  *     0-padded tables of batch_layout, src/state.py:124-128). */
 int rk_pages_init(int32_t* tables, int32_t* lens, int32_t* stack, int32_t* meta, int max_seqs, int max_blocks,

@@ -14,8 +14,9 @@
 //     table order.
 // Layout (int32, all device memory): tables [max_seqs, max_blocks] (row = sequence slot), lens [max_seqs],
 // stack [num_blocks], meta[0] = free blocks on the stack, meta[1] = status (0 ok, 1 out of blocks, 2 a sequence
-// would outgrow its table row, 3 a release would overfill the stack, 4 a row index outside [0, max_seqs)). Row indices
-// come from device memory, so every kernel checks them before it addresses anything with them.
+// would outgrow its table row, 3 a release would overfill the stack, 4 a row index outside [0, max_seqs), 5 a row named
+// twice in one step: a double allocation or a double free, which the reference's allocator refuses). Row indices come
+// from device memory, so every kernel checks them before it addresses anything with them.
 #include "rk_device.h"
 #include "rk_internal.h"
 
@@ -25,6 +26,18 @@ namespace rk {
 namespace {
 
 constexpr int kPageThreads = 1024;
+
+// Whether row rows[i] (i < n, this thread's entry, valid) also appears at an earlier entry: the n rows staged in LDS,
+// each thread compares with the entries before its own. One LDS barrier; every thread must call it.
+__device__ bool named_before(const int32_t* rows, int n, int i, bool valid, int row) {
+    __shared__ int rs[kPageThreads];
+    if (i < n) rs[i] = rows[i];
+    __syncthreads();
+    bool dup = false;
+    if (valid)
+        for (int j = 0; j < i; ++j) dup |= rs[j] == row;
+    return dup;
+}
 
 // Exclusive prefix sum over the workgroup (kPageThreads threads); *total gets the sum. Two LDS barriers.
 __device__ int block_exclusive_scan(int x, int* total) {
@@ -84,22 +97,25 @@ __global__ __launch_bounds__(kPageThreads) void pages_advance(PageArgs a) {
     const bool bad_row = b < a.B && (row_in < 0 || row_in >= a.max_seqs);
     const bool live = b < a.B && !bad_row;
     const int row = live ? row_in : 0;
-    const int pos = live ? a.lens[row] : 0;
+    const int pos_in = live ? a.lens[row] : 0;
+    const bool bad_len = pos_in < 0;      // lengths are written by these kernels only; a negative one is refused
+    const int pos = bad_len ? 0 : pos_in;
     const int end = pos + a.n_new;
     const int held = (pos + a.block_size - 1) / a.block_size;
     const int want = live ? (end + a.block_size - 1) / a.block_size : 0;
     const int need = live ? want - held : 0;
     const int top = a.meta[0];            // read by every thread before thread 0 rewrites it (after the barriers)
     if (threadIdx.x == 0) s_fail = 0;
-    __syncthreads();
-    if (live && want > a.max_blocks) atomicOr(&s_fail, 2);        // LDS atomics
+    const bool dup = named_before(a.rows, a.B, b, live, row);     // its barrier also publishes s_fail = 0
+    if ((live && want > a.max_blocks) || bad_len) atomicOr(&s_fail, 2);   // LDS atomics
     if (bad_row) atomicOr(&s_fail, 4);
+    if (dup) atomicOr(&s_fail, 8);
     int total = 0;
     const int before = block_exclusive_scan(need, &total);        // barriers also publish s_fail
     int fail = s_fail;
     if (!fail && total > top) fail = 1;
     if (fail) {                                                   // nothing taken, nothing written but the status
-        if (threadIdx.x == 0) a.meta[1] = fail & 4 ? 4 : (fail & 2 ? 2 : 1);
+        if (threadIdx.x == 0) a.meta[1] = fail & 4 ? 4 : (fail & 8 ? 5 : (fail & 2 ? 2 : 1));
         if (b < a.B && a.out_lens) a.out_lens[b] = pos;
         if (b < a.B && a.slots)
             for (int t = 0; t < a.n_new; ++t) a.slots[(long long)b * a.n_new + t] = -1;
@@ -127,15 +143,17 @@ __global__ __launch_bounds__(kPageThreads) void pages_release(PageArgs a) {
     const bool bad_row = r < a.B && (row_in < 0 || row_in >= a.max_seqs);
     const bool live = r < a.B && !bad_row;
     const int row = live ? row_in : 0;
-    const int n = live ? (a.lens[row] + a.block_size - 1) / a.block_size : 0;
+    // the blocks a row holds, never more than its table row (lengths are written by these kernels only)
+    const int n = live ? min(max((a.lens[row] + a.block_size - 1) / a.block_size, 0), a.max_blocks) : 0;
     const int top = a.meta[0];            // read by every thread before thread 0 rewrites it (after the barriers)
     if (threadIdx.x == 0) s_bad = 0;
-    __syncthreads();
+    const bool dup = named_before(a.rows, a.B, r, live, row);     // its barrier also publishes s_bad = 0
     if (bad_row) atomicOr(&s_bad, 1);
+    if (dup) atomicOr(&s_bad, 2);
     int total = 0;
     const int before = block_exclusive_scan(n, &total);
     if (s_bad || top + total > a.num_blocks) {                   // nothing returned
-        if (threadIdx.x == 0) a.meta[1] = s_bad ? 4 : 3;
+        if (threadIdx.x == 0) a.meta[1] = s_bad & 1 ? 4 : (s_bad ? 5 : 3);
         return;
     }
     const int32_t* trow = a.tables + (long long)row * a.max_blocks;

@@ -17,7 +17,8 @@ import torch
 from native.rocm_native import load
 
 STATUS = {1: "out of blocks", 2: "a sequence would outgrow its table row (max_blocks)",
-          3: "a release would return more blocks than the pool has", 4: "a row index outside the table"}
+          3: "a release would return more blocks than the pool has", 4: "a row index outside the table",
+          5: "a row named twice in one step (a double allocation or a double free)"}
 
 
 class OutOfBlocks(RuntimeError):

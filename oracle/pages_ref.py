@@ -25,6 +25,9 @@ class PagesModel:
         if any(r < 0 or r >= self.max_seqs for r in rows):
             self.status = 4
             return None
+        if len(set(rows)) != len(rows):                          # one sequence grown twice in a step
+            self.status = 5
+            return None
         needs = [self._blocks(self.lens[r] + n_new) - self._blocks(self.lens[r]) for r in rows]
         if any(self._blocks(self.lens[r] + n_new) > self.max_blocks for r in rows):
             self.status = 2
@@ -45,6 +48,9 @@ class PagesModel:
     def release(self, rows: list[int]) -> None:
         if any(r < 0 or r >= self.max_seqs for r in rows):
             self.status = 4
+            return
+        if len(set(rows)) != len(rows):                          # a double free (BlockAllocator.free refuses it)
+            self.status = 5
             return
         for r in rows:
             self.free.extend(reversed(self.tables[r]))

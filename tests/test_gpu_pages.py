@@ -83,6 +83,23 @@ def test_out_of_blocks_and_bad_rows_change_nothing():
     pages.release(torch.tensor([-1], dtype=torch.int32))
     torch.cuda.synchronize()
     assert pages.status() == 4
+    pages.meta[1].zero_()
+    # a row named twice in one call: a double allocation or a double free (BlockAllocator.free refuses the latter,
+    # src/state.py:94-99): refused with status 5, nothing taken or returned
+    model.status = 0
+    slots, lens = pages.advance(torch.tensor([1, 2, 1], dtype=torch.int32), 2)
+    assert model.advance([1, 2, 1], 2) is None and model.status == 5
+    assert slots.cpu().tolist() == [-1] * 6
+    assert_same(pages, model)
+    with pytest.raises(RuntimeError, match="twice"):
+        pages.check()
+    model.status = 0
+    pages.release(torch.tensor([0, 0], dtype=torch.int32))
+    model.release([0, 0])
+    assert model.status == 5
+    assert_same(pages, model)
+    with pytest.raises(RuntimeError, match="twice"):
+        pages.check()
 
 
 def _decode_setup(B=6, Hq=8, Hkv=2, d=128, bs=16, NB=400, S=10, seed=3):
