@@ -53,10 +53,18 @@ constexpr int kMaxKvHeads = 4;     // one wave per kv head in a split workgroup 
 constexpr int kTile = 16;
 constexpr int kStash = 2;   // segments per split workgroup whose records wait in LDS until the range is done
 // Waves of a split workgroup: 8 (two per SIMD, <= 256 VGPRs each) for up to 4 query heads per kv-head, 4 (one per
-// SIMD) for the register-heavier 8-head instances. It depends on the shape only, never on the pool dtype, so that a
-// bf16 pool and an fp32 pool holding the same (widened) values are cut and combined identically and give bit-equal
-// outputs (the fp32-pool instance at D = 256 spills some registers to do so).
-constexpr int waves_per_group(int GP) { return GP == 4 ? 8 : 4; }
+// SIMD, up to 512 registers) for the register-heavier 8-head instances and for small grids (at most kSmallTiles
+// tiles at the tile count's upper bound: a few short sequences, where each wave streams about one tile and the
+// latency of its loads is the time; one wave per SIMD then holds a whole fp32 tile in flight instead of half of
+// one, a round trip less per half). It depends on the shape only, never on the pool dtype, so that a bf16 pool and
+// an fp32 pool holding the same (widened) values are cut and combined identically and give bit-equal outputs (the
+// 8-wave fp32-pool instance at D = 256 streams half tiles to fit).
+constexpr long long kSmallTiles = 512;
+constexpr int waves_per_group(int GP, long long upper) { return GP == 4 && upper > kSmallTiles ? 8 : 4; }
+// the tile count's upper bound: every sequence at its table's full width
+inline long long tile_upper(int B, int block_size, int max_nb) {
+    return (long long)B * (((long long)max_nb * block_size + kTile - 1) / kTile);
+}
 
 struct DecodeArgs {
     float* part;
@@ -293,7 +301,7 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     // in flight; for fp32 pools at D = 256 half a tile (the sets are refilled with the tile's second half, then
     // the next tile's first half), which keeps the workgroup at two waves per SIMD without spilling. The
     // arithmetic and its order do not change.
-    constexpr bool kHalf = sizeof(T) == 4 && D == 256;
+    constexpr bool kHalf = sizeof(T) == 4 && D == 256 && WPG == 8;
     constexpr int KB = kHalf ? NIT / 2 : NIT, VB = kHalf ? NVI / 2 : NVI;
     constexpr int REC = GP * D + 2 * GP;     // floats of one (acc, m, l) record
     static_assert(REC * 4 <= NT * NIT * 64 * 16, "a combine record must fit in the wave's query operand area");
@@ -788,30 +796,30 @@ typedef void (*SplitFn)(DecodeArgs);
 typedef void (*MergeFn)(DecodeArgs);
 
 template <typename T, bool ALIGNED>
-SplitFn pick_split(int D, int GP) {
-    if (GP == 4) {
-        constexpr int W = waves_per_group(4);
-        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED, W>;
-        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED, W>;
-        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED, W>;
+SplitFn pick_split(int D, int GP, int wpg) {
+    if (GP == 4 && wpg == 8) {
+        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED, 8>;
+        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED, 8>;
+        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED, 8>;
+    } else if (GP == 4) {
+        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED, 4>;
+        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED, 4>;
+        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED, 4>;
     } else {
-        constexpr int W = waves_per_group(8);
-        if (D == 64) return paged_decode_split<T, 64, 8, ALIGNED, W>;
-        if (D == 128) return paged_decode_split<T, 128, 8, ALIGNED, W>;
-        if (D == 256) return paged_decode_split<T, 256, 8, ALIGNED, W>;
+        if (D == 64) return paged_decode_split<T, 64, 8, ALIGNED, 4>;
+        if (D == 128) return paged_decode_split<T, 128, 8, ALIGNED, 4>;
+        if (D == 256) return paged_decode_split<T, 256, 8, ALIGNED, 4>;
     }
     return nullptr;
 }
 
-SplitFn pick_split(int kv_dtype, bool aligned, int D, int GP) {
-    if (kv_dtype == RK_BF16) return aligned ? pick_split<uint16_t, true>(D, GP) : pick_split<uint16_t, false>(D, GP);
-    return aligned ? pick_split<float, true>(D, GP) : pick_split<float, false>(D, GP);
+SplitFn pick_split(int kv_dtype, bool aligned, int D, int GP, int wpg) {
+    if (kv_dtype == RK_BF16)
+        return aligned ? pick_split<uint16_t, true>(D, GP, wpg) : pick_split<uint16_t, false>(D, GP, wpg);
+    return aligned ? pick_split<float, true>(D, GP, wpg) : pick_split<float, false>(D, GP, wpg);
 }
 
-int groups_of(int Hkv, int GP) {
-    const int wpg = waves_per_group(GP);
-    return wpg / Hkv > 0 ? wpg / Hkv : 1;
-}
+int groups_of(int Hkv, int wpg) { return wpg / Hkv > 0 ? wpg / Hkv : 1; }
 
 int split_lds_bytes(int B, int Hkv, int D, int GP, int NG) {
     int per_wave = 0;
@@ -837,12 +845,12 @@ MergeFn pick_merge(int D, int GP) {
 // upper bound, capped at the waves per compute unit that stay resident all at once: 8 for 8-wave workgroups (two
 // per SIMD), 4 for 4-wave ones (their registers allow one per SIMD).
 int split_groups(int B, int Hkv, int block_size, int max_nb, int GP) {
-    const int wpg = waves_per_group(GP);
+    const long long upper = tile_upper(B, block_size, max_nb);
+    const int wpg = waves_per_group(GP, upper);
     const int per_cu = wpg == 8 ? 8 : 4;
-    const long long upper = (long long)B * (((long long)max_nb * block_size + kTile - 1) / kTile);
     int cus = device_cus();
     if (cus <= 0) cus = 256;
-    const int ng = groups_of(Hkv, GP);
+    const int ng = groups_of(Hkv, wpg);
     const long long cap = (long long)cus * per_cu / (ng * Hkv);
     const long long want = (upper + ng - 1) / ng;
     long long nw = want < cap ? want : cap;
@@ -912,11 +920,12 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     a.gate = gate;
     a.gate_ld = gate_ld;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = G; a.bs = block_size; a.max_nb = max_nb;
-    a.num_blocks = num_blocks; a.window = window; a.NW = NW; a.NG = groups_of(Hkv, GP);
+    const int wpg = waves_per_group(GP, tile_upper(B, block_size, max_nb));
+    a.num_blocks = num_blocks; a.window = window; a.NW = NW; a.NG = groups_of(Hkv, wpg);
     a.qscale = kLog2e / sqrtf((float)D);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (phase == 0) {
-        SplitFn fn = pick_split(kv_dtype, block_size % kTile == 0, D, GP);
+        SplitFn fn = pick_split(kv_dtype, block_size % kTile == 0, D, GP, wpg);
         const int lds = split_lds_bytes(B, Hkv, D, GP, a.NG);
         rc = allow_dynamic_lds(reinterpret_cast<const void*>(fn), lds);
         if (rc) return rc;
