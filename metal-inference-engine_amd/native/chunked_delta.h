@@ -149,9 +149,20 @@ constexpr int kTOff = 0;                                           // T pieces  
 constexpr int kPOff = kTP * kPieceElems;                           // P pieces   (uint16 offset)
 constexpr int kCoefOff = kTP * kPieceElems;                        // coefficients (float offset: after 2 x kTP pieces)
 
-// Lane order (bf16 inputs, read by delta_chunk_scan_cols): the A operand of row tile a and 32-token k-step k (the
-// pairs (a, k) with k <= a / 2, numbered pair_of(a, k) = 0 .. 5) is one 1 KB block per piece, block 6 pi + pair,
-// lane (q, r) holding 8 bf16 at 16 lane bytes: entries (16a + r, 32k + perm(8q + e)), where perm(8q + e) =
+// Per-chunk workspace record of the bf16-input path (delta_chunk_scan_cols): T and P as fp32 lower triangles, row i
+// holding columns 0 .. i zero-padded to a multiple of 4 floats from tri_base(i), then the coefficient rows (18 KB,
+// half the pieces' size: the scan's loading waves split the entries into pieces in LDS themselves).
+__host__ __device__ constexpr int tri_base(int i) { return 4 * (i / 4 + 1) * (2 * (i / 4) + i % 4); }
+constexpr int kTriFloats = tri_base(kC);                            // 2176
+constexpr int kLaneTOff = 0, kLanePOff = kTriFloats;                // float offsets
+constexpr int kLaneCoefOff = 2 * kTriFloats;
+constexpr int kLaneChunkFloats = kLaneCoefOff + kCoefRows * kC;     // record stride (floats)
+static_assert(kLaneChunkFloats <= kChunkFloats, "the workspace size covers both record layouts");
+static_assert(kLaneChunkFloats % 64 == 0, "records stay 256-byte aligned");
+
+// Lane order (bf16 inputs, the LDS stage of delta_chunk_scan_cols): the A operand of row tile a and 32-token k-step
+// k (the pairs (a, k) with k <= a / 2, numbered pair_of(a, k) = 0 .. 5) is one 1 KB block per piece, block 6 pi +
+// pair, lane (q, r) holding 8 bf16 at 16 lane bytes: entries (16a + r, 32k + perm(8q + e)), where perm(8q + e) =
 // 4q + e for e < 4 and 16 + 4q + (e - 4) for e >= 4. That k order is the one in which an MFMA accumulator pair (row
 // tiles 2k, 2k+1, lane (q, r) holding rows 4q + i) is already a B operand, so no operand of the scan is transposed.
 __host__ __device__ constexpr int pair_of(int a, int k) { return a < 2 ? a : 2 + 2 * (a - 2) + k; }

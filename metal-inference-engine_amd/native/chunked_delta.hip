@@ -117,11 +117,11 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
 
     // Tiles (b, w) of K K^T and of P^T = K Q^T (A = K rows of tile b from LDS, B = this wave's K / Q rows): lane (q, r)
     // holds entries (t', t) = (16b + 4q + i, 16w + r), i.e. row t of A0 and P at columns t'.
-    uint16_t* ws16 = reinterpret_cast<uint16_t*>(p.ws + ((size_t)gc * H + h) * kChunkFloats);
+    constexpr bool kLane = sizeof(In) == 2;
+    float* rec = p.ws + ((size_t)gc * H + h) * (kLane ? kLaneChunkFloats : kChunkFloats);
+    uint16_t* ws16 = reinterpret_cast<uint16_t*>(rec);
     const float Gt = __shfl(G, 16 * w + r), bt = __shfl(bl, 16 * w + r);
     const int t = 16 * w + r;
-    constexpr bool kLane = sizeof(In) == 2;
-    float pe[4];                          // lane order: P of the even block of the current k-step
     for (int b = 0; b < 2 * ((w >> 1) + 1); ++b) {
         float pv[4] = {0.f, 0.f, 0.f, 0.f};
         if (b <= w) {
@@ -155,21 +155,10 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
             }
         }
         if constexpr (kLane) {
-            // block b of P^T leaves row 16w + r, columns 16b + 4q + i in this lane: slots e and e + 4 of the lane's
-            // k-step (b >> 1) operand
-            static_assert(kTP == kNS, "lane-order pieces are exact three-piece splits");
-            if ((b & 1) == 0) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) pe[i] = pv[i];
-            } else {
-                const float x[8] = {pe[0], pe[1], pe[2], pe[3], pv[0], pv[1], pv[2], pv[3]};
-                u32x4 pc[kNS];
-                split8(x, pc);
-                const int blk = pair_of(w, b >> 1);
-#pragma unroll
-                for (int pi = 0; pi < kNS; ++pi)
-                    *reinterpret_cast<u32x4*>(ws16 + kPOff + 512 * (6 * pi + blk) + 8 * lane) = pc[pi];
-            }
+            // row t of P, columns 16b + 4q .. +3 (zero past the diagonal), as one group of its padded triangle row
+            if (16 * b + 4 * q <= t)
+                *reinterpret_cast<f32x4*>(rec + kLanePOff + tri_base(t) + 16 * b + 4 * q) =
+                    (f32x4){pv[0], pv[1], pv[2], pv[3]};
         } else {
             store_pieces4(ws16 + kPOff + rt_base(w) + r * rt_width(w) + 16 * b + 4 * q, pv);
         }
@@ -214,23 +203,17 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
         lds_barrier();
     }
 
-    // T pieces, row-tile blocks as for P; entries above the diagonal are zero
+    // T: as P (the padded triangle) for bf16 inputs, else row-tile blocks of pieces; entries above the diagonal are 0
     if constexpr (kLane) {
-        for (int idx = threadIdx.x; idx < 6 * 64; idx += 256) {
-            const int blk = idx >> 6, L = idx & 63;
-            const int a = blk < 2 ? blk : 2 + ((blk - 2) >> 1), k = blk < 2 ? 0 : ((blk - 2) & 1);
-            const int row = 16 * a + (L & 15);
-            float x[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int col = 32 * k + perm_k(8 * (L >> 4) + e);
-                x[e] = col <= row ? sT[row][col] : 0.f;
+        for (int it = 0; it < kC * 16 / 256; ++it) {
+            const int idx = threadIdx.x + 256 * it, row = idx >> 4, col = 4 * (idx & 15);
+            if (col <= row) {
+                f32x4 x;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] = col + e <= row ? sT[row][col + e] : 0.f;
+                *reinterpret_cast<f32x4*>(rec + kLaneTOff + tri_base(row) + col) = x;
             }
-            u32x4 pc[kNS];
-            split8(x, pc);
-#pragma unroll
-            for (int pi = 0; pi < kNS; ++pi)
-                *reinterpret_cast<u32x4*>(ws16 + kTOff + 512 * (6 * pi + blk) + 8 * L) = pc[pi];
         }
     } else
 #pragma unroll
@@ -246,7 +229,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     }
     if (w == 0) {
         const float Glast = __shfl(G, kC - 1);
-        float* cf = p.ws + ((size_t)gc * H + h) * kChunkFloats + kCoefOff;
+        float* cf = rec + (kLane ? kLaneCoefOff : kCoefOff);
         cf[lane] = bl;
         cf[kC + lane] = G;
         cf[2 * kC + lane] = expf(G);

@@ -107,10 +107,11 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
     const uint16_t* Qg = static_cast<const uint16_t*>(p.q);
     const uint16_t* Vg = static_cast<const uint16_t*>(p.v);
 
-    // This wave's share of the direct loads of chunk c's stage: the K, Q, T, P and V groups j with j % 2 == wave
-    // (the coefficient rows: wave 0), in three parts issued at different points of the previous chunk. Per-lane byte
-    // offsets of full chunks are fixed for the kernel; a chunk that ends early repeats its last row instead (rows past
-    // the sequence's end have beta 0, so they leave S and the rows before them untouched).
+    // This wave's share of chunk c's stage: the direct loads of the K, Q and V groups j with j % 2 == wave (and of the
+    // coefficient rows: wave 0), and T and P blocks pair_of = wave, wave + 2, wave + 4, which it loads as fp32 from
+    // the padded triangles, splits into pieces and writes to LDS. Per-lane byte offsets of full chunks are fixed for
+    // the kernel; a chunk that ends early repeats its last K / Q / V row instead (rows past the sequence's end have
+    // beta 0, so they leave S and the rows before them untouched).
     const int wv = __builtin_amdgcn_readfirstlane(ct & 1);
     uint32_t kq_off[8], v_off[2];
 #pragma unroll
@@ -123,77 +124,113 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
         const int tok = 16 * (2 * jj + wv) + (lane >> 2);
         v_off[jj] = 2u * (uint32_t)(tok * H * kDv + col0 + 8 * (lane & 3));
     }
-    // The i-th direct load of this wave for chunk c (full chunks): 0-7 K rows, 8-16 T, 17-24 Q, 25-33 P, 34-35 V,
-    // 36 the coefficient rows (wave 0 only).
-    auto load_one = [&](int c, char* stage, int i) __attribute__((always_inline)) {
-        const long long row0 = (long long)(T0 + c * kC) * H + h;
-        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats);
-        if (i < 8 || (i >= 17 && i < 25)) {
-            const int jj = i < 8 ? i : i - 17;
-            const char* base = reinterpret_cast<const char*>((i < 8 ? Kg : Qg) + row0 * kDk);
-            const int g = 2 * jj + wv;
-            load_to_lds(base + kq_off[jj], stage + (i < 8 ? ColStage::kK : ColStage::kQ) + pair_base(g) + kq_group_off(g));
-        } else if (i < 34) {
-            const bool t = i < 17;
-            const int jj = t ? i - 8 : i - 25;
-            load_to_lds(rec + 2 * (t ? kTOff : kPOff) + 1024 * wv + 2048 * jj + 16 * lane,
-                        stage + (t ? ColStage::kT : ColStage::kP) + 1024 * wv + 2048 * jj);
-        } else if (i < 36) {
-            const int jj = i - 34;
-            load_to_lds(reinterpret_cast<const char*>(Vg + row0 * kDv) + v_off[jj],
-                        stage + ColStage::kV + 1024 * wv + 2048 * jj);
-        } else if (wv == 0) {
-            load_to_lds(rec + 4 * kCoefOff + 16 * lane, stage + ColStage::kCf);
+    // T / P entries of this lane in block pair_of(a, k) = wv + 2 jj: row 16a + r, columns 32k + 4q .. +3 (half 0) and
+    // 32k + 16 + 4q .. +3 (half 1). A group past the row's diagonal is not stored: its load reads the row's first
+    // group and the value is replaced by zeros.
+    uint32_t tp_off[3][2];
+    uint32_t tp_keep[3][2];
+#pragma unroll
+    for (int jj = 0; jj < 3; ++jj) {
+        const int pr = wv + 2 * jj;
+        const int a = pr < 2 ? pr : 2 + ((pr - 2) >> 1), k = pr < 2 ? 0 : ((pr - 2) & 1);
+        const int row = 16 * a + r;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int colg = 32 * k + 16 * hf + 4 * q;
+            tp_keep[jj][hf] = mask_if(colg <= row);
+            tp_off[jj][hf] = 4u * (uint32_t)(tri_base(row) + (colg <= row ? colg : 0));
         }
+    }
+    // issue the fp32 loads of chunk c's T and P blocks
+    auto tp_issue = [&](int c, f32x4 (&tp)[2][3][2]) __attribute__((always_inline)) {
+        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kLaneChunkFloats);
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int jj = 0; jj < 3; ++jj)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    tp[m][jj][hf] = *reinterpret_cast<const f32x4*>(rec + 4 * (m ? kLanePOff : kLaneTOff) +
+                                                                    tp_off[jj][hf]);
     };
-    constexpr int kLoads = 37;
-    // All of chunk c's direct loads at once, rows past the sequence's end repeating its last row (used for the first
-    // chunk and for a chunk that ends early).
+    // split them into pieces and write the lane-order blocks of the stage
+    auto tp_store = [&](char* stage, const f32x4 (&tp)[2][3][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int jj = 0; jj < 3; ++jj) {
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    x[e] = __uint_as_float(__float_as_uint(tp[m][jj][e >> 2][e & 3]) & tp_keep[jj][e >> 2]);
+                u32x4 pc[kNS];
+                split8(x, pc);
+                char* dst = stage + (m ? ColStage::kP : ColStage::kT) + 1024 * (wv + 2 * jj) + 16 * lane;
+#pragma unroll
+                for (int pi = 0; pi < kNS; ++pi) *reinterpret_cast<u32x4*>(dst + 6 * 1024 * pi) = pc[pi];
+            }
+    };
+    // chunk c's direct loads (K, Q, V, coefficients), rows past the sequence's end repeating its last row
     auto stage_loads = [&](int c, char* stage) __attribute__((always_inline)) {
         const int nt = min(kC, Tn - c * kC);
+        const long long row0 = (long long)(T0 + c * kC) * H + h;
+        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kLaneChunkFloats);
         if (nt == kC) {
 #pragma unroll
-            for (int i = 0; i < kLoads; ++i) load_one(c, stage, i);
-            return;
-        }
-        const long long row0 = (long long)(T0 + c * kC) * H + h;
-        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kChunkFloats);
+            for (int part = 0; part < 2; ++part) {
+                const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
+                char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ);
 #pragma unroll
-        for (int part = 0; part < 2; ++part) {
-            const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
-            char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ);
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const int g = 2 * jj + wv, row = 4 * g + (lane >> 4), u = lane & 15;
-                load_to_lds(base + 2 * ((long long)min(row, nt - 1) * H * kDk + 8 * (u ^ (4 * (row & 3)))),
-                            dst + pair_base(g) + kq_group_off(g));
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int g = 2 * jj + wv;
+                    load_to_lds(base + kq_off[jj], dst + pair_base(g) + kq_group_off(g));
+                }
             }
-            const char* blocks = rec + 2 * (part == 0 ? kTOff : kPOff) + 1024 * wv + 16 * lane;
-            char* bdst = stage + (part == 0 ? ColStage::kT : ColStage::kP) + 1024 * wv;
 #pragma unroll
-            for (int jj = 0; jj < 9; ++jj) load_to_lds(blocks + 2048 * jj, bdst + 2048 * jj);
-        }
-        const char* vbase = reinterpret_cast<const char*>(Vg + row0 * kDv);
+            for (int jj = 0; jj < 2; ++jj)
+                load_to_lds(reinterpret_cast<const char*>(Vg + row0 * kDv) + v_off[jj],
+                            stage + ColStage::kV + 1024 * wv + 2048 * jj);
+        } else {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-            const int tok = 16 * (2 * jj + wv) + (lane >> 2);
-            load_to_lds(vbase + 2 * ((long long)min(tok, nt - 1) * H * kDv + col0 + 8 * (lane & 3)),
-                        stage + ColStage::kV + 1024 * wv + 2048 * jj);
+            for (int part = 0; part < 2; ++part) {
+                const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
+                char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ);
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int g = 2 * jj + wv, row = 4 * g + (lane >> 4), u = lane & 15;
+                    load_to_lds(base + 2 * ((long long)min(row, nt - 1) * H * kDk + 8 * (u ^ (4 * (row & 3)))),
+                                dst + pair_base(g) + kq_group_off(g));
+                }
+            }
+            const char* vbase = reinterpret_cast<const char*>(Vg + row0 * kDv);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int tok = 16 * (2 * jj + wv) + (lane >> 2);
+                load_to_lds(vbase + 2 * ((long long)min(tok, nt - 1) * H * kDv + col0 + 8 * (lane & 3)),
+                            stage + ColStage::kV + 1024 * wv + 2048 * jj);
+            }
         }
-        if (wv == 0) load_to_lds(rec + 4 * kCoefOff + 16 * lane, stage + ColStage::kCf);
+        if (wv == 0) load_to_lds(rec + 4 * kLaneCoefOff + 16 * lane, stage + ColStage::kCf);
+    };
+    // all of chunk c's stage: the T / P loads first, so that their wait leaves the direct loads in flight
+    auto fill_stage = [&](int c, char* stage) __attribute__((always_inline)) {
+        f32x4 tp[2][3][2];
+        tp_issue(c, tp);
+        stage_loads(c, stage);
+        tp_store(stage, tp);
     };
 
     // Waves 2 and 3 only load: every stage's direct loads are theirs (a direct load holds its issuing wave for ~90
     // cycles, which on the two computing waves would add up to a third of a chunk). All four waves meet at the one
     // barrier per chunk: after it, stage c is complete and stage c-1 is free for chunk c+1.
     if (ct >= 2) {
-        stage_loads(0, stage0);
+        fill_stage(0, stage0);
         __syncthreads();
         for (int c = 0; c < nch; c += 2) {
-            if (c + 1 < nch) stage_loads(c + 1, stage1);
+            if (c + 1 < nch) fill_stage(c + 1, stage1);
             __syncthreads();
             if (c + 1 < nch) {
-                if (c + 2 < nch) stage_loads(c + 2, stage0);
+                if (c + 2 < nch) fill_stage(c + 2, stage0);
                 __syncthreads();
             }
         }
