@@ -149,13 +149,13 @@ constexpr int kTOff = 0;                                           // T pieces  
 constexpr int kPOff = kTP * kPieceElems;                           // P pieces   (uint16 offset)
 constexpr int kCoefOff = kTP * kPieceElems;                        // coefficients (float offset: after 2 x kTP pieces)
 
-// Per-chunk workspace record of the bf16-input path (delta_chunk_scan_cols): T and P as fp32 lower triangles, row i
-// holding columns 0 .. i zero-padded to a multiple of 4 floats from tri_base(i), then the coefficient rows (18 KB,
-// half the pieces' size: the scan's loading waves split the entries into pieces in LDS themselves).
+// Per-chunk workspace record of the bf16-input path (delta_chunk_scan_cols): T as an fp32 lower triangle, row i
+// holding columns 0 .. i zero-padded to a multiple of 4 floats from tri_base(i), then the coefficient rows (9.5 KB,
+// a quarter of the pieces' size: the scan's loading waves split T into pieces in LDS themselves, and compute P from
+// the chunk's K and Q rows).
 __host__ __device__ constexpr int tri_base(int i) { return 4 * (i / 4 + 1) * (2 * (i / 4) + i % 4); }
 constexpr int kTriFloats = tri_base(kC);                            // 2176
-constexpr int kLaneTOff = 0, kLanePOff = kTriFloats;                // float offsets
-constexpr int kLaneCoefOff = 2 * kTriFloats;
+constexpr int kLaneCoefOff = kTriFloats;                            // float offsets: T at 0, then the coefficients
 constexpr int kLaneChunkFloats = kLaneCoefOff + kCoefRows * kC;     // record stride (floats)
 static_assert(kLaneChunkFloats <= kChunkFloats, "the workspace size covers both record layouts");
 static_assert(kLaneChunkFloats % 64 == 0, "records stay 256-byte aligned");

@@ -13,14 +13,16 @@
 //
 // Kernels:
 //   delta_chunk_prep  one workgroup per (chunk, head), all chunks in parallel: beta, G (summed in fp64 and rounded
-//                     once, as torch's CPU cumsum of fp32 accumulates in double), exp(G), exp(G_last - G); K K^T and
-//                     Q K^T on MFMA from K rows staged in LDS; P = Q K^T * D; T by blocked inversion of the unit lower
+//                     once, as torch's CPU cumsum of fp32 accumulates in double), exp(G), exp(G_last - G); K K^T (and
+//                     for fp32 inputs Q K^T) on MFMA from K rows staged in LDS; T by blocked inversion of the unit lower
 //                     triangular matrix (16 x 16 diagonal blocks by substitution, off-diagonal blocks by fp32 MFMA
-//                     products in three levels). T and P go to the workspace already split into bf16 pieces, in the
-//                     operand order the scan loads, so the scan workgroups of a head share them instead of each
-//                     recomputing them.
+//                     products in three levels). For fp32 inputs T and P = Q K^T * D go to the workspace already split
+//                     into bf16 pieces, in the operand order the scan loads, so the scan workgroups of a head share
+//                     them instead of each recomputing them; for bf16 inputs T goes there as an fp32 triangle.
 //   delta_chunk_scan_cols (bf16 inputs, chunked_delta_cols.hip)  one workgroup per (sequence, head, 32-column slice
 //                     of S), one wave per 16 columns over all 64 tokens of a chunk: no exchange between waves at all.
+//                     Its two loading waves, on SIMDs of their own, split T into pieces and compute P from the
+//                     chunk's K and Q rows while the previous chunk is computed.
 //   delta_chunk_scan  (fp32 inputs) one workgroup per (sequence, head, 32-column slice of S): the columns of S evolve
 //                     independently, so the serial pass over a sequence's chunks runs 4 workgroups wide per head.
 //                     Wave w owns token rows 16w..16w+15 of the chunk and state rows 32w..32w+31 (two 16-column
@@ -77,7 +79,9 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     const In* K = static_cast<const In*>(p.k);
     const In* Q = static_cast<const In*>(p.q);
 
-    // K and Q rows of row tile w, zero past the sequence's end; all loads issued up front
+    // bf16 inputs (lane order): the scan computes P itself, so only K K^T is formed here
+    constexpr bool kLane = sizeof(In) == 2;
+    // K (and Q) rows of row tile w, zero past the sequence's end; all loads issued up front
     Row8<In> ka[4], qa[4];
     {
         const int t = 16 * w + r;
@@ -86,9 +90,11 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             ka[k].load(K + off + 32 * k);
-            qa[k].load(Q + off + 32 * k);
             ka[k].keep(m);
-            qa[k].keep(m);
+            if constexpr (!kLane) {
+                qa[k].load(Q + off + 32 * k);
+                qa[k].keep(m);
+            }
         }
     }
     const bool live = lane < nt;
@@ -117,12 +123,11 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
 
     // Tiles (b, w) of K K^T and of P^T = K Q^T (A = K rows of tile b from LDS, B = this wave's K / Q rows): lane (q, r)
     // holds entries (t', t) = (16b + 4q + i, 16w + r), i.e. row t of A0 and P at columns t'.
-    constexpr bool kLane = sizeof(In) == 2;
     float* rec = p.ws + ((size_t)gc * H + h) * (kLane ? kLaneChunkFloats : kChunkFloats);
     uint16_t* ws16 = reinterpret_cast<uint16_t*>(rec);
     const float Gt = __shfl(G, 16 * w + r), bt = __shfl(bl, 16 * w + r);
     const int t = 16 * w + r;
-    for (int b = 0; b < 2 * ((w >> 1) + 1); ++b) {
+    for (int b = 0; b < (kLane ? w + 1 : 2 * ((w >> 1) + 1)); ++b) {
         float pv[4] = {0.f, 0.f, 0.f, 0.f};
         if (b <= w) {
             f32x4 kk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
@@ -140,8 +145,10 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
                 kb.pieces(pa);
                 ka[k].pieces(pb);
                 kk = mma(pa, pb, kk);
-                qa[k].pieces(pb);
-                pq = mma(pa, pb, pq);
+                if constexpr (!kLane) {
+                    qa[k].pieces(pb);
+                    pq = mma(pa, pb, pq);
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -154,14 +161,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
                 pv[i] = pq[i] * d;
             }
         }
-        if constexpr (kLane) {
-            // row t of P, columns 16b + 4q .. +3 (zero past the diagonal), as one group of its padded triangle row
-            if (16 * b + 4 * q <= t)
-                *reinterpret_cast<f32x4*>(rec + kLanePOff + tri_base(t) + 16 * b + 4 * q) =
-                    (f32x4){pv[0], pv[1], pv[2], pv[3]};
-        } else {
-            store_pieces4(ws16 + kPOff + rt_base(w) + r * rt_width(w) + 16 * b + 4 * q, pv);
-        }
+        if constexpr (!kLane) store_pieces4(ws16 + kPOff + rt_base(w) + r * rt_width(w) + 16 * b + 4 * q, pv);
     }
     lds_barrier();                         // sK is dead from here: its space holds T
 
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
         lds_barrier();
     }
 
-    // T: as P (the padded triangle) for bf16 inputs, else row-tile blocks of pieces; entries above the diagonal are 0
+    // T: the padded fp32 triangle for bf16 inputs, else row-tile blocks of pieces; entries above the diagonal are 0
     if constexpr (kLane) {
 #pragma unroll
         for (int it = 0; it < kC * 16 / 256; ++it) {
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
                 f32x4 x;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) x[e] = col + e <= row ? sT[row][col + e] : 0.f;
-                *reinterpret_cast<f32x4*>(rec + kLaneTOff + tri_base(row) + col) = x;
+                *reinterpret_cast<f32x4*>(rec + tri_base(row) + col) = x;
             }
         }
     } else

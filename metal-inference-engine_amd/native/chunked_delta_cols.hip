@@ -2,6 +2,8 @@
 // of a chunk (delta_chunk_scan_cols). Same maths and precision as chunked_delta.hip, which builds its operands
 // (delta_chunk_prep, lane order) and holds the C ABI. Built on its own so that the compiler keeps MFMA results in
 // VGPRs here (the piece splits and scalings read them every chunk) without changing the other kernels' allocation.
+#include <type_traits>
+
 #include "chunked_delta.h"
 #include "rk_internal.h"
 
@@ -107,133 +109,169 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
     const uint16_t* Qg = static_cast<const uint16_t*>(p.q);
     const uint16_t* Vg = static_cast<const uint16_t*>(p.v);
 
-    // This wave's share of chunk c's stage: the direct loads of the K, Q and V groups j with j % 2 == wave (and of the
-    // coefficient rows: wave 0), and T and P blocks pair_of = wave, wave + 2, wave + 4, which it loads as fp32 from
-    // the padded triangles, splits into pieces and writes to LDS. Per-lane byte offsets of full chunks are fixed for
-    // the kernel; a chunk that ends early repeats its last K / Q / V row instead (rows past the sequence's end have
-    // beta 0, so they leave S and the rows before them untouched).
-    const int wv = __builtin_amdgcn_readfirstlane(ct & 1);
-    uint32_t kq_off[8], v_off[2];
+    // Waves 2 and 3 only load and prepare, on SIMDs of their own (a direct load holds its issuing wave for ~90 cycles,
+    // which on the computing waves would add up to a third of a chunk). While chunk c is computed, wave WV = ct & 1
+    //  - fills its share of chunk c+1's stage: direct loads of the K, Q and V groups j with j % 2 == WV (and of the
+    //    coefficient rows: WV 0), and T blocks pair_of = WV, WV + 2, WV + 4, loaded as fp32 from the padded triangle
+    //    a chunk ahead and split into pieces;
+    //  - computes chunk c's P blocks of the same pairs into chunk c's stage, from the K and Q rows there (complete
+    //    since the last barrier): block (a, k) is tiles b = 2k, 2k+1 of P^T = K Q^T (those with b <= a; the others
+    //    are zero) times D. The computing waves read them during chunk c+1, when they form chunk c's o.
+    // All four waves meet at the one barrier per chunk: after it, stage c+1 and chunk c's P are complete and stage
+    // c-1 (whose P chunk c read) is free. A chunk that ends early repeats its last K / Q / V row (rows past the
+    // sequence's end have beta 0, so they leave S and the rows before them untouched, and their P entries meet
+    // vn = 0).
+    if (ct >= 2) {
+        auto loader = [&](auto wv_c) __attribute__((always_inline)) {
+            constexpr int WV = decltype(wv_c)::value;
+            constexpr int kA[3] = {WV, 2, 3};        // block jj = pair WV + 2 jj = (kA[jj], kKs[jj])
+            constexpr int kKs[3] = {0, WV, WV};
+            uint32_t kq_off[8], v_off[2];
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-        const int row = 4 * (2 * jj + wv) + (lane >> 4), u = lane & 15;
-        kq_off[jj] = 2u * (uint32_t)(row * H * kDk + 8 * (u ^ (4 * (row & 3))));
-    }
+            for (int jj = 0; jj < 8; ++jj) {
+                const int row = 4 * (2 * jj + WV) + (lane >> 4), u = lane & 15;
+                kq_off[jj] = 2u * (uint32_t)(row * H * kDk + 8 * (u ^ (4 * (row & 3))));
+            }
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-        const int tok = 16 * (2 * jj + wv) + (lane >> 2);
-        v_off[jj] = 2u * (uint32_t)(tok * H * kDv + col0 + 8 * (lane & 3));
-    }
-    // T / P entries of this lane in block pair_of(a, k) = wv + 2 jj: row 16a + r, columns 32k + 4q .. +3 (half 0) and
-    // 32k + 16 + 4q .. +3 (half 1). A group past the row's diagonal is not stored: its load reads the row's first
-    // group and the value is replaced by zeros.
-    uint32_t tp_off[3][2];
-    uint32_t tp_keep[3][2];
+            for (int jj = 0; jj < 2; ++jj) {
+                const int tok = 16 * (2 * jj + WV) + (lane >> 2);
+                v_off[jj] = 2u * (uint32_t)(tok * H * kDv + col0 + 8 * (lane & 3));
+            }
+            // T entries of this lane in block jj: row 16a + r, columns 32k + 4q .. +3 (half 0) and 32k + 16 + 4q ..
+            // +3 (half 1). A group past the row's diagonal is not stored: its load reads the row's first group and
+            // the value is replaced by zeros; a half past the diagonal for every lane (2k + hf > a) is not loaded.
+            uint32_t t_off[3][2], t_keep[3][2];
 #pragma unroll
-    for (int jj = 0; jj < 3; ++jj) {
-        const int pr = wv + 2 * jj;
-        const int a = pr < 2 ? pr : 2 + ((pr - 2) >> 1), k = pr < 2 ? 0 : ((pr - 2) & 1);
-        const int row = 16 * a + r;
+            for (int jj = 0; jj < 3; ++jj) {
+                const int row = 16 * kA[jj] + r;
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int colg = 32 * k + 16 * hf + 4 * q;
-            tp_keep[jj][hf] = mask_if(colg <= row);
-            tp_off[jj][hf] = 4u * (uint32_t)(tri_base(row) + (colg <= row ? colg : 0));
-        }
-    }
-    // issue the fp32 loads of chunk c's T and P blocks
-    auto tp_issue = [&](int c, f32x4 (&tp)[2][3][2]) __attribute__((always_inline)) {
-        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kLaneChunkFloats);
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int colg = 32 * kKs[jj] + 16 * hf + 4 * q;
+                    t_keep[jj][hf] = mask_if(colg <= row);
+                    t_off[jj][hf] = (uint32_t)(tri_base(row) + (colg <= row ? colg : 0));
+                }
+            }
+            f32x4 tr[3][2];                          // T entries of the next stage, requested a chunk ahead
+            auto issue = [&](int c) __attribute__((always_inline)) {
+                const float* rec = p.ws + ((size_t)(gc0 + c) * H + h) * kLaneChunkFloats;
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
+                for (int jj = 0; jj < 3; ++jj)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf)
+                        tr[jj][hf] = 2 * kKs[jj] + hf <= kA[jj] ? *reinterpret_cast<const f32x4*>(rec + t_off[jj][hf])
+                                                                : (f32x4){0.f, 0.f, 0.f, 0.f};
+            };
+            constexpr int kIssued = 5;               // loads in issue(): the T halves with 2k + hf <= a
+            // chunk c's direct loads (K, Q, V, coefficients), rows past the sequence's end repeating its last row
+            auto direct = [&](int c, char* stage) __attribute__((always_inline)) {
+                const int nt = min(kC, Tn - c * kC);
+                const long long row0 = (long long)(T0 + c * kC) * H + h;
+                const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kLaneChunkFloats);
+#pragma unroll
+                for (int part = 0; part < 2; ++part) {
+                    const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
+                    char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ);
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const int g = 2 * jj + WV, row = 4 * g + (lane >> 4), u = lane & 15;
+                        const uint32_t off = nt == kC ? kq_off[jj]
+                                                      : 2u * (uint32_t)(min(row, nt - 1) * H * kDk + 8 * (u ^ (4 * (row & 3))));
+                        load_to_lds(base + off, dst + pair_base(g) + kq_group_off(g));
+                    }
+                }
+                const char* vbase = reinterpret_cast<const char*>(Vg + row0 * kDv);
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int tok = 16 * (2 * jj + WV) + (lane >> 2);
+                    const uint32_t off = nt == kC ? v_off[jj]
+                                                  : 2u * (uint32_t)(min(tok, nt - 1) * H * kDv + col0 + 8 * (lane & 3));
+                    load_to_lds(vbase + off, stage + ColStage::kV + 1024 * WV + 2048 * jj);
+                }
+                if (WV == 0) load_to_lds(rec + 4 * kLaneCoefOff + 16 * lane, stage + ColStage::kCf);
+            };
+            // T split into pieces, written to the stage's lane-order blocks
+            auto put_t = [&](char* stage) __attribute__((always_inline)) {
+#pragma unroll
+                for (int jj = 0; jj < 3; ++jj) {
+                    float x[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        x[e] = __uint_as_float(__float_as_uint(tr[jj][e >> 2][e & 3]) & t_keep[jj][e >> 2]);
+                    u32x4 pc[kNS];
+                    split8(x, pc);
+                    char* dst = stage + ColStage::kT + 1024 * (WV + 2 * jj) + 16 * lane;
+#pragma unroll
+                    for (int pi = 0; pi < kNS; ++pi) *reinterpret_cast<u32x4*>(dst + 6 * 1024 * pi) = pc[pi];
+                }
+            };
+            // P of the chunk in `stage` (its K, Q rows and G there), split into pieces and written to its P blocks
+            auto put_p = [&](char* stage) __attribute__((always_inline)) {
+                const float* gr = reinterpret_cast<const float*>(stage + ColStage::kCf) + kC;
+#pragma unroll
+                for (int jj = 0; jj < 3; ++jj) {
+                    const int a = kA[jj], t = 16 * a + r;
+                    const float gq = gr[t];
+                    float x[8];
+#pragma unroll
+                    for (int hb = 0; hb < 2; ++hb) {
+                        const int b = 2 * kKs[jj] + hb;
+                        f32x4 pq = {0.f, 0.f, 0.f, 0.f};
+                        if (b <= a)
+#pragma unroll
+                            for (int kd = 0; kd < 4; ++kd)
+                                pq = mfma16x16x32(row_operand(stage + ColStage::kK, 16 * b + r, kd, q),
+                                                  row_operand(stage + ColStage::kQ, t, kd, q), pq);
+                        const f32x4 gk = *reinterpret_cast<const f32x4*>(gr + 16 * b + 4 * q);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            // P[t][t'] = (q_t . k_t') exp(G_t - G_t') for t' <= t (masked before exp)
+                            const int tp = 16 * b + 4 * q + i;
+                            const float d = tp <= t ? fast_exp2((gq - gk[i]) * kLog2e) : 0.f;
+                            x[4 * hb + i] = pq[i] * d;
+                        }
+                    }
+                    u32x4 pc[kNS];
+                    split8(x, pc);
+                    char* dst = stage + ColStage::kP + 1024 * (WV + 2 * jj) + 16 * lane;
+#pragma unroll
+                    for (int pi = 0; pi < kNS; ++pi) *reinterpret_cast<u32x4*>(dst + 6 * 1024 * pi) = pc[pi];
+                }
+            };
+            // Before each barrier the wave waits for its direct loads only (the in-order counter allows the kIssued
+            // newer T requests to stay in flight), then for its LDS writes; written out, as a fence would make the
+            // compiler wait for every load (it cannot tell the direct loads' LDS writes from the requests).
+            // tests/test_build.py checks kIssued against the compiled code.
+            auto sync = [&]() __attribute__((always_inline)) {
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kIssued) : "memory");
+            };
+            // stage 1's P blocks start at zero: chunk 0 forms the o of "chunk -1" from them, with zero factors
 #pragma unroll
             for (int jj = 0; jj < 3; ++jj)
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
-                    tp[m][jj][hf] = *reinterpret_cast<const f32x4*>(rec + 4 * (m ? kLanePOff : kLaneTOff) +
-                                                                    tp_off[jj][hf]);
-    };
-    // split them into pieces and write the lane-order blocks of the stage
-    auto tp_store = [&](char* stage, const f32x4 (&tp)[2][3][2]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-#pragma unroll
-            for (int jj = 0; jj < 3; ++jj) {
-                float x[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    x[e] = __uint_as_float(__float_as_uint(tp[m][jj][e >> 2][e & 3]) & tp_keep[jj][e >> 2]);
-                u32x4 pc[kNS];
-                split8(x, pc);
-                char* dst = stage + (m ? ColStage::kP : ColStage::kT) + 1024 * (wv + 2 * jj) + 16 * lane;
-#pragma unroll
-                for (int pi = 0; pi < kNS; ++pi) *reinterpret_cast<u32x4*>(dst + 6 * 1024 * pi) = pc[pi];
-            }
-    };
-    // chunk c's direct loads (K, Q, V, coefficients), rows past the sequence's end repeating its last row
-    auto stage_loads = [&](int c, char* stage) __attribute__((always_inline)) {
-        const int nt = min(kC, Tn - c * kC);
-        const long long row0 = (long long)(T0 + c * kC) * H + h;
-        const char* rec = reinterpret_cast<const char*>(p.ws + ((size_t)(gc0 + c) * H + h) * kLaneChunkFloats);
-        if (nt == kC) {
-#pragma unroll
-            for (int part = 0; part < 2; ++part) {
-                const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
-                char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ);
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int g = 2 * jj + wv;
-                    load_to_lds(base + kq_off[jj], dst + pair_base(g) + kq_group_off(g));
+                for (int pi = 0; pi < kNS; ++pi)
+                    *reinterpret_cast<u32x4*>(stage1 + ColStage::kP + 1024 * (6 * pi + WV + 2 * jj) + 16 * lane) =
+                        (u32x4){0u, 0u, 0u, 0u};
+            issue(0);
+            direct(0, stage0);
+            put_t(stage0);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(min(1, nch - 1));
+            sync();
+            for (int c = 0; c < nch; ++c) {
+                char* cur = (c & 1) ? stage1 : stage0;
+                char* nxt = (c & 1) ? stage0 : stage1;
+                if (c + 1 < nch) {
+                    direct(c + 1, nxt);
+                    put_t(nxt);
+                    __builtin_amdgcn_sched_barrier(0);      // the T requests stay after the direct loads
+                    issue(min(c + 2, nch - 1));
                 }
+                put_p(cur);
+                sync();
             }
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-                load_to_lds(reinterpret_cast<const char*>(Vg + row0 * kDv) + v_off[jj],
-                            stage + ColStage::kV + 1024 * wv + 2048 * jj);
-        } else {
-#pragma unroll
-            for (int part = 0; part < 2; ++part) {
-                const char* base = reinterpret_cast<const char*>((part == 0 ? Kg : Qg) + row0 * kDk);
-                char* dst = stage + (part == 0 ? ColStage::kK : ColStage::kQ);
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int g = 2 * jj + wv, row = 4 * g + (lane >> 4), u = lane & 15;
-                    load_to_lds(base + 2 * ((long long)min(row, nt - 1) * H * kDk + 8 * (u ^ (4 * (row & 3)))),
-                                dst + pair_base(g) + kq_group_off(g));
-                }
-            }
-            const char* vbase = reinterpret_cast<const char*>(Vg + row0 * kDv);
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int tok = 16 * (2 * jj + wv) + (lane >> 2);
-                load_to_lds(vbase + 2 * ((long long)min(tok, nt - 1) * H * kDv + col0 + 8 * (lane & 3)),
-                            stage + ColStage::kV + 1024 * wv + 2048 * jj);
-            }
-        }
-        if (wv == 0) load_to_lds(rec + 4 * kLaneCoefOff + 16 * lane, stage + ColStage::kCf);
-    };
-    // all of chunk c's stage: the T / P loads first, so that their wait leaves the direct loads in flight
-    auto fill_stage = [&](int c, char* stage) __attribute__((always_inline)) {
-        f32x4 tp[2][3][2];
-        tp_issue(c, tp);
-        stage_loads(c, stage);
-        tp_store(stage, tp);
-    };
-
-    // Waves 2 and 3 only load: every stage's direct loads are theirs (a direct load holds its issuing wave for ~90
-    // cycles, which on the two computing waves would add up to a third of a chunk). All four waves meet at the one
-    // barrier per chunk: after it, stage c is complete and stage c-1 is free for chunk c+1.
-    if (ct >= 2) {
-        fill_stage(0, stage0);
-        __syncthreads();
-        for (int c = 0; c < nch; c += 2) {
-            if (c + 1 < nch) fill_stage(c + 1, stage1);
-            __syncthreads();
-            if (c + 1 < nch) {
-                if (c + 2 < nch) fill_stage(c + 2, stage0);
-                __syncthreads();
-            }
-        }
+        };
+        if (ct == 2) loader(std::integral_constant<int, 0>{});
+        else loader(std::integral_constant<int, 1>{});
         return;
     }
 
@@ -245,10 +283,38 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
         for (int i = 0; i < 4; ++i) st[a2][i] = Sg[(long long)(16 * a2 + 4 * q + i) * kDv];
     __syncthreads();                                      // waits for this wave's loads; then both waves' are in LDS
 
-    // o^T of the previous chunk, stored one chunk late: lane (q, r) of tile a holds token 16a + r, columns
-    // 16 (wave & 1) + 4q .. +3
-    f32x4 o[4];
-    auto store_out = [&](int c) __attribute__((always_inline)) {
+    // o^T of chunk c is formed during chunk c+1 (its P is computed by the loading waves during chunk c, from chunk c's
+    // stage) and stored at once: lane (q, r) of tile a holds token 16a + r, columns 16 (wave & 1) + 4q .. +3. What
+    // it needs from chunk c is kept in registers: (Q S)^T, vn's pieces and exp(G) of the lane's tokens.
+    f32x4 qs_prev[4];
+    u32x4 vb_prev[2][kNS];
+    float egt_prev[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        qs_prev[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        egt_prev[a] = 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int pi = 0; pi < kNS; ++pi) vb_prev[k][pi] = (u32x4){0u, 0u, 0u, 0u};
+    // o of chunk c (its P in stage `pst`), stored to chunk c's rows
+    auto out_chunk = [&](int c, const char* pst) __attribute__((always_inline)) {
+        f32x4 o[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[a][i] = egt_prev[a] * qs_prev[a][i];
+#pragma unroll
+            for (int k = 0; k <= (a >> 1); ++k) {
+                u32x4 pb[kTP];
+#pragma unroll
+                for (int pi = 0; pi < kTP; ++pi)
+                    pb[pi] = *reinterpret_cast<const u32x4*>(pst + ColStage::kP + 1024 * (6 * pi + pair_of(a, k)) +
+                                                             16 * lane);
+                o[a] = mma(vb_prev[k], pb, o[a]);
+            }
+        }
         const int nt = min(kC, Tn - c * kC);
         float* orow = p.out + ((long long)(T0 + c * kC + r) * H + h) * kDv + col0 + 16 * (ct & 1) + 4 * q;
         if (nt == kC) {
@@ -261,20 +327,20 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
         }
     };
 
-    // one chunk on stage `cur` (chunk c), filling stage `nxt` with chunk c+1
-    auto step = [&](int c, const char* cur, char* nxt) __attribute__((always_inline)) {
-        (void)nxt;
-        if (c > 0) store_out(c - 1);
+    // one chunk on stage `cur` (chunk c); the o of chunk c-1 from stage `prv` (for c = 0: zeros into chunk 0's rows,
+    // which chunk 0's own o overwrites later)
+    auto step = [&](int c, const char* cur, const char* prv) __attribute__((always_inline)) {
+        out_chunk(max(c - 1, 0), prv);
         // this chunk's coefficients and values, read before they are needed
         const float* cf = reinterpret_cast<const float*>(cur + ColStage::kCf);
         const uint16_t* vs = reinterpret_cast<const uint16_t*>(cur + ColStage::kV);
         f32x4 be[4], eg[4], er[4];
-        float vv[4][4], egt[4];             // egt: exp(G) of token 16a + r (the rows of o^T's lane)
+        float vv[4][4];
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
             be[a] = *reinterpret_cast<const f32x4*>(cf + 16 * a + 4 * q);
             eg[a] = *reinterpret_cast<const f32x4*>(cf + 2 * kC + 16 * a + 4 * q);
-            egt[a] = cf[2 * kC + 16 * a + r];
+            egt_prev[a] = cf[2 * kC + 16 * a + r];          // exp(G) of token 16a + r, for this chunk's o
             er[a] = *reinterpret_cast<const f32x4*>(cf + 3 * kC + 16 * a + 4 * q);
 #pragma unroll
             for (int i = 0; i < 4; ++i) vv[a][i] = to_f32(vs[(16 * a + 4 * q + i) * kCols + 16 * ct + r]);
@@ -282,9 +348,9 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
         const float glast = cf[2 * kC + kC - 1];
 
         // ---- X = K S (B: the state, in perm_k order of its rows) and (Q S)^T (A: the same state pieces)
-        f32x4 x[4], qs[4];
+        f32x4 x[4];
 #pragma unroll
-        for (int a = 0; a < 4; ++a) x[a] = qs[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int a = 0; a < 4; ++a) x[a] = qs_prev[a] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kd = 0; kd < 4; ++kd) {
             u32x4 sb[kNS];
@@ -294,7 +360,7 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
                 const u32x4 ka[1] = {row_operand(cur + ColStage::kK, 16 * a + r, kd, q)};
                 x[a] = mma(ka, sb, x[a]);
                 const u32x4 qb[1] = {row_operand(cur + ColStage::kQ, 16 * a + r, kd, q)};
-                qs[a] = mma(sb, qb, qs[a]);
+                qs_prev[a] = mma(sb, qb, qs_prev[a]);
             }
         }
 
@@ -324,11 +390,11 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
             }
         }
 
-        // ---- o^T = (Q S)^T diag(e^G) + vn^T P^T; S = e^{G_last} S + K^T (e^{G_last - G} vn)
-        u32x4 vb[2][kNS], vq[2][kNS];
+        // ---- S = e^{G_last} S + K^T (e^{G_last - G} vn); vn's pieces kept for this chunk's o
+        u32x4 vq[2][kNS];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            pair_pieces(vn[2 * k], vn[2 * k + 1], vb[k]);
+            pair_pieces(vn[2 * k], vn[2 * k + 1], vb_prev[k]);
             f32x4 w0, w1;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -336,20 +402,6 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
                 w1[i] = er[2 * k + 1][i] * vn[2 * k + 1][i];
             }
             pair_pieces(w0, w1, vq[k]);
-        }
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[a][i] = egt[a] * qs[a][i];
-#pragma unroll
-            for (int k = 0; k <= (a >> 1); ++k) {
-                u32x4 pb[kTP];
-#pragma unroll
-                for (int pi = 0; pi < kTP; ++pi)
-                    pb[pi] = *reinterpret_cast<const u32x4*>(cur + ColStage::kP + 1024 * (6 * pi + pair_of(a, k)) +
-                                                             16 * lane);
-                o[a] = mma(vb[k], pb, o[a]);
-            }
         }
 #pragma unroll
         for (int a2 = 0; a2 < 8; ++a2)
@@ -361,14 +413,15 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
                 const u32x4 kt[1] = {kt_operand(cur + ColStage::kK, a2, k, lane)};
                 st[a2] = mma(kt, vq[k], st[a2]);
             }
-        // the loading waves have completed stage c+1 and this wave is done with stage `cur`, which they refill next
+        // the loading waves have completed stage c+1 and chunk c's P, and this wave is done with stage `prv`, which
+        // they refill next
         __syncthreads();
     };
     for (int c = 0; c < nch; c += 2) {
         step(c, stage0, stage1);
         if (c + 1 < nch) step(c + 1, stage1, stage0);
     }
-    store_out(nch - 1);
+    out_chunk(nch - 1, (nch - 1) & 1 ? stage1 : stage0);
 #pragma unroll
     for (int a2 = 0; a2 < 8; ++a2)
 #pragma unroll
