@@ -180,7 +180,8 @@ size_t rk_paged_prefill_workspace_bytes(int n_slots, int Hkv, int D);
  *   cu_chunks (device int32 [n_seqs + 1]) = prefix sums of ceil(len_i / 64), total_chunks = cu_chunks[n_seqs].
  *   State of sequence i: S + idx * s_stride (elements), [H, dk, dv] fp32, read as the initial state and
  *   overwritten with the final state; idx = seq_index[i] (device int32 [n_seqs]) or i when seq_index is NULL.
- *   workspace: rk_gated_delta_workspace_bytes(total_chunks, H) bytes (per-chunk coefficients and T); no zeroing.
+ *   workspace: rk_gated_delta_workspace_bytes(total_chunks, H) bytes (per-chunk coefficients and T, and for fp32
+ *   inputs P); no zeroing.
  * dk = dv = 128. fp32-level results: fp32 operands enter the bf16 MFMA as exact three-piece splits. */
 size_t rk_gated_delta_workspace_bytes(int total_chunks, int H);
 int rk_gated_delta_chunked(float* out, float* S, long long s_stride, const void* q, const void* k, const void* v,
