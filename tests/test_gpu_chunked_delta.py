@@ -132,3 +132,33 @@ def test_config4_full_size(backend):
     eo, es = rel_err(o, wo), rel_err(S, ws)
     print(f"config 4: 4 x 4096 tokens, 16 heads: out {eo:.2e}, state {es:.2e}")
     assert torch.isfinite(o).all() and eo < TOL and es < TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_many_short_ragged_sequences(backend, dtype):
+    """40 sequences of 0 .. 150 tokens (single-chunk and partial-chunk sequences everywhere, empty ones between):
+    the bf16 scan's loading waves repeat a short chunk's last K / Q / V row and compute P from those rows."""
+    lens = [int(x) for x in np.random.default_rng(21).integers(0, 151, size=40)]
+    lens[3] = lens[17] = 0
+    lens[5], lens[6] = 1, 64
+    case = wl.chunked_delta_case(lens, H=2, dtype=dtype, seed=22, state_scale=0.1)
+    o, S = gpu_run(backend, case)
+    wo, ws = oracle_run(case)
+    eo, es = rel_err(o, wo), rel_err(S, ws)
+    print(f"40 ragged sequences {dtype}: out {eo:.2e}, state {es:.2e}")
+    assert torch.isfinite(o).all() and eo < TOL and es < TOL
+    assert torch.equal(S[3], case.S[3]) and torch.equal(S[17], case.S[17])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_workspace_needs_no_clearing(backend, dtype):
+    """The per-chunk workspace is written in full by the prep before the scan reads it: a workspace holding NaN
+    bytes and one holding zeros give the same bits."""
+    from native import kernels
+    case = wl.chunked_delta_case([70, 129, 1, 64], H=4, dtype=dtype, seed=23, state_scale=0.1)
+    runs = []
+    for fill in (0xFF, 0x00):
+        kernels.workspace(torch.device(DEV), 16 << 20).fill_(fill)   # the buffer the launch reuses (> its need)
+        runs.append(gpu_run(backend, case))
+    assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])
+    assert torch.isfinite(runs[0][0]).all()
