@@ -19,10 +19,10 @@ namespace {
 // columns in one MFMA dimension and 64 tokens (or 128 state rows) in the other. Every operand that is a product of
 // the chunk (the state, Y, vn) is an accumulator pair of the product before, read in the k order perm_k (see
 // pair_of), so no value moves between lanes. K rows, Q rows, T, P (and K^T, by transposed reads of the K rows) come
-// from an LDS stage shared by the workgroup: waves 0 and 1 compute (32 columns), waves 2 and 3 fill the stage of
-// chunk c+1 by global_load_lds_dwordx4 (1 KB per instruction, no registers) while chunk c is computed; one barrier
-// per chunk hands the two stages over. The output of a chunk (o^T: 16-byte rows of 4 columns per lane) is stored at
-// the start of the next chunk, so the wait before a barrier never waits for fresh stores.
+// from an LDS stage shared by the workgroup: waves 0 and 1 compute (32 columns); waves 2 and 3 fill the stage of
+// chunk c+1 (K, Q, V rows by global_load_lds_dwordx4, 1 KB per instruction, no registers; T split into pieces) and
+// form chunk c's P while chunk c is computed; one barrier per chunk hands the two stages over. The output of chunk c
+// (o^T: 16-byte rows of 4 columns per lane) is formed and stored at the start of chunk c+1, when its P is ready.
 // K and Q rows: 16 groups of 4 rows (one 1 KB direct load each); the K and Q groups g share a 2 KB pair at
 // pair_base(g), each at an offset kq_group_off(g) (see kq_unit).
 __host__ __device__ constexpr int pair_base(int g) { return 2048 * g + 256 * (g >> 1); }
