@@ -43,8 +43,9 @@ static_assert(pair_base(15) + 2048 + kq_group_off(15) <= ColStage::kT, "the K / 
 // row >> 2 stores unit u at slot u ^ 4t. So:
 //  - a row operand's two 8-byte halves (units 4kd + j and 4kd + 2 + j, j < 2; 4t never has bit 1) are always 32
 //    bytes apart, one ds_read2_b64 into the operand's four registers;
-//  - the 16 rows of a row-operand read sit on 16 distinct 16-byte slots of the 256-byte bank line (slot 4t^u within a
-//    group, the groups 0 / 2 / 1 / 3 slots apart), and so do the 8 rows x 32 bytes of a transposed read.
+//  - the 8 rows x 32 bytes of a transposed read sit on distinct 16-byte slots of the 256-byte bank line (slot 4t^u
+//    within a group, the groups 0 / 2 / 1 / 3 slots apart). Row-operand reads see 2-way bank conflicts (counters),
+//    which measured no time: the computing waves' issue bounds the kernel.
 __device__ __forceinline__ int kq_unit(int row, int u) {
     const int g = row >> 2, t = row & 3;
     return pair_base(g) + kq_group_off(g) + 256 * t + 16 * (u ^ (4 * t));
