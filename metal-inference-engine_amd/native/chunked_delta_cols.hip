@@ -217,11 +217,14 @@ __global__ __launch_bounds__(256) void delta_chunk_scan_cols(DeltaArgs p) {
                     for (int hb = 0; hb < 2; ++hb) {
                         const int b = 2 * kKs[jj] + hb;
                         f32x4 pq = {0.f, 0.f, 0.f, 0.f};
+                        // operands as one 16-byte read of dims 32 kd + 8q .. +7 per lane (the same k order on both
+                        // sides; fewer bank conflicts than the computing waves' paired reads)
                         if (b <= a)
 #pragma unroll
                             for (int kd = 0; kd < 4; ++kd)
-                                pq = mfma16x16x32(row_operand(stage + ColStage::kK, 16 * b + r, kd, q),
-                                                  row_operand(stage + ColStage::kQ, t, kd, q), pq);
+                                pq = mfma16x16x32(
+                                    *reinterpret_cast<const u32x4*>(stage + ColStage::kK + kq_unit(16 * b + r, 4 * kd + q)),
+                                    *reinterpret_cast<const u32x4*>(stage + ColStage::kQ + kq_unit(t, 4 * kd + q)), pq);
                         const f32x4 gk = *reinterpret_cast<const f32x4*>(gr + 16 * b + 4 * q);
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
