@@ -7,8 +7,10 @@
 //
 // Design (split over positions, then a merge):
 //   * Work unit = one 16-position tile of one sequence. The tiles of the whole batch, in (sequence, tile) order,
-//     are cut into NW equal contiguous ranges (stream-K): workgroup w takes global tiles [U w / NW, U (w + 1) / NW)
-//     of the U in all, so every workgroup streams the same number of tiles however unequal the lengths are. A range
+//     are cut into NW contiguous ranges of equal cost (stream-K): a tile costs one unit and each sequence kSegCost
+//     more (its segment's combine and restart); workgroup w takes cost units [Uc w / NW, Uc (w + 1) / NW) of the Uc
+//     in all, so every workgroup does the same work however unequal the lengths are (with under kSegMinTiles tiles
+//     per workgroup, tiles [U w / NW, U (w + 1) / NW) of the U in all). A range
 //     may cross sequence boundaries; the workgroup writes one partial (m, l, acc) per kv-head for each sequence it
 //     touches, into slot w + b (unique: a later workgroup never touches an earlier sequence). NW is sized so that
 //     the whole grid is resident at once (no second wave of workgroups).
@@ -109,30 +111,45 @@ __device__ __forceinline__ long long kv_row(const int32_t* table, int s, int bs,
     return ((long long)(blk * (long long)bs + s % bs) * Hkv + kvh) * D;
 }
 
+// Cost units a sequence adds to a split workgroup's range besides its tiles: a segment ends with a combine of the
+// groups' states, a partial record and a query restage, and its first tiles wait on a new block-table row. Per
+// workgroup that costs about as much as streaming a few more tiles (at batch 64 the split kernel measured 100.8 /
+// 98.4 / 98.0 / 98.9 / 99.7 µs at 0 / 2 / 4 / 5 / 6 units). The ranges are cut by cost only when the workgroups
+// average at least kSegMinTiles tiles; with a tile or two per group (batch 1, small batches) a whole cost unit is
+// too coarse, and the ranges are cut by tiles.
+constexpr int kSegCost = 4;
+constexpr int kSegMinTiles = 16;
+
 // Tile prefix sums, computed by one wave: P[0] = 0, P[b + 1] = P[b] + units(b); with Ls, also Ls[b] = the clamped
-// length of sequence b. Returns U = P[B] (all tiles).
-__device__ int plan_prefix(const DecodeArgs& a, int* P, int* Ls = nullptr) {
+// length of sequence b; with V, the same sums in cost units, V[b + 1] = V[b] + units(b) + (units(b) > 0 ? kSegCost
+// : 0). Returns U = P[B] (all tiles).
+__device__ int plan_prefix(const DecodeArgs& a, int* P, int* Ls = nullptr, int* V = nullptr) {
     const int lane = threadIdx.x & 63;
-    int carry = 0;
+    int carry = 0, vcarry = 0;
     for (int b0 = 0; b0 < a.B; b0 += 64) {
         const int b = b0 + lane;
         const SeqRange sr = b < a.B ? seq_range(a, b) : SeqRange{0, 0, 0, 0};
         if (Ls && b < a.B) Ls[b] = sr.L;
-        int x = sr.units;
+        int x = sr.units, y = sr.units + (sr.units > 0 ? kSegCost : 0);
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(x, off);
-            if (lane >= off) x += y;
+            const int xu = __shfl_up(x, off), yu = __shfl_up(y, off);
+            if (lane >= off) { x += xu; y += yu; }
         }
         if (b < a.B) P[b + 1] = carry + x;
+        if (V && b < a.B) V[b + 1] = vcarry + y;
         carry += __shfl(x, 63);
+        vcarry += __shfl(y, 63);
     }
-    if (lane == 0) P[0] = 0;
+    if (lane == 0) {
+        P[0] = 0;
+        if (V) V[0] = 0;
+    }
     return carry;
 }
 
-// First global tile of workgroup w's range (U tiles over NW workgroups).
-__device__ __forceinline__ int range_lo(int U, int NW, int w) { return (int)((long long)U * w / NW); }
+// First cost unit of workgroup w's range (Uc cost units over NW workgroups).
+__device__ __forceinline__ int range_lo(int Uc, int NW, int w) { return (int)((long long)Uc * w / NW); }
 
 // Sequence of global tile g (0 <= g < P[B], g the same in every lane): the largest b in [0, B) with P[b] <= g,
 // which has P[b + 1] > g. P is non-decreasing from P[0] = 0, so b = #{b' in [1, B) : P[b'] <= g}: one ballot per 64
@@ -145,6 +162,16 @@ __device__ __forceinline__ int seq_of_tile(const int* P, int B, int g) {
         b += __popcll(__ballot(bb < B && P[bb] <= g));
     }
     return b;
+}
+
+// Global tile at cost unit v (0 <= v <= V[B]): sequence b's cost units [V[b], V[b + 1]) are its kSegCost segment
+// units, which all map to its first tile, then one unit per tile. Non-decreasing in v, P[B] at v = V[B], and a
+// sequence's first tile maps back from cost unit V[b] + kSegCost.
+__device__ __forceinline__ int tile_at(const int* P, const int* V, int B, int v) {
+    const int b = seq_of_tile(V, B, v);
+    const int n = P[b + 1] - P[b], c = n > 0 ? kSegCost : 0;
+    const int t = v - V[b] - c;
+    return P[b] + (t < 0 ? 0 : (t > n ? n : t));
 }
 
 template <typename T>
@@ -214,8 +241,9 @@ struct KVLoad<float> {
     }
 };
 
-// LDS bytes of the per-sequence plan of a split workgroup: tile prefix sums [B + 1] and clamped lengths [B].
-constexpr int seq_lds_bytes(int B) { return ((2 * B + 1) * 4 + 15) & ~15; }
+// LDS bytes of the per-sequence plan of a split workgroup: tile prefix sums [B + 1], clamped lengths [B] and cost
+// prefix sums [B + 1].
+constexpr int seq_lds_bytes(int B) { return ((3 * B + 2) * 4 + 15) & ~15; }
 
 // LDS bytes one wave of the split kernel uses: the query A operands (NT x NIT x 64 lanes x 16 B), the 16 x GP
 // probabilities of the current tile and the GP rescale factors.
@@ -318,6 +346,7 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 
     int* P = reinterpret_cast<int*>(smem);          // tile prefix sums [B + 1]
     int* Ls = P + a.B + 1;                           // clamped lengths [B]
+    int* V = Ls + a.B;                               // cost prefix sums [B + 1]
     char* wl = smem + seq_lds_bytes(a.B) + wave * wave_lds_bytes<D, GP>();
     u32x4* qop = reinterpret_cast<u32x4*>(wl);
     float* p_lds = reinterpret_cast<float*>(wl + NT * NIT * 64 * 16);
@@ -332,11 +361,13 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < NT * NIT; ++i) qop[i * 64 + lane] = u32x4{0u, 0u, 0u, 0u};
     };
-    if (wave == 0) plan_prefix(a, P, Ls);
+    if (wave == 0) plan_prefix(a, P, Ls, V);
     zero_q();
     __syncthreads();
-    const int U = P[a.B];
-    const int lo = range_lo(U, a.NW, w), hi = range_lo(U, a.NW, w + 1);
+    const int U = P[a.B], Uc = V[a.B];
+    const bool by_cost = U >= kSegMinTiles * a.NW;   // uniform: U and NW are the same in every workgroup
+    const int lo = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w)) : range_lo(U, a.NW, w);
+    const int hi = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w + 1)) : range_lo(U, a.NW, w + 1);
     if (lo >= hi) return;                            // uniform over the workgroup: no barrier is left waiting
     const int bA = seq_of_tile(P, a.B, lo), bZ = seq_of_tile(P, a.B, hi - 1);
 
@@ -664,9 +695,10 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     }
 }
 
-// One workgroup per (sequence, kv-head). Sequence b owns global tiles [P[b], P[b + 1]); the split workgroups whose
-// ranges meet it are w_first = the one holding tile P[b] .. w_last = the one holding tile P[b + 1] - 1 (empty ranges
-// in between, possible only when NW > U, are skipped), with partials in slots w + b. The workgroup's threads form SL
+// One workgroup per (sequence, kv-head). Sequence b owns global tiles [P[b], P[b + 1]), cost units V[b] + kSegCost ..
+// V[b + 1] - 1; the split workgroups whose ranges meet it are w_first = the one holding the unit (cost unit or tile,
+// as the split kernel cut the ranges) of tile P[b] .. w_last = the one holding its last unit (empty ranges in between,
+// possible only when NW exceeds the units, are skipped), with partials in slots w + b. The workgroup's threads form SL
 // slices of TS threads (TS = GP * D / 4, one float4 output of the GP x D block each); with n partials, the first
 // min(SL, ceil(n / kMergeCh)) slices take consecutive runs of them, so a sequence over many partials (few
 // sequences, many split workgroups) needs up to SL times fewer memory round trips. Within a slice the partials are combined in workgroup order, up to kMergeCh per
@@ -682,7 +714,7 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
     static_assert(TS <= kMergeThreads && kMergeThreads % TS == 0, "slices tile the workgroup");
     constexpr int REC = GP * D + 2 * GP;
     constexpr int kMergeCh = 8;                       // partials combined per memory round trip
-    __shared__ int P[kMaxBatch + 1];
+    __shared__ int P[kMaxBatch + 1], V[kMaxBatch + 1];
     __shared__ float4 num_s[SL > 1 ? SL - 1 : 1][TS];
     __shared__ float2 md_s[SL > 1 ? SL - 1 : 1][TS];  // (M, den)
     const int tid = threadIdx.x, sl = tid / TS, ti = tid % TS;
@@ -692,7 +724,7 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
     const float* grow = a.gate ? a.gate + (long long)b * a.gate_ld + (long long)kvh * a.G * D : nullptr;
     const float4 gv = sl == 0 && grow && ti < n4 ? *reinterpret_cast<const float4*>(grow + 4 * ti)
                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < 64) plan_prefix(a, P);
+    if (tid < 64) plan_prefix(a, P, nullptr, V);
     __syncthreads();
     const int U = P[a.B], pb = P[b], pe = P[b + 1];
     float4* out = reinterpret_cast<float4*>(a.out + obase);
@@ -700,8 +732,11 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
         if (sl == 0 && ti < n4) out[ti] = make_float4(0.f, 0.f, 0.f, 0.f);
         return;
     }
-    const int wf = (int)(((long long)(pb + 1) * a.NW - 1) / U);
-    const int wlast = (int)(((long long)pe * a.NW - 1) / U);
+    // the split workgroups' units (cost units or tiles, as the split kernel cut them), the first and last units of b
+    const bool by_cost = U >= kSegMinTiles * a.NW;
+    const int Uu = by_cost ? V[a.B] : U, u0 = by_cost ? V[b] + kSegCost : pb, u1 = by_cost ? V[b + 1] : pe;
+    const int wf = (int)(((long long)(u0 + 1) * a.NW - 1) / Uu);
+    const int wlast = (int)(((long long)u1 * a.NW - 1) / Uu);
     // slices in use: one per chunk of partials, up to SL (the rest hold none); partials per slice
     const int npart = wlast - wf + 1;
     const int slr = min(SL, (npart + kMergeCh - 1) / kMergeCh);
@@ -712,9 +747,9 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
     const int off = 4 * ic, hk = (4 * ic) / D;        // this thread's float4 output: element offset, head
     float M = -INFINITY, den = 0.0f;
     float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-    // a workgroup's range can be empty only when there are more split workgroups than tiles; otherwise every
-    // workgroup in [wf, wlast] holds a partial, and no range has to be recomputed per partial
-    const bool sparse = a.NW > U;
+    // a workgroup's range in [wf, wlast] can be empty only when there are more split workgroups than units;
+    // otherwise every one of them holds a partial, and no range has to be recomputed per partial
+    const bool sparse = a.NW > Uu;
     for (int w0 = s_first; w0 <= s_last; w0 += kMergeCh) {
         float4 v[kMergeCh];
         float mj[kMergeCh], lj[kMergeCh];
@@ -731,7 +766,7 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
 #pragma unroll
         for (int j = 0; j < kMergeCh; ++j) {
             const int wj = w0 + j;
-            use[j] = wj <= s_last && (!sparse || range_lo(U, a.NW, wj + 1) > range_lo(U, a.NW, wj));
+            use[j] = wj <= s_last && (!sparse || range_lo(Uu, a.NW, wj + 1) > range_lo(Uu, a.NW, wj));
         }
         float mx = M;
 #pragma unroll

@@ -143,3 +143,24 @@ def test_stale_workspace_is_never_read(backend):
     got = gpu(backend, case, gate=True)
     assert torch.isfinite(got).all()
     assert rel_err(got, oracle(case, gate=True)) < 1e-5
+
+
+def test_ranges_cut_by_cost_with_empty_and_short_sequences(backend):
+    """With at least 16 tiles per split workgroup the ranges are cut by cost (tiles plus a fixed cost per sequence):
+    here 20 sequences with empty, 1-33-position and long ones between each other, ~4,700 tiles over 256 workgroups.
+    The merge must find each sequence's workgroups under that cut, skip the ones whose range holds only another
+    sequence's cost units, and never read a slot no workgroup wrote (the workspace is NaN-filled first)."""
+    from native import kernels
+    lens = [0, 9000, 1, 0, 7000, 17, 0, 12000, 300, 0, 9000, 16, 8192, 0, 2, 11000, 33, 0, 9500, 5]
+    assert sum((n + 15) // 16 for n in lens) >= 16 * 256
+    case = wl.paged_decode_case(lens, 6000, 8, 2, 256, 16, torch.bfloat16, seed=19)
+    c = case.to(DEV)
+    need = backend.lib.lib.rk_paged_decode_workspace_bytes(len(lens), 8, 2, 256, 16, c.tables.shape[1])
+    kernels.workspace(c.q.device, need).view(torch.float32).fill_(float("nan"))
+    got = gpu(backend, case, gate=True)
+    assert torch.isfinite(got).all()
+    live = [i for i, n in enumerate(lens) if n > 0]        # the oracle, like ops.attention, needs a key
+    assert torch.equal(got[[i for i, n in enumerate(lens) if n == 0]], torch.zeros(lens.count(0), 8, 256))
+    sub = wl.PagedDecodeCase(case.q[live], case.gate[live], case.k_pool, case.v_pool, case.tables[live],
+                             case.lens[live], case.block_size)
+    assert rel_err(got[live], oracle(sub, gate=True)) < 1e-5
