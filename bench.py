@@ -17,7 +17,8 @@ each decode kernel's own access pattern with no arithmetic (librk_probe.so).
 
 Other workloads print the same record for: c1, the config-1 decode (parity/latency case); c2, the config-2 DeltaNet
 decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache); c4, the config-4
-chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention; lp, the
+chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention (c5f: the
+same batch in fp32, on the fp32-operand kernel); lp, the
 DeltaNet prefill companions (fused conv / norms / beta, g front and the gated RMSNorm) on the config-4 batch; ap,
 the config-3 decode attention layer with its q / k norm, RoPE and KV write (rk_attn_prep) in front; wd, the
 sliding-window decode (window 4096) through the grouped pool's rings; mv, every linear of a Qwen3.5-2B decode step at
@@ -338,16 +339,20 @@ def bench_deltanet(args, backend):
     }
 
 
-def bench_prefill(args, backend, chunk: bool = False):
+FP32_MFMA_PEAK_TFLOPS = 157.3     # MI355X dense fp32 matrix peak
+
+
+def bench_prefill(args, backend, chunk: bool = False, fp32: bool = False):
     """Config 5 (chunk False), or one 512-token chunk over a 32,768-token history (chunk True: the grid without
-    split key ranges would fill 32 of 256 CUs)."""
+    split key ranges would fill 32 of 256 CUs). fp32: config 5's batch in the Qwen3.5 engine's own fp32 pool and
+    activations, which runs on the fp32-operand kernel (fp32 MFMA), priced against the fp32 matrix peak."""
     import torch
     import workloads as wl
     from native import kernels
     dev = backend.device
     stream = torch.cuda.current_stream(dev)
-    case = wl.chunk_prefill() if chunk else wl.c5_prefill()
-    tag = "ck" if chunk else "c5"
+    case = wl.chunk_prefill() if chunk else wl.c5_prefill(dtype=torch.float32 if fp32 else torch.bfloat16)
+    tag = "ck" if chunk else ("c5f" if fp32 else "c5")
     c = case.to(dev)
     torch.cuda.synchronize()
 
@@ -359,7 +364,8 @@ def bench_prefill(args, backend, chunk: bool = False):
     flops = case.flops()
     tflops = flops / (ms * 1e-3) / 1e12
     N = case.q.shape[0]
-    log(f"[bench] {tag}: {ms * 1e3:.1f} us per packed prefill, {tflops:.1f} TFLOP/s")
+    peak = FP32_MFMA_PEAK_TFLOPS if fp32 else 2500.0
+    log(f"[bench] {tag}: {ms * 1e3:.1f} us per packed prefill, {tflops:.1f} TFLOP/s ({tflops / peak:.1%} of peak)")
     cpu = None
     if not args.no_cpu:
         from oracle import prefill_ref
@@ -383,6 +389,22 @@ def bench_prefill(args, backend, chunk: bool = False):
                          f"flops"}
     work, n_slots = kernels.prefill_work(case.lengths(), case.starts, None, True, kernels.PREFILL_SPLIT_TILES,
                                          case.k_pool.shape[2], kernels.device_cus(dev))
+    if fp32:
+        return {
+            "metric": "packed prefill attention tokens/s (config 5 batch, fp32 pool and activations) + TFLOP/s "
+                      "(% of fp32 MFMA peak), 1 GPU",
+            "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded)",
+            "config": {"workload": "config 5's batch with the fp32 pool, q, new K/V and gate of the Qwen3.5 engine "
+                                   "(src/models/qwen3_5.py:70-71): 8 packed segments, 8/2 heads x 256, block 16, "
+                                   "causal, gate, KV write-back; fp32 operands (fp32 MFMA)",
+                       "new_tokens": N, "flops": flops},
+            "roofline": {"bound": "mfma", "achieved": tflops, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tflops / FP32_MFMA_PEAK_TFLOPS, "traffic": traffic_for("prefill_attention_f32/c5f"),
+                         "kernel": "prefill_attention_f32 (+ prefill_kv_write)", "avg_ms": ms},
+            "cpu_baseline": cpu,
+        }
     if chunk:
         return {
             "metric": "chunked-prefill attention tokens/s (512 new on 32,768 cached) + TFLOP/s, 1 GPU",
@@ -853,7 +875,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c4", "c5", "ck", "lp", "ap", "wd", "mv", "ds"],
+                    choices=["all", "c1", "c2", "c3", "c4", "c5", "c5f", "ck", "lp", "ap", "wd", "mv", "ds"],
                     help="all (default): the config-3 headline record with configs 1, 2, 4, 5 as sub-records and "
                          "the measured access-pattern ceilings")
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
@@ -908,7 +930,8 @@ def main() -> int:
         subs = {}
         for name, fn in (("c1", c1), ("c2", lambda: bench_deltanet(args, backend)),
                          ("c4", lambda: bench_chunked_delta(args, backend)),
-                         ("c5", lambda: bench_prefill(args, backend))):
+                         ("c5", lambda: bench_prefill(args, backend)),
+                         ("c5_fp32", lambda: bench_prefill(args, backend, fp32=True))):
             sub = fn()
             subs[name] = {k: v for k, v in sub.items() if k in keep}
             torch.cuda.empty_cache()
@@ -929,6 +952,8 @@ def main() -> int:
         rec["metric"] = "sliding-window decode attn tokens/s @ batch 64 (grouped pool rings) + achieved HBM GB/s, 1 GPU"
     elif args.workload == "c5":
         rec = bench_prefill(args, backend)
+    elif args.workload == "c5f":
+        rec = bench_prefill(args, backend, fp32=True)
     elif args.workload == "ck":
         rec = bench_prefill(args, backend, chunk=True)
     elif args.workload == "c4":

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 13
+#define RK_ABI_VERSION 14
 
 /* status codes */
 #define RK_OK 0
@@ -151,10 +151,16 @@ int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float
  *   first .. first + pieces - 1 (unique, < n_slots): each piece writes its (o, m, l) there and the last to finish
  *   combines them in piece order, so the output does not depend on the finishing order.
  *   n_slots 0: no splits (partials, counters may be NULL); else partials of rk_paged_prefill_workspace_bytes(n_slots,
- *   Hkv, D) bytes (no zeroing needed) and counters of n_slots * Hkv * 4 uint32, zero before the call; every call
- *   leaves them at zero.
- *   gate NULL or [N, Hq*D] in gate_dtype (RK_F32 or RK_BF16, read as stored). Group size Hq / Hkv = 4, D in {128, 256},
- *   max_nb * block_size^2 < 2^32. bf16 MFMA operands, fp32 accumulation.
+ *   Hq, D) bytes (no zeroing needed) and n_counters >= rk_paged_prefill_counters(n_slots, Hq) uint32 counters, zero
+ *   before the call; every call leaves them at zero.
+ *   gate NULL or [N, Hq*D] in gate_dtype (RK_F32 or RK_BF16, read as stored). Any group size Hq / Hkv, D in
+ *   {64, 128, 256}, max_nb * block_size < 2^31.
+ *   Operands: the reference computes in fp32 on widened inputs (src/ops.py:84-87, 91-103). exact = 0 with q and the
+ *   pool both bf16, group size 4, D in {128, 256}, block_size >= 2 and max_nb * block_size^2 < 2^32 (config 5)
+ *   takes bf16 MFMA
+ *   operands (q, K, V as stored, the probabilities rounded to bf16; fp32 accumulation): bf16-level results. Every other call (exact = 1, an fp32 q or
+ *   pool, other shapes) takes fp32 operands (fp32 MFMA, bf16 pool rows widened exactly, fp32 probabilities):
+ *   fp32-level results.
  *   window 0 or W >= 1 (causal only): query i also sees only positions above start[s] + i - W (the sliding-window
  *   prefill of src/models/cohere2.py:155-163; ops.attention's window, src/ops.py:77-81, 97-98); blocks wholly below
  *   every query's window are never read. causal 0: every query of segment s sees positions 0 .. start[s]+n[s]-1
@@ -165,11 +171,13 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
                      int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
-                     int window, int causal, int n_slots, float* partials, size_t partial_bytes, uint32_t* counters,
-                     void* stream);
+                     int window, int causal, int exact, int n_slots, float* partials, size_t partial_bytes,
+                     uint32_t* counters, size_t n_counters, void* stream);
 
-/* Bytes of rk_paged_prefill's partial records for n_slots split pieces (kv-heads Hkv, head_dim D). */
-size_t rk_paged_prefill_workspace_bytes(int n_slots, int Hkv, int D);
+/* Bytes of rk_paged_prefill's partial records, and the count of its arrival counters, for n_slots split pieces
+ * (query heads Hq, head_dim D). */
+size_t rk_paged_prefill_workspace_bytes(int n_slots, int Hq, int D);
+size_t rk_paged_prefill_counters(int n_slots, int Hq);
 
 /* ---- P3: chunked gated delta rule (64-token chunks, WY / UT form) for packed prefill of the linear-attention
  * layers. Replaces Backend.gated_delta with T > 1 (TorchBackend.gated_delta -> ops.gated_delta_chunked,
@@ -194,8 +202,9 @@ int rk_gated_delta_chunked(float* out, float* S, long long s_stride, const void*
  *
  * rk_causal_conv1d replaces Backend.causal_conv1d (ops.causal_conv1d, src/ops.py:127-139) for one segment:
  *   x: row t (t < T) at x + t * x_ld, C channels; tail [K-1, C] fp32; w [C, K] fp32 (tap K-1 multiplies the
- *   current token). hist = [tail rounded to x's dtype; x]; u [T, C] fp32 = silu(sum_j hist[t + j] * w[:, j]);
- *   new_tail [K-1, C] in x_dtype = the last K-1 rows of hist. 2 <= K <= 8.
+ *   current token). x is widened to fp32 first, as TorchBackend.causal_conv1d does (src/backend/torch_ref.py:49-50):
+ *   hist = [tail as stored; x widened]; u [T, C] fp32 = silu(sum_j hist[t + j] * w[:, j]);
+ *   new_tail [K-1, C] fp32 = the last K-1 rows of hist. 2 <= K <= 8.
  *
  * rk_deltanet_prefill_front fuses, for n_seqs packed segments (rows cu_seqlens[s] .. cu_seqlens[s+1]-1, device
  * int32 [n_seqs + 1]), the conv, the q/k/v split, l2norm (src/ops.py:115-117), q * 1/sqrt(dk), beta = sigmoid(b)
@@ -203,7 +212,8 @@ int rk_gated_delta_chunked(float* out, float* S, long long s_stride, const void*
  *   qkv / b / a: row n at ptr + n * ld (x_dtype; C = 2*H*dk + H*dv, H and H channels) -- the columns of the fused
  *   in_proj output; q, k [N, H, dk], v [N, H, dv], beta, g [N, H] fp32 (the inputs of rk_gated_delta_chunked).
  *   Segment s's conv tail is [K-1, C] fp32 at conv_state + seq_index[s] * conv_stride: read as the old tail and
- *   overwritten with the new one (in x's dtype, widened). seq_index NULL: zero tails, conv_state untouched.
+ *   overwritten with the new one (fp32: carried rows keep their bits, x rows widened; x widened before the conv as
+ *   TorchBackend.causal_conv1d does). seq_index NULL: zero tails, conv_state untouched.
  *   Indices of non-empty segments must be distinct. dk = dv = 128, 2 <= K <= 4; qkv and conv_state 8-byte (fp32) /
  *   4-byte (bf16) aligned with even strides.
  *
@@ -211,7 +221,7 @@ int rk_gated_delta_chunked(float* out, float* S, long long s_stride, const void*
  *   out [rows, dv] fp32 = x * (1 / sqrt(mean(x^2) + eps)) * w * silu(z); x [rows, dv] fp32, w [dv] fp32; row r of
  *   z at z + (r / z_group) * z_ld + (r % z_group) * dv (contiguous: z_group 1, z_ld dv). dv in {64, 128, 256, 512};
  *   x, out, w, z and z_ld aligned to dv / 64 elements. */
-int rk_causal_conv1d(float* u, void* new_tail, const void* x, int x_dtype, long long x_ld, const float* tail,
+int rk_causal_conv1d(float* u, float* new_tail, const void* x, int x_dtype, long long x_ld, const float* tail,
                      const float* w, int T, int C, int K, void* stream);
 int rk_deltanet_prefill_front(float* q, float* k, float* v, float* beta, float* g, const void* qkv, const void* b,
                               const void* a, int x_dtype, long long ld, float* conv_state, long long conv_stride,

@@ -9,7 +9,8 @@ Method -> kernel:
   paged_attention        rk_paged_decode   (P1; + optional fused sigmoid gate)
   attention, T == 1      rk_paged_decode on the contiguous cache viewed as one block (the reference's
                          attention_decode, src/backend/metal.py:197-210)
-  attention, T > 1       rk_paged_prefill on the same one-block view, no KV write (causal, optional window)
+  attention, T > 1       rk_paged_prefill on the same one-block view, no KV write (causal, optional window); fp32
+                         operands (fp32-level results) unless q, k and v are all bf16 at the bf16 kernel's shapes
   deltanet_decode[_batch] rk_deltanet_decode (P2; states of one HybridPool in one launch, a standalone state as a
                          pool of one, src/backend/metal.py:232-256)
   paged_prefill_attention rk_paged_prefill (P4; the packed prefill of full_attention, src/models/qwen3_5.py:112-120:
@@ -111,16 +112,18 @@ class RocmBackend:
 
     # ---- P4: packed prefill attention
     def paged_prefill_attention(self, q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
-                                gate=None, window=None):
+                                gate=None, window=None, exact=False):
         """Packed prefill of one attention layer for S segments: writes k_new / v_new [N, Hkv, d] into the pool
         layer at positions start_pos[s] + i of segment s (rows cu_seqlens[s] .. cu_seqlens[s+1]-1, block-table row
         s of tables [S, max_nb]), then causal attention of q [N, Hq, d] over each segment's prefix and new keys
         -> [N, Hq, d] fp32, times sigmoid(gate [N, Hq*d]) when given. The reference runs this per segment as
         kv.write -> kv.read -> attention(causal) -> gate (src/models/qwen3_5.py:112-120). With a window W each query
         sees its last W positions (the sliding layers' prefill, src/models/cohere2.py:155-163), and blocks below
-        every query's window are never read."""
+        every query's window are never read. The reference computes in fp32 (src/ops.py:84-87): an fp32 q or pool,
+        any group size but 4 or head_dim 64 run on fp32 operands (fp32-level results); bf16 q and pool at 4 query
+        heads per kv-head run on bf16 operands unless exact=True."""
         return kernels.paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
-                                     gate, window=window)
+                                     gate, window=window, exact=exact)
 
     # ---- P3: chunked gated delta rule
     def gated_delta(self, q, k, v, beta, g, S):
@@ -159,7 +162,8 @@ class RocmBackend:
     # ---- DeltaNet prefill companions
     def causal_conv1d(self, x, tail, w):
         """Backend.causal_conv1d (src/backend/base.py:44-45): x [T, C], tail [K-1, C], w [C, K] -> (silu(conv)
-        [T, C] fp32, new tail [K-1, C] in x's dtype), ops.causal_conv1d (src/ops.py:127-139)."""
+        [T, C] fp32, new tail [K-1, C] fp32): ops.causal_conv1d (src/ops.py:127-139) on x widened to fp32, as
+        TorchBackend.causal_conv1d does (src/backend/torch_ref.py:49-50)."""
         return kernels.causal_conv1d(x, tail, w)
 
     def rms_norm_gated(self, x, z, w, eps):

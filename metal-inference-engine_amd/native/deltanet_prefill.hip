@@ -2,9 +2,11 @@
 // packed prefill does besides the projections and the delta rule itself.
 //
 // Semantics (reference): per segment, src/models/qwen3_5.py:144-162 runs
-//   u, new_tail = ops.causal_conv1d(qkv, tail, conv_w)       (src/ops.py:127-139: hist = [tail.to(x.dtype); x],
+//   u, new_tail = b.causal_conv1d(qkv, tail, conv_w)         (TorchBackend, src/backend/torch_ref.py:49-50: x widened
+//                                                              to fp32 first, then src/ops.py:127-139: hist =
+//                                                              [tail; x] all fp32 (the fp32 tail as stored),
 //                                                              y_t = sum_j hist[t + j] * w[:, j], SiLU, new tail =
-//                                                              the last K-1 rows of hist)
+//                                                              the last K-1 rows of hist, fp32)
 //   q, k, v = split(u);  beta = sigmoid(b);  g = -exp(A_log) * softplus(a + dt_bias)   (threshold 20)
 //   q = l2norm(q) * (1 / sqrt(dk));  k = l2norm(k)          (src/ops.py:115-117: x * rsqrt(sum x^2 + 1e-6))
 //   o, S = gated_delta(q, k, v, beta, g, S)                  (native/chunked_delta.hip)
@@ -47,10 +49,6 @@ __device__ __forceinline__ float2 ld_pair(const void* p, long long off, int dt) 
     }
     return reinterpret_cast<const float2*>(p)[off >> 1];
 }
-// the reference converts the old tail to x's dtype before the convolution (tail.to(x.dtype))
-__device__ __forceinline__ float as_x_dtype(float v, int dt) {
-    return dt == RK_BF16 ? bf16_bits_to_f32(f32_to_bf16_rne(v)) : v;
-}
 __device__ __forceinline__ float silu(float y) { return y / (1.0f + expf(-y)); }
 // The streaming front and norm kernels would be VALU-bound with the correctly rounded division, square root and
 // the library exp (about 3x the instructions of the loads they hide behind): there SiLU and the reciprocal norms use
@@ -66,17 +64,16 @@ __device__ __forceinline__ void stream_store2(float* p, float x0, float x1) {
 }
 
 // ---- single segment, out-of-place (Backend.causal_conv1d): thread i < T*C computes u[t][c] = silu(conv); the
-// next (K-1)*C threads copy hist rows T .. T+K-2 into new_tail (x's dtype).
-__global__ __launch_bounds__(256) void causal_conv_kernel(float* u, void* new_tail, const void* x, int x_dtype,
+// next (K-1)*C threads copy hist rows T .. T+K-2 into new_tail (fp32: bf16 x rows widened exactly).
+__global__ __launch_bounds__(256) void causal_conv_kernel(float* u, float* new_tail, const void* x, int x_dtype,
                                                           long long x_ld, const float* tail, const float* w, int T,
                                                           int C, int K) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)(T + K - 1) * C) return;
     const int r = (int)(i / C), c = (int)(i % C);
-    // hist row h: old tail row h (in x's dtype) for h < K-1, else x row h - (K-1)
+    // hist row h: old tail row h (fp32 as stored) for h < K-1, else x row h - (K-1) widened
     auto hist = [&](int h) {
-        return h < K - 1 ? as_x_dtype(tail[(long long)h * C + c], x_dtype)
-                         : ld_elem(x, (long long)(h - (K - 1)) * x_ld + c, x_dtype);
+        return h < K - 1 ? tail[(long long)h * C + c] : ld_elem(x, (long long)(h - (K - 1)) * x_ld + c, x_dtype);
     };
     if (r < T) {
         // ((h0 w0 + h1 w1) + h2 w2) + ...: products rounded, summed tap by tap, as the reference's sum()
@@ -84,10 +81,7 @@ __global__ __launch_bounds__(256) void causal_conv_kernel(float* u, void* new_ta
         for (int j = 1; j < K; ++j) y = __fadd_rn(y, __fmul_rn(hist(r + j), w[(long long)c * K + j]));
         u[(long long)r * C + c] = silu(y);
     } else {
-        const long long o = (long long)(r - T) * C + c;           // the last K-1 rows of hist
-        const float v = hist(r);
-        if (x_dtype == RK_BF16) reinterpret_cast<uint16_t*>(new_tail)[o] = f32_to_bf16_rne(v);   // exact: bf16 value
-        else reinterpret_cast<float*>(new_tail)[o] = v;
+        new_tail[(long long)(r - T) * C + c] = hist(r);           // the last K-1 rows of hist
     }
 }
 
@@ -157,14 +151,13 @@ __global__ __launch_bounds__(256) void prefill_front_kernel(FrontArgs p) {
 
     int s = segment_of_row(p.cu, p.S, n0);
     int seg_lo = p.cu[s], seg_hi = p.cu[s + 1];
-    // hist row r of segment s (r < K-1 + its length): old tail row r in x's dtype (zeros without a state) or row
-    // seg_lo + r - (K-1) of qkv
+    // hist row r of segment s (r < K-1 + its length): old tail row r, fp32 as stored (zeros without a state), or
+    // row seg_lo + r - (K-1) of qkv widened
     auto hist = [&](int r) {
         if (r < K - 1) {
             if (!p.seq) return make_float2(0.0f, 0.0f);
             const float* tail = p.conv + (long long)p.seq[s] * p.conv_stride;
-            const float2 o = *reinterpret_cast<const float2*>(tail + (long long)r * p.C + c0);
-            return make_float2(as_x_dtype(o.x, xdt), as_x_dtype(o.y, xdt));
+            return *reinterpret_cast<const float2*>(tail + (long long)r * p.C + c0);
         }
         return ld_pair(p.qkv, (long long)(seg_lo + r - (K - 1)) * p.ld + c0, xdt);
     };
@@ -226,9 +219,9 @@ __global__ __launch_bounds__(256) void prefill_front_kernel(FrontArgs p) {
     }
 }
 
-// one thread per (segment, channel): hist rows T .. T+K-2 of [old tail; x] become the segment's tail, in x's dtype
-// (stored widened to fp32). Launched after the front kernel has read every old tail; the thread reads all K-1 old
-// rows before it writes.
+// one thread per (segment, channel): hist rows T .. T+K-2 of [old tail; x] become the segment's tail (fp32: carried
+// old rows keep their bits, x rows are widened). Launched after the front kernel has read every old tail; the
+// thread reads all K-1 old rows before it writes.
 __global__ __launch_bounds__(256) void tail_handoff_kernel(FrontArgs p, float* conv) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)p.S * p.C) return;
@@ -237,7 +230,7 @@ __global__ __launch_bounds__(256) void tail_handoff_kernel(FrontArgs p, float* c
     if (T == 0) return;                              // an empty segment leaves its state as it is
     float* tail = conv + (long long)p.seq[s] * p.conv_stride;
     float old[kMaxTaps];
-    for (int r = 0; r < p.K - 1; ++r) old[r] = as_x_dtype(tail[(long long)r * p.C + c], p.x_dtype);
+    for (int r = 0; r < p.K - 1; ++r) old[r] = tail[(long long)r * p.C + c];
     for (int r = 0; r < p.K - 1; ++r) {
         const int h = T + r;
         tail[(long long)r * p.C + c] =
@@ -335,7 +328,7 @@ using namespace rk;
 
 extern "C" {
 
-int rk_causal_conv1d(float* u, void* new_tail, const void* x, int x_dtype, long long x_ld, const float* tail,
+int rk_causal_conv1d(float* u, float* new_tail, const void* x, int x_dtype, long long x_ld, const float* tail,
                      const float* w, int T, int C, int K, void* stream) {
     if (!u || !new_tail || !tail || !w || (T > 0 && !x)) return fail(RK_ERR_ARG, "rk_causal_conv1d: null pointer");
     if (T < 0 || C < 1 || K < 2 || K > kMaxTaps || (T > 0 && x_ld < C))

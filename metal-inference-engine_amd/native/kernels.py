@@ -4,6 +4,8 @@ PyTorch is used here only for device memory and the stream: every computation is
 Checks mirror the reference's host-side refusals (MetalBackend._kv_kernel raises TypeError for a KV dtype it has no
 kernel for, src/backend/metal.py:189-195) and turn shape mistakes into ValueError before anything is launched.
 """
+import math
+
 import torch
 
 from native.rocm_native import RK_BF16, RK_F32, RK_W_BF16, RK_W_INT4, RK_W_INT8, load
@@ -255,24 +257,40 @@ def prefill_work(lengths: list[int], starts: list[int], window: int | None = Non
     return [v for _, e in entries for v in e], n_slots
 
 
+PREFILL_F32_HEADS = 4       # query heads per workgroup of rk_paged_prefill's fp32-operand kernel
+
+
+def prefill_bf16_operands(q_dtype, pool_dtype, Hq: int, Hkv: int, d: int, exact: bool, max_nb: int = 1,
+                          block_size: int = 16) -> bool:
+    """Whether rk_paged_prefill runs on bf16 MFMA operands (its rule, include/rk_path.h): q and the pool both bf16,
+    4 query heads per kv-head, head_dim 128 or 256, block size >= 2, positions x block size below 2^32, and no exact
+    request. Everything else takes fp32 operands."""
+    return (not exact and q_dtype == torch.bfloat16 and pool_dtype == torch.bfloat16 and Hq == 4 * Hkv
+            and d in (128, 256) and block_size >= 2 and max_nb * block_size * block_size < 2 ** 32)
+
+
 def _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu: list[int], st: list[int], gate,
-                    window: int, causal: bool) -> None:
+                    window: int, causal: bool, exact: bool = False) -> None:
     """rk_paged_prefill with the host-side segment offsets, start positions and work list in one int32 array, and
     the partial records / arrival counters of split blocks from the device's shared workspace."""
     S = len(st)
     N, Hq, d = q.shape
     NB, bs, Hkv, _ = k_pool.shape
     dev = q.device
+    # workgroups per 32-query block: one per kv-head, times the head chunks of the fp32-operand kernel
+    wg_heads = Hkv if prefill_bf16_operands(q.dtype, k_pool.dtype, Hq, Hkv, d, exact, tables.shape[1], bs) else \
+        Hkv * -(-(Hq // Hkv) // PREFILL_F32_HEADS)
     work, n_slots = prefill_work([b - a for a, b in zip(cu, cu[1:])], st, window, causal, PREFILL_SPLIT_TILES,
-                                 Hkv, device_cus(dev))
+                                 wg_heads, device_cus(dev))
     meta = to_device(torch.tensor(cu + st + work, dtype=torch.int32), dev)
     n_work = len(work) // 5
     lib = load()
-    part_ptr, part_bytes, cnt_ptr = None, 0, None
+    part_ptr, part_bytes, cnt_ptr, n_cnt = None, 0, None, 0
     if n_slots:
-        part_bytes = lib.lib.rk_paged_prefill_workspace_bytes(n_slots, Hkv, d)
+        part_bytes = lib.lib.rk_paged_prefill_workspace_bytes(n_slots, Hq, d)
         part_ptr = workspace(dev, part_bytes).data_ptr()
-        cnt_ptr = linear_counters(dev, n_slots * Hkv * 4).data_ptr()
+        n_cnt = lib.lib.rk_paged_prefill_counters(n_slots, Hq)
+        cnt_ptr = linear_counters(dev, n_cnt).data_ptr()
     lib.call("rk_paged_prefill", out.data_ptr(), q.data_ptr(), DTYPE_CODES[q.dtype],
              k_new.data_ptr() if k_new is not None else None, v_new.data_ptr() if v_new is not None else None,
              DTYPE_CODES[k_new.dtype] if k_new is not None else DTYPE_CODES[torch.float32],
@@ -280,24 +298,25 @@ def _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu: list[int],
              meta.data_ptr(), meta.data_ptr() + 4 * (S + 1), meta.data_ptr() + 4 * (2 * S + 1), n_work, S, N, Hq,
              Hkv, d, bs, NB, gate.data_ptr() if gate is not None else None,
              DTYPE_CODES[gate.dtype] if gate is not None else DTYPE_CODES[torch.float32], int(window or 0),
-             1 if causal else 0, n_slots, part_ptr, part_bytes, cnt_ptr, _stream(dev))
+             1 if causal else 0, 1 if exact else 0, n_slots, part_ptr, part_bytes, cnt_ptr, n_cnt, _stream(dev))
 
 
 def _prefill_shape_check(name: str, Hq: int, Hkv: int, d: int) -> None:
-    if Hkv < 1 or Hq % Hkv or Hq // Hkv != 4:
-        raise NotImplementedError(f"{name}: the prefill attention kernel is built for 4 query heads per kv-head, "
-                                  f"not {Hq} / {Hkv}")
-    if d not in (128, 256):
-        raise NotImplementedError(f"{name}: the prefill attention kernel is built for head_dim 128 or 256, not {d}")
+    if Hkv < 1 or Hq < Hkv or Hq % Hkv:
+        raise ValueError(f"{name}: {Hq} query heads do not split into groups over {Hkv} kv-heads")
+    if d not in (64, 128, 256):
+        raise NotImplementedError(f"{name}: the prefill attention kernels are built for head_dim 64, 128 or 256, "
+                                  f"not {d}")
 
 
 def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size: int, gate=None,
-                  out=None, window: int | None = None) -> torch.Tensor:
+                  out=None, window: int | None = None, exact: bool = False) -> torch.Tensor:
     """Packed prefill attention (rk_paged_prefill): writes the new K/V rows into one pool layer, then causal GQA
     attention of every segment's new queries over its prefix + new keys -> [N, Hq, d] fp32 (* sigmoid(gate)); with a
     window W each query sees only its last W positions. cu_seqlens (S + 1 row offsets) and start_pos (S absolute
     positions) are host-side lists / CPU tensors, as the packing step produces them; tables [S, max_nb] int32 on
-    the device."""
+    the device. fp32 operands (fp32-level results) unless q and the pool are both bf16 at 4 query heads per kv-head
+    and head_dim 128 / 256; exact=True asks for fp32 operands there too."""
     name = "paged_prefill"
     cu = [int(x) for x in cu_seqlens]
     st = [int(x) for x in start_pos]
@@ -333,19 +352,16 @@ def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos
         out = torch.empty(N, Hq, d, dtype=torch.float32, device=dev)
     if N == 0:
         return out
-    _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu, st, gate, window or 0, True)
+    _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu, st, gate, window or 0, True, exact)
     return out
 
 
-_ONE_BLOCK = 65535          # a contiguous cache up to this many positions is viewed as one pool block
-
-
-def attention(q, k, v, causal: bool = True, window: int | None = None) -> torch.Tensor:
+def attention(q, k, v, causal: bool = True, window: int | None = None, exact: bool = False) -> torch.Tensor:
     """Backend.attention for T >= 1 queries (src/backend/base.py:32-35, ops.attention, src/ops.py:65-104):
     q [T, Hq, d], k / v [S, Hkv, d] (fp32 or bf16 read as stored, anything else widened) -> [T, Hq, d] fp32; query i
-    sits at position S - T + i. The cache is viewed as a pool of one block holding all S positions (longer caches
-    are copied into blocks of 1024) and run through rk_paged_prefill with no KV write; with a window the keys no
-    query sees are dropped first, as the reference does."""
+    sits at position S - T + i. The cache is viewed in place as a pool of one block holding all S positions and run
+    through rk_paged_prefill with no KV write; with a window the keys no query sees are dropped first, as the
+    reference does. Operands as paged_prefill (fp32 unless q, k and v are all bf16 at the bf16 kernel's shapes)."""
     name = "attention"
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
         raise ValueError(f"{name}: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
@@ -368,19 +384,17 @@ def attention(q, k, v, causal: bool = True, window: int | None = None) -> torch.
     out = torch.empty(T, Hq, d, dtype=torch.float32, device=dev)
     if T == 0:
         return out
-    if S <= _ONE_BLOCK:
-        bs, nb = S, 1
-        kp, vp = k.contiguous().view(1, S, Hkv, d), v.contiguous().view(1, S, Hkv, d)
-    else:
-        bs = 1024
-        nb = -(-S // bs)
-        kp = torch.zeros(nb * bs, Hkv, d, dtype=k.dtype, device=dev)
-        vp = torch.zeros(nb * bs, Hkv, d, dtype=v.dtype, device=dev)
-        kp[:S], vp[:S] = k, v
-        kp, vp = kp.view(nb, bs, Hkv, d), vp.view(nb, bs, Hkv, d)
+    if S >= 2 ** 31:
+        raise NotImplementedError(f"{name}: {S} positions (the kernels address positions below 2^31)")
+    # viewed in place as one block of S positions; past 65,535 positions (where the bf16 kernel's block index needs
+    # positions x block size < 2^32) as S / bs blocks of the largest power of two bs <= 16 dividing S, in order (an
+    # odd S gives blocks of one position, which only the fp32-operand kernel takes)
+    bs = S if S < 65536 else math.gcd(S, 16)
+    nb = S // bs
+    kp, vp = k.contiguous().view(nb, bs, Hkv, d), v.contiguous().view(nb, bs, Hkv, d)
     tables = torch.arange(nb, dtype=torch.int32, device=dev).view(1, nb)
     _prefill_launch(out, q, None, None, kp, vp, tables, [0, T], [S - T], None,
-                    (window or 0) if causal else 0, causal)
+                    (window or 0) if causal else 0, causal, exact)
     return out
 
 
@@ -447,7 +461,8 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
 def causal_conv1d(x, tail, w) -> tuple[torch.Tensor, torch.Tensor]:
     """Backend.causal_conv1d for one segment (rk_causal_conv1d): x [T, C] (fp32 or bf16 read as stored; rows may be
     strided, as the qkv columns of a fused projection output), tail [K-1, C], w [C, K]
-    -> (silu(conv) [T, C] fp32, new tail [K-1, C] in x's dtype)."""
+    -> (silu(conv) [T, C] fp32, new tail [K-1, C] fp32). As TorchBackend.causal_conv1d (torch_ref.py:49-50), x is
+    taken widened: the fp32 tail is used as stored and the new tail holds x's rows widened."""
     name = "causal_conv1d"
     if x.dim() != 2 or tail.dim() != 2 or w.dim() != 2:
         raise ValueError(f"{name}: x {tuple(x.shape)}, tail {tuple(tail.shape)}, w {tuple(w.shape)}")
@@ -462,7 +477,7 @@ def causal_conv1d(x, tail, w) -> tuple[torch.Tensor, torch.Tensor]:
     tail = tail.to(device=dev, dtype=torch.float32).contiguous()
     w = w.to(device=dev, dtype=torch.float32).contiguous()
     u = torch.empty(T, C, dtype=torch.float32, device=dev)
-    new_tail = torch.empty(K - 1, C, dtype=x.dtype, device=dev)
+    new_tail = torch.empty(K - 1, C, dtype=torch.float32, device=dev)
     load().call("rk_causal_conv1d", u.data_ptr(), new_tail.data_ptr(), x.data_ptr(), DTYPE_CODES[x.dtype],
                 x.stride(0), tail.data_ptr(), w.data_ptr(), T, C, K, _stream(dev))
     return u, new_tail

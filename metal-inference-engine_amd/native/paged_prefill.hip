@@ -32,7 +32,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBQ = 32;    // queries per wave
-constexpr int kMaxGroup = 4;  // query heads per kv-head (the only group size built)
+constexpr int kMaxGroup = 4;  // query heads per kv-head of the bf16-operand kernel
 constexpr int kWorkInts = 5;  // int32 per work entry
 constexpr int kKPad = 8;   // bf16 padding of a K row in LDS (16 bytes)
 constexpr int kVPad = 4;   // bf16 padding of a V^T row in LDS: rows of 18 dwords (= 2 mod 4) put 16
@@ -59,7 +59,8 @@ struct PrefillArgs {
     int q_dtype, new_dtype, pool_dtype;
     int S, n_work, N, Hq, Hkv, G, bs, max_nb, num_blocks, n_slots;
     float qscale;               // log2(e) / sqrt(D)
-    uint32_t bs_recip;          // ceil(2^32 / bs): pos / bs = mulhi(pos, bs_recip) for pos * bs < 2^32
+    uint32_t bs_recip_up;       // ceil(2^32 / bs) (bs >= 2): mulhi(pos, bs_recip_up) = pos / bs while pos * bs < 2^32
+    uint32_t bs_recip;          // floor((2^32 - 1) / bs): mulhi(pos, bs_recip) is pos / bs or one less
 };
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -247,7 +248,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int tile = t_first + t_rel;
         // pos = b * bs + r with b = mulhi(pos, ceil(2^32 / bs)): exact because pos * bs < 2^32 (checked on the host)
         auto row_of = [&](int pos) {
-            const int b = (int)__umulhi((uint32_t)pos, a.bs_recip);
+            const int b = (int)__umulhi((uint32_t)pos, a.bs_recip_up);
             int blk;
             if (TAB_LDS) {
                 blk = tab[b - b_first];
@@ -575,6 +576,321 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// ---- 3. attention with fp32 operands: the same work list, masks, splits and gate as prefill_attention, for every
+// input the bf16 kernel does not take (fp32 q or pool, group sizes other than 4, D = 64). The reference computes
+// attention in fp32 on widened inputs (src/ops.py:84-87, 91-103), so the products here are fp32 products:
+// v_mfma_f32_16x16x4_f32, bf16 pool rows widened exactly when staged, the probabilities kept in fp32.
+// blockDim = 512: wave w takes query head (blockIdx.z * 4 + w % 4) of the group (none past the group's end: that
+// wave only helps stage) and queries 16 (w / 4) .. + 15 of the work item's 32. All 8 waves stage each tile of 32
+// keys (K and V rows, fp32, rows padded by 4 floats) into a 2-stage LDS ring, one 16-byte load per lane per row
+// piece, requested a whole tile ahead. Per wave and tile, on 16 x 16 accumulators (lane l: query l % 16, rows
+// 4 (l / 16) .. + 3):
+//   S^T = K Q^T:  A = 16 keys x 4 dims from LDS (one 16-byte read feeds four MFMAs: quarter l / 16 takes dims
+//                 16 c + 4 (l / 16) + j of MFMA j), B = Q^T from registers (the same dims of the lane's query);
+//   O^T += V^T P^T: A = V^T (16 dims x 4 keys; lane l reads V[key][16 dt + l % 16] from the row-major stage, the
+//                 keys 4 (l / 16) + r of MFMA r), B = P^T, which is the score accumulator's register r as it is.
+// So every lane keeps its own query's softmax state (one reduction over the 4 quarters per tile), and O^T is
+// rescaled per lane. LDS reads are conflict-free: the padded row stride (D + 4 floats) puts 16 consecutive rows 4
+// banks apart.
+constexpr int kF32QW = 16;      // queries per wave
+constexpr int kF32Heads = 4;    // query heads per workgroup
+constexpr int kF32Pad = 4;      // fp32 padding of an LDS row
+
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int D, typename TP, bool TAB_LDS>
+__global__ __launch_bounds__(512) void prefill_attention_f32(PrefillArgs a) {
+    constexpr int ROW = D + kF32Pad;                 // LDS row stride (floats)
+    constexpr int STAGE = 2 * kBKP * ROW;            // K rows, then V rows
+    constexpr int EL = 16 / (int)sizeof(TP);         // elements per 16-byte load
+    constexpr int PER_ROW = D / EL;                  // loads per row
+    constexpr int PER_T = kBKP * PER_ROW;            // loads per tensor per tile
+    constexpr int NLD = 2 * PER_T / 512;             // loads per thread per tile
+    static_assert(NLD >= 1 && (2 * PER_T) % 512 == 0, "a tile's rows must split evenly over 512 threads");
+    constexpr int NC = D / 16;                       // 16-dim groups
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    float* lds = reinterpret_cast<float*>(smem);                               // [2 stages][K rows; V rows]
+    int* tab = reinterpret_cast<int*>(smem + 2 * STAGE * sizeof(float));       // [kTabCache] block ids
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = blockIdx.y;
+    const int gh = blockIdx.z * kF32Heads + (wave & 3);      // head within the group
+    const int half = wave >> 2;
+    const int32_t* we = a.work + (long long)kWorkInts * blockIdx.x;
+    const int item = we[0];
+    const int seg = item >> 16, qblk = item & 0xffff;
+    const int row0 = a.cu[seg] + qblk * kBQ;
+    const int nq = min(kBQ, a.cu[seg + 1] - row0);
+    const int p0 = a.start[seg] + qblk * kBQ;
+    const int n_keys = a.causal ? p0 + nq : a.start[seg] + (a.cu[seg + 1] - a.cu[seg]);
+    const int kmin = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
+    const int t_first = max(kmin / kBKP, we[1]);
+    const int n_tiles = min((n_keys + kBKP - 1) / kBKP, we[2]) - t_first;
+    const int32_t* table = a.tables + (long long)seg * a.max_nb;
+    const bool active = gh < a.G && half * kF32QW < nq;     // whole waves
+    const int head = kvh * a.G + (gh < a.G ? gh : 0);
+    // pos / bs: the estimate from floor((2^32 - 1) / bs) is exact or one short for every pos < 2^32
+    auto block_of = [&](int pos, int& r) {
+        uint32_t b = __umulhi((uint32_t)pos, a.bs_recip);
+        r = pos - (int)b * a.bs;
+        if (r >= a.bs) { ++b; r -= a.bs; }
+        return (int)b;
+    };
+    // TAB_LDS (at most kTabCache blocks per table row): the block ids of every position this entry reads (kmin ..
+    // n_keys - 1 within its tiles), clamped to the pool, cached in LDS first
+    int r0;
+    const int b_lo = n_tiles > 0 ? block_of(max(kmin, t_first * kBKP), r0) : 0;
+    if (TAB_LDS) {
+        const int b_hi = n_tiles > 0 ? block_of(min(n_keys, (t_first + n_tiles) * kBKP) - 1, r0) : -1;
+        for (int i = b_lo + tid; i <= b_hi; i += 512) {
+            const int blk = table[i];
+            tab[i - b_lo] = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+        }
+        __syncthreads();
+    }
+
+    // ---- staging: load index i = tid + 512 j: tensor i / PER_T (K, V), key (i % PER_T) / PER_ROW, piece i % PER_ROW;
+    // consecutive lanes read consecutive 16-byte pieces of one row
+    u32x4 st[NLD];
+    auto issue = [&](int t_rel) {
+        const int tile = t_first + t_rel;
+        // all block ids of the tile first (one wait for them), then the row loads
+        int blk[NLD], rr[NLD];
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int e = (tid + 512 * j) % PER_T;
+            int pos = tile * kBKP + e / PER_ROW;
+            pos = pos < n_keys ? pos : n_keys - 1;   // keys past the range read its last key (masked, never used)
+            pos = pos < kmin ? kmin : pos;           // keys below the window read its first one
+            const int b = block_of(pos, rr[j]);
+            if (TAB_LDS) {
+                blk[j] = tab[b - b_lo];
+            } else {
+                const int t = table[b];
+                blk[j] = t < 0 ? 0 : (t >= a.num_blocks ? a.num_blocks - 1 : t);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int i = tid + 512 * j;
+            const int pc = (i % PER_T) % PER_ROW;
+            const long long off = (((long long)blk[j] * a.bs + rr[j]) * a.Hkv + kvh) * D + pc * EL;
+            const TP* base = reinterpret_cast<const TP*>(i / PER_T ? a.vp : a.kp);
+            st[j] = *reinterpret_cast<const u32x4*>(base + off);
+        }
+    };
+    auto stash = [&](int stage) {
+        float* s = lds + stage * STAGE;
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int i = tid + 512 * j;
+            const int which = i / PER_T, e = i % PER_T;
+            const int key = e / PER_ROW, pc = e % PER_ROW;
+            float* dst = s + which * kBKP * ROW + key * ROW + pc * EL;
+            if constexpr (sizeof(TP) == 4) {
+                *reinterpret_cast<u32x4*>(dst) = st[j];
+            } else {                                 // 8 bf16 -> 8 fp32, exact
+                const u32x4 w = st[j];
+                *reinterpret_cast<f32x4*>(dst) = f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+                *reinterpret_cast<f32x4*>(dst + 4) = f32x4{bf16_lo(w[2]), bf16_hi(w[2]), bf16_lo(w[3]), bf16_hi(w[3])};
+            }
+        }
+    };
+
+    // ---- per-wave query state
+    const int qc = lane & 15, qq = lane >> 4;
+    const int qi = half * kF32QW + qc;               // query within the work item
+    const int qpos = a.causal ? p0 + (qi < nq ? qi : nq - 1) : n_keys - 1;
+    const int qlo = a.window > 0 ? qpos - a.window : -1;
+    const int qfirst = a.causal ? p0 + half * kF32QW : n_keys - 1;
+    const int qlast = a.causal ? p0 + min(half * kF32QW + kF32QW, nq) - 1 : n_keys - 1;
+    const int lo_edge = a.window > 0 ? qlast - a.window : INT_MIN;
+    f32x4 qv[NC];                                    // Q[query][16 c + 4 qq .. + 3]
+    f32x4 o[NC];                                     // O^T[16 dt + 4 qq + r][query]
+    float m_run = -INFINITY, l_run = 0.0f;
+    if (active) {
+        const long long qb = ((long long)(row0 + (qi < nq ? qi : nq - 1)) * a.Hq + head) * D + 4 * qq;
+        if (a.q_dtype == RK_BF16) {
+            const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) + qb;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const u32x2 w = *reinterpret_cast<const u32x2*>(qp + 16 * c);
+                qv[c] = f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+            }
+        } else {
+            const float* qp = reinterpret_cast<const float*>(a.q) + qb;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qp + 16 * c);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) o[c] = f32x4{};
+    }
+
+    auto consume = [&](int t_rel, int stage) {
+        const float* ks = lds + stage * STAGE;
+        const float* vs = ks + kBKP * ROW;
+        const int k0 = (t_first + t_rel) * kBKP;
+        f32x4 s[2] = {f32x4{}, f32x4{}};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const f32x4 kv = *reinterpret_cast<const f32x4*>(ks + (16 * kt + qc) * ROW + 16 * c + 4 * qq);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[kt] = mfma_f32(kv[j], qv[c][j], s[kt]);
+            }
+        }
+        // lane (qc, qq), register r of sub-tile kt: key k0 + 16 kt + 4 qq + r
+        if (k0 + kBKP - 1 > qfirst || k0 <= lo_edge) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * kt + 4 * qq + r;
+                    s[kt][r] = key <= qpos && key > qlo ? s[kt][r] : -INFINITY;
+                }
+        }
+        float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                           fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.qscale;
+        const float m_new = tmax > m_run + kLazy ? tmax : m_run;
+        const float mb = m_new == -INFINITY ? 0.0f : m_new;
+        float psum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[kt][r] = fast_exp2(fmaf(s[kt][r], a.qscale, -mb));
+                psum += s[kt][r];
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        if (__any(m_new != m_run)) {
+            const float alpha = fast_exp2(m_run - mb);      // 0 on the first tile (m_run = -inf)
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt) o[dt] *= alpha;
+        }
+        l_run += psum;
+        m_run = m_new;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float* vr = vs + (16 * kt + 4 * qq + r) * ROW + qc;
+#pragma unroll
+                for (int dt = 0; dt < NC; ++dt) o[dt] = mfma_f32(vr[16 * dt], s[kt][r], o[dt]);
+            }
+    };
+
+    // Stage t's rows are written after tile t - 1 is computed (stage (t - 1) & 1 is free once every wave passed the
+    // barrier that ended tile t - 2), then tile t + 1 is requested; one LDS-only barrier per tile.
+    if (n_tiles > 0) {
+        issue(0);
+        stash(0);
+        if (n_tiles > 1) issue(1);
+        lds_barrier();
+        for (int t = 0; t < n_tiles; ++t) {
+            if (active) consume(t, t & 1);
+            if (t + 1 < n_tiles) {
+                stash((t + 1) & 1);
+                if (t + 2 < n_tiles) issue(t + 2);
+            }
+            lds_barrier();
+        }
+    }
+    if (!active) return;
+
+    // Split items: the piece's (o, m, l) per (slot, head, half) of 16 queries, then the arrival count; the last piece
+    // combines all of them in piece order (the protocol of prefill_attention above).
+    const int piece = we[4] >> 16, pieces = we[4] & 0xffff;
+    const int first = we[3] >= 0 && piece < pieces && we[3] + pieces <= a.n_slots ? we[3] : -1;
+    if (first >= 0) {
+        constexpr int REC = kF32QW * D + 2 * kF32QW;
+        constexpr int kSc1 = 16;
+        auto rsrc_of = [&](int pc) {
+            const unsigned long long u = reinterpret_cast<unsigned long long>(
+                a.part + (((long long)(first + pc) * a.Hq + head) * 2 + half) * REC);
+            const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
+            const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+            return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo),
+                                                     (short)0, REC * 4, 0x00020000);
+        };
+        auto o_off = [&](int dt) { return 4 * (qc * D + 16 * dt + 4 * qq); };
+        const int m_off = 4 * (kF32QW * D + qc), l_off = 4 * (kF32QW * D + kF32QW + qc);
+        {
+            const auto rs = rsrc_of(piece);
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[dt]), rs, o_off(dt), 0, kSc1);
+            if (qq == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), rs, m_off, 0, kSc1);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), rs, l_off, 0, kSc1);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): this wave's stores have completed
+        uint32_t* counter = a.cnt + ((long long)first * a.Hq + head) * 2 + half;
+        uint32_t before = 0;
+        if (lane == 0) before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        before = __shfl(before, 0);
+        if (before != (uint32_t)(pieces - 1)) return;
+        float mx = -INFINITY;
+        for (int pc = 0; pc < pieces; ++pc)
+            mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_of(pc), m_off, 0, kSc1)));
+#pragma unroll
+        for (int dt = 0; dt < NC; ++dt) o[dt] = f32x4{};
+        l_run = 0.0f;
+        for (int pc = 0; pc < pieces; ++pc) {
+            const auto rs = rsrc_of(pc);
+            u32x4 v[NC];
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt) v[dt] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off(dt), 0, kSc1);
+            const float mp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, m_off, 0, kSc1));
+            const float lp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, l_off, 0, kSc1));
+            const float sc = mp == -INFINITY ? 0.0f : fast_exp2(mp - mx);
+            l_run = fmaf(sc, lp, l_run);
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[dt][r] = fmaf(sc, __uint_as_float(v[dt][r]), o[dt][r]);
+        }
+        if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    if (qi < nq) {
+        const float inv = 1.0f / l_run;
+        const long long orow = (long long)(row0 + qi) * a.Hq + head;
+        float4 gv[NC];
+        if (a.gate) {
+            if (a.gate_dtype == RK_BF16) {
+                const uint16_t* gp = reinterpret_cast<const uint16_t*>(a.gate) + orow * D + 4 * qq;
+#pragma unroll
+                for (int dt = 0; dt < NC; ++dt) {
+                    const u32x2 w = *reinterpret_cast<const u32x2*>(gp + 16 * dt);
+                    gv[dt] = make_float4(bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1]));
+                }
+            } else {
+                const float* gp = reinterpret_cast<const float*>(a.gate) + orow * D + 4 * qq;
+#pragma unroll
+                for (int dt = 0; dt < NC; ++dt) gv[dt] = *reinterpret_cast<const float4*>(gp + 16 * dt);
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < NC; ++dt) {
+            float v[4] = {o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv};
+            if (a.gate) {
+                const float g[4] = {gv[dt].x, gv[dt].y, gv[dt].z, gv[dt].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = v[i] * (1.0f / (1.0f + expf(-g[i])));
+            }
+            *reinterpret_cast<float4*>(a.out + orow * D + 16 * dt + 4 * qq) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace rk
 
@@ -582,23 +898,30 @@ using namespace rk;
 
 extern "C" {
 
-size_t rk_paged_prefill_workspace_bytes(int n_slots, int Hkv, int D) {
-    if (n_slots <= 0 || Hkv <= 0 || D <= 0) return 0;
-    return (size_t)n_slots * Hkv * kMaxGroup * (kBQ * (size_t)D + 2 * kBQ) * sizeof(float);
+size_t rk_paged_prefill_workspace_bytes(int n_slots, int Hq, int D) {
+    if (n_slots <= 0 || Hq <= 0 || D <= 0) return 0;
+    return (size_t)n_slots * Hq * (kBQ * (size_t)D + 2 * kBQ) * sizeof(float);
+}
+
+size_t rk_paged_prefill_counters(int n_slots, int Hq) {
+    if (n_slots <= 0 || Hq <= 0) return 0;
+    return (size_t)n_slots * Hq * 2;
 }
 
 int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, const void* v_new, int new_dtype,
                      void* k_pool, void* v_pool, int pool_dtype, const int32_t* tables, int max_nb,
                      const int32_t* cu_seqlens, const int32_t* start_pos, const int32_t* work, int n_work, int S,
                      int N, int Hq, int Hkv, int D, int block_size, int num_blocks, const void* gate, int gate_dtype,
-                     int window, int causal, int n_slots, float* partials, size_t partial_bytes, uint32_t* counters,
-                     void* stream) {
+                     int window, int causal, int exact, int n_slots, float* partials, size_t partial_bytes,
+                     uint32_t* counters, size_t n_counters, void* stream) {
     if (N == 0) return RK_OK;
     if (n_slots < 0 || (n_slots > 0 && (!partials || !counters)))
         return fail(RK_ERR_ARG, "rk_paged_prefill: %d partial slots need partials and counters", n_slots);
-    if (n_slots > 0 && partial_bytes < rk_paged_prefill_workspace_bytes(n_slots, Hkv, D))
-        return fail(RK_ERR_WORKSPACE, "rk_paged_prefill: %zu partial bytes for %d slots (need %zu)", partial_bytes,
-                    n_slots, rk_paged_prefill_workspace_bytes(n_slots, Hkv, D));
+    if (n_slots > 0 && (partial_bytes < rk_paged_prefill_workspace_bytes(n_slots, Hq, D) ||
+                        n_counters < rk_paged_prefill_counters(n_slots, Hq)))
+        return fail(RK_ERR_WORKSPACE, "rk_paged_prefill: %zu partial bytes and %zu counters for %d slots (need %zu "
+                    "and %zu)", partial_bytes, n_counters, n_slots, rk_paged_prefill_workspace_bytes(n_slots, Hq, D),
+                    rk_paged_prefill_counters(n_slots, Hq));
     if (!out || !q || !k_pool || !v_pool || !tables || !cu_seqlens || !start_pos || !work)
         return fail(RK_ERR_ARG, "rk_paged_prefill: null pointer");
     if (!k_new != !v_new) return fail(RK_ERR_ARG, "rk_paged_prefill: k_new and v_new must both be given or both null");
@@ -607,13 +930,19 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     if (S < 1 || N < 1 || n_work < 1 || n_work > 65535 * 8 || max_nb < 1 || block_size < 1 || num_blocks < 1)
         return fail(RK_ERR_ARG, "rk_paged_prefill: S %d N %d n_work %d max_nb %d block_size %d", S, N, n_work, max_nb,
                     block_size);
-    if (Hkv < 1 || Hq % Hkv || Hq / Hkv != 4)
-        return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d query heads over %d kv heads (built for groups of 4)",
-                    Hq, Hkv);
-    if (D != 128 && D != 256) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: head_dim %d not in {128, 256}", D);
-    if ((unsigned long long)max_nb * block_size * block_size >= (1ull << 32))
-        return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d blocks of %d positions (positions x block size must stay "
-                    "below 2^32)", max_nb, block_size);
+    if (Hkv < 1 || Hq < Hkv || Hq % Hkv)
+        return fail(RK_ERR_ARG, "rk_paged_prefill: %d query heads over %d kv heads", Hq, Hkv);
+    if (D != 64 && D != 128 && D != 256)
+        return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: head_dim %d not in {64, 128, 256}", D);
+    if ((unsigned long long)max_nb * block_size >= (1ull << 31))
+        return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d blocks of %d positions (positions must stay below 2^31)",
+                    max_nb, block_size);
+    // bf16 operands only where every input already is bf16 (q and the pool), the shape has an instance and the
+    // producers' one-multiply block index is exact: positions x block size below 2^32, and block_size >= 2 (the
+    // reciprocal ceil(2^32 / bs) must fit 32 bits)
+    const bool bf16_ops = !exact && q_dtype == RK_BF16 && pool_dtype == RK_BF16 && Hq == kMaxGroup * Hkv &&
+                          (D == 128 || D == 256) && block_size >= 2 &&
+                          (unsigned long long)max_nb * block_size * block_size < (1ull << 32);
     for (int dt : {q_dtype, k_new ? new_dtype : RK_F32, pool_dtype, gate ? gate_dtype : RK_F32})
         if (dt != RK_F32 && dt != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: dtype %d", dt);
     PrefillArgs a;
@@ -625,29 +954,40 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     a.max_nb = max_nb; a.num_blocks = num_blocks;
     a.part = partials; a.cnt = counters; a.n_slots = n_slots;
     a.qscale = kLog2e / sqrtf((float)D);
-    a.bs_recip = (uint32_t)(0xffffffffu / (uint32_t)block_size + 1u);
+    a.bs_recip_up = block_size >= 2 ? 0xffffffffu / (uint32_t)block_size + 1u : 0u;   // used only when bs >= 2
+    a.bs_recip = 0xffffffffu / (uint32_t)block_size;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (k_new) {
         const long long threads = (long long)N * (Hkv * D / 8);
         hipLaunchKernelGGL(prefill_kv_write, dim3((unsigned)ceil_div((size_t)threads, 256)), dim3(256), 0, s, a, D);
         if (int rc = check_launch("prefill_kv_write")) return rc;
     }
-    const bool tab_lds = max_nb <= kTabCache;
-    const size_t lds = (tab_lds ? kTabCache * 4 : 0) +
-                       (size_t)kStages * (kBKP * (D + kKPad) + D * (kBKP + kVPad)) * sizeof(uint16_t);
-    const dim3 grid(n_work, Hkv), block(2 * 64 * a.G);
     typedef void (*AttnFn)(PrefillArgs);
     AttnFn fn;
-    if (D == 256) {
-        if (pool_dtype == RK_BF16) fn = tab_lds ? prefill_attention<256, uint16_t, true> : prefill_attention<256, uint16_t, false>;
-        else fn = tab_lds ? prefill_attention<256, float, true> : prefill_attention<256, float, false>;
-    } else {
-        if (pool_dtype == RK_BF16) fn = tab_lds ? prefill_attention<128, uint16_t, true> : prefill_attention<128, uint16_t, false>;
-        else fn = tab_lds ? prefill_attention<128, float, true> : prefill_attention<128, float, false>;
+    if (bf16_ops) {
+        const bool tab_lds = max_nb <= kTabCache;
+        const size_t lds = (tab_lds ? kTabCache * 4 : 0) +
+                           (size_t)kStages * (kBKP * (D + kKPad) + D * (kBKP + kVPad)) * sizeof(uint16_t);
+        if (D == 256) fn = tab_lds ? prefill_attention<256, uint16_t, true> : prefill_attention<256, uint16_t, false>;
+        else fn = tab_lds ? prefill_attention<128, uint16_t, true> : prefill_attention<128, uint16_t, false>;
+        if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
+        hipLaunchKernelGGL(fn, dim3(n_work, Hkv), dim3(2 * 64 * a.G), lds, s, a);
+        return check_launch("prefill_attention");
     }
+    const bool tab_lds = max_nb <= kTabCache;
+    const size_t lds = (size_t)2 * 2 * kBKP * (D + kF32Pad) * sizeof(float) + (tab_lds ? kTabCache * sizeof(int) : 0);
+    const bool f32_pool = pool_dtype == RK_F32;
+#define RK_F32_PICK(DD)                                                                                      \
+    fn = f32_pool ? (tab_lds ? prefill_attention_f32<DD, float, true> : prefill_attention_f32<DD, float, false>)  \
+                  : (tab_lds ? prefill_attention_f32<DD, uint16_t, true> : prefill_attention_f32<DD, uint16_t, false>)
+    if (D == 256) RK_F32_PICK(256);
+    else if (D == 128) RK_F32_PICK(128);
+    else RK_F32_PICK(64);
+#undef RK_F32_PICK
     if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
-    hipLaunchKernelGGL(fn, grid, block, lds, s, a);
-    return check_launch("prefill_attention");
+    const int chunks = (a.G + kF32Heads - 1) / kF32Heads;
+    hipLaunchKernelGGL(fn, dim3(n_work, Hkv, chunks), dim3(512), lds, s, a);
+    return check_launch("prefill_attention_f32");
 }
 
 }  // extern "C"

@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 RK_F32, RK_BF16 = 0, 1
 RK_W_BF16, RK_W_INT8, RK_W_INT4 = 1, 2, 3
@@ -39,8 +39,9 @@ SIGNATURES = {
     "rk_pages_gather": (c_int, [P, P, c_int, c_int, c_int, P, c_int, c_int, P, P]),
     "rk_deltanet_decode": (c_int, [P] * 5 + [c_longlong] * 3 + [P] * 7 + [c_int] * 7 + [c_float, P]),
     "rk_paged_prefill": (c_int, [P, P, c_int, P, P, c_int, P, P, c_int, P, c_int, P, P, P] + [c_int] * 8
-                         + [P, c_int, c_int, c_int, c_int, P, c_size_t, P, P]),
+                         + [P, c_int, c_int, c_int, c_int, c_int, P, c_size_t, P, c_size_t, P]),
     "rk_paged_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "rk_paged_prefill_counters": (c_size_t, [c_int, c_int]),
     "rk_gated_delta_workspace_bytes": (c_size_t, [c_int, c_int]),
     "rk_gated_delta_chunked": (c_int, [P, P, c_longlong, P, P, P, c_int, P, P, P, P, P] + [c_int] * 5
                                + [P, c_size_t, P]),

@@ -15,6 +15,8 @@ Pinning status (what checks each function; see tests/test_oracle.py):
   backend_ref.paged_attention  closed-form address map (brute gather) bit-exact; paged == contiguous exactly
   ops_ref.causal_conv1d        float64 brute force; torch.nn.functional.conv1d depthwise (transformers'
                                causal_conv1d_update formulation)
+  backend_ref.causal_conv1d    float64 brute force on the widened inputs (bf16 x, fp32 tail not representable in
+                               bf16); the fp32 new tail equal to the widened rows
   ops_ref.l2norm, rms_norm_gated  float64 closed forms; transformers l2norm
   ops_ref.gated_delta_recurrent  float64 brute force; transformers torch_recurrent_gated_delta_rule (fixtures)
   ops_ref.gated_delta_chunked  == recurrent (float64); transformers torch_chunk_gated_delta_rule (fixtures);

@@ -15,11 +15,17 @@ def gated_delta(q, k, v, beta, g, S):
     return ops_ref.gated_delta_chunked(q, k, v, beta, g, S)
 
 
+def causal_conv1d(x, tail, w):
+    """TorchBackend.causal_conv1d (torch_ref.py:49-50): x is widened to fp32 BEFORE ops.causal_conv1d, so the old
+    tail is used as stored (tail.to(x.dtype) is then a no-op on an fp32 tail) and the new tail comes back fp32."""
+    return ops_ref.causal_conv1d(x.float(), tail, w)
+
+
 def deltanet_decode(qkv, z, b, a, state, slot, conv_w, A_log, dt_bias, norm_w, eps, dims):
     """One token of one DeltaNet layer, torch_ref.py:61-73. Returns [1, H * dv]; updates state.conv_tail[slot] and
     state.S[slot] in place."""
     H, dk, dv, key_dim = dims
-    u, state.conv_tail[slot] = ops_ref.causal_conv1d(qkv, state.conv_tail[slot], conv_w)   # qkv as given (:65)
+    u, state.conv_tail[slot] = causal_conv1d(qkv, state.conv_tail[slot], conv_w)   # self.causal_conv1d (:65)
     q = ops_ref.l2norm(u[:, :key_dim].reshape(1, H, dk).float()) * (1.0 / dk ** 0.5)
     k = ops_ref.l2norm(u[:, key_dim:2 * key_dim].reshape(1, H, dk).float())
     v = u[:, 2 * key_dim:].reshape(1, H, dv).float()
@@ -38,10 +44,11 @@ def deltanet_decode_batch(qkv, z, b, a, states, slot, conv_w, A_log, dt_bias, no
 
 def linear_attention_front(qkv, b, a, tail, conv_w, A_log, dt_bias, dims):
     """One prefill segment's conv, split, beta / g and l2norm, src/models/qwen3_5.py:145-155
-    -> (q, k [T, H, dk], v [T, H, dv], beta, g [T, H], new conv tail [K-1, C] in qkv's dtype)."""
+    -> (q, k [T, H, dk], v [T, H, dv], beta, g [T, H], new conv tail [K-1, C] fp32). The conv is the backend's
+    (b.causal_conv1d at :145), which widens qkv first (torch_ref.py:49-50)."""
     H, dk, dv, key_dim = dims
     T = qkv.shape[0]
-    u, new_tail = ops_ref.causal_conv1d(qkv, tail, conv_w)                 # conv BEFORE the split (:145)
+    u, new_tail = causal_conv1d(qkv, tail, conv_w)                         # conv BEFORE the split (:145)
     q = u[:, :key_dim].reshape(T, H, dk)
     k = u[:, key_dim:2 * key_dim].reshape(T, H, dk)
     v = u[:, 2 * key_dim:].reshape(T, H, dv)

@@ -127,6 +127,31 @@ def test_workspace_size_formula(lib):
     assert lib.lib.rk_paged_decode_workspace_bytes(0, 8, 2, 256, 16, 512) == 0
 
 
+def test_paged_prefill_checked_on_host(lib):
+    """rk_paged_prefill refuses bad shapes and short workspaces before any launch: head_dim 96 (no instance), query
+    heads that do not split over the kv-heads, position counts past 2^31, and split partials / counters below the
+    size functions' figures. Any group size and head_dim 64 / 128 / 256 pass validation (reached here only with an
+    invalid dtype, refused next)."""
+    fake = 4096
+
+    def call(Hq=8, Hkv=2, D=256, max_nb=4, bs=16, q_dtype=0, n_slots=0, part_bytes=0, n_cnt=0, exact=0):
+        return lib.lib.rk_paged_prefill(fake, fake, q_dtype, fake, fake, 0, fake, fake, 0, fake, max_nb, fake, fake,
+                                        fake, 1, 1, 8, Hq, Hkv, D, bs, 64, None, 0, 0, 1, exact, n_slots,
+                                        fake if n_slots else None, part_bytes, fake if n_slots else None, n_cnt, None)
+    assert call(D=96) == 2 and "head_dim 96" in lib.last_error()
+    assert call(Hq=6, Hkv=4) == 1 and "6 query heads" in lib.last_error()
+    assert call(max_nb=1 << 20, bs=4096) == 2 and "2^31" in lib.last_error()
+    for Hq, Hkv, D in ((14, 2, 64), (8, 8, 128), (32, 4, 256), (7, 1, 64)):
+        assert call(Hq, Hkv, D, q_dtype=7) == 2 and "dtype 7" in lib.last_error()
+    need = lib.lib.rk_paged_prefill_workspace_bytes(3, 8, 256)
+    cnt = lib.lib.rk_paged_prefill_counters(3, 8)
+    assert need == 3 * 8 * (32 * 256 + 64) * 4 and cnt == 3 * 8 * 2
+    assert call(n_slots=3, part_bytes=need - 4, n_cnt=cnt) == 3 and "partial bytes" in lib.last_error()
+    assert call(n_slots=3, part_bytes=need, n_cnt=cnt - 1) == 3
+    assert call(n_slots=3, part_bytes=need, n_cnt=cnt, q_dtype=7) == 2            # sizes accepted, dtype refused
+    assert lib.lib.rk_paged_prefill_workspace_bytes(0, 8, 256) == 0 and lib.lib.rk_paged_prefill_counters(0, 8) == 0
+
+
 def test_gated_delta_arguments_checked_on_host(lib):
     fake = 4096
     ws = lib.lib.rk_gated_delta_workspace_bytes(256, 16)

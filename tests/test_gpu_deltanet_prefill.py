@@ -1,12 +1,14 @@
 """Parity of the DeltaNet prefill companions (the linear-attention segment around P3, src/models/qwen3_5.py:136-162)
-with the CPU oracle: rk_causal_conv1d vs ops.causal_conv1d (src/ops.py:127-139), rk_rms_norm_gated vs
+with the CPU oracle: rk_causal_conv1d vs TorchBackend.causal_conv1d (src/backend/torch_ref.py:49-50, x widened, then
+src/ops.py:127-139), rk_rms_norm_gated vs
 ops.rms_norm_gated (src/ops.py:120-124), rk_deltanet_prefill_front vs the segment front of qwen3_5.py:145-155 and
 RocmBackend.deltanet_prefill (front + chunked delta rule + gated norm) vs the oracle's per-segment loop, whose
 composition is pinned on the CPU against chained decode steps and split prefills.
 
-Bars: fp32 results within 1e-5 relative (max|diff| / max|ref|); conv tails are copies of raw inputs (rounded to the
-input dtype, as the reference's tail.to(x.dtype)) and must match exactly; state slots outside the batch and other
-layers' slots must be untouched. Packing segments into one launch must give bit-identical rows to running each
+Bars: fp32 results within 1e-5 relative (max|diff| / max|ref|), bf16 inputs included: TorchBackend.causal_conv1d
+widens x before the conv (src/backend/torch_ref.py:49-50), so the fp32 old tail is used as stored and the new tail is
+fp32; conv tails are copies of the widened raw inputs and carried old rows, and must match exactly; state slots
+outside the batch and other layers' slots must be untouched. Packing segments into one launch must give bit-identical rows to running each
 segment alone.
 """
 import pytest
@@ -47,10 +49,10 @@ def test_causal_conv1d(backend, dtype, T):
     lw, g_ = layer(T)
     y = projection(T, dtype, g_)
     x = cols(y)[0]                                                    # strided rows, as the model passes them
-    tail = torch.randn(K - 1, C, generator=g_)
-    u_ref, t_ref = ops_ref.causal_conv1d(x, tail, lw["conv_w"])
+    tail = torch.randn(K - 1, C, generator=g_)                        # fp32 values bf16 cannot hold
+    u_ref, t_ref = backend_ref.causal_conv1d(x, tail, lw["conv_w"])
     u, t = backend.causal_conv1d(x.to(DEV), tail.to(DEV), lw["conv_w"].to(DEV))
-    assert u.dtype == torch.float32 and t.dtype == dtype
+    assert u.dtype == torch.float32 and t.dtype == torch.float32
     e = rel_err(u, u_ref)
     print(f"causal_conv1d T {T} {dtype}: rel {e:.2e}")
     assert e < TOL
@@ -125,7 +127,8 @@ def test_front_packed_with_state_handoff(backend, dtype, lengths):
                                                   lw["dt_bias"], DIMS)
         for gt, wt in zip(got, want[:5]):
             worst = max(worst, rel_err(gt[lo:hi], wt))
-        assert torch.equal(conv[s, slot], want[5].float()), f"segment {i} tail"
+        assert want[5].dtype == torch.float32
+        assert torch.equal(conv[s, slot], want[5]), f"segment {i} tail"
         assert torch.equal(conv[s, 0], conv0[s, 0])                    # the other layer's slot
     print(f"front {dtype}: worst rel {worst:.2e}")
     assert worst < TOL

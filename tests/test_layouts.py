@@ -128,3 +128,26 @@ def test_prefill_auto_split():
     lengths = torch.randint(64, 2049, (8,), generator=gen).tolist()
     starts = torch.randint(0, 16385, (8,), generator=gen).tolist()
     assert kernels.prefill_work(lengths, starts, None, True, None, 2, 256)[1] == 0   # config 5: not split
+
+
+def test_prefill_block_index_division():
+    """The prefill kernels' block index pos // bs without a divide: the fp32-operand kernel takes mulhi(pos,
+    floor((2^32 - 1) / bs)) plus one correction, exact for every pos < 2^32 and bs >= 1; the bf16-operand kernel
+    takes mulhi(pos, ceil(2^32 / bs)) alone, exact while pos * bs < 2^32, and only for bs >= 2 (the reciprocal of 1
+    does not fit 32 bits). Checked over block sizes 1 .. 4096 at edge and random positions."""
+    import numpy as np
+    rng = np.random.default_rng(5)
+    for bs in list(range(1, 130)) + [255, 256, 1000, 1024, 4095, 4096, 65535, 65536, 70003]:
+        lo = (2 ** 32 - 1) // bs
+        edge = [0, 1, bs - 1, bs, bs + 1, 2 ** 31 - 1, 2 ** 31 - bs, (2 ** 31 - 1) // bs * bs]
+        pos = np.array(edge + rng.integers(0, 2 ** 31, 2000).tolist(), dtype=np.uint64)
+        q = (pos * np.uint64(lo)) >> np.uint64(32)
+        r = pos - q * np.uint64(bs)
+        q = q + (r >= bs)
+        assert np.array_equal(q, pos // np.uint64(bs)), bs
+        if bs >= 2:
+            up = (2 ** 32 - 1) // bs + 1
+            assert up < 2 ** 32
+            ok = pos[pos * np.uint64(bs) < np.uint64(2 ** 32)]
+            assert np.array_equal((ok * np.uint64(up)) >> np.uint64(32), ok // np.uint64(bs)), bs
+    assert (2 ** 32 - 1) // 1 + 1 == 2 ** 32                    # bs = 1: the rounded-up reciprocal overflows

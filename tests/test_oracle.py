@@ -108,6 +108,28 @@ def test_conv_fixture_and_library_conv1d():
     assert rel_err(out, b_out) < 1e-6
 
 
+def test_backend_conv_widens_bf16_input_before_the_tail():
+    """TorchBackend.causal_conv1d (torch_ref.py:49-50) widens x to fp32 before ops.causal_conv1d, so a bf16 x meets
+    the fp32 tail as stored (not rounded to bf16) and the new tail is fp32. Pinned against float64 on the widened
+    inputs; a tail rounded to bf16 first (ops.causal_conv1d on the bf16 x as given) must miss that bar."""
+    g_ = torch.Generator().manual_seed(41)
+    T, C, K = 5, 96, 4
+    x = torch.randn(T, C, generator=g_).to(torch.bfloat16)
+    tail = torch.randn(K - 1, C, generator=g_)                  # fp32 values that bf16 cannot hold
+    assert not torch.equal(tail.to(torch.bfloat16).float(), tail)
+    w = 0.5 * torch.randn(C, K, generator=g_)
+    u, new_tail = backend_ref.causal_conv1d(x, tail, w)
+    b_out, _ = brute.conv_silu(x.double().numpy(), tail.double().numpy(), w.double().numpy())
+    assert u.dtype == torch.float32 and new_tail.dtype == torch.float32
+    assert rel_err(u, b_out) < 1e-6
+    assert torch.equal(new_tail, torch.cat([tail, x.float()])[-(K - 1):])
+    # T < K - 1: the carried old rows keep their fp32 bits
+    _, short = backend_ref.causal_conv1d(x[:1], tail, w)
+    assert torch.equal(short, torch.cat([tail[1:], x[:1].float()]))
+    u_rounded, _ = ops_ref.causal_conv1d(x, tail, w)            # the unwidened call rounds the tail to bf16
+    assert rel_err(u_rounded.float(), b_out) > 1e-4
+
+
 def test_l2norm_is_transformers_l2norm():
     from transformers.models.qwen3_5 import modeling_qwen3_5 as hf
     x = torch.randn(5, 16, 128)
