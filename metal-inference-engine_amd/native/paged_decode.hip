@@ -151,9 +151,10 @@ __device__ int plan_prefix(const DecodeArgs& a, int* P, int* Ls = nullptr, int* 
 // First cost unit of workgroup w's range (Uc cost units over NW workgroups).
 __device__ __forceinline__ int range_lo(int Uc, int NW, int w) { return (int)((long long)Uc * w / NW); }
 
-// Sequence of global tile g (0 <= g < P[B], g the same in every lane): the largest b in [0, B) with P[b] <= g,
-// which has P[b + 1] > g. P is non-decreasing from P[0] = 0, so b = #{b' in [1, B) : P[b'] <= g}: one ballot per 64
-// sequences, with independent LDS reads (a binary search would chain log2(B) dependent ones).
+// Sequence of global tile g (0 <= g <= P[B], g the same in every lane): the largest b in [0, B) with P[b] <= g,
+// which for g < P[B] has P[b + 1] > g; g = P[B] (the end of the last range) gives B - 1. P is non-decreasing from
+// P[0] = 0, so b = #{b' in [1, B) : P[b'] <= g}: one ballot per 64 sequences, with independent LDS reads (a binary
+// search would chain log2(B) dependent ones). tile_at calls it on the cost sums V with v up to V[B] inclusive.
 __device__ __forceinline__ int seq_of_tile(const int* P, int B, int g) {
     const int lane = threadIdx.x & 63;
     int b = 0;

@@ -472,9 +472,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // pieces to finish reads all of them back in piece order and combines them: m = max m_p,
     // l = sum 2^(m_p - m) l_p, o = sum 2^(m_p - m) o_p, so the result depends only on the pieces, not on which
     // finishes last. It then leaves the counter at zero and goes on to the normal output below.
-    // The records go through a buffer resource of exactly one record with the sc1 cache policy (the bit that
-    // agent-scope atomic loads and stores carry: coherent across the device's L2s), as 16-byte transfers issued
-    // back to back, with one wait per piece; the stores complete (vmcnt 0) before the wave counts itself in.
+    // Memory ordering. The records go through a buffer resource of exactly one record with the sc1 cache policy:
+    // the bit the compiler puts on agent-scope atomic stores and loads for gfx950, which makes each 16-byte store
+    // and load an access at the device's coherence point rather than in one XCD's L2 alone. The protocol is
+    // therefore: agent-scope stores of the records, a wait for their completion (s_waitcnt vmcnt(0): a store
+    // counts as complete once the coherence point has it), an agent-scope atomic increment of the counter issued
+    // only after that wait, and, in the wave whose increment returns pieces - 1, agent-scope loads issued only
+    // after the increment returned. Every piece's records are thus complete at the coherence point before the
+    // counter can reach its final value, and the reader's loads fetch them from there. A release / acquire pair on
+    // the counter would give the same order through the memory model, but at agent scope on gfx950 it emits a
+    // write-back of the writer's whole L2 (buffer_wbl2) and an invalidate of the reader's (buffer_inv) at every
+    // arrival; these records are never held dirty in an L2, so the completion wait is the part of the release
+    // that they need. tests/test_gpu_prefill.py (split blocks, several pieces per block, repeated calls) checks
+    // the combined output against the oracle and across calls.
     const int piece = we[4] >> 16, pieces = we[4] & 0xffff;
     const int first = we[3] >= 0 && piece < pieces && we[3] + pieces <= a.n_slots ? we[3] : -1;   // slots in range
     if (first >= 0) {
@@ -805,7 +815,7 @@ __global__ __launch_bounds__(512) void prefill_attention_f32(PrefillArgs a) {
     if (!active) return;
 
     // Split items: the piece's (o, m, l) per (slot, head, half) of 16 queries, then the arrival count; the last piece
-    // combines all of them in piece order (the protocol of prefill_attention above).
+    // combines all of them in piece order (the protocol and memory ordering of prefill_attention above).
     const int piece = we[4] >> 16, pieces = we[4] & 0xffff;
     const int first = we[3] >= 0 && piece < pieces && we[3] + pieces <= a.n_slots ? we[3] : -1;
     if (first >= 0) {

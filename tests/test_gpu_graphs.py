@@ -1,8 +1,10 @@
-"""HIP graph replays of the decode-step launches that keep state between calls (the linears' arrival counters, the
-paged decode's workspace): a chain of a residual linear with tile sums of squares, the RMSNorm fused into the next
-linear, the SwiGLU down projection with its sums, and config-3 paged decode with the gate, captured once and
-replayed three times with eager calls of the same launches (which share the counters) in between. Every replay must
-give the eager bits: the counters come back to zero after every launch, and nothing in the chain is a memset."""
+"""HIP graph replays of the launches that keep state between calls (the linears' arrival counters, the paged decode's
+workspace, the chunked delta rule's workspace): a chain of a residual linear with tile sums of squares, the RMSNorm
+fused into the next linear, the SwiGLU down projection with its sums, and config-3 paged decode with the gate,
+captured once and replayed three times with eager calls of the same launches (which share the counters) in between;
+and two chunked-delta calls on different inputs through one workspace, the second consuming the first's state.
+Every replay must give the eager bits: the counters come back to zero after every launch, nothing in the chain is a
+memset, and no launch starts before the one it depends on has finished."""
 import pytest
 import torch
 
@@ -83,3 +85,65 @@ def test_replay_after_the_workspace_grew():
         assert torch.equal(out, want), f"replay {rep}"
         assert all(torch.isnan(j).all() for j in junk)              # the replay wrote nothing into them
         assert torch.equal(decode(), want)                          # eager, on the grown buffer
+
+
+def test_chunked_delta_calls_replay_in_order():
+    """Two config-4-sized rk_gated_delta_chunked calls on different inputs, both on one workspace (each call's prep
+    writes the T / coefficient records its scan reads) and one state (the second call consumes what the first
+    leaves), captured in one HIP graph twice over (A, B, A, B). Every replay gives the eager bits. A replay in which
+    a call's prep started while the previous call's scan was still reading the workspace, or a scan before the
+    previous scan had written the state, would change them: the inputs differ, so the records differ."""
+    from native import kernels
+    from native.rocm_native import load
+    lib = load()
+    g = torch.Generator().manual_seed(43)
+    cases = [wl.c4_chunked_delta(seed=s).to(DEV) for s in (41, 42)]
+    N, H, dk = cases[0].q.shape
+    dv = cases[0].v.shape[2]
+    cu = cases[0].cu_seqlens
+    cuc = [0]
+    for lo, hi in zip(cu, cu[1:]):
+        cuc.append(cuc[-1] + -(-(hi - lo) // kernels.DELTA_CHUNK))
+    n = len(cu) - 1
+    meta = torch.tensor(cu + cuc, dtype=torch.int32).to(DEV)
+    ws = torch.empty(lib.lib.rk_gated_delta_workspace_bytes(cuc[-1], H), dtype=torch.uint8, device=DEV)
+    S0 = (0.05 * torch.randn(n, H, dk, dv, generator=g)).to(DEV)
+    S = S0.clone()
+    outs = [torch.empty(N, H, dv, device=DEV) for _ in range(4)]
+
+    def call(c, out):
+        lib.call("rk_gated_delta_chunked", out.data_ptr(), S.data_ptr(), S.stride(0), c.q.data_ptr(), c.k.data_ptr(),
+                 c.v.data_ptr(), 1, c.beta.data_ptr(), c.g.data_ptr(), meta.data_ptr(), meta.data_ptr() + 4 * (n + 1),
+                 None, n, cuc[-1], H, dk, dv, ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+
+    def chain():
+        for i in range(4):
+            call(cases[i % 2], outs[i])
+
+    chain()
+    torch.cuda.synchronize()
+    want = [o.clone() for o in outs] + [S.clone()]
+    assert not torch.equal(want[0], want[2])              # the second A call starts from another state
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        S.copy_(S0)
+        chain()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain()
+    for rep in range(3):
+        S.copy_(S0)
+        ws.fill_(0xFF)                                    # stale records: NaN patterns, never read
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (got, ref) in enumerate(zip(outs + [S], want)):
+            assert torch.equal(got, ref), f"replay {rep}: {'output ' + str(i) if i < 4 else 'state'}"
+        S.copy_(S0)
+        chain()                                           # the same launches eagerly between replays
+        torch.cuda.synchronize()
+        for got, ref in zip(outs + [S], want):
+            assert torch.equal(got, ref)
