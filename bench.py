@@ -145,7 +145,10 @@ def cpu_time(fn, runs: int = 3) -> tuple[float, int, float]:
     return statistics.median(ts), len(ts), sum(ts)
 
 
-def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
+PLAN_LAYERS = 6     # full-attention layers of Qwen3.5-2B: the decode-step layers that share one batch layout plan
+
+
+def bench_paged_decode(case, args, backend, workload_name: str, config: dict, plan_layers: int = 0):
     import torch
     from native import kernels
     from native.rocm_native import load
@@ -161,44 +164,74 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
     torch.cuda.synchronize()
     B, Hq, d = case.q.shape
     it = [0]
+    NB0, bs0, Hkv0, _ = case.k_pool.shape
 
-    def step():
+    def call():
         c = sets[it[0] % len(sets)]
         it[0] += 1
         backend.paged_attention(c.q, c.k_pool, c.v_pool, c.tables, c.lens, c.block_size, c.window, gate=c.gate)
 
+    def make_plan(c):
+        return backend.decode_plan(c.tables, c.lens, c.block_size, Hq, Hkv0, d, NB0, c.window)
+
+    def planned_step():
+        # one decode step's attention work: the batch layout plan once, then the model's attention layers, each on
+        # its own pool (the sets alternate, so consecutive layers never re-read a cache), all with that plan
+        c0 = sets[0]                                 # the step's tables and lens, shared by its layers
+        plan = make_plan(c0)
+        for layer in range(plan_layers):
+            c = sets[(it[0] + layer) % len(sets)]
+            backend.paged_attention(c.q, c.k_pool, c.v_pool, c0.tables, c0.lens, c.block_size, c.window, gate=c.gate,
+                                    plan=plan)
+        it[0] += plan_layers
+
+    per = plan_layers if plan_layers else 1
+    step = planned_step if plan_layers else call
     settle(step, stream)
     log(f"[bench] {workload_name}: timing {args.steps} steps after {args.warmup} warm-up")
-    eager_ms = time_region(step, args.steps, args.warmup, stream)
+    eager_ms = time_region(step, args.steps, args.warmup, stream) / per
     t = time.perf_counter()
     for _ in range(args.steps):
         step()
-    host_us = (time.perf_counter() - t) / args.steps * 1e6
+    host_us = (time.perf_counter() - t) / (args.steps * per) * 1e6
     torch.cuda.synchronize()
-    ms = graph_time(step, args.steps, stream)
+    ms = graph_time(step, args.steps, stream) / per
+    single_ms = graph_time(call, args.steps, stream) if plan_layers else ms
 
-    # the split-K launch alone: back-to-back launches through the C ABI with prebuilt arguments
+    # the split-K launch alone: back-to-back launches through the C ABI with prebuilt arguments (with the step's
+    # plan when the step has one: the plan is made once per step, outside the layers' split launches)
     lib = load()
     outs = [torch.empty(B, Hq, d, device=dev) for _ in sets]
     NB, bs, Hkv, _ = case.k_pool.shape
     max_nb = case.tables.shape[1]
     need = lib.lib.rk_paged_decode_workspace_bytes(B, Hq, Hkv, d, bs, max_nb)
     ws = kernels.workspace(dev, need)
-    argsets = [(0, o.data_ptr(), c.q.data_ptr(), c.k_pool.data_ptr(), c.v_pool.data_ptr(),
-                kernels.DTYPE_CODES[c.k_pool.dtype], c.tables.data_ptr(), c.lens.data_ptr(), B, Hq, Hkv, d, bs, max_nb,
-                NB, int(c.window or 0), c.gate.data_ptr(), c.gate.stride(0), ws.data_ptr(), ws.numel(),
-                stream.cuda_stream)
-               for o, c in zip(outs, sets)]
+    plan = make_plan(sets[0]) if plan_layers else None
+    pl = (plan.buf.data_ptr(), plan.buf.numel()) if plan is not None else (None, 0)
+
+    def argsets_for(pl):
+        t = sets[0]                                  # one batch layout (tables, lens) for every pool copy
+        return [(0, o.data_ptr(), c.q.data_ptr(), c.k_pool.data_ptr(), c.v_pool.data_ptr(),
+                 kernels.DTYPE_CODES[c.k_pool.dtype], t.tables.data_ptr(), t.lens.data_ptr(), B, Hq, Hkv, d, bs,
+                 max_nb, NB, int(c.window or 0), c.gate.data_ptr(), c.gate.stride(0), *pl, ws.data_ptr(),
+                 ws.numel(), stream.cuda_stream)
+                for o, c in zip(outs, sets)]
     fn = lib.lib.rk_paged_decode_phase
-    j = [0]
 
-    def split():
-        a = argsets[j[0] % len(argsets)]
-        j[0] += 1
-        if fn(*a) != 0:
-            raise RuntimeError(lib.last_error())
+    def split_of(argsets):
+        j = [0]
 
-    split_ms = time_region(split, args.steps, args.warmup, stream)
+        def split():
+            a = argsets[j[0] % len(argsets)]
+            j[0] += 1
+            if fn(*a) != 0:
+                raise RuntimeError(lib.last_error())
+        return split
+
+    split_ms = time_region(split_of(argsets_for(pl)), args.steps, args.warmup, stream)
+    split_unplanned_ms = time_region(split_of(argsets_for((None, 0))), args.steps, args.warmup, stream) \
+        if plan_layers else split_ms
+    plan_ms = graph_time(lambda: make_plan(sets[0]), args.steps, stream) if plan_layers else 0.0
     ceiling = block_stream_ceiling(case, sets, args, stream) if getattr(args, "ceiling", False) else None
     kv = case.kv_bytes()
     split_bytes = kv + B * Hq * d * 4 + 4 * case.table_entries() + 4 * B
@@ -207,6 +240,10 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
     log(f"[bench] {workload_name}: step {ms * 1e3:.1f} us in a graph ({step_gbs:.0f} GB/s algorithmic), "
         f"{eager_ms * 1e3:.1f} us eager (host {host_us:.1f} us per call), split kernel {split_ms * 1e3:.1f} us "
         f"({achieved:.0f} GB/s)")
+    if plan_layers:
+        log(f"[bench] {workload_name}: per layer call with the step's plan shared by {plan_layers} layers; "
+            f"plan {plan_ms * 1e3:.1f} us per step, one call without a plan {single_ms * 1e3:.1f} us, split kernel "
+            f"without a plan {split_unplanned_ms * 1e3:.1f} us")
 
     cpu = None
     if not args.no_cpu:
@@ -232,8 +269,14 @@ def bench_paged_decode(case, args, backend, workload_name: str, config: dict):
         "hbm_gbs_step": step_gbs, "hbm_frac_step": step_gbs / HBM_PEAK_GBS,
         "timing": "value and ms_per_step: K steps captured in one HIP graph, replayed between two events behind one "
                   "untimed replay (after about 60 ms of untimed steps to settle the clock); eager_ms_per_step: the "
-                  "same K calls issued from Python",
+                  "same K steps issued from Python" + (
+                      f"; a step is one decode step's attention work for a model with {plan_layers} attention "
+                      f"layers: the batch layout plan (rk_paged_decode_plan) once, then {plan_layers} paged "
+                      f"attention calls over alternating pools that read it; ms_per_step is per attention-layer call "
+                      f"(the step's time / {plan_layers})" if plan_layers else ""),
         "eager_ms_per_step": eager_ms, "host_us_per_call": host_us,
+        **({"plan": {"layers_per_plan": plan_layers, "plan_ms": plan_ms, "single_call_ms": single_ms,
+                     "split_ms_without_plan": split_unplanned_ms}} if plan_layers else {}),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(f"paged_decode_split/{workload_name}"),
                      "kernel": "paged_decode_split", "bytes_per_launch": split_bytes, "avg_ms": split_ms},
@@ -944,7 +987,7 @@ def main() -> int:
                               "block 16, lengths U[128, 8192], pool 1.25 x positions, sigmoid gate",
                   "batch": 64, "total_positions": int(lens.sum()), "num_blocks": int(case.k_pool.shape[0]),
                   "kv_bytes": case.kv_bytes()}
-        return bench_paged_decode(case, args, backend, "c3", config)
+        return bench_paged_decode(case, args, backend, "c3", config, plan_layers=PLAN_LAYERS)
 
     def c1():
         case = wl.c1_paged_decode()

@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 14
+#define RK_ABI_VERSION 15
 
 /* status codes */
 #define RK_OK 0
@@ -73,12 +73,33 @@ int rk_paged_decode_noalloc(float* out, const float* q, const void* k_pool, cons
                             const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
                             int max_nb, int num_blocks, int window, const float* gate, long long gate_ld,
                             void* stream);
+/* The batch layout plan of a decode step. Every attention layer of a step decodes the same batch: the same block
+ * tables and lengths (src/state.py:119-129 builds them once per step; src/models/qwen3_5.py:263 and
+ * src/models/cohere2.py:263-271 pass them to each layer). rk_paged_decode_plan turns them, once, into what the split
+ * kernel otherwise derives at the start of every call: the tiles' prefix sums, each split workgroup's range and
+ * each wave group's first 64 tiles with their physical blocks. rk_paged_decode_planned then issues its first K / V
+ * loads after a single 16-byte load. No counterpart in the reference (its Metal kernel has no split partition).
+ *   plan: device int32, rk_paged_decode_plan_ints(...) ints, 16-byte aligned, written by rk_paged_decode_plan for
+ *   the same tables, lens, window and shape arguments as the decode calls that read it (a plan for other lengths
+ *   gives wrong outputs, but every index it supplies is clamped into the batch, the tables and the pool). */
+size_t rk_paged_decode_plan_ints(int B, int Hq, int Hkv, int D, int block_size, int max_nb);
+int rk_paged_decode_plan(int32_t* plan, size_t plan_ints, const int32_t* tables, const int32_t* lens, int B, int Hq,
+                         int Hkv, int D, int block_size, int max_nb, int num_blocks, int window, void* stream);
+/* rk_paged_decode reading a plan of rk_paged_decode_plan instead of deriving the layout itself: the same partition,
+ * the same arithmetic and order, bit-identical outputs. */
+int rk_paged_decode_planned(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                            const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
+                            int max_nb, int num_blocks, int window, const float* gate, long long gate_ld,
+                            const int32_t* plan, size_t plan_ints, void* workspace, size_t workspace_bytes,
+                            void* stream);
 /* The two launches of rk_paged_decode, separately (phase 0: split-K partials into the workspace; phase 1: merge,
- * gate, write out). Used to time the dominant phase on its own; rk_paged_decode == phase 0 then phase 1. */
+ * gate, write out), with an optional plan (NULL: derived in the kernels). Used to time the dominant phase on its
+ * own; rk_paged_decode == phase 0 then phase 1 without a plan. */
 int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
                           int kv_dtype, const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D,
                           int block_size, int max_nb, int num_blocks, int window, const float* gate,
-                          long long gate_ld, void* workspace, size_t workspace_bytes, void* stream);
+                          long long gate_ld, const int32_t* plan, size_t plan_ints, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* ---- paged KV cache write (scatter) and read (gather)
  * rk_kv_write replaces PagedKVPool.write_batch / PagedSequence.write (src/state.py:131-134, 163-170):

@@ -79,14 +79,20 @@ class RocmBackend:
         return w.to(device=self.device, dtype=self.weight_dtype)
 
     # ---- P1: decode attention
-    def paged_attention(self, q, k_pool, v_pool, tables, lens, block_size, window=None, gate=None):
+    def paged_attention(self, q, k_pool, v_pool, tables, lens, block_size, window=None, gate=None, plan=None):
         """q [B, Hq, d]; k_pool / v_pool one layer [blocks, bs, Hkv, d] (fp32 or bf16, read in place); tables
         [B, max_nb] int32; lens [B] int32 -> [B, Hq, d] fp32. gate [B, Hq * d] (optional): the sigmoid output gate of
-        src/models/qwen3_5.py:271 applied in the same launch sequence."""
+        src/models/qwen3_5.py:271 applied in the same launch sequence. plan (optional): decode_plan of this step's
+        tables and lens, shared by the step's attention layers (same bits, a shorter start per call)."""
         if k_pool.dtype != v_pool.dtype or k_pool.dtype not in KV_DTYPES:
             raise TypeError(f"paged_attention: keys and values must both be float32 or bfloat16, not "
                             f"{k_pool.dtype} / {v_pool.dtype}")
-        return kernels.paged_decode(q, k_pool, v_pool, tables, lens, block_size, window, gate)
+        return kernels.paged_decode(q, k_pool, v_pool, tables, lens, block_size, window, gate, plan=plan)
+
+    def decode_plan(self, tables, lens, block_size, n_heads, n_kv_heads, head_dim, num_blocks, window=None):
+        """The batch layout plan of a decode step (rk_paged_decode_plan), made once from the step's tables and lens
+        and passed to every paged_attention of the step (its attention layers all decode the same batch)."""
+        return kernels.decode_plan(tables, lens, block_size, n_heads, n_kv_heads, head_dim, num_blocks, window)
 
     def attention(self, q, k, v, causal=True, window=None):
         """Backend.attention (src/backend/base.py:32-35): q [T, Hq, d], k/v [S, Hkv, d] -> [T, Hq, d] fp32; query i

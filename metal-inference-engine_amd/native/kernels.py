@@ -73,12 +73,47 @@ def device_cus(dev: torch.device) -> int:
     return _cus[idx]
 
 
+class DecodePlan:
+    """A decode step's batch layout plan (rk_paged_decode_plan): made once from the step's block tables and lengths,
+    read by every attention layer's paged_decode of that step. It records the layout it was made for; paged_decode
+    refuses it for another one. It does not follow later writes into the same tables / lens tensors: make a new
+    plan whenever they change (every decode step)."""
+
+    def __init__(self, buf: torch.Tensor, key: tuple):
+        self.buf, self.key = buf, key
+
+
+def _plan_key(tables, lens, block_size, Hq, Hkv, d, num_blocks, window):
+    return (tables.data_ptr(), lens.data_ptr(), tuple(tables.shape), int(block_size), int(Hq), int(Hkv), int(d),
+            int(num_blocks), int(window or 0))
+
+
+def decode_plan(tables, lens, block_size: int, Hq: int, Hkv: int, d: int, num_blocks: int,
+                window: int | None = None) -> DecodePlan:
+    """rk_paged_decode_plan: the split partition and each wave group's first tiles of one decode step's batch
+    (tables [B, max_nb] int32, lens [B] int32 on the device) for pools of num_blocks blocks of block_size positions,
+    Hq / Hkv heads of head_dim d; one launch, no host sync."""
+    name = "decode_plan"
+    B, max_nb = tables.shape
+    if lens.shape != (B,) or tables.dtype != torch.int32 or lens.dtype != torch.int32:
+        raise ValueError(f"{name}: tables {tuple(tables.shape)} {tables.dtype}, lens {tuple(lens.shape)} {lens.dtype}")
+    dev = _need_cuda(name, tables, lens)
+    _contig(name, tables, "tables"); _contig(name, lens, "lens")
+    lib = load()
+    n = lib.lib.rk_paged_decode_plan_ints(B, Hq, Hkv, d, block_size, max_nb)
+    buf = torch.empty(n, dtype=torch.int32, device=dev)
+    lib.call("rk_paged_decode_plan", buf.data_ptr(), n, tables.data_ptr(), lens.data_ptr(), B, Hq, Hkv, d,
+             int(block_size), max_nb, int(num_blocks), int(window or 0), _stream(dev))
+    return DecodePlan(buf, _plan_key(tables, lens, block_size, Hq, Hkv, d, num_blocks, window))
+
+
 def paged_decode(q, k_pool, v_pool, tables, lens, block_size: int, window: int | None = None, gate=None,
-                 out=None, phase: int | None = None) -> torch.Tensor:
+                 out=None, phase: int | None = None, plan: DecodePlan | None = None) -> torch.Tensor:
     """Batched decode attention over one layer of a paged pool (rk_paged_decode). q [B, Hq, d] -> [B, Hq, d] fp32.
     k_pool / v_pool [num_blocks, block_size, Hkv, d] fp32 or bf16; tables [B, max_nb] int32; lens [B] int32;
-    gate None or [B, Hq * d] (out *= sigmoid(gate); rows may be strided). phase 0 / 1 runs one of the two launches
-    (for timing)."""
+    gate None or [B, Hq * d] (out *= sigmoid(gate); rows may be strided). plan: the step's decode_plan for these
+    tables and lens (rk_paged_decode_planned; the same bits, a shorter start). phase 0 / 1 runs one of the two
+    launches (for timing)."""
     name = "paged_attention"
     if k_pool.dtype != v_pool.dtype or k_pool.dtype not in KV_DTYPES:
         raise TypeError(f"{name}: keys and values must both be float32 or bfloat16, not "
@@ -113,14 +148,19 @@ def paged_decode(q, k_pool, v_pool, tables, lens, block_size: int, window: int |
     max_nb = tables.shape[1]
     need = lib.lib.rk_paged_decode_workspace_bytes(B, Hq, Hkv, d, bs, max_nb)
     ws = workspace(dev, need)
-    args = (out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype],
+    if plan is not None and plan.key != _plan_key(tables, lens, bs, Hq, Hkv, d, NB, window):
+        raise ValueError(f"{name}: the plan was made for another batch layout or shape")
+    head = (out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), DTYPE_CODES[k_pool.dtype],
             tables.data_ptr(), lens.data_ptr(), B, Hq, Hkv, d, bs, max_nb, NB, int(window or 0),
-            gate.data_ptr() if gate is not None else None, gate.stride(0) if gate is not None else 0, ws.data_ptr(),
-            ws.numel(), _stream(dev))
-    if phase is None:
-        lib.call("rk_paged_decode", *args)
+            gate.data_ptr() if gate is not None else None, gate.stride(0) if gate is not None else 0)
+    tail = (ws.data_ptr(), ws.numel(), _stream(dev))
+    pl = (plan.buf.data_ptr(), plan.buf.numel()) if plan is not None else (None, 0)
+    if phase is not None:
+        lib.call("rk_paged_decode_phase", int(phase), *head, *pl, *tail)
+    elif plan is not None:
+        lib.call("rk_paged_decode_planned", *head, *pl, *tail)
     else:
-        lib.call("rk_paged_decode_phase", int(phase), *args)
+        lib.call("rk_paged_decode", *head, *tail)
     return out
 
 

@@ -69,6 +69,7 @@ inline long long tile_upper(int B, int block_size, int max_nb) {
 }
 
 struct DecodeArgs {
+    const int32_t* plan;  // the batch layout plan of rk_paged_decode_plan, or null (computed in the kernels)
     float* part;
     float* out;
     const float* q;
@@ -246,6 +247,18 @@ struct KVLoad<float> {
 // prefix sums [B + 1].
 constexpr int seq_lds_bytes(int B) { return ((3 * B + 2) * 4 + 15) & ~15; }
 
+// The batch layout plan (rk_paged_decode_plan), int32: a header of kPlanHdr ints (U, Uc, NW, NG, B, by_cost,
+// max_nb, block_size), then the per-sequence arrays in the split kernel's LDS layout (P [B + 1], Ls [B], V [B + 1],
+// padded to seq_lds_bytes), then per split workgroup w {lo, hi, bA, bZ} (its tile range and first / last
+// sequence), then per (w, group g) the group's first 64 tile list entries, one int4 {b, tpos, L, blk} per lane
+// (b = -1: no tile): what the split kernel otherwise derives from the lengths and the block table before its first
+// K / V load. The entries start 16-byte aligned.
+constexpr int kPlanHdr = 8;
+constexpr int plan_seq_ints(int B) { return seq_lds_bytes(B) / 4; }
+inline size_t plan_ints(int B, int NW, int NG) {
+    return kPlanHdr + plan_seq_ints(B) + 4 * (size_t)NW + (size_t)4 * 64 * NW * NG;
+}
+
 // LDS bytes one wave of the split kernel uses: the query A operands (NT x NIT x 64 lanes x 16 B), the 16 x GP
 // probabilities of the current tile and the GP rescale factors.
 template <int D, int GP>
@@ -310,6 +323,59 @@ __device__ __forceinline__ TileRows<NVI, TPI, LPT, ALIGNED> tile_rows(const Deco
     return r;
 }
 
+// Group g's share of split workgroup w's tile range [lo, hi) (first / last sequences bA, bZ), and the entries of the
+// group's tile list: within each sequence segment of the range the group takes the segment's tiles g, g + NG, ...;
+// entry e of the list is (sequence, first position, clamped length, first visible position, physical block). The
+// split kernel and the plan kernel both derive their entries here, so a plan holds exactly what the split kernel
+// would compute itself.
+struct GroupRange {
+    const int* P;           // tile prefix sums [B + 1]
+    const int* Ls;          // clamped lengths [B]
+    int lo, hi, bA, bZ, g, NG;
+    __device__ int seg_lo(int b) const { const int x = P[b]; return (x > lo ? x : lo) - lo; }
+    __device__ int seg_hi(int b) const { const int x = P[b + 1]; return (x < hi ? x : hi) - lo; }
+    __device__ int count(int b) const {
+        const int len = seg_hi(b) - seg_lo(b);
+        return len > g ? (len - g + NG - 1) / NG : 0;
+    }
+    __device__ int total() const {
+        int t = 0;
+        for (int b = bA; b <= bZ; ++b) t += count(b);
+        return t;
+    }
+};
+
+struct TileEntry {
+    int b, tpos, L, s0, blk;
+};
+
+// Entry e (clamped to [0, total)) of the group's tile list; bA .. bZ is the same in every lane, so the loop is
+// uniform and each lane keeps the segment holding its entry.
+template <bool ALIGNED>
+__device__ __forceinline__ TileEntry tile_entry(const DecodeArgs& a, const GroupRange& r, int e, int total) {
+    e = e < total ? e : total - 1;
+    int b = r.bA, k = 0;
+    for (int bb = r.bA; bb <= r.bZ; ++bb) {
+        const int c = r.count(bb);
+        if (e >= 0 && e < c) { b = bb; k = e; }
+        e -= c;
+    }
+    const int gt = r.lo + r.seg_lo(b) + r.g + k * r.NG;   // global tile
+    TileEntry x;
+    x.b = b;
+    x.L = r.Ls[b];
+    x.s0 = (a.window > 0 && x.L > a.window) ? x.L - a.window : 0;
+    x.tpos = (x.s0 / kTile + gt - r.P[b]) * kTile;
+    x.blk = 0;
+    if (ALIGNED) {
+        int ti = x.tpos / a.bs;                          // < ceil(L / bs) <= max_nb for a consistent plan
+        ti = ti < 0 ? 0 : (ti >= a.max_nb ? a.max_nb - 1 : ti);
+        const int blk = a.tables[(long long)b * a.max_nb + ti];
+        x.blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+    }
+    return x;
+}
+
 // One workgroup = NG groups of Hkv waves (NG = WPG / Hkv, WPG = waves_per_group()); wave g * Hkv + k serves
 // kv-head k for group g. The Hkv waves of a group walk the same tiles, so both halves of every interleaved pool row ([bs][Hkv][D]) are
 // fetched together. Within each sequence segment of the workgroup's range, group g takes the segment's tiles
@@ -362,50 +428,22 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < NT * NIT; ++i) qop[i * 64 + lane] = u32x4{0u, 0u, 0u, 0u};
     };
-    if (wave == 0) plan_prefix(a, P, Ls, V);
-    zero_q();
-    __syncthreads();
-    const int U = P[a.B], Uc = V[a.B];
-    const bool by_cost = U >= kSegMinTiles * a.NW;   // uniform: U and NW are the same in every workgroup
-    const int lo = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w)) : range_lo(U, a.NW, w);
-    const int hi = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w + 1)) : range_lo(U, a.NW, w + 1);
-    if (lo >= hi) return;                            // uniform over the workgroup: no barrier is left waiting
-    const int bA = seq_of_tile(P, a.B, lo), bZ = seq_of_tile(P, a.B, hi - 1);
-
-    // segment of sequence b inside the range: range-relative tiles [sa, sb); group g's tiles in it
-    auto seg_lo = [&](int b) { const int x = P[b]; return (x > lo ? x : lo) - lo; };
-    auto seg_hi = [&](int b) { const int x = P[b + 1]; return (x < hi ? x : hi) - lo; };
-    auto my_count = [&](int b) {
-        const int len = seg_hi(b) - seg_lo(b);
-        return len > g ? (len - g + NG - 1) / NG : 0;
+    typename LD::Vec kv[KB], vv[VB];
+    TileRows<NVI, TPI, LPT, ALIGNED> cur;
+    // issue order K then V, here and in the loop, so that waiting for a tile's keys never waits for its values
+    // (the scheduling barriers keep the compiler from reordering the two groups of loads)
+    auto issue_first = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int it = 0; it < KB; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int vi = 0; vi < VB; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
+        __builtin_amdgcn_sched_barrier(0);
     };
-    int my_total = 0;
-    for (int b = bA; b <= bZ; ++b) my_total += my_count(b);
-
     // per-lane description of this group's tile list entry j0 + lane: sequence, first position, clamped length,
     // first visible position and (ALIGNED) physical block
     int b_l = 0, tpos_l = 0, L_l = 0, s0_l = 0, blk_l = 0;
-    auto refill = [&](int j0) {
-        int e = j0 + lane;
-        e = e < my_total ? e : my_total - 1;
-        int b = bA, k = 0;
-        for (int bb = bA; bb <= bZ; ++bb) {          // uniform loop; each lane keeps the segment holding entry e
-            const int c = my_count(bb);
-            if (e >= 0 && e < c) { b = bb; k = e; }
-            e -= c;
-        }
-        const int gt = lo + seg_lo(b) + g + k * NG;  // global tile
-        const int L = Ls[b];
-        const int s0 = (a.window > 0 && L > a.window) ? L - a.window : 0;
-        b_l = b;
-        L_l = L;
-        s0_l = s0;
-        tpos_l = (s0 / kTile + gt - P[b]) * kTile;
-        if (ALIGNED) {
-            const int blk = a.tables[(long long)b * a.max_nb + tpos_l / a.bs];   // < ceil(L / bs) <= max_nb
-            blk_l = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
-        }
-    };
     auto rows_of = [&](int jj) {
         const int b = __builtin_amdgcn_readlane(b_l, jj);
         const int blk = ALIGNED ? __builtin_amdgcn_readlane(blk_l, jj) : 0;
@@ -414,6 +452,77 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
                                                   __builtin_amdgcn_readlane(L_l, jj),
                                                   __builtin_amdgcn_readlane(tpos_l, jj), blk, kvh, D, lane);
     };
+    bool planned = false;
+    int lo, hi, bA, bZ;
+    if (a.plan) {
+        // With a plan, the group's first 64 tile list entries (one 16-byte load per lane) and the workgroup's range
+        // are all the first tile needs: its K / V loads are issued before the per-sequence arrays are staged and
+        // before the workgroup's barrier, with no block-table load in between. The per-sequence arrays are requested
+        // first, so that staging them waits for them alone (loads complete in issue order). The first loads are
+        // issued unconditionally (a group without tiles reads position 0 of its first table row, unused): a branch
+        // around them would make every later wait a wait for all loads in flight. Entries are clamped into the
+        // batch and the pool, so a plan for other lengths gives wrong numbers but never an access outside them.
+        constexpr int kSeqPer = (plan_seq_ints(kMaxBatch) + 64 * WPG - 1) / (64 * WPG);
+        const int n_seq = plan_seq_ints(a.B);
+        const int32_t* pseq = a.plan + kPlanHdr;
+        const int4 ev = reinterpret_cast<const int4*>(pseq + n_seq + 4 * a.NW)[(w * NG + g) * 64 + lane];
+        const int wv = pseq[n_seq + 4 * w + (lane & 3)];
+        int seqv[kSeqPer];
+#pragma unroll
+        for (int k = 0; k < kSeqPer; ++k) {
+            const int i = threadIdx.x + 64 * WPG * k;
+            seqv[k] = pseq[i < n_seq ? i : n_seq - 1];
+        }
+        const bool has = __builtin_amdgcn_readfirstlane(ev.x) >= 0;
+        const int cap = a.max_nb * a.bs;
+        b_l = has ? (ev.x >= a.B ? a.B - 1 : ev.x) : 0;
+        L_l = has ? (ev.z < 1 ? 1 : (ev.z > cap ? cap : ev.z)) : 1;
+        s0_l = (a.window > 0 && L_l > a.window) ? L_l - a.window : 0;
+        tpos_l = has ? (ev.y < 0 ? 0 : (ev.y >= cap ? (cap - 1) / kTile * kTile : ev.y)) : 0;
+        blk_l = has ? (ev.w < 0 ? 0 : (ev.w >= a.num_blocks ? a.num_blocks - 1 : ev.w)) : 0;
+        cur = rows_of(0);
+        issue_first();
+        planned = has;
+#pragma unroll
+        for (int k = 0; k < kSeqPer; ++k) {
+            const int i = threadIdx.x + 64 * WPG * k;
+            if (i < n_seq) P[i] = seqv[k];           // P, Ls, V
+        }
+        lo = __builtin_amdgcn_readlane(wv, 0);
+        hi = __builtin_amdgcn_readlane(wv, 1);
+        bA = __builtin_amdgcn_readlane(wv, 2);
+        bZ = __builtin_amdgcn_readlane(wv, 3);
+        zero_q();
+        __syncthreads();
+        if (lo >= hi) return;                        // uniform over the workgroup: no barrier is left waiting
+        bA = bA < 0 ? 0 : (bA >= a.B ? a.B - 1 : bA);
+        bZ = bZ < bA ? bA : (bZ >= a.B ? a.B - 1 : bZ);
+    } else {
+        if (wave == 0) plan_prefix(a, P, Ls, V);
+        zero_q();
+        __syncthreads();
+        const int U = P[a.B], Uc = V[a.B];
+        const bool by_cost = U >= kSegMinTiles * a.NW;   // uniform: U and NW are the same in every workgroup
+        lo = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w)) : range_lo(U, a.NW, w);
+        hi = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w + 1)) : range_lo(U, a.NW, w + 1);
+        if (lo >= hi) return;                        // uniform over the workgroup: no barrier is left waiting
+        bA = seq_of_tile(P, a.B, lo);
+        bZ = seq_of_tile(P, a.B, hi - 1);
+    }
+    const GroupRange rg{P, Ls, lo, hi, bA, bZ, g, NG};
+    auto seg_lo = [&](int b) { return rg.seg_lo(b); };
+    auto seg_hi = [&](int b) { return rg.seg_hi(b); };
+    auto my_count = [&](int b) { return rg.count(b); };
+    const int my_total = rg.total();
+
+    auto set_entry = [&](const TileEntry& x) {
+        b_l = x.b;
+        tpos_l = x.tpos;
+        L_l = x.L;
+        s0_l = x.s0;
+        blk_l = x.blk;
+    };
+    auto refill = [&](int j0) { set_entry(tile_entry<ALIGNED>(a, rg, j0 + lane, my_total)); };
 
     float m_run[4], l_run[4];
     float acc[GP][8];
@@ -545,21 +654,13 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     auto part_of = [&](int b) { return a.part + ((long long)(w + b) * a.Hkv + kvh) * REC; };
 
     reset();
-    typename LD::Vec kv[KB], vv[VB];
-    TileRows<NVI, TPI, LPT, ALIGNED> cur;
     int j0 = 0;                                      // first entry held by the lane arrays
     if (my_total > 0) {
-        refill(0);
-        cur = rows_of(0);
-        // issue order K then V, here and in the loop, so that waiting for a tile's keys never waits for its values
-        // (the scheduling barriers keep the compiler from reordering the two groups of loads)
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int it = 0; it < KB; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int vi = 0; vi < VB; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
-        __builtin_amdgcn_sched_barrier(0);
+        if (!planned) {                              // with a plan, entries 0 .. 63 and the first loads are in place
+            refill(0);
+            cur = rows_of(0);
+            issue_first();
+        }
         fetch_q(next_mine(bA - 1));
     }
     int j = 0;                                       // this group's next tile list entry
@@ -725,7 +826,15 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
     const float* grow = a.gate ? a.gate + (long long)b * a.gate_ld + (long long)kvh * a.G * D : nullptr;
     const float4 gv = sl == 0 && grow && ti < n4 ? *reinterpret_cast<const float4*>(grow + 4 * ti)
                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < 64) plan_prefix(a, P, nullptr, V);
+    if (a.plan) {
+        const int32_t* pseq = a.plan + kPlanHdr;
+        for (int i = tid; i <= a.B; i += kMergeThreads) {
+            P[i] = pseq[i];
+            V[i] = pseq[2 * a.B + 1 + i];
+        }
+    } else if (tid < 64) {
+        plan_prefix(a, P, nullptr, V);
+    }
     __syncthreads();
     const int U = P[a.B], pb = P[b], pe = P[b + 1];
     float4* out = reinterpret_cast<float4*>(a.out + obase);
@@ -736,8 +845,13 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
     // the split workgroups' units (cost units or tiles, as the split kernel cut them), the first and last units of b
     const bool by_cost = U >= kSegMinTiles * a.NW;
     const int Uu = by_cost ? V[a.B] : U, u0 = by_cost ? V[b] + kSegCost : pb, u1 = by_cost ? V[b + 1] : pe;
-    const int wf = (int)(((long long)(u0 + 1) * a.NW - 1) / Uu);
-    const int wlast = (int)(((long long)u1 * a.NW - 1) / Uu);
+    if (Uu <= 0) {                                   // only from a plan for other lengths: nothing to merge
+        if (sl == 0 && ti < n4) out[ti] = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    // (clamped to the split grid: a plan for other lengths must not send the loads below past the workspace)
+    const int wf = max(0, min(a.NW - 1, (int)(((long long)(u0 + 1) * a.NW - 1) / Uu)));
+    const int wlast = max(wf, min(a.NW - 1, (int)(((long long)u1 * a.NW - 1) / Uu)));
     // slices in use: one per chunk of partials, up to SL (the rest hold none); partials per slice
     const int npart = wlast - wf + 1;
     const int slr = min(SL, (npart + kMergeCh - 1) / kMergeCh);
@@ -826,6 +940,54 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge(DecodeArgs a
         o.w *= 1.0f / (1.0f + expf(-gv.w));
     }
     out[ti] = o;
+}
+
+// The batch layout plan: split workgroup w's range and each group's first 64 tile list entries, computed by the same
+// functions as the split kernel (one workgroup of NG waves per split workgroup; workgroup 0 also writes the
+// per-sequence arrays and the header). Written once per decode step and read by every attention layer's split and
+// merge launches of that step.
+template <bool ALIGNED>
+__global__ __launch_bounds__(512) void paged_decode_plan(DecodeArgs a, int32_t* plan) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    int* P = reinterpret_cast<int*>(smem);
+    int* Ls = P + a.B + 1;
+    int* V = Ls + a.B;
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6, w = blockIdx.x;
+    if (g == 0) plan_prefix(a, P, Ls, V);
+    __syncthreads();
+    const int U = P[a.B], Uc = V[a.B];
+    const bool by_cost = U >= kSegMinTiles * a.NW;
+    const int lo = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w)) : range_lo(U, a.NW, w);
+    const int hi = by_cost ? tile_at(P, V, a.B, range_lo(Uc, a.NW, w + 1)) : range_lo(U, a.NW, w + 1);
+    const int bA = lo < hi ? seq_of_tile(P, a.B, lo) : 0, bZ = lo < hi ? seq_of_tile(P, a.B, hi - 1) : 0;
+    int32_t* pseq = plan + kPlanHdr;
+    if (w == 0) {
+        for (int i = threadIdx.x; i < plan_seq_ints(a.B); i += blockDim.x) pseq[i] = i < 3 * a.B + 2 ? P[i] : 0;
+        if (threadIdx.x < kPlanHdr) {
+            const int hdr[kPlanHdr] = {U, Uc, a.NW, a.NG, a.B, by_cost ? 1 : 0, a.max_nb, a.bs};
+            int v = 0;
+#pragma unroll
+            for (int i = 0; i < kPlanHdr; ++i) v = (int)threadIdx.x == i ? hdr[i] : v;
+            plan[threadIdx.x] = v;
+        }
+    }
+    if (threadIdx.x < 4) {
+        const int wr[4] = {lo, hi, bA, bZ};
+        int v = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v = (int)threadIdx.x == i ? wr[i] : v;
+        pseq[plan_seq_ints(a.B) + 4 * w + threadIdx.x] = v;
+    }
+    int4 e = make_int4(-1, 0, 0, 0);                 // b = -1: the group has no tile in the range
+    if (lo < hi) {
+        const GroupRange rg{P, Ls, lo, hi, bA, bZ, g, a.NG};
+        const int total = rg.total();
+        if (total > 0) {
+            const TileEntry x = tile_entry<ALIGNED>(a, rg, lane, total);
+            e = make_int4(x.b, x.tpos, x.L, x.blk);
+        }
+    }
+    reinterpret_cast<int4*>(pseq + plan_seq_ints(a.B) + 4 * a.NW)[(w * a.NG + g) * 64 + lane] = e;
 }
 
 typedef void (*SplitFn)(DecodeArgs);
@@ -927,10 +1089,43 @@ size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_
     return workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb, GP));
 }
 
-int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
-                          int kv_dtype, const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D,
-                          int block_size, int max_nb, int num_blocks, int window, const float* gate,
-                          long long gate_ld, void* workspace, size_t workspace_bytes_, void* stream) {
+size_t rk_paged_decode_plan_ints(int B, int Hq, int Hkv, int D, int block_size, int max_nb) {
+    if (B < 1 || Hkv < 1 || Hq < Hkv || block_size < 1 || max_nb < 1) return 0;
+    const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
+    const int wpg = waves_per_group(GP, tile_upper(B, block_size, max_nb));
+    return plan_ints(B, split_groups(B, Hkv, block_size, max_nb, GP), groups_of(Hkv, wpg));
+}
+
+int rk_paged_decode_plan(int32_t* plan, size_t plan_ints_, const int32_t* tables, const int32_t* lens, int B, int Hq,
+                         int Hkv, int D, int block_size, int max_nb, int num_blocks, int window, void* stream) {
+    float dummy = 0.0f;   // validate() checks the pointers the decode itself needs; the plan reads none of these
+    int rc = validate(&dummy, &dummy, &dummy, &dummy, RK_BF16, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                      num_blocks, window);
+    if (rc) return rc;
+    const size_t need = rk_paged_decode_plan_ints(B, Hq, Hkv, D, block_size, max_nb);
+    if (!plan || plan_ints_ < need || reinterpret_cast<uintptr_t>(plan) % 16)
+        return fail(RK_ERR_WORKSPACE, "rk_paged_decode_plan: plan of %zu ints (need %zu, 16-byte aligned)", plan_ints_,
+                    need);
+    const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
+    DecodeArgs a{};
+    a.tables = tables;
+    a.lens = lens;
+    a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.bs = block_size; a.max_nb = max_nb;
+    a.num_blocks = num_blocks; a.window = window;
+    a.NW = split_groups(B, Hkv, block_size, max_nb, GP);
+    a.NG = groups_of(Hkv, waves_per_group(GP, tile_upper(B, block_size, max_nb)));
+    auto fn = block_size % kTile == 0 ? paged_decode_plan<true> : paged_decode_plan<false>;
+    hipLaunchKernelGGL(fn, dim3(a.NW), dim3(64 * a.NG), seq_lds_bytes(B), static_cast<hipStream_t>(stream), a, plan);
+    return check_launch("paged_decode_plan");
+}
+
+namespace rk {
+namespace {
+
+int decode_launch(int phase, float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                  const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
+                  int max_nb, int num_blocks, int window, const float* gate, long long gate_ld, const int32_t* plan,
+                  size_t plan_ints_, void* workspace, size_t workspace_bytes_, void* stream) {
     int rc = validate(out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
                       num_blocks, window);
     if (rc) return rc;
@@ -938,6 +1133,10 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
         return fail(RK_ERR_ARG, "rk_paged_decode: gate rows of %lld elements (>= %d, a multiple of 4, 16-byte "
                     "aligned)", gate_ld, Hq * D);
     if (phase != 0 && phase != 1) return fail(RK_ERR_ARG, "rk_paged_decode_phase: phase %d", phase);
+    if (plan && (plan_ints_ < rk_paged_decode_plan_ints(B, Hq, Hkv, D, block_size, max_nb) ||
+                 reinterpret_cast<uintptr_t>(plan) % 16))
+        return fail(RK_ERR_WORKSPACE, "rk_paged_decode: plan of %zu ints (need %zu, 16-byte aligned)", plan_ints_,
+                    rk_paged_decode_plan_ints(B, Hq, Hkv, D, block_size, max_nb));
     const int G = Hq / Hkv;
     const int GP = G <= 4 ? 4 : 8;
     const int NW = split_groups(B, Hkv, block_size, max_nb, GP);
@@ -946,6 +1145,7 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
         return fail(RK_ERR_WORKSPACE, "rk_paged_decode: workspace %zu bytes < %zu needed", workspace_bytes_, need);
 
     DecodeArgs a;
+    a.plan = plan;
     a.part = static_cast<float*>(workspace);
     a.out = out;
     a.q = q;
@@ -970,6 +1170,31 @@ int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_p
     }
     hipLaunchKernelGGL(pick_merge(D, GP), dim3(B * Hkv), dim3(kMergeThreads), 0, s, a);
     return check_launch("paged_decode_merge");
+}
+
+}  // namespace
+}  // namespace rk
+
+int rk_paged_decode_phase(int phase, float* out, const float* q, const void* k_pool, const void* v_pool,
+                          int kv_dtype, const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D,
+                          int block_size, int max_nb, int num_blocks, int window, const float* gate,
+                          long long gate_ld, const int32_t* plan, size_t plan_ints_, void* workspace,
+                          size_t workspace_bytes_, void* stream) {
+    return decode_launch(phase, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                         num_blocks, window, gate, gate_ld, plan, plan_ints_, workspace, workspace_bytes_, stream);
+}
+
+int rk_paged_decode_planned(float* out, const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                            const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
+                            int max_nb, int num_blocks, int window, const float* gate, long long gate_ld,
+                            const int32_t* plan, size_t plan_ints_, void* workspace, size_t workspace_bytes_,
+                            void* stream) {
+    if (!plan) return fail(RK_ERR_ARG, "rk_paged_decode_planned: null plan");
+    int rc = decode_launch(0, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                           num_blocks, window, gate, gate_ld, plan, plan_ints_, workspace, workspace_bytes_, stream);
+    if (rc) return rc;
+    return decode_launch(1, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                         num_blocks, window, gate, gate_ld, plan, plan_ints_, workspace, workspace_bytes_, stream);
 }
 
 size_t rk_paged_decode_noalloc_max_bytes(void) { return kScratchBytes; }
@@ -1013,11 +1238,11 @@ int rk_paged_decode(float* out, const float* q, const void* k_pool, const void* 
                     const int32_t* tables, const int32_t* lens, int B, int Hq, int Hkv, int D, int block_size,
                     int max_nb, int num_blocks, int window, const float* gate, long long gate_ld, void* workspace,
                     size_t workspace_bytes_, void* stream) {
-    int rc = rk_paged_decode_phase(0, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size,
-                                   max_nb, num_blocks, window, gate, gate_ld, workspace, workspace_bytes_, stream);
+    int rc = decode_launch(0, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                           num_blocks, window, gate, gate_ld, nullptr, 0, workspace, workspace_bytes_, stream);
     if (rc) return rc;
-    return rk_paged_decode_phase(1, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size,
-                                 max_nb, num_blocks, window, gate, gate_ld, workspace, workspace_bytes_, stream);
+    return decode_launch(1, out, q, k_pool, v_pool, kv_dtype, tables, lens, B, Hq, Hkv, D, block_size, max_nb,
+                         num_blocks, window, gate, gate_ld, nullptr, 0, workspace, workspace_bytes_, stream);
 }
 
 }  // extern "C"

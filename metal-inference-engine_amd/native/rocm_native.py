@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 RK_F32, RK_BF16 = 0, 1
 RK_W_BF16, RK_W_INT8, RK_W_INT4 = 1, 2, 3
@@ -28,7 +28,11 @@ SIGNATURES = {
     "rk_paged_decode_workspace_bytes": (c_size_t, [c_int] * 6),
     "rk_paged_decode": (c_int, [P, P, P, P, c_int, P, P] + [c_int] * 8 + [P, c_longlong, P, c_size_t, P]),
     "rk_paged_decode_phase": (c_int, [c_int, P, P, P, P, c_int, P, P] + [c_int] * 8
-                              + [P, c_longlong, P, c_size_t, P]),
+                              + [P, c_longlong, P, c_size_t, P, c_size_t, P]),
+    "rk_paged_decode_plan_ints": (c_size_t, [c_int] * 6),
+    "rk_paged_decode_plan": (c_int, [P, c_size_t, P, P] + [c_int] * 8 + [P]),
+    "rk_paged_decode_planned": (c_int, [P, P, P, P, c_int, P, P] + [c_int] * 8
+                                + [P, c_longlong, P, c_size_t, P, c_size_t, P]),
     "rk_paged_decode_noalloc_max_bytes": (c_size_t, []),
     "rk_paged_decode_noalloc": (c_int, [P, P, P, P, c_int, P, P] + [c_int] * 8 + [P, c_longlong, P]),
     "rk_kv_write": (c_int, [P, P, c_int, P, P, P, c_int] + [c_int] * 5 + [P]),

@@ -164,3 +164,71 @@ def test_ranges_cut_by_cost_with_empty_and_short_sequences(backend):
     sub = wl.PagedDecodeCase(case.q[live], case.gate[live], case.k_pool, case.v_pool, case.tables[live],
                              case.lens[live], case.block_size)
     assert rel_err(got[live], oracle(sub, gate=True)) < 1e-5
+
+
+def planned(backend, case, gate=True):
+    """The same call with the batch layout plan made first (rk_paged_decode_plan -> rk_paged_decode_planned)."""
+    c = case.to(DEV)
+    NB, bs, Hkv, d = c.k_pool.shape
+    plan = backend.decode_plan(c.tables, c.lens, c.block_size, c.q.shape[1], Hkv, d, NB, c.window)
+    out = backend.paged_attention(c.q, c.k_pool, c.v_pool, c.tables, c.lens, c.block_size, c.window,
+                                  gate=c.gate if gate else None, plan=plan)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+PLAN_CASES = {
+    "config3": lambda: wl.c3_paged_decode(),
+    "config1": lambda: wl.c1_paged_decode(),
+    "reference_lengths_bf16": lambda: wl.paged_decode_case(REF_LENS, 32, 8, 2, 256, 16, torch.bfloat16, seed=21),
+    "reference_lengths_fp32_14_2_64": lambda: wl.paged_decode_case(REF_LENS, 32, 14, 2, 64, 16, seed=22),
+    "group8_16_2_128": lambda: wl.paged_decode_case([5, 900, 77, 3000], 400, 16, 2, 128, 16, torch.bfloat16,
+                                                    seed=23),
+    "block_size_4": lambda: wl.paged_decode_case(REF_LENS + [700], 300, 8, 2, 256, 4, torch.bfloat16, seed=24),
+    "block_size_32": lambda: wl.paged_decode_case(REF_LENS + [4000], 300, 16, 4, 128, 32, torch.bfloat16, seed=25),
+    "window_128": lambda: wl.paged_decode_case([3, 130, 700, 5000], 500, 8, 2, 256, 16, torch.bfloat16, seed=26,
+                                               window=128),
+    "by_cost_with_empty": lambda: wl.paged_decode_case(
+        [0, 9000, 1, 0, 7000, 17, 0, 12000, 300, 0, 9000, 16, 8192, 0, 2, 11000, 33, 0, 9500, 5], 6000, 8, 2, 256,
+        16, torch.bfloat16, seed=27),
+    "batch_300": lambda: wl.paged_decode_case([(37 * i) % 2500 + 1 for i in range(300)], 50000, 8, 2, 256, 16,
+                                              torch.bfloat16, seed=28),
+}
+
+
+@pytest.mark.parametrize("name", list(PLAN_CASES))
+def test_plan_gives_the_same_bits(backend, name):
+    """rk_paged_decode_planned reads the partition, the ranges and each group's first tiles from the plan instead of
+    deriving them: the same partition and arithmetic, so bit-identical outputs, over both split instances (8-wave
+    config 3, 4-wave small grids), the group-8 instance, unaligned and larger blocks, a window, ranges cut by cost
+    with empty sequences, and a batch past 64 sequences (per-sequence arrays past one wave's lanes). The workspace
+    is NaN-filled first."""
+    from native import kernels
+    case = PLAN_CASES[name]()
+    want = gpu(backend, case, gate=True)
+    NB, bs, Hkv, d = case.k_pool.shape
+    need = backend.lib.lib.rk_paged_decode_workspace_bytes(case.q.shape[0], case.q.shape[1], Hkv, d, bs,
+                                                           case.tables.shape[1])
+    kernels.workspace(torch.device(DEV), need).view(torch.float32).fill_(float("nan"))
+    got = planned(backend, case, gate=True)
+    assert torch.equal(got, want), name
+
+
+def test_plan_shared_by_layers_and_refused_for_another_layout(backend):
+    """One plan serves several layers' pools with the same tables and lengths (each layer's bits equal its own
+    unplanned call); a plan made for other tables is refused on the host."""
+    from native import kernels
+    case = wl.c3_paged_decode()
+    c = case.to(DEV)
+    NB, bs, Hkv, d = c.k_pool.shape
+    plan = backend.decode_plan(c.tables, c.lens, bs, 8, Hkv, d, NB)
+    g = torch.Generator().manual_seed(29)
+    for layer in range(3):
+        kp = (torch.randn(c.k_pool.shape, generator=g) * (layer + 1)).to(torch.bfloat16).to(DEV)
+        vp = torch.randn(c.v_pool.shape, generator=g).to(torch.bfloat16).to(DEV)
+        a = backend.paged_attention(c.q, kp, vp, c.tables, c.lens, bs, gate=c.gate, plan=plan)
+        b = backend.paged_attention(c.q, kp, vp, c.tables, c.lens, bs, gate=c.gate)
+        assert torch.equal(a, b), f"layer {layer}"
+    other = c.tables.clone()
+    with pytest.raises(ValueError):
+        backend.paged_attention(c.q, c.k_pool, c.v_pool, other, c.lens, bs, plan=plan)
