@@ -634,7 +634,8 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
     KV write are the one fused attention_prep call, the output gate is fused into paged_attention, and (with a
     backend that has silu_mul_linear) SwiGLU's silu * up runs inside the down projection, and (with one that has
     rms_norm_linear) every RMSNorm after the first runs inside the linear that follows it, from the sums of squares
-    the linear before it returned; the sequences' lengths are not advanced (a benchmark replays the same step)."""
+    the linear before it returned; with one that has decode_plan, the attention layers share one batch layout plan;
+    the sequences' lengths are not advanced (a benchmark replays the same step)."""
     cfg = st.cfg
     B = tokens.shape[0]
     slots, tables, lens, positions = layout
@@ -653,6 +654,12 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
         return backend.linear(x, wt, residual=h), None
 
     h = backend.embedding(w["embed_tokens.weight"], tokens)
+    # every attention layer of the step decodes the same batch layout: its plan is made once (with a backend that
+    # has decode_plan) and read by each layer's paged attention
+    plan = None
+    if hasattr(backend, "decode_plan") and any(cfg.is_full(i) for i in range(cfg.layers)):
+        k0 = st.k[st.slot[next(i for i in range(cfg.layers) if cfg.is_full(i))]]
+        plan = backend.decode_plan(tables, lens, cfg.block_size, cfg.Hq, cfg.Hkv, cfg.d, k0.shape[0])
     for i in range(cfg.layers):
         p = f"layers.{i}."
         L = st.slot[i]
@@ -661,7 +668,8 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
             y = norm_linear(h, w[p + "input_layernorm.weight"], w[a + "qkvg.weight"])
             q, gate = backend.attention_prep(y, w[a + "q_norm.weight"], w[a + "k_norm.weight"], cfg.eps, positions,
                                              cfg.theta, cfg.rot, (cfg.Hq, cfg.Hkv, cfg.d), st.k[L], st.v[L], slots)
-            o = backend.paged_attention(q, st.k[L], st.v[L], tables, lens, cfg.block_size, gate=gate)
+            o = backend.paged_attention(q, st.k[L], st.v[L], tables, lens, cfg.block_size, gate=gate,
+                                        **({"plan": plan} if plan is not None else {}))
             h, ss = residual_linear(o.reshape(B, cfg.Hq * cfg.d), w[a + "o_proj.weight"], h)
         else:
             a = p + "linear_attn."
