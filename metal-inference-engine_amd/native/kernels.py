@@ -249,28 +249,39 @@ PREFILL_BLOCK = 32          # queries per work item of rk_paged_prefill
 PREFILL_TILE = 32           # key positions per tile of rk_paged_prefill
 PREFILL_SPLIT_TILES = None  # None: split only when the blocks x KV heads leave CUs idle; an int forces a split size
 PREFILL_MIN_SPLIT = 32      # the smallest automatic piece, in tiles (1024 keys: the merge stays a small fraction)
+PREFILL_BALANCE_PIECES = 4  # balance split: no piece above 1/4 of a CU's share of the tiles
 
 
-def prefill_split_tiles(spans: list[int], heads: int, n_cu: int) -> int:
+def prefill_split_tiles(spans: list[int], heads: int, n_cu: int, balance: bool = False) -> int:
     """The automatic split size of rk_paged_prefill's work list, from the key span (in tiles) of each 32-query
-    block: 0 (no split) when the blocks times the KV heads already give every CU a workgroup, else the size that
-    cuts the total into about one workgroup per CU, at least PREFILL_MIN_SPLIT tiles. A split block costs a partial
-    record per piece and a merge, which only pays where CUs would otherwise idle (one long chunk over a long
-    prefix: a 512-query chunk is 16 blocks, 32 workgroups with 2 KV heads, on 256 CUs)."""
-    if not spans or len(spans) * heads >= n_cu:
+    block. When the blocks times the KV heads (workgroups per block) leave CUs without a workgroup: the size that
+    cuts the total into about one workgroup per CU, at least PREFILL_MIN_SPLIT tiles (one long chunk over a long
+    prefix: a 512-query chunk is 16 blocks, 32 workgroups with 2 KV heads, on 256 CUs). Otherwise 0 (no split),
+    unless balance: then blocks longer than 1/PREFILL_BALANCE_PIECES of a CU's share are cut to that size (at least
+    2 PREFILL_MIN_SPLIT tiles), so that the last workgroups to start end close together. balance is for the
+    fp32-operand kernel (one workgroup per CU, where a packed batch like config 5's 632 uneven workgroups on 256
+    CUs leaves ~14% of the CU time idle at the end); a piece costs a partial record and its share of the merge,
+    and on the bf16-operand kernel the longer start-up of its producer pipeline outweighs the gain."""
+    if not spans:
         return 0
-    per_cu = -(-sum(spans) * heads // n_cu)
-    return max(PREFILL_MIN_SPLIT, per_cu)
+    total = sum(spans) * heads
+    if len(spans) * heads < n_cu:
+        return max(PREFILL_MIN_SPLIT, -(-total // n_cu))
+    if balance:
+        size = max(2 * PREFILL_MIN_SPLIT, -(-total // (n_cu * PREFILL_BALANCE_PIECES)))
+        return size if max(spans) > size else 0
+    return 0
 
 
 def prefill_work(lengths: list[int], starts: list[int], window: int | None = None, causal: bool = True,
                  split_tiles: int | None = PREFILL_SPLIT_TILES, heads: int = 1,
-                 n_cu: int = 256) -> tuple[list[int], int]:
+                 n_cu: int = 256, balance: bool = False) -> tuple[list[int], int]:
     """The work list of rk_paged_prefill -> (entries, partial slots used). One entry of 5 int32 per block of 32 new
     queries, {(segment << 16) | block, first tile, end tile, first slot or -1, (piece << 16) | pieces}; a block whose
     key range spans more than split_tiles tiles of 32 positions is split at absolute multiples of split_tiles into
     pieces (consecutive partial slots), which the kernel combines in piece order. split_tiles None takes
-    prefill_split_tiles over the blocks (heads = KV heads, n_cu = the device's CUs); 0 never splits. For a given
+    prefill_split_tiles over the blocks (heads = workgroups per block, n_cu = the device's CUs, balance as there);
+    0 never splits. For a given
     split size, where a block is cut depends only on the block, so a segment packed with others gives the same
     bits as the segment alone under the same split size. Entries go longest first, so the longest start first (a
     window bounds a block's range to about W + 32 keys; without causal masking every block of a segment reads all
@@ -282,7 +293,7 @@ def prefill_work(lengths: list[int], starts: list[int], window: int | None = Non
             lo = max(0, p + qb * PREFILL_BLOCK - window + 1) if window else 0
             blocks.append(((s << 16) | qb, lo // PREFILL_TILE, -(-hi // PREFILL_TILE)))
     if split_tiles is None:
-        split_tiles = prefill_split_tiles([t1 - t0 for _, t0, t1 in blocks], heads, n_cu)
+        split_tiles = prefill_split_tiles([t1 - t0 for _, t0, t1 in blocks], heads, n_cu, balance)
     entries, n_slots = [], 0
     for word, t0, t1 in blocks:
         if split_tiles <= 0 or t1 - t0 <= split_tiles:
@@ -318,10 +329,10 @@ def _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu: list[int],
     NB, bs, Hkv, _ = k_pool.shape
     dev = q.device
     # workgroups per 32-query block: one per kv-head, times the head chunks of the fp32-operand kernel
-    wg_heads = Hkv if prefill_bf16_operands(q.dtype, k_pool.dtype, Hq, Hkv, d, exact, tables.shape[1], bs) else \
-        Hkv * -(-(Hq // Hkv) // PREFILL_F32_HEADS)
+    bf16_ops = prefill_bf16_operands(q.dtype, k_pool.dtype, Hq, Hkv, d, exact, tables.shape[1], bs)
+    wg_heads = Hkv if bf16_ops else Hkv * -(-(Hq // Hkv) // PREFILL_F32_HEADS)
     work, n_slots = prefill_work([b - a for a, b in zip(cu, cu[1:])], st, window, causal, PREFILL_SPLIT_TILES,
-                                 wg_heads, device_cus(dev))
+                                 wg_heads, device_cus(dev), balance=not bf16_ops)
     meta = to_device(torch.tensor(cu + st + work, dtype=torch.int32), dev)
     n_work = len(work) // 5
     lib = load()

@@ -592,16 +592,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // v_mfma_f32_16x16x4_f32, bf16 pool rows widened exactly when staged, the probabilities kept in fp32.
 // blockDim = 512: wave w takes query head (blockIdx.z * 4 + w % 4) of the group (none past the group's end: that
 // wave only helps stage) and queries 16 (w / 4) .. + 15 of the work item's 32. All 8 waves stage each tile of 32
-// keys (K and V rows, fp32, rows padded by 4 floats) into a 2-stage LDS ring, one 16-byte load per lane per row
-// piece, requested a whole tile ahead. Per wave and tile, on 16 x 16 accumulators (lane l: query l % 16, rows
-// 4 (l / 16) .. + 3):
+// keys into a 2-stage LDS ring, requested a whole tile ahead: K row-major ([32 keys][D + 4 floats]) and V transposed
+// ([D dims][32 + 4 floats]), both fp32. A staging unit is one 16-byte piece of 4 consecutive key rows (4 loads);
+// the V unit's 4 x 4 (fp32) or 4 x 8 (bf16) values are transposed in registers into 16-byte V^T writes. Per wave and
+// tile, on 16 x 16 accumulators (lane l: query l % 16, rows 4 (l / 16) .. + 3):
 //   S^T = K Q^T:  A = 16 keys x 4 dims from LDS (one 16-byte read feeds four MFMAs: quarter l / 16 takes dims
 //                 16 c + 4 (l / 16) + j of MFMA j), B = Q^T from registers (the same dims of the lane's query);
-//   O^T += V^T P^T: A = V^T (16 dims x 4 keys; lane l reads V[key][16 dt + l % 16] from the row-major stage, the
-//                 keys 4 (l / 16) + r of MFMA r), B = P^T, which is the score accumulator's register r as it is.
+//   O^T += V^T P^T: A = 16 dims x 4 keys from V^T (one 16-byte read of V^T[16 dt + l % 16][16 kt + 4 (l / 16) ..
+//                 + 3] feeds MFMAs r = 0 .. 3: keys 4 (l / 16) + r), B = P^T, the score accumulator's register r.
 // So every lane keeps its own query's softmax state (one reduction over the 4 quarters per tile), and O^T is
-// rescaled per lane. LDS reads are conflict-free: the padded row stride (D + 4 floats) puts 16 consecutive rows 4
-// banks apart.
+// rescaled per lane. LDS reads are conflict-free: the padded strides put 16 consecutive K rows, and 16 consecutive
+// V^T rows, 4 banks apart. Staging writes are conflict-free for V^T (consecutive lanes take consecutive key groups
+// of one piece) and at most 2-way for K (consecutive lanes take consecutive pieces of one row group).
 constexpr int kF32QW = 16;      // queries per wave
 constexpr int kF32Heads = 4;    // query heads per workgroup
 constexpr int kF32Pad = 4;      // fp32 padding of an LDS row
@@ -611,17 +613,21 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
 }
 
 template <int D, typename TP, bool TAB_LDS>
-__global__ __launch_bounds__(512) void prefill_attention_f32(PrefillArgs a) {
-    constexpr int ROW = D + kF32Pad;                 // LDS row stride (floats)
-    constexpr int STAGE = 2 * kBKP * ROW;            // K rows, then V rows
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attention_f32(PrefillArgs a) {
+    constexpr int ROW = D + kF32Pad;                 // K row stride (floats)
+    constexpr int ROWT = kBKP + kF32Pad;             // V^T row stride (floats)
+    constexpr int KST = kBKP * ROW;                  // K floats per stage
+    constexpr int STAGE = KST + D * ROWT;            // K rows, then V^T rows
     constexpr int EL = 16 / (int)sizeof(TP);         // elements per 16-byte load
-    constexpr int PER_ROW = D / EL;                  // loads per row
-    constexpr int PER_T = kBKP * PER_ROW;            // loads per tensor per tile
-    constexpr int NLD = 2 * PER_T / 512;             // loads per thread per tile
-    static_assert(NLD >= 1 && (2 * PER_T) % 512 == 0, "a tile's rows must split evenly over 512 threads");
+    constexpr int PER_ROW = D / EL;                  // 16-byte pieces per row
+    constexpr int GROUPS = kBKP / 4;                 // groups of 4 key rows per tile
+    constexpr int UNITS_T = GROUPS * PER_ROW;        // staging units per tensor per tile
+    constexpr int NU = (2 * UNITS_T + 511) / 512;    // units per thread per tile
+    static_assert(UNITS_T % 64 == 0 && (UNITS_T % 512 == 0 || 512 % UNITS_T == 0),
+                  "each unit slot of a wave must take one tensor");
     constexpr int NC = D / 16;                       // 16-dim groups
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    float* lds = reinterpret_cast<float*>(smem);                               // [2 stages][K rows; V rows]
+    float* lds = reinterpret_cast<float*>(smem);                               // [2 stages][K rows; V^T rows]
     int* tab = reinterpret_cast<int*>(smem + 2 * STAGE * sizeof(float));       // [kTabCache] block ids
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -661,50 +667,90 @@ __global__ __launch_bounds__(512) void prefill_attention_f32(PrefillArgs a) {
         __syncthreads();
     }
 
-    // ---- staging: load index i = tid + 512 j: tensor i / PER_T (K, V), key (i % PER_T) / PER_ROW, piece i % PER_ROW;
-    // consecutive lanes read consecutive 16-byte pieces of one row
-    u32x4 st[NLD];
+    // ---- staging: unit u = tid + 512 j (u < 2 UNITS_T) of tensor u / UNITS_T (K, V), e = u % UNITS_T; K: piece
+    // e % PER_ROW of rows 4 (e / PER_ROW) .. + 3, V: piece e / GROUPS of rows 4 (e % GROUPS) .. + 3. Load r of a unit
+    // is row 4 g + r; every load of a wave reads whole 128-byte row segments.
+    u32x4 st[NU][4];
+    auto unit_of = [&](int j, int& g, int& pc) {
+        const int u = tid + 512 * j, e = u % UNITS_T;
+        const bool is_v = u >= UNITS_T;
+        g = is_v ? e % GROUPS : e / PER_ROW;
+        pc = is_v ? e / GROUPS : e % PER_ROW;
+        return is_v;
+    };
     auto issue = [&](int t_rel) {
         const int tile = t_first + t_rel;
         // all block ids of the tile first (one wait for them), then the row loads
-        int blk[NLD], rr[NLD];
+        int blk[NU][4], rr[NU][4];
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int e = (tid + 512 * j) % PER_T;
-            int pos = tile * kBKP + e / PER_ROW;
-            pos = pos < n_keys ? pos : n_keys - 1;   // keys past the range read its last key (masked, never used)
-            pos = pos < kmin ? kmin : pos;           // keys below the window read its first one
-            const int b = block_of(pos, rr[j]);
-            if (TAB_LDS) {
-                blk[j] = tab[b - b_lo];
-            } else {
-                const int t = table[b];
-                blk[j] = t < 0 ? 0 : (t >= a.num_blocks ? a.num_blocks - 1 : t);
+        for (int j = 0; j < NU; ++j) {
+            int g, pc;
+            unit_of(j, g, pc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int pos = tile * kBKP + 4 * g + r;
+                pos = pos < n_keys ? pos : n_keys - 1;   // keys past the range read its last key (masked, never used)
+                pos = pos < kmin ? kmin : pos;           // keys below the window read its first one
+                const int b = block_of(pos, rr[j][r]);
+                if (TAB_LDS) {
+                    blk[j][r] = tab[b - b_lo];
+                } else {
+                    const int t = table[b];
+                    blk[j][r] = t < 0 ? 0 : (t >= a.num_blocks ? a.num_blocks - 1 : t);
+                }
             }
         }
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int i = tid + 512 * j;
-            const int pc = (i % PER_T) % PER_ROW;
-            const long long off = (((long long)blk[j] * a.bs + rr[j]) * a.Hkv + kvh) * D + pc * EL;
-            const TP* base = reinterpret_cast<const TP*>(i / PER_T ? a.vp : a.kp);
-            st[j] = *reinterpret_cast<const u32x4*>(base + off);
+        for (int j = 0; j < NU; ++j) {
+            if (tid + 512 * j < 2 * UNITS_T) {           // whole waves (UNITS_T is a multiple of 64)
+                int g, pc;
+                const bool is_v = unit_of(j, g, pc);
+                const TP* base = reinterpret_cast<const TP*>(is_v ? a.vp : a.kp);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const long long off = (((long long)blk[j][r] * a.bs + rr[j][r]) * a.Hkv + kvh) * D + pc * EL;
+                    st[j][r] = *reinterpret_cast<const u32x4*>(base + off);
+                }
+            }
         }
     };
     auto stash = [&](int stage) {
         float* s = lds + stage * STAGE;
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) {
-            const int i = tid + 512 * j;
-            const int which = i / PER_T, e = i % PER_T;
-            const int key = e / PER_ROW, pc = e % PER_ROW;
-            float* dst = s + which * kBKP * ROW + key * ROW + pc * EL;
-            if constexpr (sizeof(TP) == 4) {
-                *reinterpret_cast<u32x4*>(dst) = st[j];
-            } else {                                 // 8 bf16 -> 8 fp32, exact
-                const u32x4 w = st[j];
-                *reinterpret_cast<f32x4*>(dst) = f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
-                *reinterpret_cast<f32x4*>(dst + 4) = f32x4{bf16_lo(w[2]), bf16_hi(w[2]), bf16_lo(w[3]), bf16_hi(w[3])};
+        for (int j = 0; j < NU; ++j) {
+            if (tid + 512 * j >= 2 * UNITS_T) continue;
+            int g, pc;
+            if (unit_of(j, g, pc)) {                 // V^T[pc EL + d][4 g .. + 3]
+                float* dst = s + KST + pc * EL * ROWT + 4 * g;
+                if constexpr (sizeof(TP) == 4) {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+                        *reinterpret_cast<f32x4*>(dst + d * ROWT) = f32x4{
+                            __uint_as_float(st[j][0][d]), __uint_as_float(st[j][1][d]),
+                            __uint_as_float(st[j][2][d]), __uint_as_float(st[j][3][d])};
+                } else {                             // bf16 -> fp32, exact
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        *reinterpret_cast<f32x4*>(dst + (2 * d) * ROWT) = f32x4{
+                            bf16_lo(st[j][0][d]), bf16_lo(st[j][1][d]), bf16_lo(st[j][2][d]), bf16_lo(st[j][3][d])};
+                        *reinterpret_cast<f32x4*>(dst + (2 * d + 1) * ROWT) = f32x4{
+                            bf16_hi(st[j][0][d]), bf16_hi(st[j][1][d]), bf16_hi(st[j][2][d]), bf16_hi(st[j][3][d])};
+                    }
+                }
+            } else {                                 // K[4 g + r][pc EL ..]
+                float* dst = s + 4 * g * ROW + pc * EL;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (sizeof(TP) == 4) {
+                        *reinterpret_cast<u32x4*>(dst + r * ROW) = st[j][r];
+                    } else {
+                        const u32x4 w = st[j][r];
+                        *reinterpret_cast<f32x4*>(dst + r * ROW) =
+                            f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
+                        *reinterpret_cast<f32x4*>(dst + r * ROW + 4) =
+                            f32x4{bf16_lo(w[2]), bf16_hi(w[2]), bf16_lo(w[3]), bf16_hi(w[3])};
+                    }
+                }
             }
         }
     };
@@ -740,7 +786,7 @@ __global__ __launch_bounds__(512) void prefill_attention_f32(PrefillArgs a) {
 
     auto consume = [&](int t_rel, int stage) {
         const float* ks = lds + stage * STAGE;
-        const float* vs = ks + kBKP * ROW;
+        const float* vs = ks + KST;
         const int k0 = (t_first + t_rel) * kBKP;
         f32x4 s[2] = {f32x4{}, f32x4{}};
 #pragma unroll
@@ -786,14 +832,21 @@ __global__ __launch_bounds__(512) void prefill_attention_f32(PrefillArgs a) {
         }
         l_run += psum;
         m_run = m_new;
+        // V^T reads one dim group ahead of their MFMAs
+        const float* vt = vs + qc * ROWT + 4 * qq;
+        f32x4 vv = *reinterpret_cast<const f32x4*>(vt);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // the first read,
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int i = 0; i < 2 * NC; ++i) {
+            const int kt = i / NC, dt = i % NC;
+            const f32x4 cur = vv;
+            if (i + 1 < 2 * NC)
+                vv = *reinterpret_cast<const f32x4*>(vt + 16 * ((i + 1) % NC) * ROWT + 16 * ((i + 1) / NC));
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // the next read,
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // then this group's four MFMAs
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float* vr = vs + (16 * kt + 4 * qq + r) * ROW + qc;
-#pragma unroll
-                for (int dt = 0; dt < NC; ++dt) o[dt] = mfma_f32(vr[16 * dt], s[kt][r], o[dt]);
-            }
+            for (int r = 0; r < 4; ++r) o[dt] = mfma_f32(cur[r], s[kt][r], o[dt]);
+        }
     };
 
     // Stage t's rows are written after tile t - 1 is computed (stage (t - 1) & 1 is free once every wave passed the
@@ -985,7 +1038,8 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
         return check_launch("prefill_attention");
     }
     const bool tab_lds = max_nb <= kTabCache;
-    const size_t lds = (size_t)2 * 2 * kBKP * (D + kF32Pad) * sizeof(float) + (tab_lds ? kTabCache * sizeof(int) : 0);
+    const size_t lds = (size_t)2 * (kBKP * (D + kF32Pad) + D * (kBKP + kF32Pad)) * sizeof(float) +
+                       (tab_lds ? kTabCache * sizeof(int) : 0);
     const bool f32_pool = pool_dtype == RK_F32;
 #define RK_F32_PICK(DD)                                                                                      \
     fn = f32_pool ? (tab_lds ? prefill_attention_f32<DD, float, true> : prefill_attention_f32<DD, float, false>)  \

@@ -130,6 +130,28 @@ def test_prefill_auto_split():
     assert kernels.prefill_work(lengths, starts, None, True, None, 2, 256)[1] == 0   # config 5: not split
 
 
+def test_prefill_balance_split():
+    """The balance split of the fp32-operand kernel: with enough workgroups to fill the CUs, blocks longer than a
+    quarter of a CU's share of the tiles are cut to that size (never below two minimum pieces), and nothing is cut
+    when every block is already that short."""
+    from native import kernels
+    gen = torch.Generator().manual_seed(5)                                  # config 5's draw
+    lengths = torch.randint(64, 2049, (8,), generator=gen).tolist()
+    starts = torch.randint(0, 16385, (8,), generator=gen).tolist()
+    spans = [-(-(p + min(n, (qb + 1) * 32)) // 32) for n, p in zip(lengths, starts) for qb in range(-(-n // 32))]
+    size = kernels.prefill_split_tiles(spans, 2, 256, balance=True)
+    assert size == max(2 * kernels.PREFILL_MIN_SPLIT, -(-sum(spans) * 2 // (256 * kernels.PREFILL_BALANCE_PIECES)))
+    assert 0 < size < max(spans)
+    assert kernels.prefill_split_tiles(spans, 2, 256) == 0                  # the bf16-operand kernel: not split
+    work, n_slots = kernels.prefill_work(lengths, starts, None, True, None, 2, 256, balance=True)
+    ents = [work[i:i + 5] for i in range(0, len(work), 5)]
+    assert n_slots > 0 and max(e[2] - e[1] for e in ents) <= size
+    assert sum(e[2] - e[1] for e in ents) == sum(spans)                      # every tile once
+    assert kernels.prefill_split_tiles([100] * 1000, 2, 256, balance=True) == 0      # short blocks stay whole
+    # too few workgroups: the one-piece-per-CU rule holds with or without balance
+    assert kernels.prefill_split_tiles([1024] * 16, 2, 256, balance=True) == kernels.prefill_split_tiles([1024] * 16, 2, 256)
+
+
 def test_prefill_block_index_division():
     """The prefill kernels' block index pos // bs without a divide: the fp32-operand kernel takes mulhi(pos,
     floor((2^32 - 1) / bs)) plus one correction, exact for every pos < 2^32 and bs >= 1; the bf16-operand kernel
