@@ -177,11 +177,10 @@ int rk_deltanet_decode(float* out, const float* qkv, const float* z, const float
  *   gate NULL or [N, Hq*D] in gate_dtype (RK_F32 or RK_BF16, read as stored). Any group size Hq / Hkv, D in
  *   {64, 128, 256}, max_nb * block_size < 2^31.
  *   Operands: the reference computes in fp32 on widened inputs (src/ops.py:84-87, 91-103). exact = 0 with q and the
- *   pool both bf16, group size 4, D in {128, 256}, block_size >= 2 and max_nb * block_size^2 < 2^32 (config 5)
- *   takes bf16 MFMA
- *   operands (q, K, V as stored, the probabilities rounded to bf16; fp32 accumulation): bf16-level results. Every other call (exact = 1, an fp32 q or
- *   pool, other shapes) takes fp32 operands (fp32 MFMA, bf16 pool rows widened exactly, fp32 probabilities):
- *   fp32-level results.
+ *   pool both bf16 takes bf16 MFMA operands (q, K, V as stored, the probabilities rounded to bf16; fp32
+ *   accumulation): bf16-level results, on 32 queries per wave at group size 4, D in {128, 256}, block_size >= 2 and
+ *   max_nb * block_size^2 < 2^32 (config 5), on 16 queries per wave otherwise. exact = 1 or an fp32 q or pool takes
+ *   fp32 operands (fp32 MFMA, bf16 pool rows widened exactly, fp32 probabilities): fp32-level results.
  *   window 0 or W >= 1 (causal only): query i also sees only positions above start[s] + i - W (the sliding-window
  *   prefill of src/models/cohere2.py:155-163; ops.attention's window, src/ops.py:77-81, 97-98); blocks wholly below
  *   every query's window are never read. causal 0: every query of segment s sees positions 0 .. start[s]+n[s]-1

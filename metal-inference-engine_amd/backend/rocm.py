@@ -10,7 +10,7 @@ Method -> kernel:
   attention, T == 1      rk_paged_decode on the contiguous cache viewed as one block (the reference's
                          attention_decode, src/backend/metal.py:197-210)
   attention, T > 1       rk_paged_prefill on the same one-block view, no KV write (causal, optional window); fp32
-                         operands (fp32-level results) unless q, k and v are all bf16 at the bf16 kernel's shapes
+                         operands (fp32-level results) unless q, k and v are all bf16 (then bf16 operands)
   deltanet_decode[_batch] rk_deltanet_decode (P2; states of one HybridPool in one launch, a standalone state as a
                          pool of one, src/backend/metal.py:232-256)
   paged_prefill_attention rk_paged_prefill (P4; the packed prefill of full_attention, src/models/qwen3_5.py:112-120:
@@ -125,9 +125,9 @@ class RocmBackend:
         -> [N, Hq, d] fp32, times sigmoid(gate [N, Hq*d]) when given. The reference runs this per segment as
         kv.write -> kv.read -> attention(causal) -> gate (src/models/qwen3_5.py:112-120). With a window W each query
         sees its last W positions (the sliding layers' prefill, src/models/cohere2.py:155-163), and blocks below
-        every query's window are never read. The reference computes in fp32 (src/ops.py:84-87): an fp32 q or pool,
-        any group size but 4 or head_dim 64 run on fp32 operands (fp32-level results); bf16 q and pool at 4 query
-        heads per kv-head run on bf16 operands unless exact=True."""
+        every query's window are never read. The reference computes in fp32 (src/ops.py:84-87): an fp32 q or pool
+        runs on fp32 operands (fp32-level results); bf16 q and pool run on bf16 operands (probabilities rounded to
+        bf16) unless exact=True."""
         return kernels.paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos, block_size,
                                      gate, window=window, exact=exact)
 

@@ -308,16 +308,26 @@ def prefill_work(lengths: list[int], starts: list[int], window: int | None = Non
     return [v for _, e in entries for v in e], n_slots
 
 
-PREFILL_F32_HEADS = 4       # query heads per workgroup of rk_paged_prefill's fp32-operand kernel
+PREFILL_F32_HEADS = 4       # query heads per workgroup of rk_paged_prefill's 16-query kernels (fp32 and bf16 operands)
+
+
+def prefill_kernel(q_dtype, pool_dtype, Hq: int, Hkv: int, d: int, exact: bool, max_nb: int = 1,
+                   block_size: int = 16) -> str:
+    """Which kernel rk_paged_prefill runs (its rule, include/rk_path.h): "bf16_32" (bf16 operands, 32 queries per
+    wave) for bf16 q and pool at 4 query heads per kv-head, head_dim 128 / 256, block size >= 2 and positions x
+    block size below 2^32; "bf16_16" (bf16 operands, 16 queries per wave) for every other bf16 q and pool; "fp32"
+    (fp32 operands) for an fp32 q or pool and for exact requests."""
+    if exact or q_dtype != torch.bfloat16 or pool_dtype != torch.bfloat16:
+        return "fp32"
+    if Hq == 4 * Hkv and d in (128, 256) and block_size >= 2 and max_nb * block_size * block_size < 2 ** 32:
+        return "bf16_32"
+    return "bf16_16"
 
 
 def prefill_bf16_operands(q_dtype, pool_dtype, Hq: int, Hkv: int, d: int, exact: bool, max_nb: int = 1,
                           block_size: int = 16) -> bool:
-    """Whether rk_paged_prefill runs on bf16 MFMA operands (its rule, include/rk_path.h): q and the pool both bf16,
-    4 query heads per kv-head, head_dim 128 or 256, block size >= 2, positions x block size below 2^32, and no exact
-    request. Everything else takes fp32 operands."""
-    return (not exact and q_dtype == torch.bfloat16 and pool_dtype == torch.bfloat16 and Hq == 4 * Hkv
-            and d in (128, 256) and block_size >= 2 and max_nb * block_size * block_size < 2 ** 32)
+    """Whether rk_paged_prefill runs on bf16 MFMA operands: q and the pool both bf16 and no exact request."""
+    return prefill_kernel(q_dtype, pool_dtype, Hq, Hkv, d, exact, max_nb, block_size) != "fp32"
 
 
 def _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu: list[int], st: list[int], gate,
@@ -328,11 +338,11 @@ def _prefill_launch(out, q, k_new, v_new, k_pool, v_pool, tables, cu: list[int],
     N, Hq, d = q.shape
     NB, bs, Hkv, _ = k_pool.shape
     dev = q.device
-    # workgroups per 32-query block: one per kv-head, times the head chunks of the fp32-operand kernel
-    bf16_ops = prefill_bf16_operands(q.dtype, k_pool.dtype, Hq, Hkv, d, exact, tables.shape[1], bs)
-    wg_heads = Hkv if bf16_ops else Hkv * -(-(Hq // Hkv) // PREFILL_F32_HEADS)
+    # workgroups per 32-query block: one per kv-head, times the head chunks of the 16-query kernels
+    which = prefill_kernel(q.dtype, k_pool.dtype, Hq, Hkv, d, exact, tables.shape[1], bs)
+    wg_heads = Hkv if which == "bf16_32" else Hkv * -(-(Hq // Hkv) // PREFILL_F32_HEADS)
     work, n_slots = prefill_work([b - a for a, b in zip(cu, cu[1:])], st, window, causal, PREFILL_SPLIT_TILES,
-                                 wg_heads, device_cus(dev), balance=not bf16_ops)
+                                 wg_heads, device_cus(dev), balance=which == "fp32")
     meta = to_device(torch.tensor(cu + st + work, dtype=torch.int32), dev)
     n_work = len(work) // 5
     lib = load()
@@ -366,8 +376,8 @@ def paged_prefill(q, k_new, v_new, k_pool, v_pool, tables, cu_seqlens, start_pos
     attention of every segment's new queries over its prefix + new keys -> [N, Hq, d] fp32 (* sigmoid(gate)); with a
     window W each query sees only its last W positions. cu_seqlens (S + 1 row offsets) and start_pos (S absolute
     positions) are host-side lists / CPU tensors, as the packing step produces them; tables [S, max_nb] int32 on
-    the device. fp32 operands (fp32-level results) unless q and the pool are both bf16 at 4 query heads per kv-head
-    and head_dim 128 / 256; exact=True asks for fp32 operands there too."""
+    the device. fp32 operands (fp32-level results) unless q and the pool are both bf16 (then bf16 MFMA operands,
+    probabilities rounded to bf16); exact=True asks for fp32 operands there too."""
     name = "paged_prefill"
     cu = [int(x) for x in cu_seqlens]
     st = [int(x) for x in start_pos]
@@ -412,7 +422,7 @@ def attention(q, k, v, causal: bool = True, window: int | None = None, exact: bo
     q [T, Hq, d], k / v [S, Hkv, d] (fp32 or bf16 read as stored, anything else widened) -> [T, Hq, d] fp32; query i
     sits at position S - T + i. The cache is viewed in place as a pool of one block holding all S positions and run
     through rk_paged_prefill with no KV write; with a window the keys no query sees are dropped first, as the
-    reference does. Operands as paged_prefill (fp32 unless q, k and v are all bf16 at the bf16 kernel's shapes)."""
+    reference does. Operands as paged_prefill (fp32 unless q, k and v are all bf16 and exact is False)."""
     name = "attention"
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
         raise ValueError(f"{name}: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
@@ -437,9 +447,9 @@ def attention(q, k, v, causal: bool = True, window: int | None = None, exact: bo
         return out
     if S >= 2 ** 31:
         raise NotImplementedError(f"{name}: {S} positions (the kernels address positions below 2^31)")
-    # viewed in place as one block of S positions; past 65,535 positions (where the bf16 kernel's block index needs
-    # positions x block size < 2^32) as S / bs blocks of the largest power of two bs <= 16 dividing S, in order (an
-    # odd S gives blocks of one position, which only the fp32-operand kernel takes)
+    # viewed in place as one block of S positions; past 65,535 positions (where the 32-query bf16 kernel's block
+    # index needs positions x block size < 2^32) as S / bs blocks of the largest power of two bs <= 16 dividing S, in
+    # order (an odd S gives blocks of one position, which the 16-query kernels take)
     bs = S if S < 65536 else math.gcd(S, 16)
     nb = S // bs
     kp, vp = k.contiguous().view(nb, bs, Hkv, d), v.contiguous().view(nb, bs, Hkv, d)

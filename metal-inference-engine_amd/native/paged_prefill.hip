@@ -612,6 +612,117 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// The lazy running maximum of a 16-query wave (scores s[kt][r] of lane l: query l % 16, keys 16 kt + 4 (l / 16) + r):
+// m is raised to the tile's maximum (scaled by qscale) only where that exceeds m by more than kLazy, so
+// p = 2^(s qscale - m) stays <= 2^kLazy (exact in fp32, representable in bf16). Each lane first compares its own 8
+// scores; only when some lane of the wave exceeds the bound is the maximum over the query's 4 lanes formed, so the
+// result equals max-then-compare over all 32 keys while the common case needs no cross-lane exchange (scaling by
+// qscale > 0 is monotonic, so it commutes with max).
+__device__ __forceinline__ void lazy_max(const f32x4 (&s)[2], float& m, float qscale) {
+    float t = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                    fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3]))) * qscale;
+    if (__any(t > m + kLazy)) {
+        t = fmaxf(t, __shfl_xor(t, 16));
+        t = fmaxf(t, __shfl_xor(t, 32));
+        m = t > m + kLazy ? t : m;
+    }
+}
+
+// The end of a 16-query wave of the fp32- and bf16-operand kernels: o[dt] holds O^T[16 dt + 4 (lane / 16) + r][query
+// lane % 16] for D / 16 dim tiles, with the running (m, l) of the lane's query. Split items: the piece's (o, m, l) per
+// (slot, head, half) of 16 queries, then the arrival count; the last piece combines all of them in piece order (the
+// protocol and memory ordering of prefill_attention above). Then the rows are divided by l, gated and stored.
+template <int D>
+__device__ __forceinline__ void finish_queries(const PrefillArgs& a, const int32_t* we, f32x4 (&o)[D / 16],
+                                               float m_run, float l_run, int head, int half, int row0, int nq) {
+    constexpr int NC = D / 16;
+    const int lane = threadIdx.x & 63, qc = lane & 15, qq = lane >> 4;
+    const int qi = half * kF32QW + qc;
+    const int piece = we[4] >> 16, pieces = we[4] & 0xffff;
+    const int first = we[3] >= 0 && piece < pieces && we[3] + pieces <= a.n_slots ? we[3] : -1;
+    if (first >= 0) {
+        constexpr int REC = kF32QW * D + 2 * kF32QW;
+        constexpr int kSc1 = 16;
+        auto rsrc_of = [&](int pc) {
+            const unsigned long long u = reinterpret_cast<unsigned long long>(
+                a.part + (((long long)(first + pc) * a.Hq + head) * 2 + half) * REC);
+            const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
+            const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
+            return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo),
+                                                     (short)0, REC * 4, 0x00020000);
+        };
+        auto o_off = [&](int dt) { return 4 * (qc * D + 16 * dt + 4 * qq); };
+        const int m_off = 4 * (kF32QW * D + qc), l_off = 4 * (kF32QW * D + kF32QW + qc);
+        {
+            const auto rs = rsrc_of(piece);
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[dt]), rs, o_off(dt), 0, kSc1);
+            if (qq == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), rs, m_off, 0, kSc1);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), rs, l_off, 0, kSc1);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): this wave's stores have completed
+        uint32_t* counter = a.cnt + ((long long)first * a.Hq + head) * 2 + half;
+        uint32_t before = 0;
+        if (lane == 0) before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        before = __shfl(before, 0);
+        if (before != (uint32_t)(pieces - 1)) return;
+        float mx = -INFINITY;
+        for (int pc = 0; pc < pieces; ++pc)
+            mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_of(pc), m_off, 0, kSc1)));
+#pragma unroll
+        for (int dt = 0; dt < NC; ++dt) o[dt] = f32x4{};
+        l_run = 0.0f;
+        for (int pc = 0; pc < pieces; ++pc) {
+            const auto rs = rsrc_of(pc);
+            u32x4 v[NC];
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt) v[dt] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off(dt), 0, kSc1);
+            const float mp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, m_off, 0, kSc1));
+            const float lp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, l_off, 0, kSc1));
+            const float sc = mp == -INFINITY ? 0.0f : fast_exp2(mp - mx);
+            l_run = fmaf(sc, lp, l_run);
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[dt][r] = fmaf(sc, __uint_as_float(v[dt][r]), o[dt][r]);
+        }
+        if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    if (qi < nq) {
+        const float inv = 1.0f / l_run;
+        const long long orow = (long long)(row0 + qi) * a.Hq + head;
+        float4 gv[NC];
+        if (a.gate) {
+            if (a.gate_dtype == RK_BF16) {
+                const uint16_t* gp = reinterpret_cast<const uint16_t*>(a.gate) + orow * D + 4 * qq;
+#pragma unroll
+                for (int dt = 0; dt < NC; ++dt) {
+                    const u32x2 w = *reinterpret_cast<const u32x2*>(gp + 16 * dt);
+                    gv[dt] = make_float4(bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1]));
+                }
+            } else {
+                const float* gp = reinterpret_cast<const float*>(a.gate) + orow * D + 4 * qq;
+#pragma unroll
+                for (int dt = 0; dt < NC; ++dt) gv[dt] = *reinterpret_cast<const float4*>(gp + 16 * dt);
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < NC; ++dt) {
+            float v[4] = {o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv};
+            if (a.gate) {
+                const float g[4] = {gv[dt].x, gv[dt].y, gv[dt].z, gv[dt].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = v[i] * (1.0f / (1.0f + expf(-g[i])));
+            }
+            *reinterpret_cast<float4*>(a.out + orow * D + 16 * dt + 4 * qq) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
 template <int D, typename TP, bool TAB_LDS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attention_f32(PrefillArgs a) {
     constexpr int ROW = D + kF32Pad;                 // K row stride (floats)
@@ -866,92 +977,286 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
     if (!active) return;
+    finish_queries<D>(a, we, o, m_run, l_run, head, half, row0, nq);
+}
 
-    // Split items: the piece's (o, m, l) per (slot, head, half) of 16 queries, then the arrival count; the last piece
-    // combines all of them in piece order (the protocol and memory ordering of prefill_attention above).
-    const int piece = we[4] >> 16, pieces = we[4] & 0xffff;
-    const int first = we[3] >= 0 && piece < pieces && we[3] + pieces <= a.n_slots ? we[3] : -1;
-    if (first >= 0) {
-        constexpr int REC = kF32QW * D + 2 * kF32QW;
-        constexpr int kSc1 = 16;
-        auto rsrc_of = [&](int pc) {
-            const unsigned long long u = reinterpret_cast<unsigned long long>(
-                a.part + (((long long)(first + pc) * a.Hq + head) * 2 + half) * REC);
-            const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)u);
-            const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(u >> 32));
-            return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo),
-                                                     (short)0, REC * 4, 0x00020000);
+// ---- 4. attention on bf16 operands, 16 queries per consumer wave, for bf16 q and pool (v_mfma_f32_16x16x32_bf16).
+// blockDim = 768, warp-specialised: waves 0 .. 7 are consumers (wave w: query head blockIdx.z * 4 + w % 4 of the
+// group, queries 16 (w / 4) .. + 15 of the work item: the fp32-operand kernel's split of the work, its work list,
+// masks, split records and epilogue), waves 8 .. 11 are producers. Three waves per SIMD: two consumers, so one's
+// softmax and LDS waits hide behind the other's MFMAs, and a producer, whose loads and LDS writes overlap both.
+// Producers keep kB16Depth tiles of 32 keys in flight in their registers (per lane and tile one staging unit of K and
+// one of V: a 16-byte piece, 8 dims, of 4 consecutive key rows) and per tile move the oldest into a 2-stage LDS
+// ring, K as rows, V transposed to [dim][key] (bf16 as stored), then request the next; one LDS-only barrier per tile.
+// Per consumer wave and tile, on 16 x 16 accumulators (lane l: query l % 16, rows 4 (l / 16) .. + 3):
+//   S^T = K Q^T:  A = 16 keys x 32 dims (one 16-byte LDS read: row 16 kt + l % 16, dims 32 c + 8 (l / 16) .. + 7),
+//                 B = Q^T from registers (the same dims of the lane's query);
+//   O^T += V^T P^T: one MFMA per 16 dims over all 32 keys. k-slot 8 (l / 16) + j stands for key 4 (l / 16) + j
+//                 (j < 4) or 16 + 4 (l / 16) + j - 4, which are exactly the keys of the lane's own scores
+//                 s[0][0..3], s[1][0..3]: the B operand is those 8 probabilities rounded to bf16, and V^T rows hold
+//                 their keys in that order, so A is one 16-byte read at slot 8 (l / 16) of the dim's row.
+// LDS banks: a 16-byte read (ds_read_b128) is conflict-free on gfx950 when, within each half wave (32 lanes), the
+// lanes' 16-byte offsets are distinct modulo 512 bytes (measured: 16 consecutive rows of a 33-unit stride, read at
+// two column offsets, conflict, 32 consecutive rows do not). Here lanes l and l + 16 read 16 consecutive rows at
+// columns 16 bytes apart, so row strides of 2 x odd 16-byte units (K: D + 16 bf16, V^T: 48 bf16) put the 32 pieces
+// on 32 distinct units. The 8-byte V^T writes of a half wave cover 4 dims 8 apart; with a 96-byte stride those rows
+// would share banks, so dim d lives in V^T row vt_row(d) = 8 (d / 8) + (d % 8 + 2 (d / 8)) % 8 (a rotation within
+// each group of 8 rows), which spreads the 4 rows over the banks (measured: the write rate of a linear layout) and
+// leaves the reads' 16 consecutive dims on 16 distinct rows of a 16-row group.
+constexpr int kB16Depth = 4;    // tiles in flight in producer registers
+constexpr int kB16KPad = 16;    // bf16 padding of a K row in LDS
+constexpr int kB16VRow = 48;    // bf16 per V^T row in LDS: 32 keys + 16 padding
+constexpr int kB16Ahead = 4;    // K and V^T operand reads in flight ahead of their MFMAs
+constexpr int kB16Threads = 768;
+
+template <int D, bool TAB_LDS>
+__global__ __launch_bounds__(kB16Threads) void prefill_attention_b16(PrefillArgs a) {
+    constexpr int KROW = D + kB16KPad;               // K row stride (bf16)
+    constexpr int KBUF = kBKP * KROW;                // K bf16 per stage
+    constexpr int STAGE = KBUF + D * kB16VRow;       // bf16 per stage: K rows, then V^T rows
+    constexpr int PER_ROW = D / 8;                   // 16-byte pieces per row
+    constexpr int GROUPS = kBKP / 4;                 // groups of 4 key rows per tile
+    constexpr int UNITS_T = GROUPS * PER_ROW;        // staging units per tensor per tile
+    static_assert(UNITS_T <= 256 && UNITS_T % 64 == 0, "one K and one V unit per producer lane, whole waves");
+    constexpr int DEPTH = kB16Depth;
+    static_assert(DEPTH % 2 == 0, "the stage of tile i + d is d % 2 in the loop unrolled by DEPTH");
+    constexpr int NC = D / 16;                       // dim tiles of O^T
+    constexpr int NQ = D / 32;                       // k-steps of S^T
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    uint16_t* lds = reinterpret_cast<uint16_t*>(smem);                                 // [2 stages][K; V^T]
+    int* tab = reinterpret_cast<int*>(smem + 2 * STAGE * sizeof(uint16_t));             // [kTabCache] block ids
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool producer = wave >= 8;
+    const int kvh = blockIdx.y;
+    const int gh = blockIdx.z * kF32Heads + (wave & 3);      // head within the group (consumers)
+    const int half = (wave >> 2) & 1;
+    const int32_t* we = a.work + (long long)kWorkInts * blockIdx.x;
+    const int item = we[0];
+    const int seg = item >> 16, qblk = item & 0xffff;
+    const int row0 = a.cu[seg] + qblk * kBQ;
+    const int nq = min(kBQ, a.cu[seg + 1] - row0);
+    const int p0 = a.start[seg] + qblk * kBQ;
+    const int n_keys = a.causal ? p0 + nq : a.start[seg] + (a.cu[seg + 1] - a.cu[seg]);
+    const int kmin = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
+    const int t_first = max(kmin / kBKP, we[1]);
+    const int n_tiles = min((n_keys + kBKP - 1) / kBKP, we[2]) - t_first;
+    if (n_tiles <= 0) return;                        // whole workgroup (the host never lists an empty entry)
+    const int32_t* table = a.tables + (long long)seg * a.max_nb;
+    const bool active = !producer && gh < a.G && half * kF32QW < nq;     // whole waves
+    const int head = kvh * a.G + (gh < a.G ? gh : 0);
+    // pos / bs: the estimate from floor((2^32 - 1) / bs) is exact or one short for every pos < 2^32
+    auto block_of = [&](int pos, int& r) {
+        uint32_t b = __umulhi((uint32_t)pos, a.bs_recip);
+        r = pos - (int)b * a.bs;
+        if (r >= a.bs) { ++b; r -= a.bs; }
+        return (int)b;
+    };
+    // every position a producer reads lies in [b_lo's first row, the entry's last key]: groups are clamped into
+    // the entry's key range (rounded down to 4 for groups below the window)
+    int r0;
+    const int b_lo = block_of(max(kmin, t_first * kBKP) / 4 * 4, r0);
+    if (TAB_LDS) {
+        const int b_hi = block_of(min(n_keys, (t_first + n_tiles) * kBKP) - 1, r0);
+        for (int i = b_lo + tid; i <= b_hi; i += kB16Threads) {
+            const int blk = table[i];
+            tab[i - b_lo] = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+        }
+        __syncthreads();
+    }
+    const int n_iter = (n_tiles + DEPTH - 1) / DEPTH * DEPTH;
+
+    if (producer) {
+        // ---- producer lane pl: K unit pl (piece pl % PER_ROW of rows 4 (pl / PER_ROW) .. + 3: consecutive lanes,
+        // consecutive pieces of one row group) and V unit pl (piece pl / GROUPS of rows 4 (pl % GROUPS) .. + 3:
+        // consecutive lanes, consecutive key groups). The same code for every lane: a branch between K and V work
+        // would make the compiler wait for all loads in flight where the branches join.
+        const int pl = tid - 8 * 64;
+        if (__builtin_amdgcn_readfirstlane(pl) >= UNITS_T) {     // whole waves without a unit (D < 256)
+            for (int k = 0; k <= n_iter; ++k) lds_barrier();
+            return;
+        }
+        const int gk = pl / PER_ROW, pk = pl % PER_ROW;
+        const int gv = pl % GROUPS, pv = pl / GROUPS;
+        const uint16_t* ksrc = reinterpret_cast<const uint16_t*>(a.kp) + (long long)kvh * D + pk * 8;
+        const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(a.vp) + (long long)kvh * D + pv * 8;
+        const long long rstride = (long long)a.Hkv * D;  // elements between consecutive pool rows
+        const bool rows4 = a.bs % 4 == 0;                // a group of 4 aligned keys lies in one block
+        auto pool_block = [&](int b) {
+            if (TAB_LDS) return tab[b - b_lo];
+            const int t = table[b];
+            return t < 0 ? 0 : (t >= a.num_blocks ? a.num_blocks - 1 : t);
         };
-        auto o_off = [&](int dt) { return 4 * (qc * D + 16 * dt + 4 * qq); };
-        const int m_off = 4 * (kF32QW * D + qc), l_off = 4 * (kF32QW * D + kF32QW + qc);
-        {
-            const auto rs = rsrc_of(piece);
+        // pool row offsets (elements) of keys 4 g .. + 3 of tile t_rel; prefetches past the entry's last tile re-read
+        // it, so every position read lies in the entry's own key range, whose block ids are the ones cached
+        auto rows_of = [&](int t_rel, int g, long long (&off)[4]) {
+            const int p4 = (t_first + min(t_rel, n_tiles - 1)) * kBKP + 4 * g;
+            if (rows4) {
+                // groups past the end re-read the group holding the last key, groups below the window the one
+                // holding its first key: the same block either way (masked, never used)
+                int pos = p4 + 3 < n_keys ? p4 : (n_keys - 1) / 4 * 4;
+                pos = pos < kmin ? kmin / 4 * 4 : pos;
+                int r;
+                const int b = block_of(pos, r);
+                const long long row = ((long long)pool_block(b) * a.bs + r) * rstride;
 #pragma unroll
-            for (int dt = 0; dt < NC; ++dt)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[dt]), rs, o_off(dt), 0, kSc1);
-            if (qq == 0) {
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_run), rs, m_off, 0, kSc1);
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l_run), rs, l_off, 0, kSc1);
+                for (int j = 0; j < 4; ++j) off[j] = row + j * rstride;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    int pos = p4 + j;
+                    pos = pos < n_keys ? pos : n_keys - 1;
+                    pos = pos < kmin ? kmin : pos;
+                    int r;
+                    const int b = block_of(pos, r);
+                    off[j] = ((long long)pool_block(b) * a.bs + r) * rstride;
+                }
+            }
+        };
+        auto issue = [&](int t_rel, u32x4 (&slot)[8]) {
+            long long ok[4], ov[4];
+            rows_of(t_rel, gk, ok);
+            rows_of(t_rel, gv, ov);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) slot[j] = *reinterpret_cast<const u32x4*>(ksrc + ok[j]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) slot[4 + j] = *reinterpret_cast<const u32x4*>(vsrc + ov[j]);
+        };
+        auto stash = [&](const u32x4 (&slot)[8], int stage) {
+            uint16_t* s = lds + stage * STAGE;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(s + (4 * gk + j) * KROW + pk * 8) = slot[j];
+            // dim 8 pv + d goes to V^T row vt_row(8 pv + d), keys 4 gv .. + 3 at slots 8 gv (gv < 4) or
+            // 8 (gv - 4) + 4; one byte permute per word takes the same 16-bit half (low: even d, high: odd d) of two
+            // key rows
+            uint16_t* vt = s + KBUF + pv * 8 * kB16VRow + (gv < 4 ? 8 * gv : 8 * (gv - 4) + 4);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const uint32_t sel = d & 1 ? 0x07060302u : 0x05040100u;
+                const uint32_t w0 = __builtin_amdgcn_perm(slot[5][d / 2], slot[4][d / 2], sel);
+                const uint32_t w1 = __builtin_amdgcn_perm(slot[7][d / 2], slot[6][d / 2], sel);
+                *reinterpret_cast<u32x2*>(vt + ((d + 2 * pv) & 7) * kB16VRow) = u32x2{w0, w1};
+            }
+        };
+        // tile t sits in slot t % DEPTH, then in stage t % 2; at iteration t the slot of tile t + 1 goes to LDS (into
+        // tile t - 1's stage, released by the barrier that ended iteration t - 1) and is refilled with tile
+        // t + 1 + DEPTH. The loop body has no branch, so the compiler counts the loads in flight exactly.
+        u32x4 st[DEPTH][8];
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) issue(d, st[d]);
+        stash(st[0], 0);
+        issue(DEPTH, st[0]);
+        lds_barrier();
+        for (int i = 0; i < n_iter; i += DEPTH) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                stash(st[(d + 1) % DEPTH], (d + 1) & 1);
+                issue(i + d + 1 + DEPTH, st[(d + 1) % DEPTH]);
+                lds_barrier();
             }
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): this wave's stores have completed
-        uint32_t* counter = a.cnt + ((long long)first * a.Hq + head) * 2 + half;
-        uint32_t before = 0;
-        if (lane == 0) before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        before = __shfl(before, 0);
-        if (before != (uint32_t)(pieces - 1)) return;
-        float mx = -INFINITY;
-        for (int pc = 0; pc < pieces; ++pc)
-            mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_of(pc), m_off, 0, kSc1)));
-#pragma unroll
-        for (int dt = 0; dt < NC; ++dt) o[dt] = f32x4{};
-        l_run = 0.0f;
-        for (int pc = 0; pc < pieces; ++pc) {
-            const auto rs = rsrc_of(pc);
-            u32x4 v[NC];
-#pragma unroll
-            for (int dt = 0; dt < NC; ++dt) v[dt] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off(dt), 0, kSc1);
-            const float mp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, m_off, 0, kSc1));
-            const float lp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, l_off, 0, kSc1));
-            const float sc = mp == -INFINITY ? 0.0f : fast_exp2(mp - mx);
-            l_run = fmaf(sc, lp, l_run);
-#pragma unroll
-            for (int dt = 0; dt < NC; ++dt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) o[dt][r] = fmaf(sc, __uint_as_float(v[dt][r]), o[dt][r]);
-        }
-        if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
     }
 
-    if (qi < nq) {
-        const float inv = 1.0f / l_run;
-        const long long orow = (long long)(row0 + qi) * a.Hq + head;
-        float4 gv[NC];
-        if (a.gate) {
-            if (a.gate_dtype == RK_BF16) {
-                const uint16_t* gp = reinterpret_cast<const uint16_t*>(a.gate) + orow * D + 4 * qq;
+    // ---- consumer wave
+    const int qc = lane & 15, qq = lane >> 4;
+    const int qi = half * kF32QW + qc;
+    const int qpos = a.causal ? p0 + (qi < nq ? qi : nq - 1) : n_keys - 1;
+    const int qlo = a.window > 0 ? qpos - a.window : -1;
+    const int qfirst = a.causal ? p0 + half * kF32QW : n_keys - 1;
+    const int qlast = a.causal ? p0 + min(half * kF32QW + kF32QW, nq) - 1 : n_keys - 1;
+    const int lo_edge = a.window > 0 ? qlast - a.window : INT_MIN;
+    u32x4 qop[NQ];                                   // Q[query][32 c + 8 qq .. + 7]
+    f32x4 o[NC];                                     // O^T[16 dt + 4 qq + r][query]
+    float m_run = -INFINITY, l_run = 0.0f;
+    {
+        const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.q) +
+                             ((long long)(row0 + (qi < nq ? qi : nq - 1)) * a.Hq + head) * D + 8 * qq;
 #pragma unroll
-                for (int dt = 0; dt < NC; ++dt) {
-                    const u32x2 w = *reinterpret_cast<const u32x2*>(gp + 16 * dt);
-                    gv[dt] = make_float4(bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1]));
-                }
-            } else {
-                const float* gp = reinterpret_cast<const float*>(a.gate) + orow * D + 4 * qq;
+        for (int c = 0; c < NQ; ++c) qop[c] = *reinterpret_cast<const u32x4*>(qp + 32 * c);
 #pragma unroll
-                for (int dt = 0; dt < NC; ++dt) gv[dt] = *reinterpret_cast<const float4*>(gp + 16 * dt);
-            }
+        for (int c = 0; c < NC; ++c) o[c] = f32x4{};
+    }
+
+    auto consume = [&](int t_rel, int stage) {
+        const uint16_t* ks = lds + stage * STAGE;
+        const uint16_t* kr = ks + qc * KROW + 8 * qq;
+        // V^T rows of dims 16 dt + qc: vt_row = 16 dt + 8 (qc / 8) + (qc % 8 + 2 (qc / 8) + 4 (dt % 2)) % 8
+        const uint16_t* vr0 = ks + KBUF + (8 * (qc >> 3) + (((qc & 7) + 2 * (qc >> 3)) & 7)) * kB16VRow + 8 * qq;
+        const uint16_t* vr1 = ks + KBUF + (8 * (qc >> 3) + (((qc & 7) + 2 * (qc >> 3) + 4) & 7)) * kB16VRow + 8 * qq;
+        auto vread = [&](int dt) {
+            return *reinterpret_cast<const u32x4*>((dt & 1 ? vr1 : vr0) + 16 * dt * kB16VRow);
+        };
+        const int k0 = (t_first + t_rel) * kBKP;
+        f32x4 s[2] = {f32x4{}, f32x4{}};
+        // K operands kB16Ahead reads ahead of their MFMAs (read i: dims 32 (i / 2), keys 16 (i % 2) ..); the
+        // scheduling fences keep the compiler from moving the reads back next to their uses
+        auto kread = [&](int i) {
+            return *reinterpret_cast<const u32x4*>(kr + 16 * (i % 2) * KROW + 32 * (i / 2));
+        };
+        u32x4 ka[kB16Ahead];
+#pragma unroll
+        for (int i = 0; i < kB16Ahead; ++i) ka[i] = kread(i);
+#pragma unroll
+        for (int i = 0; i < 2 * NQ; ++i) {
+            const u32x4 cur = ka[i % kB16Ahead];
+            if (i + kB16Ahead < 2 * NQ) ka[i % kB16Ahead] = kread(i + kB16Ahead);
+            __builtin_amdgcn_sched_barrier(0);
+            s[i % 2] = mfma16x16x32(cur, qop[i / 2], s[i % 2]);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        // lane (qc, qq), register r of sub-tile kt: key k0 + 16 kt + 4 qq + r
+        if (k0 + kBKP - 1 > qfirst || k0 <= lo_edge) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * kt + 4 * qq + r;
+                    s[kt][r] = key <= qpos && key > qlo ? s[kt][r] : -INFINITY;
+                }
+        }
+        // the first V^T operands are requested before the softmax, so their latency passes during it
+        u32x4 va[kB16Ahead];
+#pragma unroll
+        for (int i = 0; i < kB16Ahead; ++i) va[i] = vread(i);
+        __builtin_amdgcn_sched_barrier(0);
+        const float m_prev = m_run;
+        lazy_max(s, m_run, a.qscale);
+        const float mb = m_run == -INFINITY ? 0.0f : m_run;
+        if (__any(m_run != m_prev)) {
+            const float alpha = fast_exp2(m_prev - mb);     // 0 on the first tile (m_prev = -inf)
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt) o[dt] *= alpha;
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[kt][r] = fast_exp2(fmaf(s[kt][r], a.qscale, -mb));
+                l_run += s[kt][r];
+            }
+        const u32x4 pop = u32x4{pack_bf16x2_rne(s[0][0], s[0][1]), pack_bf16x2_rne(s[0][2], s[0][3]),
+                                pack_bf16x2_rne(s[1][0], s[1][1]), pack_bf16x2_rne(s[1][2], s[1][3])};
 #pragma unroll
         for (int dt = 0; dt < NC; ++dt) {
-            float v[4] = {o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv};
-            if (a.gate) {
-                const float g[4] = {gv[dt].x, gv[dt].y, gv[dt].z, gv[dt].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = v[i] * (1.0f / (1.0f + expf(-g[i])));
-            }
-            *reinterpret_cast<float4*>(a.out + orow * D + 16 * dt + 4 * qq) = make_float4(v[0], v[1], v[2], v[3]);
+            const u32x4 cur = va[dt % kB16Ahead];
+            if (dt + kB16Ahead < NC) va[dt % kB16Ahead] = vread(dt + kB16Ahead);
+            __builtin_amdgcn_sched_barrier(0);
+            o[dt] = mfma16x16x32(cur, pop, o[dt]);
+            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+
+    lds_barrier();                                   // the producers' first tile is in stage 0
+    for (int t = 0; t < n_iter; ++t) {
+        if (active && t < n_tiles) consume(t, t & 1);
+        lds_barrier();
     }
+    if (!active) return;
+    l_run += __shfl_xor(l_run, 16);                  // each lane summed the probabilities of its own keys
+    l_run += __shfl_xor(l_run, 32);
+    finish_queries<D>(a, we, o, m_run, l_run, head, half, row0, nq);
 }
 
 }  // namespace
@@ -1000,12 +1305,14 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     if ((unsigned long long)max_nb * block_size >= (1ull << 31))
         return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d blocks of %d positions (positions must stay below 2^31)",
                     max_nb, block_size);
-    // bf16 operands only where every input already is bf16 (q and the pool), the shape has an instance and the
-    // producers' one-multiply block index is exact: positions x block size below 2^32, and block_size >= 2 (the
-    // reciprocal ceil(2^32 / bs) must fit 32 bits)
-    const bool bf16_ops = !exact && q_dtype == RK_BF16 && pool_dtype == RK_BF16 && Hq == kMaxGroup * Hkv &&
-                          (D == 128 || D == 256) && block_size >= 2 &&
-                          (unsigned long long)max_nb * block_size * block_size < (1ull << 32);
+    // Which kernel. fp32 operands (prefill_attention_f32) for an fp32 q or pool and for exact requests; bf16
+    // operands where q and the pool both are bf16: the 32-query kernel (prefill_attention) at 4 query heads per
+    // kv-head and head_dim 128 / 256 where its producers' one-multiply block index is exact (positions x block size
+    // below 2^32, block_size >= 2: the reciprocal ceil(2^32 / bs) must fit 32 bits), the 16-query kernel
+    // (prefill_attention_b16) for every other shape.
+    const bool bf16_ops = !exact && q_dtype == RK_BF16 && pool_dtype == RK_BF16;
+    const bool wide_q = bf16_ops && Hq == kMaxGroup * Hkv && (D == 128 || D == 256) && block_size >= 2 &&
+                        (unsigned long long)max_nb * block_size * block_size < (1ull << 32);
     for (int dt : {q_dtype, k_new ? new_dtype : RK_F32, pool_dtype, gate ? gate_dtype : RK_F32})
         if (dt != RK_F32 && dt != RK_BF16) return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: dtype %d", dt);
     PrefillArgs a;
@@ -1027,8 +1334,9 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     }
     typedef void (*AttnFn)(PrefillArgs);
     AttnFn fn;
-    if (bf16_ops) {
-        const bool tab_lds = max_nb <= kTabCache;
+    const bool tab_lds = max_nb <= kTabCache;
+    const int chunks = (a.G + kF32Heads - 1) / kF32Heads;   // head chunks of the 16-query kernels
+    if (wide_q) {
         const size_t lds = (tab_lds ? kTabCache * 4 : 0) +
                            (size_t)kStages * (kBKP * (D + kKPad) + D * (kBKP + kVPad)) * sizeof(uint16_t);
         if (D == 256) fn = tab_lds ? prefill_attention<256, uint16_t, true> : prefill_attention<256, uint16_t, false>;
@@ -1037,7 +1345,16 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
         hipLaunchKernelGGL(fn, dim3(n_work, Hkv), dim3(2 * 64 * a.G), lds, s, a);
         return check_launch("prefill_attention");
     }
-    const bool tab_lds = max_nb <= kTabCache;
+    if (bf16_ops) {
+        const size_t lds = (size_t)2 * (kBKP * (D + kB16KPad) + D * kB16VRow) * sizeof(uint16_t) +
+                           (tab_lds ? kTabCache * sizeof(int) : 0);
+        if (D == 256) fn = tab_lds ? prefill_attention_b16<256, true> : prefill_attention_b16<256, false>;
+        else if (D == 128) fn = tab_lds ? prefill_attention_b16<128, true> : prefill_attention_b16<128, false>;
+        else fn = tab_lds ? prefill_attention_b16<64, true> : prefill_attention_b16<64, false>;
+        if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
+        hipLaunchKernelGGL(fn, dim3(n_work, Hkv, chunks), dim3(kB16Threads), lds, s, a);
+        return check_launch("prefill_attention_b16");
+    }
     const size_t lds = (size_t)2 * (kBKP * (D + kF32Pad) + D * (kBKP + kF32Pad)) * sizeof(float) +
                        (tab_lds ? kTabCache * sizeof(int) : 0);
     const bool f32_pool = pool_dtype == RK_F32;
@@ -1049,7 +1366,6 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     else RK_F32_PICK(64);
 #undef RK_F32_PICK
     if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
-    const int chunks = (a.G + kF32Heads - 1) / kF32Heads;
     hipLaunchKernelGGL(fn, dim3(n_work, Hkv, chunks), dim3(512), lds, s, a);
     return check_launch("prefill_attention_f32");
 }

@@ -1,11 +1,11 @@
 """P4 parity: the packed prefill attention kernel (rk_paged_prefill) vs the CPU oracle (oracle/prefill_ref.py, the
 reference's per-segment write -> read -> causal attention -> gate).
 
-The reference computes in fp32 on widened inputs (src/ops.py:84-87). bf16 q and pool at 4 query heads per kv-head
-(config 5) run on bf16 MFMA operands (probabilities rounded to bf16) with fp32 accumulation and are held to the bar
-for bf16 outputs, 1e-2 relative (max|diff| / max|ref|) of the fp32 oracle; fp32 inputs (the Qwen3.5 engine's own
-fp32 pools, src/models/qwen3_5.py:70-71), other group sizes and head_dim 64, and exact=True run on fp32 operands and
-are held to 1e-5. The KV write-back is a copy (with fp32 -> bf16 rounding to nearest even) and must leave
+The reference computes in fp32 on widened inputs (src/ops.py:84-87). bf16 q and pool run on bf16 MFMA operands
+(probabilities rounded to bf16) with fp32 accumulation: 32 queries per wave at 4 query heads per kv-head (config 5),
+16 queries per wave for every other group size, head_dim 64 and block size 1; they are held to the bar for bf16
+outputs, 1e-2 relative (max|diff| / max|ref|) of the fp32 oracle. fp32 inputs (the Qwen3.5 engine's own fp32 pools,
+src/models/qwen3_5.py:70-71) and exact=True run on fp32 operands and are held to 1e-5. The KV write-back is a copy (with fp32 -> bf16 rounding to nearest even) and must leave
 the pool bit-identical to the oracle's; packing segments together must give bit-identical rows to running each
 segment alone under one split size (a block's cuts depend only on the block; the automatic size depends on the
 whole batch, so under it a segment alone may be cut where the packed batch is not).
@@ -44,8 +44,6 @@ def run_oracle(case, gate=True):
 @pytest.mark.parametrize("dtype,exact,tol", [(torch.bfloat16, False, TOL_BF16), (torch.bfloat16, True, TOL_F32),
                                              (torch.float32, False, TOL_F32)])
 def test_small_segments(backend, Hq, Hkv, d, dtype, exact, tol):
-    if dtype == torch.bfloat16 and not exact and Hq != 4 * Hkv:
-        tol = TOL_F32                                 # no bf16-operand instance: the fp32-operand kernel runs
     case = wl.prefill_case([5, 40, 100, 1, 33], [0, 17, 64, 200, 31], Hq, Hkv, d, 16, dtype, seed=7)
     got, gk, gv = run_gpu(backend, case, exact=exact)
     want, wk, wv = run_oracle(case)
@@ -67,15 +65,13 @@ def test_packed_equals_segment_by_segment(backend, dtype):
         assert torch.equal(alone, packed[lo:hi])
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, TOL_BF16), (torch.float32, TOL_F32)])
+@pytest.mark.parametrize("dtype,exact,tol", [(torch.bfloat16, False, TOL_BF16), (torch.bfloat16, True, TOL_F32),
+                                             (torch.float32, False, TOL_F32)])
 @pytest.mark.parametrize("bs", [32, 1, 5])
-def test_block_sizes_and_no_gate(backend, dtype, tol, bs):
-    """Block sizes 32, 5 and 1 (no bf16-operand instance at block size 1: the fp32-operand kernel runs, so a bf16
-    pool there meets the fp32 bar too)."""
-    if bs == 1:
-        tol = TOL_F32
+def test_block_sizes_and_no_gate(backend, dtype, exact, tol, bs):
+    """Block sizes 32, 5 and 1 (a bf16 pool of one-position blocks runs on the 16-query bf16 kernel)."""
     case = wl.prefill_case([64, 65, 17], [96, 3, 0], block_size=bs, dtype=dtype, seed=9)
-    got, _, _ = run_gpu(backend, case, gate=False)
+    got, _, _ = run_gpu(backend, case, gate=False, exact=exact)
     want, _, _ = run_oracle(case, gate=False)
     assert rel_err(got, want) < tol
 
@@ -96,12 +92,13 @@ def test_config5_full_size(backend, dtype, exact, tol):
 
 
 @pytest.mark.parametrize("dtype,Hq,Hkv,d,tol", [(torch.bfloat16, 8, 2, 256, TOL_BF16), (torch.float32, 8, 2, 256, TOL_F32),
-                                                (torch.bfloat16, 14, 2, 64, TOL_F32)])
+                                                (torch.bfloat16, 14, 2, 64, TOL_BF16), (torch.float32, 14, 2, 64, TOL_F32)])
 def test_split_blocks(backend, monkeypatch, dtype, Hq, Hkv, d, tol):
     """Blocks whose key range is cut into pieces (here every 2 tiles, so up to ~30 pieces per block): within the bar
     of the oracle, equal across two calls (the pieces are combined in piece order whatever finishes last), and a
     packed call gives the bits of each segment alone (the cuts depend only on the block). The arrival counters are
-    left at zero. Both kernels: bf16 operands, and fp32 operands (fp32 pool; a group of 7 over two head chunks)."""
+    left at zero. All three kernels: bf16 operands on 32 and on 16 queries per wave (a group of 7 over two head
+    chunks), fp32 operands (fp32 pool)."""
     from native import kernels
     case = wl.prefill_case([70, 129, 3, 40], [50, 900, 500, 0], Hq, Hkv, d, dtype=dtype, seed=11)
     want, wk, wv = run_oracle(case)
