@@ -601,9 +601,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //   O^T += V^T P^T: A = 16 dims x 4 keys from V^T (one 16-byte read of V^T[16 dt + l % 16][16 kt + 4 (l / 16) ..
 //                 + 3] feeds MFMAs r = 0 .. 3: keys 4 (l / 16) + r), B = P^T, the score accumulator's register r.
 // So every lane keeps its own query's softmax state (one reduction over the 4 quarters per tile), and O^T is
-// rescaled per lane. LDS reads are conflict-free: the padded strides put 16 consecutive K rows, and 16 consecutive
-// V^T rows, 4 banks apart. Staging writes are conflict-free for V^T (consecutive lanes take consecutive key groups
-// of one piece) and at most 2-way for K (consecutive lanes take consecutive pieces of one row group).
+// rescaled per lane. LDS reads are conflict-free: keys and dims are stored in permuted row orders (at the kernel)
+// that put each half wave's 32 16-byte reads on distinct units modulo 512 bytes. Staging writes are conflict-free
+// for V^T (consecutive lanes take consecutive key groups of one piece) and at most 2-way for K (consecutive lanes
+// take consecutive pieces of one row group).
 constexpr int kF32QW = 16;      // queries per wave
 constexpr int kF32Heads = 4;    // query heads per workgroup
 constexpr int kF32Pad = 4;      // fp32 padding of an LDS row
@@ -782,6 +783,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // e % PER_ROW of rows 4 (e / PER_ROW) .. + 3, V: piece e / GROUPS of rows 4 (e % GROUPS) .. + 3. Load r of a unit
     // is row 4 g + r; every load of a wave reads whole 128-byte row segments.
     u32x4 st[NU][4];
+    // LDS rows are permuted so that a half wave's 16-byte operand reads (16 consecutive rows, at two column offsets
+    // 16 bytes apart) fall on 32 distinct 16-byte units modulo 512 bytes, which gfx950 serves without bank conflicts:
+    // key 16 kt + i of a tile sits in K row 2 i + kt, dim 32 a + 16 b + i in V^T row 32 a + 2 i + b. With the odd
+    // 16-byte strides (D + 4 and 36 floats) rows 2 i then lie 2 units apart and the second column offset takes the
+    // odd units between them.
+    auto k_row = [](int key) { return 2 * (key & 15) + (key >> 4); };
+    auto v_row = [](int dim) { return (dim & ~31) + 2 * (dim & 15) + ((dim >> 4) & 1); };
     auto unit_of = [&](int j, int& g, int& pc) {
         const int u = tid + 512 * j, e = u % UNITS_T;
         const bool is_v = u >= UNITS_T;
@@ -831,34 +839,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int j = 0; j < NU; ++j) {
             if (tid + 512 * j >= 2 * UNITS_T) continue;
             int g, pc;
-            if (unit_of(j, g, pc)) {                 // V^T[pc EL + d][4 g .. + 3]
-                float* dst = s + KST + pc * EL * ROWT + 4 * g;
+            if (unit_of(j, g, pc)) {                 // V^T[v_row(pc EL + d)][4 g .. + 3]
+                float* dst = s + KST + 4 * g;
                 if constexpr (sizeof(TP) == 4) {
 #pragma unroll
                     for (int d = 0; d < 4; ++d)
-                        *reinterpret_cast<f32x4*>(dst + d * ROWT) = f32x4{
+                        *reinterpret_cast<f32x4*>(dst + v_row(pc * EL + d) * ROWT) = f32x4{
                             __uint_as_float(st[j][0][d]), __uint_as_float(st[j][1][d]),
                             __uint_as_float(st[j][2][d]), __uint_as_float(st[j][3][d])};
                 } else {                             // bf16 -> fp32, exact
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
-                        *reinterpret_cast<f32x4*>(dst + (2 * d) * ROWT) = f32x4{
+                        *reinterpret_cast<f32x4*>(dst + v_row(pc * EL + 2 * d) * ROWT) = f32x4{
                             bf16_lo(st[j][0][d]), bf16_lo(st[j][1][d]), bf16_lo(st[j][2][d]), bf16_lo(st[j][3][d])};
-                        *reinterpret_cast<f32x4*>(dst + (2 * d + 1) * ROWT) = f32x4{
+                        *reinterpret_cast<f32x4*>(dst + v_row(pc * EL + 2 * d + 1) * ROWT) = f32x4{
                             bf16_hi(st[j][0][d]), bf16_hi(st[j][1][d]), bf16_hi(st[j][2][d]), bf16_hi(st[j][3][d])};
                     }
                 }
-            } else {                                 // K[4 g + r][pc EL ..]
-                float* dst = s + 4 * g * ROW + pc * EL;
+            } else {                                 // K[k_row(4 g + r)][pc EL ..]
+                float* dst = s + pc * EL;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if constexpr (sizeof(TP) == 4) {
-                        *reinterpret_cast<u32x4*>(dst + r * ROW) = st[j][r];
+                        *reinterpret_cast<u32x4*>(dst + k_row(4 * g + r) * ROW) = st[j][r];
                     } else {
                         const u32x4 w = st[j][r];
-                        *reinterpret_cast<f32x4*>(dst + r * ROW) =
+                        *reinterpret_cast<f32x4*>(dst + k_row(4 * g + r) * ROW) =
                             f32x4{bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1])};
-                        *reinterpret_cast<f32x4*>(dst + r * ROW + 4) =
+                        *reinterpret_cast<f32x4*>(dst + k_row(4 * g + r) * ROW + 4) =
                             f32x4{bf16_lo(w[2]), bf16_hi(w[2]), bf16_lo(w[3]), bf16_hi(w[3])};
                     }
                 }
@@ -904,7 +912,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int c = 0; c < NC; ++c) {
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                const f32x4 kv = *reinterpret_cast<const f32x4*>(ks + (16 * kt + qc) * ROW + 16 * c + 4 * qq);
+                const f32x4 kv = *reinterpret_cast<const f32x4*>(ks + (2 * qc + kt) * ROW + 16 * c + 4 * qq);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) s[kt] = mfma_f32(kv[j], qv[c][j], s[kt]);
             }
@@ -919,40 +927,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     s[kt][r] = key <= qpos && key > qlo ? s[kt][r] : -INFINITY;
                 }
         }
-        float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                           fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.qscale;
-        const float m_new = tmax > m_run + kLazy ? tmax : m_run;
-        const float mb = m_new == -INFINITY ? 0.0f : m_new;
-        float psum = 0.0f;
+        const float m_prev = m_run;
+        lazy_max(s, m_run, a.qscale);
+        const float mb = m_run == -INFINITY ? 0.0f : m_run;
+        if (__any(m_run != m_prev)) {
+            const float alpha = fast_exp2(m_prev - mb);     // 0 on the first tile (m_prev = -inf)
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NC; ++dt) o[dt] *= alpha;
+        }
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 s[kt][r] = fast_exp2(fmaf(s[kt][r], a.qscale, -mb));
-                psum += s[kt][r];
+                l_run += s[kt][r];                   // this lane's keys; the 4 lanes of a query are summed at the end
             }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
-        if (__any(m_new != m_run)) {
-            const float alpha = fast_exp2(m_run - mb);      // 0 on the first tile (m_run = -inf)
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < NC; ++dt) o[dt] *= alpha;
-        }
-        l_run += psum;
-        m_run = m_new;
-        // V^T reads one dim group ahead of their MFMAs
-        const float* vt = vs + qc * ROWT + 4 * qq;
-        f32x4 vv = *reinterpret_cast<const f32x4*>(vt);
+        // V^T reads one dim group ahead of their MFMAs (group i: dims 16 (i % NC) + qc, keys 16 (i / NC) + 4 qq ..)
+        const float* vt = vs + 2 * qc * ROWT + 4 * qq;
+        auto vread = [&](int i) {
+            const int dt = i % NC, kt = i / NC;
+            return *reinterpret_cast<const f32x4*>(vt + (32 * (dt >> 1) + (dt & 1)) * ROWT + 16 * kt);
+        };
+        f32x4 vv = vread(0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // the first read,
 #pragma unroll
         for (int i = 0; i < 2 * NC; ++i) {
             const int kt = i / NC, dt = i % NC;
             const f32x4 cur = vv;
-            if (i + 1 < 2 * NC)
-                vv = *reinterpret_cast<const f32x4*>(vt + 16 * ((i + 1) % NC) * ROWT + 16 * ((i + 1) / NC));
+            if (i + 1 < 2 * NC) vv = vread(i + 1);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // the next read,
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // then this group's four MFMAs
 #pragma unroll
@@ -977,6 +980,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
     if (!active) return;
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
     finish_queries<D>(a, we, o, m_run, l_run, head, half, row0, nq);
 }
 
