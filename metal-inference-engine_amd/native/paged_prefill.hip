@@ -352,15 +352,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 s[r] = key <= qpos && key > qlo ? s[r] : -INFINITY;
             }
         }
+        // the lane compares its own 16 scores first; only when some lane exceeds m + kLazy is the maximum over the
+        // column's two lanes formed (the same m as max-then-compare over all 32 keys: scaling by qscale > 0 is
+        // monotonic, so it commutes with max)
         float tmax = s[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * a.qscale;
-        const float m_new = tmax > m_run + kLazy ? tmax : m_run;
+        tmax *= a.qscale;
+        const float m_prev = m_run;
+        if (__any(tmax > m_run + kLazy)) {
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            m_run = tmax > m_run + kLazy ? tmax : m_run;
+        }
         // -inf only while every key this column has seen was masked (a window starting past the first tile); then
         // the exponents are taken against 0, so the masked keys give 0 (not NaN) and nothing is rescaled
-        const float mb = m_new == -INFINITY ? 0.0f : m_new;
-        float psum = 0.0f;
+        const float mb = m_run == -INFINITY ? 0.0f : m_run;
+        if (__any(m_run != m_prev)) {
+            const float alpha = fast_exp2(m_prev - mb);     // 0 on the first tile (m_prev = -inf)
+            l_run *= alpha;
+#pragma unroll
+            for (int t = 0; t < NDT; ++t) o[t] *= alpha;
+        }
         u32x4 pop[2];                                // B operands of the 2 key k-steps
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -368,22 +380,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 pv[e] = fast_exp2(fmaf(s[8 * half + e], a.qscale, -mb));
-                psum += pv[e];
+                l_run += pv[e];                      // this lane's 16 keys; the column's two lanes are summed at the end
             }
             u32x4 w;
 #pragma unroll
             for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2_rne(pv[2 * j], pv[2 * j + 1]);
             pop[half] = w;
         }
-        psum += __shfl_xor(psum, 32);
-        if (__any(m_new != m_run)) {
-            const float alpha = fast_exp2(m_run - mb);      // 0 on the first tile (m_run = -inf)
-            l_run *= alpha;
-#pragma unroll
-            for (int t = 0; t < NDT; ++t) o[t] *= alpha;
-        }
-        l_run += psum;
-        m_run = m_new;
         // ---- O^T += V^T P^T: k-step u covers keys 16 u + 8 (e / 4) + 4 kg + e % 4
         // (the V^T operands of the next 32-dim block are requested before this block's MFMAs)
         auto vread = [&](int dt, u32x4 (&va)[2]) {
@@ -467,6 +470,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (t < n_tiles) consume(t, t & (kStages - 1));
         lds_barrier();
     }
+    l_run += __shfl_xor(l_run, 32);
 
     // A piece of a split item stores its (o, m, l) for its head, then counts itself in; the last of the item's
     // pieces to finish reads all of them back in piece order and combines them: m = max m_p,
