@@ -98,7 +98,8 @@ ALGORITHMIC = {
     "chunked_delta/c4": (346.0, "q, k, v bf16, beta, g, o fp32, final states; + the T / coefficient workspace"),
     "delta_chunk_scan/c4": (None, "the scan alone"),
     "prefill_attention/c5": (356.7, "bf16 operands; K / V re-read once per 32-query block"),
-    "prefill_attention_f32/c5f": (631.7, "fp32 pool and q; K / V re-read once per 32-query block"),
+    "prefill_attention_f32/c5f": (631.7, "fp32 pool and q; K / V re-read once per 32-query block; balance-split "
+                                         "pieces write partial records"),
     "deltanet_prefill_front/lp": (810.2, "qkv / b / a columns + K-1 rows per 32-token run; q, k, v, beta, g written"),
     "rms_norm_gated/lp": (402.7, "x and z read, out written once"),
     "linear_rows/mv": (14.8, "mean of the step's 97 launches; x re-read per row group, K-split partials"),
