@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 15
+#define RK_ABI_VERSION 16
 
 /* status codes */
 #define RK_OK 0

@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 RK_F32, RK_BF16 = 0, 1
 RK_W_BF16, RK_W_INT8, RK_W_INT4 = 1, 2, 3
