@@ -18,7 +18,7 @@ each decode kernel's own access pattern with no arithmetic (librk_probe.so).
 Other workloads print the same record for: c1, the config-1 decode (parity/latency case); c2, the config-2 DeltaNet
 decode step (batch 8; state slots rotated so reads come from HBM, not the 256 MB Infinity Cache); c4, the config-4
 chunked gated delta prefill (4 x 4096 tokens, both kernels); c5, the config-5 packed prefill attention (c5f: the
-same batch in fp32, on the fp32-operand kernel); lp, the
+same batch in fp32, on the fp32-operand kernel; c5g: at 14/2 heads x 64, on the 16-query bf16 kernel); lp, the
 DeltaNet prefill companions (fused conv / norms / beta, g front and the gated RMSNorm) on the config-4 batch; ap,
 the config-3 decode attention layer with its q / k norm, RoPE and KV write (rk_attn_prep) in front; wd, the
 sliding-window decode (window 4096) through the grouped pool's rings; mv, every linear of a Qwen3.5-2B decode step at
@@ -415,17 +415,24 @@ def bench_deltanet(args, backend):
 FP32_MFMA_PEAK_TFLOPS = 157.3     # MI355X dense fp32 matrix peak
 
 
-def bench_prefill(args, backend, chunk: bool = False, fp32: bool = False):
+def bench_prefill(args, backend, chunk: bool = False, fp32: bool = False, g7: bool = False):
     """Config 5 (chunk False), or one 512-token chunk over a 32,768-token history (chunk True: the grid without
     split key ranges would fill 32 of 256 CUs). fp32: config 5's batch in the Qwen3.5 engine's own fp32 pool and
-    activations, which runs on the fp32-operand kernel (fp32 MFMA), priced against the fp32 matrix peak."""
+    activations, which runs on the fp32-operand kernel (fp32 MFMA), priced against the fp32 matrix peak. g7: config
+    5's batch at 14/2 heads x 64 (the reference's own kernel-test shape, tests/test_kernels.py:107-114), bf16, which
+    runs on the 16-query bf16-operand kernel."""
     import torch
     import workloads as wl
     from native import kernels
     dev = backend.device
     stream = torch.cuda.current_stream(dev)
-    case = wl.chunk_prefill() if chunk else wl.c5_prefill(dtype=torch.float32 if fp32 else torch.bfloat16)
-    tag = "ck" if chunk else ("c5f" if fp32 else "c5")
+    if chunk:
+        case = wl.chunk_prefill()
+    elif g7:
+        case = wl.c5_prefill(Hq=14, Hkv=2, d=64)
+    else:
+        case = wl.c5_prefill(dtype=torch.float32 if fp32 else torch.bfloat16)
+    tag = "ck" if chunk else ("c5f" if fp32 else ("c5g" if g7 else "c5"))
     c = case.to(dev)
     torch.cuda.synchronize()
 
@@ -477,6 +484,22 @@ def bench_prefill(args, backend, chunk: bool = False, fp32: bool = False):
             "roofline": {"bound": "mfma", "achieved": tflops, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tflops / FP32_MFMA_PEAK_TFLOPS, "traffic": traffic_for("prefill_attention_f32/c5f"),
                          "kernel": "prefill_attention_f32 (+ prefill_kv_write)", "avg_ms": ms},
+            "cpu_baseline": cpu,
+        }
+    if g7:
+        return {
+            "metric": "packed prefill attention tokens/s (config 5 batch at 14/2 heads x 64) + TFLOP/s (% of bf16 "
+                      "MFMA peak), 1 GPU",
+            "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded)",
+            "config": {"workload": "config 5's segments (8 packed, new U[64, 2048] on prefixes U[0, 16384]) at 14/2 "
+                                   "heads x 64, the reference's kernel-test shape (group 7: the 16-query bf16 "
+                                   "kernel, two head chunks), block 16, causal, gate, KV write-back",
+                       "new_tokens": N, "flops": flops},
+            "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": tflops / 2500.0, "traffic": traffic_for("prefill_attention_b16/c5g"),
+                         "kernel": "prefill_attention_b16 (+ prefill_kv_write)", "avg_ms": ms},
             "cpu_baseline": cpu,
         }
     if chunk:
@@ -956,7 +979,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "c1", "c2", "c3", "c4", "c5", "c5f", "ck", "lp", "ap", "wd", "mv", "ds"],
+                    choices=["all", "c1", "c2", "c3", "c4", "c5", "c5f", "c5g", "ck", "lp", "ap", "wd", "mv", "ds"],
                     help="all (default): the config-3 headline record with configs 1, 2, 4, 5 as sub-records and "
                          "the measured access-pattern ceilings")
     ap.add_argument("--sets", type=int, default=2, help="distinct input copies rotated between steps")
@@ -1012,7 +1035,8 @@ def main() -> int:
         for name, fn in (("c1", c1), ("c2", lambda: bench_deltanet(args, backend)),
                          ("c4", lambda: bench_chunked_delta(args, backend)),
                          ("c5", lambda: bench_prefill(args, backend)),
-                         ("c5_fp32", lambda: bench_prefill(args, backend, fp32=True))):
+                         ("c5_fp32", lambda: bench_prefill(args, backend, fp32=True)),
+                         ("c5_g7", lambda: bench_prefill(args, backend, g7=True))):
             sub = fn()
             subs[name] = {k: v for k, v in sub.items() if k in keep}
             torch.cuda.empty_cache()
@@ -1035,6 +1059,8 @@ def main() -> int:
         rec = bench_prefill(args, backend)
     elif args.workload == "c5f":
         rec = bench_prefill(args, backend, fp32=True)
+    elif args.workload == "c5g":
+        rec = bench_prefill(args, backend, g7=True)
     elif args.workload == "ck":
         rec = bench_prefill(args, backend, chunk=True)
     elif args.workload == "c4":

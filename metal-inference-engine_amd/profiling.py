@@ -100,6 +100,7 @@ ALGORITHMIC = {
     "prefill_attention/c5": (356.7, "bf16 operands; K / V re-read once per 32-query block"),
     "prefill_attention_f32/c5f": (631.7, "fp32 pool and q; K / V re-read once per 32-query block; balance-split "
                                          "pieces write partial records"),
+    "prefill_attention_b16/c5g": (119.9, "14/2 x 64 heads: K / V re-read once per 32-query block and head chunk"),
     "deltanet_prefill_front/lp": (810.2, "qkv / b / a columns + K-1 rows per 32-token run; q, k, v, beta, g written"),
     "rms_norm_gated/lp": (402.7, "x and z read, out written once"),
     "linear_rows/mv": (14.8, "mean of the step's 97 launches; x re-read per row group, K-split partials"),

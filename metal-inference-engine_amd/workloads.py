@@ -300,14 +300,15 @@ def prefill_case(lengths: list[int], starts: list[int], Hq: int = HQ, Hkv: int =
     return PrefillCase(q, k_new, v_new, gate, k_pool, v_pool, tables, cu, list(starts), block_size)
 
 
-def c5_prefill(seed: int = 5, dtype=torch.bfloat16) -> PrefillCase:
+def c5_prefill(seed: int = 5, dtype=torch.bfloat16, Hq: int = HQ, Hkv: int = HKV, d: int = HEAD_DIM) -> PrefillCase:
     """Config 5: 8 segments, new lengths U[64, 2048], prefixes U[0, 16384], bf16 everything, 8/2 heads x 256,
     block 16, sigmoid gate; the prefix K/V are the random pool contents under each segment's table. dtype fp32 gives
-    the same batch in the Qwen3.5 engine's own fp32 pool and activations (src/models/qwen3_5.py:70-71)."""
+    the same batch in the Qwen3.5 engine's own fp32 pool and activations (src/models/qwen3_5.py:70-71); Hq / Hkv / d
+    the same batch at other heads."""
     gen = torch.Generator().manual_seed(seed)
     lengths = torch.randint(64, 2049, (8,), generator=gen).tolist()
     starts = torch.randint(0, 16385, (8,), generator=gen).tolist()
-    return prefill_case(lengths, starts, dtype=dtype, seed=seed + 1000)
+    return prefill_case(lengths, starts, Hq, Hkv, d, dtype=dtype, seed=seed + 1000)
 
 
 def chunk_prefill(seed: int = 6) -> PrefillCase:
