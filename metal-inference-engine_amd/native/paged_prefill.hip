@@ -1050,7 +1050,6 @@ __global__ __launch_bounds__(kB16Threads) void prefill_attention_b16(PrefillArgs
     const int kmin = a.window > 0 ? max(0, p0 - a.window + 1) : 0;
     const int t_first = max(kmin / kBKP, we[1]);
     const int n_tiles = min((n_keys + kBKP - 1) / kBKP, we[2]) - t_first;
-    if (n_tiles <= 0) return;                        // whole workgroup (the host never lists an empty entry)
     const int32_t* table = a.tables + (long long)seg * a.max_nb;
     const bool active = !producer && gh < a.G && half * kF32QW < nq;     // whole waves
     const int head = kvh * a.G + (gh < a.G ? gh : 0);
@@ -1064,16 +1063,18 @@ __global__ __launch_bounds__(kB16Threads) void prefill_attention_b16(PrefillArgs
     // every position a producer reads lies in [b_lo's first row, the entry's last key]: groups are clamped into
     // the entry's key range (rounded down to 4 for groups below the window)
     int r0;
-    const int b_lo = block_of(max(kmin, t_first * kBKP) / 4 * 4, r0);
+    const int b_lo = n_tiles > 0 ? block_of(max(kmin, t_first * kBKP) / 4 * 4, r0) : 0;
     if (TAB_LDS) {
-        const int b_hi = block_of(min(n_keys, (t_first + n_tiles) * kBKP) - 1, r0);
+        const int b_hi = n_tiles > 0 ? block_of(min(n_keys, (t_first + n_tiles) * kBKP) - 1, r0) : -1;
         for (int i = b_lo + tid; i <= b_hi; i += kB16Threads) {
             const int blk = table[i];
             tab[i - b_lo] = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
         }
         __syncthreads();
     }
-    const int n_iter = (n_tiles + DEPTH - 1) / DEPTH * DEPTH;
+    // an entry without tiles (not produced by the host's work lists) stages nothing; its consumers still write
+    // their (empty) split record, so a split item is always combined
+    const int n_iter = n_tiles > 0 ? (n_tiles + DEPTH - 1) / DEPTH * DEPTH : 0;
 
     if (producer) {
         // ---- producer lane pl: K unit pl (piece pl % PER_ROW of rows 4 (pl / PER_ROW) .. + 3: consecutive lanes,
@@ -1081,8 +1082,8 @@ __global__ __launch_bounds__(kB16Threads) void prefill_attention_b16(PrefillArgs
         // consecutive lanes, consecutive key groups). The same code for every lane: a branch between K and V work
         // would make the compiler wait for all loads in flight where the branches join.
         const int pl = tid - 8 * 64;
-        if (__builtin_amdgcn_readfirstlane(pl) >= UNITS_T) {     // whole waves without a unit (D < 256)
-            for (int k = 0; k <= n_iter; ++k) lds_barrier();
+        if (__builtin_amdgcn_readfirstlane(pl) >= UNITS_T || n_tiles <= 0) {   // whole waves without a unit
+            for (int k = 0; k <= n_iter; ++k) lds_barrier();                     // (D < 256), or nothing to stage
             return;
         }
         const int gk = pl / PER_ROW, pk = pl % PER_ROW;

@@ -156,3 +156,50 @@ def test_unsupported_head_dim_refused(backend):
                                           case.k_pool.shape[0], None, 0, 0, 1, 0, 0, None, 0, None, 0,
                                           kernels._stream(torch.device(DEV)))
     assert rc == 2
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv,d,tol", [(torch.bfloat16, 8, 2, 256, TOL_BF16), (torch.bfloat16, 14, 2, 64, TOL_BF16),
+                                                (torch.float32, 8, 2, 256, TOL_F32)])
+def test_split_item_with_an_empty_piece(backend, dtype, Hq, Hkv, d, tol):
+    """A work list written by hand (through the C ABI) whose split block has a first piece lying wholly below the
+    block's window, so that piece has no tiles: it still writes its (empty) record and counts in, and the block's
+    output is the other piece's, within the bar of the oracle. All three kernels (32- and 16-query bf16 operands,
+    fp32 operands)."""
+    from native import kernels
+    from oracle import ops_ref
+    W, n, p = 40, 32, 300                          # one 32-query block at positions 300 .. 331, window 40
+    case = wl.prefill_case([n], [p], Hq, Hkv, d, 16, dtype, seed=21)
+    c = case.to(DEV)
+    out = torch.empty(n, Hq, d, dtype=torch.float32, device=DEV)
+    kmin = p - W + 1                               # the block's first visible key: tile kmin // 32 = 8
+    t_lo, t_hi = kmin // 32, -(-(p + n) // 32)
+    # piece 0 covers tiles [2, 8): below the window; piece 1 covers [8, t_hi)
+    work = [0, 2, t_lo, 0, (0 << 16) | 2, 0, t_lo, t_hi, 0, (1 << 16) | 2]
+    meta = torch.tensor(list(case.cu_seqlens) + list(case.starts) + work, dtype=torch.int32, device=DEV)
+    lib = kernels.load()
+    part_bytes = lib.lib.rk_paged_prefill_workspace_bytes(2, Hq, d)
+    n_cnt = lib.lib.rk_paged_prefill_counters(2, Hq)
+    part = torch.full((part_bytes // 4,), float("nan"), device=DEV)
+    cnt = torch.zeros(n_cnt, dtype=torch.int32, device=DEV)
+    code = kernels.DTYPE_CODES[dtype]
+    NB, bs = c.k_pool.shape[0], c.k_pool.shape[1]
+    lib.call("rk_paged_prefill", out.data_ptr(), c.q.data_ptr(), code, c.k_new.data_ptr(), c.v_new.data_ptr(), code,
+             c.k_pool.data_ptr(), c.v_pool.data_ptr(), code, c.tables.data_ptr(), c.tables.shape[1], meta.data_ptr(),
+             meta.data_ptr() + 4 * 2, meta.data_ptr() + 4 * 3, 2, 1, n, Hq, Hkv, d, bs, NB, None,
+             kernels.DTYPE_CODES[torch.float32], W, 1, 0, 2, part.data_ptr(), part_bytes, cnt.data_ptr(), n_cnt,
+             torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = case.clone()
+    table = ref.tables[0].long()
+    pos = torch.arange(p, p + n)
+    ref.k_pool[table[pos // bs], pos % bs] = ref.k_new.to(ref.k_pool.dtype)
+    ref.v_pool[table[pos // bs], pos % bs] = ref.v_new.to(ref.v_pool.dtype)
+    nb = -(-(p + n) // bs)
+    K = ref.k_pool[table[:nb]].flatten(0, 1)[:p + n]
+    V = ref.v_pool[table[:nb]].flatten(0, 1)[:p + n]
+    want = ops_ref.attention(ref.q, K, V, causal=True, window=W)
+    err = rel_err(out, want)
+    which = kernels.prefill_kernel(dtype, dtype, Hq, Hkv, d, False, c.tables.shape[1], bs)
+    print(f"empty split piece, {which} {Hq}/{Hkv}x{d}: rel err {err:.2e}")
+    assert torch.isfinite(out).all() and err < tol
+    assert int(cnt.abs().sum()) == 0
