@@ -606,7 +606,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //                 + 3] feeds MFMAs r = 0 .. 3: keys 4 (l / 16) + r), B = P^T, the score accumulator's register r.
 // So every lane keeps its own query's softmax state (one reduction over the 4 quarters per tile), and O^T is
 // rescaled per lane. LDS reads are conflict-free: keys and dims are stored in permuted row orders (at the kernel)
-// that put each half wave's 32 16-byte reads on distinct units modulo 512 bytes. Staging writes are conflict-free
+// under which the 16 rows a wave's lanes read lie an effective 2 (mod 4) 16-byte units apart, in lane order (the
+// rule measured for 16-byte reads on gfx950, at the 16-query bf16 kernel). Staging writes are conflict-free
 // for V^T (consecutive lanes take consecutive key groups of one piece) and at most 2-way for K (consecutive lanes
 // take consecutive pieces of one row group).
 constexpr int kF32QW = 16;      // queries per wave
@@ -787,11 +788,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // e % PER_ROW of rows 4 (e / PER_ROW) .. + 3, V: piece e / GROUPS of rows 4 (e % GROUPS) .. + 3. Load r of a unit
     // is row 4 g + r; every load of a wave reads whole 128-byte row segments.
     u32x4 st[NU][4];
-    // LDS rows are permuted so that a half wave's 16-byte operand reads (16 consecutive rows, at two column offsets
-    // 16 bytes apart) fall on 32 distinct 16-byte units modulo 512 bytes, which gfx950 serves without bank conflicts:
-    // key 16 kt + i of a tile sits in K row 2 i + kt, dim 32 a + 16 b + i in V^T row 32 a + 2 i + b. With the odd
-    // 16-byte strides (D + 4 and 36 floats) rows 2 i then lie 2 units apart and the second column offset takes the
-    // odd units between them.
+    // LDS rows are permuted so that the 16 rows a wave's lanes read for one 16-byte operand (lane l: row l % 16,
+    // column piece l / 16) lie 2 (mod 4) 16-byte units apart, in lane order, which gfx950 serves without bank
+    // conflicts: key 16 kt + i of a tile sits in K row 2 i + kt, dim 32 a + 16 b + i in V^T row 32 a + 2 i + b, so
+    // with the odd 16-byte strides (D + 4 and 36 floats) lane i's row is 2 i rows (2 x odd units) from lane 0's.
     auto k_row = [](int key) { return 2 * (key & 15) + (key >> 4); };
     auto v_row = [](int dim) { return (dim & ~31) + 2 * (dim & 15) + ((dim >> 4) & 1); };
     auto unit_of = [&](int j, int& g, int& pc) {
@@ -1004,14 +1004,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //                 (j < 4) or 16 + 4 (l / 16) + j - 4, which are exactly the keys of the lane's own scores
 //                 s[0][0..3], s[1][0..3]: the B operand is those 8 probabilities rounded to bf16, and V^T rows hold
 //                 their keys in that order, so A is one 16-byte read at slot 8 (l / 16) of the dim's row.
-// LDS banks: a 16-byte read (ds_read_b128) is conflict-free on gfx950 when, within each half wave (32 lanes), the
-// lanes' 16-byte offsets are distinct modulo 512 bytes (measured: 16 consecutive rows of a 33-unit stride, read at
-// two column offsets, conflict, 32 consecutive rows do not). Here lanes l and l + 16 read 16 consecutive rows at
-// columns 16 bytes apart, so row strides of 2 x odd 16-byte units (K: D + 16 bf16, V^T: 48 bf16) put the 32 pieces
-// on 32 distinct units. The 8-byte V^T writes of a half wave cover 4 dims 8 apart; with a 96-byte stride those rows
-// would share banks, so dim d lives in V^T row vt_row(d) = 8 (d / 8) + (d % 8 + 2 (d / 8)) % 8 (a rotation within
-// each group of 8 rows), which spreads the 4 rows over the banks (measured: the write rate of a linear layout) and
-// leaves the reads' 16 consecutive dims on 16 distinct rows of a 16-row group.
+// LDS banks (measured on gfx950 with SQ_LDS_BANK_CONFLICT, one probe dispatch per row stride S in 16-byte units):
+// 16-byte reads (ds_read_b128) where lane l takes row l % 16 at column piece l / 16 are conflict-free exactly when
+// S = 2 (mod 4) and the rows are taken in lane order; any other stride, or the same rows permuted among the lanes,
+// conflicts (and with lane l taking row l % 32 at piece l / 32, odd S). So K rows are D + 16 bf16 (S = D / 8 + 2)
+// and V^T rows 48 bf16 (S = 6), read in lane order. The producers' 8-byte V^T writes, whose half wave covers 4
+// dims 8 apart, share banks under that stride; they are 8x fewer than the reads (a rotation of the V^T rows that
+// spread them made every read conflict: 2,545 against 2,343 us at config 5's batch on 16/2 heads x 256).
 constexpr int kB16Depth = 4;    // tiles in flight in producer registers
 constexpr int kB16KPad = 16;    // bf16 padding of a K row in LDS
 constexpr int kB16VRow = 48;    // bf16 per V^T row in LDS: 32 keys + 16 padding
@@ -1136,16 +1135,15 @@ __global__ __launch_bounds__(kB16Threads) void prefill_attention_b16(PrefillArgs
             uint16_t* s = lds + stage * STAGE;
 #pragma unroll
             for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(s + (4 * gk + j) * KROW + pk * 8) = slot[j];
-            // dim 8 pv + d goes to V^T row vt_row(8 pv + d), keys 4 gv .. + 3 at slots 8 gv (gv < 4) or
-            // 8 (gv - 4) + 4; one byte permute per word takes the same 16-bit half (low: even d, high: odd d) of two
-            // key rows
+            // V^T row 8 pv + d, keys 4 gv .. + 3 at slots 8 gv (gv < 4) or 8 (gv - 4) + 4; one byte permute per word
+            // takes the same 16-bit half (low: even d, high: odd d) of two key rows
             uint16_t* vt = s + KBUF + pv * 8 * kB16VRow + (gv < 4 ? 8 * gv : 8 * (gv - 4) + 4);
 #pragma unroll
             for (int d = 0; d < 8; ++d) {
                 const uint32_t sel = d & 1 ? 0x07060302u : 0x05040100u;
                 const uint32_t w0 = __builtin_amdgcn_perm(slot[5][d / 2], slot[4][d / 2], sel);
                 const uint32_t w1 = __builtin_amdgcn_perm(slot[7][d / 2], slot[6][d / 2], sel);
-                *reinterpret_cast<u32x2*>(vt + ((d + 2 * pv) & 7) * kB16VRow) = u32x2{w0, w1};
+                *reinterpret_cast<u32x2*>(vt + d * kB16VRow) = u32x2{w0, w1};
             }
         };
         // tile t sits in slot t % DEPTH, then in stage t % 2; at iteration t the slot of tile t + 1 goes to LDS (into
@@ -1191,12 +1189,8 @@ __global__ __launch_bounds__(kB16Threads) void prefill_attention_b16(PrefillArgs
     auto consume = [&](int t_rel, int stage) {
         const uint16_t* ks = lds + stage * STAGE;
         const uint16_t* kr = ks + qc * KROW + 8 * qq;
-        // V^T rows of dims 16 dt + qc: vt_row = 16 dt + 8 (qc / 8) + (qc % 8 + 2 (qc / 8) + 4 (dt % 2)) % 8
-        const uint16_t* vr0 = ks + KBUF + (8 * (qc >> 3) + (((qc & 7) + 2 * (qc >> 3)) & 7)) * kB16VRow + 8 * qq;
-        const uint16_t* vr1 = ks + KBUF + (8 * (qc >> 3) + (((qc & 7) + 2 * (qc >> 3) + 4) & 7)) * kB16VRow + 8 * qq;
-        auto vread = [&](int dt) {
-            return *reinterpret_cast<const u32x4*>((dt & 1 ? vr1 : vr0) + 16 * dt * kB16VRow);
-        };
+        const uint16_t* vr = ks + KBUF + qc * kB16VRow + 8 * qq;      // V^T row 16 dt + qc
+        auto vread = [&](int dt) { return *reinterpret_cast<const u32x4*>(vr + 16 * dt * kB16VRow); };
         const int k0 = (t_first + t_rel) * kBKP;
         f32x4 s[2] = {f32x4{}, f32x4{}};
         // K operands kB16Ahead reads ahead of their MFMAs (read i: dims 32 (i / 2), keys 16 (i % 2) ..); the
