@@ -7,11 +7,13 @@
 // src/ops.py:65-104, src/models/packing.py:21-31). Here:
 //   1. prefill_kv_write: the new K/V rows go into the pool first (rounded to the pool's type), so attention reads
 //      exactly what the reference's gather reads back.
-//   2. prefill_attention: one workgroup per (segment, block of 32 queries, kv-head): one consumer wave per query
-//      head of the group (MFMA products and online softmax) and as many producer waves, which stream the key range
-//      through a 2-stage LDS ring with 4 tiles of 32 keys in flight in their registers (details at the kernel).
-//      fp32 accumulation throughout; operands are bf16 (q, k, v as stored; p rounded), so results carry bf16-level
-//      error.
+//   2. attention, one of three kernels by the inputs (the host's rule at rk_paged_prefill): for bf16 q and pool,
+//      prefill_attention (one workgroup per (segment, block of 32 queries, kv-head): one consumer wave per query
+//      head of a group of 4, MFMA products and online softmax, and as many producer waves, which stream the key
+//      range through a 2-stage LDS ring with 4 tiles of 32 keys in flight in their registers) or, at every other
+//      bf16 shape, prefill_attention_b16 (16 queries per consumer wave); both on bf16 operands (q, k, v as stored;
+//      p rounded; fp32 accumulation), so results carry bf16-level error. For an fp32 q or pool, or an exact
+//      request, prefill_attention_f32 (fp32 products and probabilities). Details at each kernel.
 //   3. The output is divided by the softmax sum, gated and written as fp32 [N, Hq, D].
 // With a window W (causal only), query i also sees only keys above position p[s]+i-W (src/ops.py:77-81, 97-98): a
 // work item starts at the tile holding its first query's first visible key, so whole tiles below every query's
@@ -152,47 +154,24 @@ constexpr int kStages = 2;      // LDS ring stages
 constexpr int kTabCache = 4096; // block ids cached in LDS (max_nb above it takes the table from global memory)
 constexpr float kLazy = 8.0f;   // log2 headroom before the running maximum is raised
 
-template <typename TP>
-struct PoolRow;                 // 8 consecutive pool elements of one row, as loaded (converted when staged)
-template <>
-struct PoolRow<uint16_t> {
-#ifndef RK_PREFILL_DEPTH
-#define RK_PREFILL_DEPTH 4
-#endif
-    static constexpr int kDepth = RK_PREFILL_DEPTH;
+// 8 consecutive bf16 elements of one pool row, as a producer loads them
+struct PoolRow {
+    static constexpr int kDepth = 4;     // tiles in flight per producer lane
     u32x4 w;
     __device__ void load(const void* base, long long off) {
         w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
     }
     __device__ u32x4 bf16() const { return w; }
 };
-template <>
-struct PoolRow<float> {
-    static constexpr int kDepth = 2;
-    u32x4 w0, w1;
-    __device__ void load(const void* base, long long off) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(base) + off);
-        w0 = p[0];
-        w1 = p[1];
-    }
-    __device__ u32x4 bf16() const {
-        u32x4 r;
-        r[0] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w0[0])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w0[1])) << 16);
-        r[1] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w0[2])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w0[3])) << 16);
-        r[2] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w1[0])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w1[1])) << 16);
-        r[3] = (uint32_t)f32_to_bf16_rne(__uint_as_float(w1[2])) | ((uint32_t)f32_to_bf16_rne(__uint_as_float(w1[3])) << 16);
-        return r;
-    }
-};
 
-template <int D, typename TP, bool TAB_LDS>
+template <int D, bool TAB_LDS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_attention(PrefillArgs a) {
     constexpr int NKS = D / 16;          // k-steps of S^T (dims)
     constexpr int NDT = D / 32;          // 32-row tiles of O^T (dims)
     constexpr int KROW = D + kKPad;      // LDS K row stride (bf16)
     constexpr int VROW = kBKP + kVPad;   // LDS V^T row stride (bf16)
     constexpr int KBUF = kBKP * KROW, VBUF = D * VROW;
-    constexpr int DEPTH = PoolRow<TP>::kDepth;
+    constexpr int DEPTH = PoolRow::kDepth;
     constexpr int NJ = (kBKP / 4) * (D / 8);   // jobs of 4 keys x 8 dims per tile
     extern __shared__ __attribute__((aligned(16))) char smem[];
     int* tab = reinterpret_cast<int*>(smem);                                  // [kTabCache] when TAB_LDS
@@ -239,12 +218,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // spread over all banks; dim-chunk-major lanes would put 16 lanes on 2 bank groups)
     const int kqk = job / (D / 8), dck = job % (D / 8);
     const int kqv = job % (kBKP / 4), dcv = job / (kBKP / 4);
-    PoolRow<TP> buf[DEPTH][8];                       // [0..3] K rows of keys 4 kqk + j, [4..7] V rows of 4 kqv + j
+    PoolRow buf[DEPTH][8];                       // [0..3] K rows of keys 4 kqk + j, [4..7] V rows of 4 kqv + j
     // the 4 keys of a job: one block lookup and one base address when they lie in one block (block_size % 4 == 0:
     // rows then differ by a constant stride), one per key otherwise
     const bool rows4 = a.bs % 4 == 0;
     const long long rstride = (long long)a.Hkv * D;
-    auto issue = [&](int t_rel, PoolRow<TP> (&slot)[8]) {
+    auto issue = [&](int t_rel, PoolRow (&slot)[8]) {
         const int tile = t_first + t_rel;
         // pos = b * bs + r with b = mulhi(pos, ceil(2^32 / bs)): exact because pos * bs < 2^32 (checked on the host)
         auto row_of = [&](int pos) {
@@ -258,7 +237,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
             return (long long)blk * a.bs + (pos - b * a.bs);
         };
-        auto group = [&](int kq, int dc, const void* base, PoolRow<TP>* rows) {
+        auto group = [&](int kq, int dc, const void* base, PoolRow* rows) {
             const int p4 = tile * kBKP + 4 * kq;
             if (rows4) {
                 // tiles past the end re-read the last key (never used); a clamped group of 4 stays in its block;
@@ -281,7 +260,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         group(kqk, dck, a.kp, slot);
         group(kqv, dcv, a.vp, slot + 4);
     };
-    auto stash = [&](const PoolRow<TP> (&slot)[8], int stage) {
+    auto stash = [&](const PoolRow (&slot)[8], int stage) {
         uint16_t* ks = kst + stage * KBUF;
         uint16_t* vt = vst + stage * VBUF;
         u32x4 v[4];
@@ -443,25 +422,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return;
     }
     {
-        // one branch on the dtype around all the loads, so they are all in flight together
-        const long long base = ((long long)(row0 + (col < nq ? col : nq - 1)) * a.Hq + head) * D + 8 * kg;
-        if (a.q_dtype == RK_BF16) {
-            const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q) + base;
+        // q is bf16 here (the host's rule for this kernel): its rows are the operands as they are
+        const uint16_t* qb = reinterpret_cast<const uint16_t*>(a.q) +
+                             ((long long)(row0 + (col < nq ? col : nq - 1)) * a.Hq + head) * D + 8 * kg;
 #pragma unroll
-            for (int t = 0; t < NKS; ++t) qop[t] = *reinterpret_cast<const u32x4*>(qb + 16 * t);
-        } else {
-            const float* qf = reinterpret_cast<const float*>(a.q) + base;
-            float4 x[NKS][2];
-#pragma unroll
-            for (int t = 0; t < NKS; ++t) {
-                x[t][0] = *reinterpret_cast<const float4*>(qf + 16 * t);
-                x[t][1] = *reinterpret_cast<const float4*>(qf + 16 * t + 4);
-            }
-#pragma unroll
-            for (int t = 0; t < NKS; ++t)
-                qop[t] = u32x4{pack_bf16x2_rne(x[t][0].x, x[t][0].y), pack_bf16x2_rne(x[t][0].z, x[t][0].w),
-                               pack_bf16x2_rne(x[t][1].x, x[t][1].y), pack_bf16x2_rne(x[t][1].z, x[t][1].w)};
-        }
+        for (int t = 0; t < NKS; ++t) qop[t] = *reinterpret_cast<const u32x4*>(qb + 16 * t);
 #pragma unroll
         for (int t = 0; t < NDT; ++t) o[t] = f32x16{};
     }
@@ -590,8 +555,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-// ---- 3. attention with fp32 operands: the same work list, masks, splits and gate as prefill_attention, for every
-// input the bf16 kernel does not take (fp32 q or pool, group sizes other than 4, D = 64). The reference computes
+// ---- 3. attention with fp32 operands: the same work list, masks, splits and gate as prefill_attention, for an
+// fp32 q or pool and for exact requests (any group size, D = 64 / 128 / 256). The reference computes
 // attention in fp32 on widened inputs (src/ops.py:84-87, 91-103), so the products here are fp32 products:
 // v_mfma_f32_16x16x4_f32, bf16 pool rows widened exactly when staged, the probabilities kept in fp32.
 // blockDim = 512: wave w takes query head (blockIdx.z * 4 + w % 4) of the group (none past the group's end: that
@@ -1343,8 +1308,8 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     if (wide_q) {
         const size_t lds = (tab_lds ? kTabCache * 4 : 0) +
                            (size_t)kStages * (kBKP * (D + kKPad) + D * (kBKP + kVPad)) * sizeof(uint16_t);
-        if (D == 256) fn = tab_lds ? prefill_attention<256, uint16_t, true> : prefill_attention<256, uint16_t, false>;
-        else fn = tab_lds ? prefill_attention<128, uint16_t, true> : prefill_attention<128, uint16_t, false>;
+        if (D == 256) fn = tab_lds ? prefill_attention<256, true> : prefill_attention<256, false>;
+        else fn = tab_lds ? prefill_attention<128, true> : prefill_attention<128, false>;
         if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
         hipLaunchKernelGGL(fn, dim3(n_work, Hkv), dim3(2 * 64 * a.G), lds, s, a);
         return check_launch("prefill_attention");
