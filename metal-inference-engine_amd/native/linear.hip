@@ -69,17 +69,24 @@ __device__ __forceinline__ u32x4 int8_bf16(uint32_t lo, uint32_t hi) {
     return o;
 }
 
-// 8 INT4 codes (4 bytes; byte j holds elements 2j in the low nibble, 2j+1 in the high one) as bf16 bits
+// 8 INT4 codes (4 bytes; byte j holds elements 2j in the low nibble, 2j+1 in the high one) as bf16 bits, in the
+// element order 0 2 4 6 1 3 5 7 (kInt4Order; the activations are staged in the same order, so the MFMA's k-sum
+// is unchanged). A code q alone in a byte, read as an fp8 e4m3 pattern 0000qqqq, is exactly q * 2^-9 (codes 0-7
+// are subnormals m * 2^-9, 8-15 the first normal binade (8 + m) * 2^-9), so v_cvt_scalef32_pk_bf16_fp8 with the
+// scale 2^9 turns two such bytes into two exact bf16 integers: 7 instructions for 8 codes.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 int4_bf16(uint32_t v) {
+    const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;   // codes 0 2 4 6 | 1 3 5 7, one per byte
     u32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float f0 = (float)__builtin_amdgcn_ubfe(v, 8 * j, 4);
-        const float f1 = (float)__builtin_amdgcn_ubfe(v, 8 * j + 4, 4);
-        o[j] = pack_hi2(__float_as_uint(f0), __float_as_uint(f1));
-    }
+    o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, false));
+    o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, true));
+    o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, false));
+    o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, true));
     return o;
 }
+// element pairs of the four bf16-pair registers of an INT4 operand (int4_bf16), and of the activation pieces staged
+// against it
+constexpr int kInt4Order[4][2] = {{0, 2}, {4, 6}, {1, 3}, {5, 7}};
 
 // 4 x 4 transpose over the wave's four 16-lane groups: afterwards register d of lane group g holds what register g
 // of lane group d held. v_permlane32_swap exchanges the upper 32 lanes of its first operand with the lower 32 of its
@@ -251,7 +258,8 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
         u32x4 pc[3];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const Split3 s0 = split3(v[2 * q]), s1 = split3(v[2 * q + 1]);
+            const int e0 = WT == RK_W_INT4 ? kInt4Order[q][0] : 2 * q, e1 = WT == RK_W_INT4 ? kInt4Order[q][1] : 2 * q + 1;
+            const Split3 s0 = split3(v[e0]), s1 = split3(v[e1]);
             pc[0][q] = pack_hi2(s0.hi, s1.hi);
             pc[1][q] = pack_hi2(s0.mid, s1.mid);
             pc[2][q] = pack_hi2(s0.lo, s1.lo);
