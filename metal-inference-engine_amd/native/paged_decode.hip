@@ -431,11 +431,14 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     typename LD::Vec kv[KB], vv[VB];
     TileRows<NVI, TPI, LPT, ALIGNED> cur;
     // issue order K then V, here and in the loop, so that waiting for a tile's keys never waits for its values
-    // (the scheduling barriers keep the compiler from reordering the two groups of loads)
-    auto issue_first = [&]() {
+    // (the scheduling barriers keep the compiler from reordering the two groups of loads); `mid` issues loads
+    // between the two (the first sequence's queries: staging them then waits for the keys, not the values)
+    auto issue_first = [&](auto mid) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int it = 0; it < KB; ++it) kv[it] = LD::load(a.kp, cur.krow + 32 * it + 8 * grp);
+        __builtin_amdgcn_sched_barrier(0);
+        mid();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int vi = 0; vi < VB; ++vi) vv[vi] = LD::load(a.vp, cur.vrow(vi));
@@ -451,6 +454,23 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
                                                   __builtin_amdgcn_readlane(s0_l, jj),
                                                   __builtin_amdgcn_readlane(L_l, jj),
                                                   __builtin_amdgcn_readlane(tpos_l, jj), blk, kvh, D, lane);
+    };
+    // Query operands. Row m = s * GP + h of the A tiles holds split s of head h, scaled by log2(e)/sqrt(D); element
+    // (it, grp, e) of a row is dim 32 it + 8 grp + e. The queries of the next sequence this wave has tiles in are
+    // fetched into registers (coalesced: 4 consecutive dims per lane and step) a whole segment ahead, so a sequence
+    // switch waits on no load (the first sequence's before the first tile's K / V, so that staging them waits for
+    // no K / V load); there the pieces are split and scattered into the operand layout.
+    float4 qn[QV];
+    // (branch-free: every lane loads, from a clamped index, and stage_q skips the pieces past the group's heads; a
+    // conditional load would put branches between the loads and make the compiler's load counts inexact)
+    auto fetch_q = [&](int b) {
+        const float* qb = a.q + ((long long)b * a.Hq + (long long)kvh * a.G) * D;
+        const int n4 = a.G * (D / 4);
+#pragma unroll
+        for (int k = 0; k < QV; ++k) {
+            const int e4 = lane + 64 * k;
+            qn[k] = *reinterpret_cast<const float4*>(qb + 4 * (e4 < n4 ? e4 : n4 - 1));
+        }
     };
     bool planned = false;
     int lo, hi, bA, bZ;
@@ -481,7 +501,8 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         tpos_l = has ? (ev.y < 0 ? 0 : (ev.y >= cap ? (cap - 1) / kTile * kTile : ev.y)) : 0;
         blk_l = has ? (ev.w < 0 ? 0 : (ev.w >= a.num_blocks ? a.num_blocks - 1 : ev.w)) : 0;
         cur = rows_of(0);
-        issue_first();
+        // the group's first tile's sequence's queries (unused without tiles), between its keys and values
+        issue_first([&]() { fetch_q(__builtin_amdgcn_readlane(b_l, 0)); });
         planned = has;
 #pragma unroll
         for (int k = 0; k < kSeqPer; ++k) {
@@ -535,19 +556,6 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
             for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
     };
 
-    // Query operands. Row m = s * GP + h of the A tiles holds split s of head h, scaled by log2(e)/sqrt(D); element
-    // (it, grp, e) of a row is dim 32 it + 8 grp + e. The queries of the next sequence this wave has tiles in are
-    // fetched into registers (coalesced: 4 consecutive dims per lane and step) a whole segment ahead, so a sequence
-    // switch waits on no load; there the pieces are split and scattered into the operand layout.
-    float4 qn[QV];
-    auto fetch_q = [&](int b) {
-        const float* qb = a.q + ((long long)b * a.Hq + (long long)kvh * a.G) * D;
-#pragma unroll
-        for (int k = 0; k < QV; ++k) {
-            const int e4 = lane + 64 * k;
-            qn[k] = e4 < a.G * (D / 4) ? *reinterpret_cast<const float4*>(qb + 4 * e4) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
     auto stage_q = [&]() {
 #pragma unroll
         for (int k = 0; k < QV; ++k) {
@@ -655,13 +663,11 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
 
     reset();
     int j0 = 0;                                      // first entry held by the lane arrays
-    if (my_total > 0) {
-        if (!planned) {                              // with a plan, entries 0 .. 63 and the first loads are in place
-            refill(0);
-            cur = rows_of(0);
-            issue_first();
-        }
+    if (my_total > 0 && !planned) {                  // with a plan, entries 0 .. 63 and the first loads are in place
         fetch_q(next_mine(bA - 1));
+        refill(0);
+        cur = rows_of(0);
+        issue_first([]() {});
     }
     int j = 0;                                       // this group's next tile list entry
     for (int b = bA; b <= bZ; ++b) {
