@@ -705,6 +705,7 @@ def attn_prep(y, q_w, k_w, eps: float, positions, theta: float, rot: int, dims, 
 W_TYPES = {"int8": RK_W_INT8, "int4": RK_W_INT4}
 LINEAR_ROWS = 16            # activation rows per rk_linear_rows launch (the MFMA's 16 columns)
 KERNEL_ROWS = 32            # up to here: the matvec kernel in groups of 16; beyond: dequantize + GEMM
+LINEAR_LONG_ROWS = 65536    # rk_linear_rows' persistent kernel for INT8 weights from this many rows (M <= 8)
 
 
 def _weight_args(w):
@@ -832,11 +833,13 @@ def rms_norm_linear(x, ss, norm_w, eps: float, w, bias=None, residual=None) -> t
     """linear(rms_norm(x, norm_w, eps), w, bias, residual) with the norm applied while rk_linear_rows_ex2 stages x
     (one launch), from ss = the sums of squares of x's 16-column tiles that the linear producing x wrote
     (linear_ss / silu_mul_linear_ss). Without ss, beyond 8 rows, K % 256 != 0 or K > 2048, and for long matrices
-    (N > 16384: every workgroup recomputes the rows' rms, which costs more than the separate launch there):
+    (N > 16384 outside the persistent INT8 kernel's shapes: every workgroup recomputes the rows' rms, which costs
+    more than the separate launch there):
     rms_norm, then linear (the same results within 1e-5)."""
     wt, data, scales, mins, N, K = _weight_args(w)
     M = x.shape[0]
-    if (ss is None or x.dim() != 2 or x.shape[1] != K or M > 8 or K % 256 or K > 2048 or N > 16384
+    long_int8 = wt == RK_W_INT8 and N >= LINEAR_LONG_ROWS and K % 1024 == 0      # the persistent kernel's shapes
+    if (ss is None or x.dim() != 2 or x.shape[1] != K or M > 8 or K % 256 or K > 2048 or (N > 16384 and not long_int8)
             or ss.shape != (M, K // 16) or norm_w.numel() != K):
         return linear(rms_norm(x, norm_w, eps), w, bias, residual)
     _need_cuda("linear", x, ss, norm_w, data)

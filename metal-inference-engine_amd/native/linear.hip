@@ -74,7 +74,6 @@ __device__ __forceinline__ u32x4 int8_bf16(uint32_t lo, uint32_t hi) {
 // is unchanged). A code q alone in a byte, read as an fp8 e4m3 pattern 0000qqqq, is exactly q * 2^-9 (codes 0-7
 // are subnormals m * 2^-9, 8-15 the first normal binade (8 + m) * 2^-9), so v_cvt_scalef32_pk_bf16_fp8 with the
 // scale 2^9 turns two such bytes into two exact bf16 integers: 7 instructions for 8 codes.
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 int4_bf16(uint32_t v) {
     const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;   // codes 0 2 4 6 | 1 3 5 7, one per byte
     u32x4 o;
@@ -281,16 +280,16 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     f32x4 acc[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const u32x4 zero4 = {0u, 0u, 0u, 0u};
-    const bool col_ok = COLS == 16 || r < COLS;
+    // with 8 staged rows, lanes r >= 8 supply A rows 8 .. 15 as copies of rows 0 .. 7: row m of D depends on A's row
+    // m alone, and D's rows 8 .. 15 are never stored (M <= 8), so they need no zeroing
     const int cr = COLS == 16 ? r : (r & (COLS - 1));
 #pragma unroll
     for (int j = 0; j < kWaveBlocks; ++j) {
         if (j < nbw) {                              // uniform per wave: the last split may hold fewer blocks
             const int kg = 4 * (wave * kWaveBlocks + j) + grp;
-            const u32x4 p0 = col_ok ? xs[(0 * KG + kg) * COLS + cr] : zero4;
-            const u32x4 p1 = col_ok ? xs[(1 * KG + kg) * COLS + cr] : zero4;
-            const u32x4 p2 = col_ok ? xs[(2 * KG + kg) * COLS + cr] : zero4;
+            const u32x4 p0 = xs[(0 * KG + kg) * COLS + cr];
+            const u32x4 p1 = xs[(1 * KG + kg) * COLS + cr];
+            const u32x4 p2 = xs[(2 * KG + kg) * COLS + cr];
             f32x4 bs = {0.f, 0.f, 0.f, 0.f};
             if constexpr (WT == RK_W_INT4) {
                 if (4 * grp < COLS) bs = *reinterpret_cast<const f32x4*>(&bsum_s[(wave * kWaveBlocks + j) * COLS + 4 * grp]);
@@ -421,6 +420,189 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     if (tid == 0) __hip_atomic_store(&a.cnt[rg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Long INT8 matrices (the tied LM head: N ~ 2.5e5 rows, half a GB): a persistent grid of one 8-wave workgroup per
+// CU. linear_rows_kernel gives such a matrix thousands of short workgroups, each staging the activations again and
+// adding its K-split through memory, with no weight loads in flight between one workgroup's requests and the next's.
+// Here each workgroup stages the (up to 8) activation rows once for the whole K (three bf16 pieces, 48 K bytes of
+// LDS; the RMSNorm of XF 2 applied as in linear_rows_kernel), then every wave streams whole 16-row tiles of its
+// share of the rows over the full K, in chunks of 512 weights per row, one chunk ahead in a two-slot register ring:
+// no cross-wave or cross-workgroup reduction, and every output's blocks are added in order (a different order from
+// linear_rows_kernel's, within 1e-6 of it). The grid's waves take the tiles in turn (wave g of W: tiles g, g + W,
+// ...), so that at any time all of them read one contiguous stretch of the matrix (4 % faster than contiguous
+// shares per workgroup), in rounds of up to kLongRound tiles. Inside a round the stream holds loads only: the loads
+// of chunk s + 1 are issued (from a clamped index, so unconditionally) before chunk s is used, and a finished tile's outputs
+// go to the wave's LDS area, so that the compiler's count of loads in flight stays exact (a store or a conditional
+// load in the stream makes it wait for every load); the round's outputs are written (with bias, residual and sums
+// of squares) after its stream.
+constexpr int kLongWaves = 8;                      // waves per workgroup (two per SIMD)
+constexpr int kLongChunk = 512;                    // weights per row and chunk: 16 blocks
+constexpr int kLongRound = 12;                     // tiles per wave and round (their outputs wait in LDS); even
+constexpr int kLongSlots = 2;                      // chunks held per wave: one in flight while one is used
+constexpr int kLongMinRows = 65536;                // the long path from this many output rows
+
+template <int XF>
+__global__ __launch_bounds__(64 * kLongWaves) void linear_long_int8_kernel(LinArgs a) {
+    constexpr int COLS = 8;
+    constexpr int CB = kLongChunk / kQB;           // blocks per chunk (16)
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);    // [piece][k-group][activation row]
+    __shared__ float rms_s[COLS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: the tile arithmetic stays scalar
+    const int r = lane & 15, grp = lane >> 4;
+    const int K = a.K, KG = K / 8, nblk = K / kQB, nch = K / kLongChunk;   // nch even (K % 1024 == 0)
+    float* outs = reinterpret_cast<float*>(smem + (size_t)3 * KG * COLS * sizeof(u32x4)) + wave * kLongRound * COLS * 16;
+
+    // ---- staging, once: XF 2 first needs each row's 1 / rms (wave v < 8: row v, from its K / 16 tile sums)
+    if constexpr (XF == 2) {
+        if (wave < COLS) {                         // uniform per wave
+            const int n_ss = K / 16;
+            const size_t row = (size_t)min(wave, a.M - 1);
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kMaxSsTiles / 64; ++q) {
+                const int i = lane + 64 * q;
+                const float v = a.aux[row * a.aux_ld + min(i, n_ss - 1)];
+                t += i < n_ss ? v : 0.0f;
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+            if (lane == 0) rms_s[wave] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(t, (float)K), a.eps)));
+        }
+        __syncthreads();
+    }
+    for (int id = tid; id < KG * COLS; id += 64 * kLongWaves) {
+        const int col = id % COLS, kg = id / COLS;
+        const bool ok = col < a.M;
+        const f32x4* p = reinterpret_cast<const f32x4*>(a.x + (size_t)min(col, a.M - 1) * a.x_ld + 8 * kg);
+        const f32x4 x0 = p[0], x1 = p[1];
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = ok ? x0[e] : 0.0f;
+            v[4 + e] = ok ? x1[e] : 0.0f;
+        }
+        if constexpr (XF == 2) {
+            const f32x4* pw = reinterpret_cast<const f32x4*>(a.nw + 8 * kg);
+            const f32x4 w0 = pw[0], w1 = pw[1];
+            const float ir = rms_s[col];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = __fmul_rn(__fmul_rn(v[e], ir), w0[e]);
+                v[4 + e] = __fmul_rn(__fmul_rn(v[4 + e], ir), w1[e]);
+            }
+        }
+        u32x4 pc[3];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const Split3 s0 = split3(v[2 * q]), s1 = split3(v[2 * q + 1]);
+            pc[0][q] = pack_hi2(s0.hi, s1.hi);
+            pc[1][q] = pack_hi2(s0.mid, s1.mid);
+            pc[2][q] = pack_hi2(s0.lo, s1.lo);
+        }
+#pragma unroll
+        for (int pp = 0; pp < 3; ++pp) xs[(pp * KG + kg) * COLS + col] = pc[pp];
+    }
+    __syncthreads();
+
+    // ---- the wave's tiles
+    const int T = (a.N + 15) / 16;
+    const int NWV = gridDim.x * kLongWaves, gv = blockIdx.x * kLongWaves + wave;   // the grid's waves; this one
+    const int my_tiles = T > gv ? (T - gv + NWV - 1) / NWV : 0;
+    const int cr = r & (COLS - 1);                 // lanes r >= 8: copies of rows 0 .. 7 (D's rows 8 .. 15 unused)
+    auto tile_of = [&](int i) { return gv + NWV * i; };   // the wave's i-th tile
+
+    u32x4 raw[kLongSlots][8], sc[kLongSlots][2];
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int t0 = 0; t0 < my_tiles; t0 += kLongRound) {
+        // S_real chunks; the stream runs S, a multiple of the ring's 4 slots: with 2 chunks per tile an odd tile
+        // count gets one more tile, computed from the round's last chunk again and never written out (its LDS
+        // outputs lie past the round's tiles, within the area: kLongRound is even)
+        const int nt = min(kLongRound, my_tiles - t0), S_real = nt * nch;
+        const int S = (kLongSlots > 2 && nch == 2 ? (nt + 1) & ~1 : nt) * nch;
+        // chunk s of the round: the wave's tile t0 + s / nch, blocks 16 (s % nch) .. +15; lane group g loads blocks
+        // 4q + g (32 bytes: two 16-byte loads) of row 16 tile + r, and every lane its row's 16 scales of the chunk
+        auto load = [&](int s, int slot) {
+            s = min(s, S_real - 1);
+            const int b0 = CB * (s % nch);
+            const size_t n = (size_t)min(16 * tile_of(t0 + s / nch) + r, a.N - 1);
+            const uint8_t* wrow = static_cast<const uint8_t*>(a.w) + n * (size_t)K;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32x4* p = reinterpret_cast<const u32x4*>(wrow + (size_t)kQB * (b0 + 4 * q + grp));
+                raw[slot][2 * q] = p[0];
+                raw[slot][2 * q + 1] = p[1];
+            }
+            const u32x4* ps = reinterpret_cast<const u32x4*>(a.scales + n * nblk + b0);
+            sc[slot][0] = ps[0];
+            sc[slot][1] = ps[1];
+        };
+        auto compute = [&](int s, int slot) {
+            const int c = s % nch, b0 = CB * c;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // qword k (k-group k of the lane group's block) = dwords (2k, 2k+1) of the block's two 16-byte pieces
+                const u32x4 c0 = raw[slot][2 * q], c1 = raw[slot][2 * q + 1];
+                const u32x4 xl = xpose4(c0[0], c0[2], c1[0], c1[2]);
+                const u32x4 xh = xpose4(c0[1], c0[3], c1[1], c1[3]);
+                const u32x4 w2[2] = {{xl[0], xh[0], xl[1], xh[1]}, {xl[2], xh[2], xl[3], xh[3]}};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int blk = 4 * q + d;     // block of the chunk
+                    const int kg = 4 * (b0 + blk) + grp;
+                    const u32x4 p0 = xs[(0 * KG + kg) * COLS + cr];
+                    const u32x4 p1 = xs[(1 * KG + kg) * COLS + cr];
+                    const u32x4 p2 = xs[(2 * KG + kg) * COLS + cr];
+                    const u32x4 bw = int8_bf16(w2[d >> 1][2 * (d & 1)], w2[d >> 1][2 * (d & 1) + 1]);
+                    f32x4 dd = mfma16x16x32(p0, bw, (f32x4){0.f, 0.f, 0.f, 0.f});
+                    dd = mfma16x16x32(p1, bw, dd);
+                    dd = mfma16x16x32(p2, bw, dd);
+                    const float sv = half_to_f32((uint16_t)(sc[slot][blk >> 3][(blk & 7) >> 1] >> (16 * (blk & 1))));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i] = fmaf(sv, dd[i], acc[i]);
+                }
+            }
+            if (c == nch - 1) {                    // tile done: lane (r, g < 2) holds rows 4g + i, column r
+                if (grp < 2)
+                    *reinterpret_cast<f32x4*>(&outs[((s / nch) * COLS + 4 * grp) * 16 + 4 * r]) = acc;
+                acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+            }
+        };
+        // (the scheduling barriers keep each chunk's loads ahead of the previous chunk's arithmetic)
+#pragma unroll
+        for (int u = 0; u < kLongSlots - 1; ++u) load(u, u);
+        for (int s = 0; s < S; s += kLongSlots) {  // S is a multiple of the slot count
+#pragma unroll
+            for (int u = 0; u < kLongSlots; ++u) {
+                load(s + u + kLongSlots - 1, (u + kLongSlots - 1) % kLongSlots);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(s + u, u);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        wave_lds_sync();
+        // the round's outputs: element e = (tile i, row m, column j) of the wave's area, 16 columns per 16 lanes
+        for (int e = lane; e < nt * COLS * 16; e += 64) {
+            const int i = e / (COLS * 16), m = (e / 16) % COLS, j = e % 16;
+            const int tile = tile_of(t0 + i), n = 16 * tile + j;
+            const f32x4 q4 = *reinterpret_cast<const f32x4*>(&outs[(i * COLS + (m & ~3)) * 16 + 4 * j]);
+            float v = q4[m & 3];
+            const bool ok = m < a.M && n < a.N;
+            if (ok && a.bias) v = __fadd_rn(v, a.bias[n]);
+            if (ok && a.res) v = __fadd_rn(v, a.res[(size_t)m * a.N + n]);
+            if (ok) a.y[(size_t)m * a.N + n] = v;
+            if (a.ss) {                            // uniform
+                float q2 = ok ? v * v : 0.0f;
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) q2 += __shfl_xor(q2, o);
+                if (j == 0 && m < a.M) a.ss[(size_t)m * T + tile] = q2;
+            }
+        }
+        wave_lds_sync();                           // the area is rewritten by the next round
+    }
+}
+
 // Row tiles per workgroup: the most (4; 2 for bf16, whose weight slots are 4x wider than INT4's) that still leave
 // min_groups workgroups, down to 1: 512, and 256 for the fused silu * up input, whose workgroups stage twice the
 // activation bytes (gate and up rows), so more weight rows per workgroup pay for them. Staged activation rows: 8 for M <= 8, else 16. Neither changes any output's summation
@@ -522,6 +704,23 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
                 return fail(RK_ERR_ARG, "rk_linear_rows: %d sums of squares per row (at most %d) at a stride of %lld",
                             K / 16, kMaxSsTiles, aux_ld);
         }
+    }
+    // long INT8 matrices: the persistent kernel (no partials or counters used)
+    if (w_type == RK_W_INT8 && M <= 8 && N >= kLongMinRows && K % (2 * kLongChunk) == 0 && K / 16 <= kMaxSsTiles && pv &&
+        (x_op == RK_X_PLAIN || x_op == RK_X_RMS_NORM)) {
+        LinArgs a{};
+        a.y = y; a.x = x; a.w = w; a.scales = static_cast<const uint16_t*>(scales);
+        a.bias = bias; a.res = residual; a.aux = aux; a.x_ld = x_ld; a.aux_ld = aux_ld;
+        a.nw = norm_w; a.ss = ss_out; a.eps = eps; a.M = M; a.N = N; a.K = K; a.S = 1;
+        int cus = device_cus();
+        if (cus <= 0) cus = 256;
+        const int T = (N + 15) / 16;
+        const size_t lds = (size_t)3 * (K / 8) * 8 * sizeof(u32x4) + (size_t)kLongWaves * kLongRound * 8 * 16 * 4;
+        const auto fn = x_op == RK_X_RMS_NORM ? linear_long_int8_kernel<2> : linear_long_int8_kernel<0>;
+        if (int rc = allow_dynamic_lds((const void*)fn, lds)) return rc;
+        hipLaunchKernelGGL(fn, dim3((unsigned)(cus < T ? cus : T)), dim3(64 * kLongWaves), lds,
+                           static_cast<hipStream_t>(stream), a);
+        return check_launch("linear_long_int8");
     }
     const LinPlan p = lin_plan(M, N, K, w_type, x_op == RK_X_SILU_MUL ? 256 : 512);
     const size_t need = rk_linear_workspace_bytes(M, N, K, w_type);

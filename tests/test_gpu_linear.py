@@ -43,8 +43,10 @@ def test_dequant_rows_bit_exact(backend, kind):
 
 
 # 33000 x 1024 takes four 16-row tiles per workgroup (ragged last group), (100, 96) and (65, 2080) the unaligned
-# parameter loads and a last K-split of one block
-SHAPES = [(5120, 1024), (1024, 3584), (7168, 1024), (8224, 2048), (2048, 6144), (33000, 1024), (100, 96), (65, 2080)]
+# parameter loads and a last K-split of one block; (70001, 2048) is a long matrix (INT8 at up to 8 rows: the
+# persistent kernel, a ragged last tile)
+SHAPES = [(5120, 1024), (1024, 3584), (7168, 1024), (8224, 2048), (2048, 6144), (33000, 1024), (100, 96), (65, 2080),
+          (70001, 2048)]
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
@@ -117,7 +119,7 @@ def tile_sums(y):
     return (pad * pad).view(M, -1, 16).sum(-1)
 
 
-@pytest.mark.parametrize("N,K", [(2048, 2048), (2048, 6144), (2064, 1024), (100, 96), (8224, 2048)])
+@pytest.mark.parametrize("N,K", [(2048, 2048), (2048, 6144), (2064, 1024), (100, 96), (8224, 2048), (65552, 1024)])
 @pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
 def test_linear_with_tile_sums_of_squares(backend, kind, N, K):
     """rk_linear_rows_ex2 with ss_out: y bit-identical to the plain launch, and the tile sums of squares within 1e-6
@@ -158,3 +160,29 @@ def test_rms_norm_fused_into_the_linear(backend, kind, N, K):
         assert rel_err(got, want) < TOL
         got_by_m[M] = got.cpu()
     assert torch.equal(got_by_m[1][0], got_by_m[8][0])
+
+
+@pytest.mark.parametrize("N,K", [(248320, 2048), (65541, 1024), (131072, 2048)])
+def test_long_int8_matrix_on_the_persistent_grid(backend, N, K):
+    """INT8 matrices of 65536+ rows at up to 8 activation rows (the tied LM head, N = 248320) run on one persistent
+    workgroup per CU streaming whole 16-row tiles: against the dequantized reference within 1e-5 with bias and
+    residual, the tile sums of squares within 1e-6 of the fp64 sums of y, a row's result independent of the batch
+    (M = 1 and M = 8 bit-identical), and a ragged last tile."""
+    from native import kernels
+    w, deq = weight("int8", N, K, N + 3 * K)
+    wd = to_dev(w)
+    g = torch.Generator().manual_seed(N % 1000)
+    x8 = torch.randn(8, K, generator=g)
+    b, r8 = torch.randn(N, generator=g), torch.randn(8, N, generator=g)
+    rows = {}
+    for M in (8, 3, 1):
+        x, r = x8[:M], r8[:M]
+        want = quant_ref.linear(x, deq, b, r)
+        got = backend.linear(x.to(DEV), wd, b.to(DEV), r.to(DEV))
+        e = rel_err(got, want)
+        print(f"long int8 {N}x{K}, M {M}: rel {e:.2e}")
+        assert e < TOL
+        y, ss = kernels.linear_ss(x.to(DEV), wd, residual=r.to(DEV))
+        assert rel_err(ss, tile_sums(y.cpu().double()).float()) < 1e-6
+        rows[M] = got.cpu()
+    assert torch.equal(rows[1][0], rows[8][0]) and torch.equal(rows[3], rows[8][:3])
