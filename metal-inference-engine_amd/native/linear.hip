@@ -112,35 +112,38 @@ constexpr int kSplitBlocks = 4 * kWaveBlocks;      // blocks per workgroup (its 
 // wave order). With S > 1 splits the workgroup stores its partial sums (device-coherent stores), counts itself in
 // for its row group, and the last to arrive adds the S partials in split order (deterministic, whatever the arrival
 // order), the bias and the residual, and writes y. Every output's summation order depends on K alone.
-template <int WT, int COLS, int RT, bool PV, int XF>
-__global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
+template <int WT, int COLS, int RT, bool PV, int XF, int NW>
+__global__ __launch_bounds__(64 * NW) void linear_rows_kernel(LinArgs a) {
     using TR = WTraits<WT>;
     constexpr bool QUANT = WT != RK_W_BF16;
-    constexpr int KG = 4 * kSplitBlocks;           // 8-element k-groups of the split
-    constexpr int XI = COLS * KG / 256;            // staged k-groups (8 activations of one row) per thread
-    __shared__ __align__(16) u32x4 xs[3 * KG * COLS];          // [piece][k-group][activation row]
-    __shared__ __align__(16) float bsum_s[WT == RK_W_INT4 ? kSplitBlocks * COLS : 4];   // [block][activation row]
+    constexpr int SB = NW * kWaveBlocks;           // blocks of the workgroup's K-split (1024 or 2048 weights)
+    constexpr int KG = 4 * SB;                     // 8-element k-groups of the split
+    constexpr int NT = 64 * NW;                    // threads
+    constexpr int XI = COLS * KG / NT;             // staged k-groups (8 activations of one row) per thread
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);    // [piece][k-group][activation row]: 3 KG COLS (linear_xs_bytes)
+    __shared__ __align__(16) float bsum_s[WT == RK_W_INT4 ? SB * COLS : 4];   // [block][activation row]
     __shared__ int is_last;
-    static_assert(4 * RT * 64 * sizeof(f32x4) <= sizeof(xs), "wave sums reuse the staging buffer");
+    static_assert(NW * RT * 64 * sizeof(f32x4) <= 3 * KG * COLS * sizeof(u32x4), "wave sums reuse the staging buffer");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, grp = lane >> 4;
     const int rg = blockIdx.x / a.S, sp = blockIdx.x % a.S;
     const int row0 = rg * 16 * RT;
     const int nblk = a.K / kQB;
-    const int b0 = sp * kSplitBlocks;
-    const int nb = min(kSplitBlocks, nblk - b0);   // blocks of this split (>= 1)
+    const int b0 = sp * SB;
+    const int nb = min(SB, nblk - b0);             // blocks of this split (>= 1)
     const int wb0 = b0 + wave * kWaveBlocks;       // this wave's first block
     const int nbw = max(0, min(kWaveBlocks, nblk - wb0));
 
     // ---- requests: activations, parameters, weights (in this order, all before any use)
-    // activations: thread k-groups id = tid + 256u, activation row id % COLS, k-group id / COLS (the row varies
+    // activations: thread k-groups id = tid + NT u, activation row id % COLS, k-group id / COLS (the row varies
     // fastest, so consecutive lanes write consecutive 16 bytes of the staging buffer: no LDS bank conflicts)
     // XF 1: also the up rows
     f32x4 xv[XI][2], xa[XF != 0 ? XI : 1][2];
 #pragma unroll
     for (int u = 0; u < XI; ++u) {
-        const int id = tid + 256 * u;
+        const int id = tid + NT * u;
         const int col = id % COLS, kg = id / COLS;
         const size_t row = (size_t)min(col, a.M - 1);
         const int kk = 8 * min(kg, 4 * nb - 1);
@@ -157,14 +160,14 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
             xa[u][1] = pw[1];
         }
     }
-    // XF 2: the sums of squares of the rows this wave normalises (rows wave + 4j), up to 8 per lane, branch-free
-    constexpr int SSR = XF == 2 ? COLS / 4 : 1;
+    // XF 2: the sums of squares of the rows this wave normalises (rows wave + NW j), up to 8 per lane, branch-free
+    constexpr int SSR = XF == 2 ? (COLS / NW > 0 ? COLS / NW : 1) : 1;
     float ssv[SSR][kMaxSsTiles / 64];
     const int n_ss = a.K / 16;
     if constexpr (XF == 2) {
 #pragma unroll
         for (int j = 0; j < SSR; ++j) {
-            const size_t row = (size_t)min(wave + 4 * j, a.M - 1);
+            const size_t row = (size_t)min(wave + NW * j, a.M - 1);
 #pragma unroll
             for (int q = 0; q < kMaxSsTiles / 64; ++q)
                 ssv[j][q] = a.aux[row * a.aux_ld + min(lane + 64 * q, n_ss - 1)];
@@ -225,7 +228,8 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
             for (int q = 0; q < kMaxSsTiles / 64; ++q) t += lane + 64 * q < n_ss ? ssv[j][q] : 0.0f;
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
-            if (lane == 0) rms_s[wave + 4 * j] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(t, (float)a.K), a.eps)));
+            if (lane == 0 && wave + NW * j < COLS)
+                rms_s[wave + NW * j] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(t, (float)a.K), a.eps)));
         }
         __syncthreads();
     }
@@ -234,7 +238,7 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     // lanes i, i + COLS, i + 2 COLS, i + 3 COLS and are added pairwise, (s0 + s1) + (s2 + s3), identically in all four)
 #pragma unroll
     for (int u = 0; u < XI; ++u) {
-        const int id = tid + 256 * u;
+        const int id = tid + NT * u;
         const int col = id % COLS, kg = id / COLS;
         const bool ok = col < a.M && kg < 4 * nb;
         float v[8];
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
         }
     }
 
-    // ---- the four waves' sums, in wave order; thread (t, l) then owns outputs m = 4(l/16) + i, n = row0 + 16t + l%16
+    // ---- the NW waves' sums, in wave order; thread (t, l) then owns outputs m = 4(l/16) + i, n = row0 + 16t + l%16
     __syncthreads();                                // every wave has finished reading the staging buffer
     f32x4* red = reinterpret_cast<f32x4*>(xs);
 #pragma unroll
@@ -350,12 +354,23 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     __syncthreads();
     if (tid < RT * 64) {
         const int t = tid >> 6, l = tid & 63;
-        f32x4 s = red[t * 64 + l];
+        // waves in order within groups of 4, the groups in order: with 8 waves over the whole K, the association of
+        // two 4-wave K-splits added by the last arriver, so a row's result does not depend on which form ran
+        f32x4 s;
 #pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            const f32x4 o = red[(w * RT + t) * 64 + l];
+        for (int g4 = 0; g4 < NW / 4; ++g4) {
+            f32x4 sg = red[(4 * g4 * RT + t) * 64 + l];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s[i] += o[i];
+            for (int w = 4 * g4 + 1; w < 4 * g4 + 4; ++w) {
+                const f32x4 o = red[(w * RT + t) * 64 + l];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sg[i] += o[i];
+            }
+            if (g4 == 0) s = sg;
+            else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[i] += sg[i];
+            }
         }
         const int n = row0 + 16 * t + (l & 15), m0 = 4 * (l >> 4);
         float sq[4] = {0.f, 0.f, 0.f, 0.f};
@@ -399,7 +414,7 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinArgs a) {
     if (!is_last) return;
     // the 16 outputs of one 16-column tile are 16 consecutive lanes (16 RT divides the row's count), so the tile's
     // sum of squares is a 16-lane tree (lane 0's sum)
-    for (int i = tid; i < a.M * 16 * RT; i += 256) {
+    for (int i = tid; i < a.M * 16 * RT; i += NT) {
         const int m = i / (16 * RT), n = row0 + i % (16 * RT);
         float v = 0.0f;
         if (n < a.N) {
@@ -605,22 +620,50 @@ __global__ __launch_bounds__(64 * kLongWaves) void linear_long_int8_kernel(LinAr
 
 // Row tiles per workgroup: the most (4; 2 for bf16, whose weight slots are 4x wider than INT4's) that still leave
 // min_groups workgroups, down to 1: 512, and 256 for the fused silu * up input, whose workgroups stage twice the
-// activation bytes (gate and up rows), so more weight rows per workgroup pay for them. Staged activation rows: 8 for M <= 8, else 16. Neither changes any output's summation
-// order (blocks in order within a wave, waves in order, splits in order).
+// activation bytes (gate and up rows), so more weight rows per workgroup pay for them. Staged activation rows: 8 for
+// M <= 8, else 16. Quantized weights with K = 2048 at up to 8 rows (`wide`: 16-byte parameter loads, no silu * up
+// input) instead take one 8-wave workgroup over the whole K, with no K-split and so no reduction through memory,
+// and the row tiles per workgroup (1 to 4) that fit the tiles into the fewest rounds of one workgroup per CU, then
+// the fewest rounds. None of this changes any output's summation order (blocks in order within a wave, waves in
+// order, splits in order).
 struct LinPlan {
-    int cols, rt, S, groups;
+    int cols, rt, S, groups, nw;
 };
 
-LinPlan lin_plan(int M, int N, int K, int w_type, int min_groups = 512) {
+constexpr bool kWideLinears = true;
+
+LinPlan lin_plan(int M, int N, int K, int w_type, int min_groups = 512, bool wide = false) {
     LinPlan p;
     p.cols = M <= 8 ? 8 : 16;
+    p.nw = 4;
     const int nblk = K / kQB;
+    if (kWideLinears && wide && p.cols == 8 && w_type != RK_W_BF16 && nblk == 8 * kWaveBlocks) {
+        int cus = device_cus();
+        if (cus <= 0) cus = 256;
+        const long long T = (N + 15) / 16;
+        long long best_cost = -1, best_rounds = 0;
+        for (int rt = 1; rt <= 4; ++rt) {
+            const long long g = (T + rt - 1) / rt, rounds = (g + cus - 1) / cus, cost = rounds * rt;
+            if (best_cost < 0 || cost < best_cost || (cost == best_cost && rounds < best_rounds)) {
+                best_cost = cost;
+                best_rounds = rounds;
+                p.rt = rt;
+            }
+        }
+        p.nw = 8;
+        p.S = 1;
+        p.groups = (int)((T + p.rt - 1) / p.rt);
+        return p;
+    }
     p.S = (nblk + kSplitBlocks - 1) / kSplitBlocks;
     p.rt = w_type == RK_W_BF16 ? 2 : 4;
     while (p.rt > 1 && (long long)((N + 16 * p.rt - 1) / (16 * p.rt)) * p.S < min_groups) p.rt /= 2;
     p.groups = (N + 16 * p.rt - 1) / (16 * p.rt);
     return p;
 }
+
+// the staging buffer of linear_rows_kernel: three bf16 pieces of COLS rows over the workgroup's K-split
+constexpr size_t linear_xs_bytes(int cols, int nw) { return (size_t)3 * 4 * nw * kWaveBlocks * cols * 16; }
 
 // rows of W as fp32 (the reference's dequantize, src/quant.py:45-56: q * scale, + min for INT4, each rounded):
 // out[i, k] for i < n_rows, source row rows ? rows[i] : row0 + i. One thread per 8 weights.
@@ -722,8 +765,9 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
                            static_cast<hipStream_t>(stream), a);
         return check_launch("linear_long_int8");
     }
-    const LinPlan p = lin_plan(M, N, K, w_type, x_op == RK_X_SILU_MUL ? 256 : 512);
-    const size_t need = rk_linear_workspace_bytes(M, N, K, w_type);
+    const LinPlan p = lin_plan(M, N, K, w_type, x_op == RK_X_SILU_MUL ? 256 : 512,
+                               pv && (x_op == RK_X_PLAIN || x_op == RK_X_RMS_NORM));
+    const size_t need = p.S == 1 ? 0 : rk_linear_workspace_bytes(M, N, K, w_type);
     if (need && (!partials || partial_bytes < need || !counters || n_counters < p.groups))
         return fail(RK_ERR_WORKSPACE, "rk_linear_rows: partials %zu bytes (need %zu), %d counters (need %d)",
                     partial_bytes, need, n_counters, p.groups);
@@ -739,19 +783,28 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
     using Fn = void (*)(LinArgs);
     Fn fn = nullptr;
 #define RK_LIN_PICK(C, R, V, X)                                                                                \
-    if (p.cols == C && p.rt == R && pv == V && x_op == X)                                                      \
-        fn = w_type == RK_W_BF16 ? linear_rows_kernel<RK_W_BF16, C, (R > 2 ? 2 : R), V, X>                     \
-             : w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, C, R, V, X>                                 \
-                                   : linear_rows_kernel<RK_W_INT4, C, R, V, X>;
+    if (p.nw == 4 && p.cols == C && p.rt == R && pv == V && x_op == X)                                         \
+        fn = w_type == RK_W_BF16 ? linear_rows_kernel<RK_W_BF16, C, (R > 2 ? 2 : R), V, X, 4>                  \
+             : w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, C, R, V, X, 4>                              \
+                                   : linear_rows_kernel<RK_W_INT4, C, R, V, X, 4>;
+#define RK_LIN_WIDE(R, X)                                                                                      \
+    if (p.nw == 8 && p.rt == R && x_op == X)                                                                   \
+        fn = w_type == RK_W_INT8 ? linear_rows_kernel<RK_W_INT8, 8, R, true, X, 8>                             \
+                                 : linear_rows_kernel<RK_W_INT4, 8, R, true, X, 8>;
     RK_LIN_PICK(8, 1, true, 0) RK_LIN_PICK(8, 2, true, 0) RK_LIN_PICK(8, 4, true, 0)
     RK_LIN_PICK(16, 1, true, 0) RK_LIN_PICK(16, 2, true, 0) RK_LIN_PICK(16, 4, true, 0)
     RK_LIN_PICK(8, 1, false, 0) RK_LIN_PICK(8, 2, false, 0) RK_LIN_PICK(8, 4, false, 0)
     RK_LIN_PICK(16, 1, false, 0) RK_LIN_PICK(16, 2, false, 0) RK_LIN_PICK(16, 4, false, 0)
     RK_LIN_PICK(8, 1, true, 1) RK_LIN_PICK(8, 2, true, 1) RK_LIN_PICK(8, 4, true, 1)
     RK_LIN_PICK(8, 1, true, 2) RK_LIN_PICK(8, 2, true, 2) RK_LIN_PICK(8, 4, true, 2)
+    RK_LIN_WIDE(1, 0) RK_LIN_WIDE(2, 0) RK_LIN_WIDE(3, 0) RK_LIN_WIDE(4, 0)
+    RK_LIN_WIDE(1, 2) RK_LIN_WIDE(2, 2) RK_LIN_WIDE(3, 2) RK_LIN_WIDE(4, 2)
 #undef RK_LIN_PICK
+#undef RK_LIN_WIDE
     if (!fn) return fail(RK_ERR_ARG, "rk_linear_rows: no kernel for %d columns, %d row tiles", p.cols, p.rt);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(p.groups * p.S)), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    const size_t lds = linear_xs_bytes(p.cols, p.nw);
+    if (int rc = allow_dynamic_lds((const void*)fn, lds)) return rc;
+    hipLaunchKernelGGL(fn, dim3((unsigned)(p.groups * p.S)), dim3(64 * p.nw), lds, static_cast<hipStream_t>(stream), a);
     return check_launch("linear_rows");
 }
 
