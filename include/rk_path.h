@@ -18,7 +18,7 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 16
+#define RK_ABI_VERSION 17
 
 /* status codes */
 #define RK_OK 0
@@ -319,6 +319,20 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
                        long long aux_ld, const float* norm_w, float eps, int M, int N, int K, const void* w,
                        int w_type, const void* scales, const void* mins, const float* bias, const float* residual,
                        float* partials, size_t partial_bytes, uint32_t* counters, int n_counters, void* stream);
+
+/* rk_swiglu_rows: y [M, F] = silu(x @ gate^T) * (x @ up^T) for w = [gate; up] stacked [2F, K] in one launch: replaces
+ * Backend.swiglu (src/backend/base.py:40-41; MetalBackend.swiglu, src/backend/metal.py:145-157, whose fused
+ * matvec_swiglu_bf16 kernel, src/kernels/matvec.metal:80, covers one bf16 row; TorchBackend.swiglu,
+ * src/backend/torch_ref.py:43-46). The linear is rk_linear_rows_ex2's over the 2F rows (the same sums, bit for
+ * bit, with x_op RK_X_PLAIN or RK_X_RMS_NORM and its aux / aux_ld / norm_w / eps); each gate output g and its up
+ * output u then give (g / (1 + exp(-g))) * u with the hardware exp2 and reciprocal, the form of RK_X_SILU_MUL, so
+ * rk_swiglu_rows then rk_linear_rows equals rk_linear_rows_ex2 then rk_linear_rows_ex(RK_X_SILU_MUL) bit for bit.
+ * F % 8 == 0 (else RK_ERR_UNSUPPORTED); workspace rk_linear_workspace_bytes(M, 2F, K, w_type) and ceil(2F / 16)
+ * counters as rk_linear_rows. No bias, residual or sums of squares (SwiGLU has none). */
+int rk_swiglu_rows(float* y, const float* x, long long x_ld, int x_op, const float* aux, long long aux_ld,
+                   const float* norm_w, float eps, int M, int F, int K, const void* w, int w_type, const void* scales,
+                   const void* mins, float* partials, size_t partial_bytes, uint32_t* counters, int n_counters,
+                   void* stream);
 
 /* ---- the rest of a decode step (native/decode_ops.hip): the row norms, RoPE and SwiGLU's silu * up
  * Replace Backend.rms_norm / layer_norm / rope / silu_mul (src/backend/base.py:26-40, the protocol's v1 and v3

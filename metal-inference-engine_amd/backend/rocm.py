@@ -25,7 +25,10 @@ Method -> kernel:
                          layer (src/models/qwen3_5.py:251-262, 100-110) in one launch
   linear, embedding      rk_linear_rows (bf16 / INT8 / INT4 weights, up to 32 rows), rk_dequant_rows (+ a BLAS GEMM
                          beyond 32 rows; embedding rows), src/backend/metal.py:50-133
-  swiglu, silu_mul       rk_linear_rows on the stacked [gate; up] weight, then rk_silu_mul on its two halves in place
+  swiglu                 rk_swiglu_rows: the linear on the stacked [gate; up] weight with silu * up of each gate / up
+                         output pair in its epilogue (one launch; beyond 32 rows the linear then rk_silu_mul)
+  rms_norm_swiglu        rk_swiglu_rows with the RMSNorm applied while x is staged (the MLP of a decode step)
+  silu_mul               rk_silu_mul on the two halves of a gate_up output, in place
   silu_mul_linear        rk_linear_rows_ex: SwiGLU's silu * up applied while the down projection stages its
                          activations (one launch instead of two)
   rms_norm, layer_norm   rk_rms_norm, rk_layer_norm (src/ops.py:7-24)
@@ -223,11 +226,16 @@ class RocmBackend:
         return table[ids.to(table.device)].float()
 
     def swiglu(self, x, w_gate_up):
-        """silu(x @ gate.T) * (x @ up.T) for w_gate_up = [gate; up] stacked [2F, K] (src/backend/base.py:41-42): one
-        linear over the stacked weight, then silu * up over the two column halves of its output, read in place."""
-        y = self.linear(x, w_gate_up)
-        F = w_gate_up.shape[0] // 2
-        return kernels.silu_mul(y[:, :F], y[:, F:])
+        """silu(x @ gate.T) * (x @ up.T) for w_gate_up = [gate; up] stacked [2F, K] (src/backend/base.py:40-41): up
+        to 32 rows one rk_swiglu_rows launch per 16 (the linear over the stacked weight with silu * up of each gate /
+        up output pair in its epilogue, as MetalBackend.swiglu's fused matvec_swiglu_bf16, src/backend/metal.py:
+        145-157); beyond, the linear then silu * up over the two column halves of its output, read in place."""
+        return kernels.swiglu(x, w_gate_up)
+
+    def rms_norm_swiglu(self, x, ss, norm_w, eps, w_gate_up):
+        """swiglu(rms_norm(x, norm_w, eps), w_gate_up) in one launch from the sums of squares ss that the linear
+        producing x returned (the MLP input of src/models/qwen3_5.py:166-170 follows a residual add)."""
+        return kernels.rms_norm_swiglu(x, ss, norm_w, eps, w_gate_up)
 
     def silu_mul_linear(self, gate, up, w, b=None, residual=None):
         """linear(silu_mul(gate, up), w, b, residual): SwiGLU's down projection (src/models/qwen3_5.py:166-170)

@@ -25,8 +25,14 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-# per-source additions: the bf16 delta scan splits and scales its MFMA results every chunk, so they stay in VGPRs
-SOURCE_FLAGS = {"chunked_delta_cols.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# per-source additions: the bf16 delta scan splits and scales its MFMA results every chunk, so they stay in VGPRs;
+# the sources that restate the reference's elementwise steps with each product and sum rounded (__fmul_rn /
+# __fadd_rn, which HIP defines as the plain operators) are compiled with FMA contraction inside one expression only,
+# so that hipcc's default (contraction across statements) does not fuse a rounded product into the sum after it
+_ROUNDED = ["-ffp-contract=on"]
+SOURCE_FLAGS = {"chunked_delta_cols.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "deltanet_step.hip": _ROUNDED,
+                "decode_ops.hip": _ROUNDED, "deltanet_prefill.hip": _ROUNDED, "attn_prep.hip": _ROUNDED,
+                "linear.hip": _ROUNDED}
 
 
 def _compile(src: str, verbose: bool) -> Path:

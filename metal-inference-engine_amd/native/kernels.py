@@ -853,6 +853,73 @@ def rms_norm_linear(x, ss, norm_w, eps: float, w, bias=None, residual=None) -> t
                 residual=residual)
     return y
 
+def _swiglu_launch(x, x_ld: int, w, x_op: int, aux=None, aux_ld: int = 0, norm_w=None, eps: float = 0.0):
+    """One rk_swiglu_rows launch over M <= 16 rows of x (fp32, row stride x_ld) and w = [gate; up] -> [M, F]."""
+    wt, data, scales, mins, N, K = _weight_args(w)
+    M, F = x.shape[0], N // 2
+    dev = x.device
+    out = torch.empty(M, F, dtype=torch.float32, device=dev)
+    lib = load()
+    cnt = linear_counters(dev, -(-N // 16))
+    need = lib.lib.rk_linear_workspace_bytes(M, N, K, wt)
+    part = workspace(dev, need) if need else None
+    lib.call("rk_swiglu_rows", out.data_ptr(), x.data_ptr(), x_ld, x_op, aux.data_ptr() if aux is not None else None,
+             aux_ld, norm_w.data_ptr() if norm_w is not None else None, float(eps), M, F, K, data.data_ptr(), wt,
+             scales.data_ptr() if scales is not None else None, mins.data_ptr() if mins is not None else None,
+             part.data_ptr() if part is not None else None, part.numel() if part is not None else 0, cnt.data_ptr(),
+             cnt.numel(), _stream(dev))
+    return out
+
+
+def _swiglu_fused(w, K: int) -> bool:
+    """Whether rk_swiglu_rows covers a [2F, K] weight: F a multiple of 8, K of 32."""
+    wt, data, scales, mins, N, Kw = _weight_args(w)
+    return N % 16 == 0 and K == Kw and K % 32 == 0
+
+
+def swiglu(x, w) -> torch.Tensor:
+    """Backend.swiglu (src/backend/base.py:40-41): silu(x @ gate^T) * (x @ up^T) for w = [gate; up] stacked [2F, K]
+    (bf16 or a QuantTensor) -> [M, F] fp32. Up to KERNEL_ROWS rows: rk_swiglu_rows, one launch per 16 rows (the
+    linear's sums, then silu * up on each gate / up pair in the same launch); beyond that, or for F % 8 != 0, the
+    linear and then silu_mul on its two halves (the same results within 1e-5)."""
+    N, K = w.shape
+    M = x.shape[0]
+    if x.dim() != 2 or x.shape[1] != K or N % 2:
+        raise ValueError(f"swiglu: x {tuple(x.shape)} for a [{N}, {K}] stacked [gate; up] weight")
+    from quant import QuantTensor
+    if M > KERNEL_ROWS or not (isinstance(w, QuantTensor) or w.dtype == torch.bfloat16) or not _swiglu_fused(w, K):
+        y = linear(x, w)
+        return silu_mul(y[:, :N // 2], y[:, N // 2:])
+    _need_cuda("swiglu", x, w.data if isinstance(w, QuantTensor) else w)
+    xr, ld = _rows_k(x, K)
+    from native.rocm_native import RK_X_PLAIN
+    if M <= LINEAR_ROWS:
+        return _swiglu_launch(xr, ld, w, RK_X_PLAIN)
+    return torch.cat([_swiglu_launch(xr[m0:m0 + LINEAR_ROWS], ld, w, RK_X_PLAIN) for m0 in range(0, M, LINEAR_ROWS)])
+
+
+def rms_norm_swiglu(x, ss, norm_w, eps: float, w) -> torch.Tensor:
+    """swiglu(rms_norm(x, norm_w, eps), w) in one launch (rk_swiglu_rows with the RMSNorm input transform), from
+    ss = the sums of squares of x's 16-column tiles that the linear producing x wrote; the cases rms_norm_linear
+    sends to the separate norm (no ss, more than 8 rows, K % 256 != 0 or K > 2048, more than 16384 weight rows)
+    and the weights swiglu does not fuse: rms_norm, then swiglu (the same results within 1e-5)."""
+    N, K = w.shape
+    M = x.shape[0]
+    from quant import QuantTensor
+    if (ss is None or x.dim() != 2 or x.shape[1] != K or M > 8 or K % 256 or K > 2048 or N > 16384
+            or ss.shape != (M, K // 16) or norm_w.numel() != K
+            or not (isinstance(w, QuantTensor) or w.dtype == torch.bfloat16) or not _swiglu_fused(w, K)):
+        return swiglu(rms_norm(x, norm_w, eps), w)
+    _need_cuda("swiglu", x, ss, norm_w, w.data if isinstance(w, QuantTensor) else w)
+    xr, ld = _rows_k(x, K)
+    nw = norm_w.to(torch.float32).contiguous()
+    if nw.data_ptr() % 16:
+        nw = nw.clone()
+    ssr = ss.to(torch.float32).contiguous()
+    from native.rocm_native import RK_X_RMS_NORM
+    return _swiglu_launch(xr, ld, w, RK_X_RMS_NORM, aux=ssr, aux_ld=ssr.stride(0), norm_w=nw, eps=eps)
+
+
 _linear_cnt: dict[int, torch.Tensor] = {}
 
 

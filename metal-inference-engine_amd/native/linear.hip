@@ -41,6 +41,7 @@ struct LinArgs {
     float* ss;                     // [M, ceil(N / 16)] sums of squares of y's 16-column tiles, or null
     float eps;                     // XF 2
     int M, N, K, S;
+    int glu;                       // 1: W = [gate; up] (N = 2F rows), y [M, F] = silu(x gate^T) * (x up^T)
 };
 
 constexpr int kMaxSsTiles = 128;   // XF 2: at most 128 sums of squares per row (K <= 2048)
@@ -52,6 +53,26 @@ template <> struct WTraits<RK_W_INT8> { static constexpr int BPB = 32; };
 template <> struct WTraits<RK_W_INT4> { static constexpr int BPB = 16; };
 
 __device__ __forceinline__ float half_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// silu(g) * u = g / (1 + exp(-g)) * u with the hardware exp2 and reciprocal: SwiGLU's product, in the one form that
+// both the silu * up input transform (XF 1) and the paired [gate; up] output (glu) compute, so they give equal bits.
+// The result is the rounded fp32 product, as the reference hands silu * up to the next op as an fp32 tensor: the
+// empty asm makes it opaque, since an inlined product would otherwise be contracted into the activation split that
+// consumes it (x - hi as fma(a, u, -hi)), whose pieces would then carry the unrounded product.
+__device__ __forceinline__ float silu_times(float g, float u) {
+    const float d = 1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+    float h = g * __builtin_amdgcn_rcpf(d) * u;
+    asm("" : "+v"(h));
+    return h;
+}
+
+// the weight row behind output row lr of the kernel: lr itself, or with glu (W = [gate; up], N = 2F rows, F % 8 == 0)
+// gate rows 8T .. 8T+7 then up rows F + 8T .. F + 8T+7 for 16-row tile T, so that in the MFMA result each gate
+// output's up partner is 8 lanes away and the tile's 8 outputs silu(gate) * up are columns 8T .. 8T+7 of y
+__device__ __forceinline__ size_t weight_row(const LinArgs& a, int lr) {
+    const int c = lr & 15, base = 8 * (lr >> 4) + (c & 7);
+    return (size_t)(a.glu ? (c < 8 ? base : (a.N >> 1) + base) : lr);
+}
 
 // 8 INT8 codes (one lane's MFMA slots of one block: bytes of lo then hi) as bf16 bits; q in [-127, 127] is exact in
 // bf16, and the top half of the fp32 value is its bf16 pattern
@@ -181,7 +202,7 @@ __global__ __launch_bounds__(64 * NW) void linear_rows_kernel(LinArgs a) {
     if constexpr (QUANT) {
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const size_t rowp = (size_t)min(row0 + 16 * t + r, a.N - 1) * nblk;
+            const size_t rowp = weight_row(a, min(row0 + 16 * t + r, a.N - 1)) * nblk;
             if constexpr (PV) {
                 const size_t i0 = rowp + min(wb0, nblk - kWaveBlocks);
                 sc[t] = *reinterpret_cast<const u32x4*>(a.scales + i0);
@@ -205,7 +226,7 @@ __global__ __launch_bounds__(64 * NW) void linear_rows_kernel(LinArgs a) {
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
         const uint8_t* wrow = static_cast<const uint8_t*>(a.w) +
-                              (size_t)min(row0 + 16 * t + r, a.N - 1) * ((size_t)nblk * TR::BPB);
+                              weight_row(a, min(row0 + 16 * t + r, a.N - 1)) * ((size_t)nblk * TR::BPB);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             size_t off;
@@ -247,12 +268,9 @@ __global__ __launch_bounds__(64 * NW) void linear_rows_kernel(LinArgs a) {
             v[e] = ok ? xv[u][0][e] : 0.0f;
             v[4 + e] = ok ? xv[u][1][e] : 0.0f;
         }
-        if constexpr (XF == 1) {                    // silu(gate) * up = g / (1 + exp(-g)) * u, hardware exp / rcp
+        if constexpr (XF == 1) {                    // silu(gate) * up
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float d = 1.0f + __builtin_amdgcn_exp2f(-v[e] * 1.4426950408889634f);
-                v[e] = v[e] * __builtin_amdgcn_rcpf(d) * (ok ? xa[u][e >> 2][e & 3] : 0.0f);
-            }
+            for (int e = 0; e < 8; ++e) v[e] = silu_times(v[e], ok ? xa[u][e >> 2][e & 3] : 0.0f);
         } else if constexpr (XF == 2) {             // rms_norm: (x * (1 / rms)) * w, each rounded
             const float ir = rms_s[col];
 #pragma unroll
@@ -374,7 +392,16 @@ __global__ __launch_bounds__(64 * NW) void linear_rows_kernel(LinArgs a) {
         }
         const int n = row0 + 16 * t + (l & 15), m0 = 4 * (l >> 4);
         float sq[4] = {0.f, 0.f, 0.f, 0.f};
-        if (n < a.N) {
+        if (a.glu && a.S == 1) {                    // uniform: lanes l % 16 < 8 hold gates, l % 16 >= 8 their ups
+            float u[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[i] = __shfl_xor(s[i], 8);
+            if ((l & 8) == 0 && n < a.N) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (m0 + i < a.M) a.y[(size_t)(m0 + i) * (a.N >> 1) + 8 * (n >> 4) + (l & 7)] = silu_times(s[i], u[i]);
+            }
+        } else if (n < a.N) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = m0 + i;
@@ -423,7 +450,11 @@ __global__ __launch_bounds__(64 * NW) void linear_rows_kernel(LinArgs a) {
                                        __HIP_MEMORY_SCOPE_AGENT);
             if (a.bias) v = __fadd_rn(v, a.bias[n]);
             if (a.res) v = __fadd_rn(v, a.res[(size_t)m * a.N + n]);
-            a.y[(size_t)m * a.N + n] = v;
+            if (!a.glu) a.y[(size_t)m * a.N + n] = v;
+        }
+        if (a.glu) {                                // uniform: the up partner of output n is output n + 8, 8 lanes on
+            const float u = __shfl_xor(v, 8);
+            if ((n & 8) == 0 && n < a.N) a.y[(size_t)m * (a.N >> 1) + 8 * (n >> 4) + (n & 7)] = silu_times(v, u);
         }
         if (a.ss) {                                 // uniform
             float q2 = v * v;
@@ -716,10 +747,15 @@ size_t rk_linear_workspace_bytes(int M, int N, int K, int w_type) {
     return p.S == 1 ? 0 : (size_t)p.S * M * N * sizeof(float);
 }
 
-int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, int x_op, const float* aux,
-                       long long aux_ld, const float* norm_w, float eps, int M, int N, int K, const void* w,
-                       int w_type, const void* scales, const void* mins, const float* bias, const float* residual,
-                       float* partials, size_t partial_bytes, uint32_t* counters, int n_counters, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// rk_linear_rows_ex2, and with glu rk_swiglu_rows (N = 2F weight rows, y [M, F]; no bias, residual or sums of squares)
+int linear_rows_impl(float* y, float* ss_out, const float* x, long long x_ld, int x_op, const float* aux,
+                     long long aux_ld, const float* norm_w, float eps, int M, int N, int K, const void* w, int w_type,
+                     const void* scales, const void* mins, const float* bias, const float* residual, float* partials,
+                     size_t partial_bytes, uint32_t* counters, int n_counters, bool glu, void* stream) {
     if (M == 0 || N == 0) return RK_OK;
     const bool quant = w_type == RK_W_INT8 || w_type == RK_W_INT4;
     if (!y || !x || !w || (quant && !scales) || (w_type == RK_W_INT4 && !mins) || (x_op != RK_X_PLAIN && !aux))
@@ -749,7 +785,7 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
         }
     }
     // long INT8 matrices: the persistent kernel (no partials or counters used)
-    if (w_type == RK_W_INT8 && M <= 8 && N >= kLongMinRows && K % (2 * kLongChunk) == 0 && K / 16 <= kMaxSsTiles && pv &&
+    if (!glu && w_type == RK_W_INT8 && M <= 8 && N >= kLongMinRows && K % (2 * kLongChunk) == 0 && K / 16 <= kMaxSsTiles && pv &&
         (x_op == RK_X_PLAIN || x_op == RK_X_RMS_NORM)) {
         LinArgs a{};
         a.y = y; a.x = x; a.w = w; a.scales = static_cast<const uint16_t*>(scales);
@@ -779,7 +815,7 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
     a.part = partials;
     a.aux = aux; a.x_ld = x_ld; a.aux_ld = aux_ld;
     a.nw = norm_w; a.ss = ss_out; a.eps = eps;
-    a.M = M; a.N = N; a.K = K; a.S = p.S;
+    a.M = M; a.N = N; a.K = K; a.S = p.S; a.glu = glu ? 1 : 0;
     using Fn = void (*)(LinArgs);
     Fn fn = nullptr;
 #define RK_LIN_PICK(C, R, V, X)                                                                                \
@@ -806,6 +842,29 @@ int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, 
     if (int rc = allow_dynamic_lds((const void*)fn, lds)) return rc;
     hipLaunchKernelGGL(fn, dim3((unsigned)(p.groups * p.S)), dim3(64 * p.nw), lds, static_cast<hipStream_t>(stream), a);
     return check_launch("linear_rows");
+}
+
+}  // namespace
+
+extern "C" {
+
+int rk_linear_rows_ex2(float* y, float* ss_out, const float* x, long long x_ld, int x_op, const float* aux,
+                       long long aux_ld, const float* norm_w, float eps, int M, int N, int K, const void* w,
+                       int w_type, const void* scales, const void* mins, const float* bias, const float* residual,
+                       float* partials, size_t partial_bytes, uint32_t* counters, int n_counters, void* stream) {
+    return linear_rows_impl(y, ss_out, x, x_ld, x_op, aux, aux_ld, norm_w, eps, M, N, K, w, w_type, scales, mins, bias,
+                            residual, partials, partial_bytes, counters, n_counters, false, stream);
+}
+
+int rk_swiglu_rows(float* y, const float* x, long long x_ld, int x_op, const float* aux, long long aux_ld,
+                   const float* norm_w, float eps, int M, int F, int K, const void* w, int w_type, const void* scales,
+                   const void* mins, float* partials, size_t partial_bytes, uint32_t* counters, int n_counters,
+                   void* stream) {
+    if (x_op != RK_X_PLAIN && x_op != RK_X_RMS_NORM) return fail(RK_ERR_ARG, "rk_swiglu_rows: input transform %d", x_op);
+    if (F < 0 || F > (1 << 29)) return fail(RK_ERR_ARG, "rk_swiglu_rows: F %d", F);
+    if (F % 8) return fail(RK_ERR_UNSUPPORTED, "rk_swiglu_rows: F %d (a multiple of 8)", F);
+    return linear_rows_impl(y, nullptr, x, x_ld, x_op, aux, aux_ld, norm_w, eps, M, 2 * F, K, w, w_type, scales, mins,
+                            nullptr, nullptr, partials, partial_bytes, counters, n_counters, true, stream);
 }
 
 int rk_linear_rows_ex(float* y, const float* x, long long x_ld, int x_op, const float* aux, long long aux_ld, int M,

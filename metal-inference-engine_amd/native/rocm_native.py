@@ -11,7 +11,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "librk_path.so"
 HEADER = HERE.parent.parent / "include" / "rk_path.h"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 RK_F32, RK_BF16 = 0, 1
 RK_W_BF16, RK_W_INT8, RK_W_INT4 = 1, 2, 3
@@ -62,6 +62,8 @@ SIGNATURES = {
                                   c_size_t, P, c_int, P]),
     "rk_linear_rows_ex2": (c_int, [P, P, P, c_longlong, c_int, P, c_longlong, P, c_float, c_int, c_int, c_int, P, c_int,
                                    P, P, P, P, P, c_size_t, P, c_int, P]),
+    "rk_swiglu_rows": (c_int, [P, P, c_longlong, c_int, P, c_longlong, P, c_float, c_int, c_int, c_int, P, c_int, P, P,
+                               P, c_size_t, P, c_int, P]),
     "rk_rms_norm": (c_int, [P, P, c_int, c_longlong, P, c_int, c_int, c_int, c_float, P]),
     "rk_layer_norm": (c_int, [P, P, c_int, c_longlong, P, c_int, c_int, c_int, c_float, P]),
     "rk_rope": (c_int, [P, P, P, P, c_int, c_int, c_int, P]),

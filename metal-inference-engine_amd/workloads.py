@@ -633,8 +633,9 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
     """One decode step for the batch through the backend protocol, in the order of Qwen3_5Model.decode_batch
     (src/models/qwen3_5.py:228-290) -> logits [B, vocab] fp32. The attention layer's q / k norms, partial RoPE and
     KV write are the one fused attention_prep call, the output gate is fused into paged_attention, and (with a
-    backend that has silu_mul_linear) SwiGLU's silu * up runs inside the down projection, and (with one that has
-    rms_norm_linear) every RMSNorm after the first runs inside the linear that follows it, from the sums of squares
+    backend that has rms_norm_swiglu) the MLP is the reference's swiglu then linear, with silu * up in the gate_up
+    projection's epilogue (else, with one that has silu_mul_linear, inside the down projection), and (with one that
+    has rms_norm_linear) every RMSNorm after the first runs inside the linear that follows it, from the sums of squares
     the linear before it returned; with one that has decode_plan, the attention layers share one batch layout plan;
     the sequences' lengths are not advanced (a benchmark replays the same step)."""
     cfg = st.cfg
@@ -642,6 +643,7 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
     slots, tables, lens, positions = layout
     fused = hasattr(backend, "silu_mul_linear")
     fused_norm = hasattr(backend, "rms_norm_linear")
+    fused_swiglu = fused_norm and hasattr(backend, "rms_norm_swiglu")
     ss = None                       # sums of squares of h's 16-column tiles, from the linear that wrote h
 
     def norm_linear(h, norm_w, wt):
@@ -680,6 +682,11 @@ def hybrid_decode_step(backend, w: dict, st: HybridDecodeState, tokens: torch.Te
                                               st.seqs, L, w[a + "conv1d.weight"], w[a + "A_log"], w[a + "dt_bias"],
                                               w[a + "norm.weight"], cfg.eps, (H, cfg.dk, cfg.dv, H * cfg.dk))
             h, ss = residual_linear(o, w[a + "out_proj.weight"], h)
+        if fused_swiglu:
+            act = backend.rms_norm_swiglu(h, ss, w[p + "post_attention_layernorm.weight"], cfg.eps,
+                                          w[p + "mlp.gate_up.weight"])
+            h, ss = residual_linear(act, w[p + "mlp.down_proj.weight"], h)
+            continue
         gu = norm_linear(h, w[p + "post_attention_layernorm.weight"], w[p + "mlp.gate_up.weight"])
         F = gu.shape[1] // 2
         if fused_norm:

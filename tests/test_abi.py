@@ -239,10 +239,11 @@ def test_linear_arguments_checked_on_host(lib):
     assert call(K=2047) == 1
     assert call(wt=3, m=None) == 1 and "null pointer" in lib.last_error()
     assert call(y=fake + 4, x=fake + 8) == 1 and "aligned" in lib.last_error()
-    need = lib.lib.rk_linear_workspace_bytes(8, 2048, 2048, 2)
-    assert need == 2 * 8 * 2048 * 4                            # 2 K-splits of 32 blocks
-    assert call(pb=need - 1) == 3 and "partials" in lib.last_error()
-    assert call(nc=127) == 3 and "counters" in lib.last_error()    # 128 groups of 16 rows
+    # (K = 4096: quantized K = 2048 at up to 8 rows runs whole-K workgroups with no workspace, and would launch)
+    need = lib.lib.rk_linear_workspace_bytes(8, 2048, 4096, 2)
+    assert need == 4 * 8 * 2048 * 4                            # 4 K-splits of 32 blocks
+    assert call(K=4096, pb=need - 1) == 3 and "partials" in lib.last_error()
+    assert call(K=4096, nc=127) == 3 and "counters" in lib.last_error()    # 128 groups of 16 rows
     assert lib.lib.rk_linear_workspace_bytes(8, 2048, 1024, 2) == 0      # one split: no workspace
     assert lib.lib.rk_linear_workspace_bytes(12, 2048, 2048, 1) == 2 * 12 * 2048 * 4
     assert lib.lib.rk_linear_workspace_bytes(3, 100, 6144, 3) == 6 * 3 * 100 * 4
@@ -307,6 +308,17 @@ def test_linear_ex2_checked_on_host(lib):
     assert call(auxld=127) == 1 and "sums of squares" in lib.last_error()
     assert call(K=4096, xld=4096, auxld=256) == 1 and "sums of squares" in lib.last_error()
     assert call(M=9) == 2 and "M <= 8" in lib.last_error()
+    sw = dict(y=fake, x=fake, xld=2048, op=2, aux=fake + 8192, auxld=128, nw=fake, eps=1e-6, M=8, F=6144, K=2048,
+              w=fake, wt=3, s=fake, m=fake, p=fake, pb=1 << 30, c=fake, nc=1024)
+
+    def swiglu(**kw):
+        return L.rk_swiglu_rows(*dict(sw, **kw).values(), None)
+
+    assert swiglu(op=1) == 1 and "input transform 1" in lib.last_error()
+    assert swiglu(F=6148) == 2 and "multiple of 8" in lib.last_error()
+    assert swiglu(nw=None) == 1 and "norm weight" in lib.last_error()
+    assert swiglu(M=9) == 2 and "M <= 8" in lib.last_error()
+    assert swiglu(M=0) == 0 and swiglu(F=0) == 0
     ex = dict(y=fake, x=fake, xld=2048, op=2, aux=fake, auxld=2048, M=8, N=2048, K=2048, w=fake, wt=3, s=fake, m=fake,
               b=None, r=None, p=fake, pb=1 << 30, c=fake, nc=1024)
     assert L.rk_linear_rows_ex(*ex.values(), None) == 1 and "input transform 2" in lib.last_error()

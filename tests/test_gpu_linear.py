@@ -111,6 +111,69 @@ def test_silu_mul_fused_into_the_linear(backend, kind, N, K):
     assert torch.equal(backend.silu_mul_linear(yd[3:4, :K], yd[3:4, K:], wd), full[3:4])
 
 
+@pytest.mark.parametrize("F,K", [(6144, 2048), (3584, 1024), (1024, 3072), (520, 2080), (48, 256)])
+@pytest.mark.parametrize("kind", ["bf16", "int8", "int4"])
+def test_swiglu_rows(backend, kind, F, K):
+    """rk_swiglu_rows (RocmBackend.swiglu): silu(x gate^T) * (x up^T) over the stacked [gate; up] weight in one
+    launch == the oracle's linear then silu_mul within 1e-5 at 1, 5, 8, 16 and 20 rows (20: two launches; 33: the
+    GEMM then silu_mul); a row's result does not depend on the batch; where the fused silu * up down projection
+    covers the shape (M <= 8, F % 256 == 0), swiglu then the down projection equals the plain linear then that fused
+    projection bit for bit (the gate / up sums are the linear's, and silu * up is computed in the same form)."""
+    from native import kernels
+    from oracle import ops_ref
+    w, deq = weight(kind, 2 * F, K, 3 * F + K)
+    wdn, _ = weight("int4", 256, F, F) if F % 32 == 0 else weight("bf16", 256, F, F)
+    wd, wdnd = to_dev(w), to_dev(wdn)
+    g = torch.Generator().manual_seed(F + K)
+    x33 = torch.randn(33, K, generator=g)
+    got_by_m = {}
+    for M in (8, 1, 5, 16, 20, 33):
+        x = x33[:M]
+        y = quant_ref.linear(x, deq, None, None)
+        want = ops_ref.silu_mul(y[:, :F], y[:, F:])
+        got = backend.swiglu(x.to(DEV), wd)
+        assert got.shape == (M, F)
+        assert rel_err(got, want) < TOL, f"M {M}"
+        got_by_m[M] = got.cpu()
+        if M <= 8 and F % 256 == 0:
+            xd = x.to(DEV)
+            gu = kernels.linear(xd, wd)
+            two = kernels.silu_mul_linear(gu[:, :F], gu[:, F:], wdnd)
+            assert torch.equal(kernels.linear(got, wdnd), two), f"M {M}"
+    assert torch.equal(got_by_m[1][0], got_by_m[8][0])
+    assert torch.equal(got_by_m[5], got_by_m[8][:5])
+
+
+@pytest.mark.parametrize("kind", ["int4", "int8", "bf16"])
+def test_rms_norm_swiglu_is_the_decode_mlp(backend, kind):
+    """The decode step's MLP at Qwen3.5-2B widths: rms_norm_swiglu (the norm from the producer's tile sums while x is
+    staged, silu * up in the epilogue) then the down projection with its tile sums == rms_norm_linear over gate_up
+    then silu_mul_linear_ss bit for bit (both outputs and sums) at 1, 5 and 8 rows, and the oracle's
+    h + down(silu_mul(linear(rms_norm(h)))) within 1e-5; beyond 8 rows the separate norm runs (same bar)."""
+    from native import kernels
+    from oracle import ops_ref
+    F, K = 6144, 2048
+    w, deq = weight(kind, 2 * F, K, 11)
+    wdn, deq_dn = weight(kind, K, F, 12)
+    wp, _ = weight("int4", K, 2048, 13)                 # the producer of h
+    wd, wdnd, wpd = to_dev(w), to_dev(wdn), to_dev(wp)
+    g = torch.Generator().manual_seed(14)
+    nw = (1.0 + 0.1 * torch.randn(K, generator=g)).to(DEV)
+    o12, r12 = torch.randn(12, 2048, generator=g), torch.randn(12, K, generator=g)
+    for M in (8, 1, 5, 12):
+        h, ss = kernels.linear_ss(o12[:M].to(DEV), wpd, residual=r12[:M].to(DEV))
+        act = kernels.rms_norm_swiglu(h, ss, nw, 1e-6, wd)
+        y, ss2 = kernels.linear_ss(act, wdnd, residual=h)
+        want_act = ops_ref.silu_mul(*quant_ref.linear(ops_ref.rms_norm(h.cpu(), nw.cpu(), 1e-6), deq, None,
+                                                      None).split(F, dim=1))
+        assert rel_err(act, want_act) < TOL, f"M {M}"
+        assert rel_err(y, quant_ref.linear(want_act, deq_dn, None, h.cpu())) < TOL, f"M {M}"
+        if M <= 8:
+            gu = kernels.rms_norm_linear(h, ss, nw, 1e-6, wd)
+            y2, ss3 = kernels.silu_mul_linear_ss(gu[:, :F], gu[:, F:], wdnd, residual=h)
+            assert torch.equal(y, y2) and torch.equal(ss2, ss3), f"M {M}"
+
+
 def tile_sums(y):
     """Sums of squares of y's 16-column tiles [M, ceil(N / 16)] (the last tile zero-padded)."""
     M, N = y.shape
