@@ -1,6 +1,7 @@
 """HIP graph replays of the launches that keep state between calls (the linears' arrival counters, the paged decode's
 workspace, the chunked delta rule's workspace): a chain of a residual linear with tile sums of squares, the RMSNorm
-fused into the next linear, the SwiGLU down projection with its sums, and config-3 paged decode with the gate,
+fused into the next linear, the SwiGLU down projection with its sums, the same MLP as rms_norm_swiglu then the plain
+down projection (equal bits), a bf16 swiglu (K-split, counters), and config-3 paged decode with the gate,
 captured once and replayed three times with eager calls of the same launches (which share the counters) in between;
 and two chunked-delta calls on different inputs through one workspace, the second consuming the first's state.
 Every replay must give the eager bits: the counters come back to zero after every launch, nothing in the chain is a
@@ -26,15 +27,21 @@ def test_decode_launch_chain_replays_bit_identical():
     nw = (1.0 + 0.1 * torch.randn(2048, generator=g)).to(DEV)
     c = wl.c3_paged_decode().to(DEV)
 
+    w_gu_bf = (torch.randn(12288, 2048, generator=g) * 0.02).to(torch.bfloat16).to(DEV)   # K-split: counters
+
     def chain():
         h, ss = kernels.linear_ss(o, w_out, residual=h0)
         gu = kernels.rms_norm_linear(h, ss, nw, 1e-6, w_gu)
         h2, ss2 = kernels.silu_mul_linear_ss(gu[:, :6144], gu[:, 6144:], w_dn, residual=h)
+        act = kernels.rms_norm_swiglu(h, ss, nw, 1e-6, w_gu)
+        h3, ss3 = kernels.linear_ss(act, w_dn, residual=h)
+        act_bf = kernels.swiglu(o, w_gu_bf)
         att = kernels.paged_decode(c.q, c.k_pool, c.v_pool, c.tables, c.lens, c.block_size, gate=c.gate)
-        return h, ss, gu, h2, ss2, att
+        return h, ss, gu, h2, ss2, act, h3, ss3, act_bf, att
 
     want = [t.clone() for t in chain()]
     torch.cuda.synchronize()
+    assert torch.equal(want[6], want[3]) and torch.equal(want[7], want[4])   # swiglu then down == the fused down
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -47,7 +54,8 @@ def test_decode_launch_chain_replays_bit_identical():
     for rep in range(3):
         graph.replay()
         torch.cuda.synchronize()
-        for name, got, ref in zip(("h", "ss", "gate_up", "h2", "ss2", "attention"), outs, want):
+        for name, got, ref in zip(("h", "ss", "gate_up", "h2", "ss2", "swiglu", "h3", "ss3", "swiglu_bf16",
+                                   "attention"), outs, want):
             assert torch.equal(got, ref), f"replay {rep}: {name}"
         eager = chain()                                  # the same launches between replays (shared counters)
         torch.cuda.synchronize()
