@@ -429,6 +429,12 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         for (int i = 0; i < NT * NIT; ++i) qop[i * 64 + lane] = u32x4{0u, 0u, 0u, 0u};
     };
     typename LD::Vec kv[KB], vv[VB];
+    // With whole-tile sets, the next tile's first VE value steps are requested into vn right after its keys, before
+    // this tile's softmax, and the rest as this tile's values are used: more bytes in flight per wave through the
+    // scores and the softmax (half a tile's values is what the 256 registers of the 8-wave instance leave room for;
+    // the unaligned-table instance, one register short, keeps the later requests)
+    constexpr int VE = (kHalf || !ALIGNED) ? 0 : VB / 2;
+    typename LD::Vec vn[VE > 0 ? VE : 1];
     TileRows<NVI, TPI, LPT, ALIGNED> cur;
     // issue order K then V, here and in the loop, so that waiting for a tile's keys never waits for its values
     // (the scheduling barriers keep the compiler from reordering the two groups of loads); `mid` issues loads
@@ -716,6 +722,12 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
                         sacc[tt] = mfma16x16x32(qop[(tt * NIT + it) * 64 + lane], kb[ks], sacc[tt]);
             }
 
+            if constexpr (VE > 0) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int vi = 0; vi < VE; ++vi) vn[vi] = LD::load(a.vp, nxt.vrow(vi));
+                __builtin_amdgcn_sched_barrier(0);
+            }
             // sum the three query splits: lane (grp, row) then holds heads 4 * (grp % HB) + i of position row
             float sc[4];
 #pragma unroll
@@ -765,9 +777,11 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
                 float vf[8];
                 LD::keep_if(vv[vi % VB], cur_now.vvalid(vi));
                 LD::widen(vv[vi % VB], vf);
-                __builtin_amdgcn_sched_barrier(0);
-                vv[vi % VB] = LD::load(a.vp, vi + VB < NVI ? cur_now.vrow(vi + VB) : nxt.vrow(vi + VB - NVI));
-                __builtin_amdgcn_sched_barrier(0);
+                if (vi >= VE) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    vv[vi % VB] = LD::load(a.vp, vi + VB < NVI ? cur_now.vrow(vi + VB) : nxt.vrow(vi + VB - NVI));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 const int pos = vi * TPI + lane / LPT;
                 float ph[GP];
 #pragma unroll
@@ -779,6 +793,10 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
                 for (int h = 0; h < GP; ++h)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(ph[h], vf[e], acc[h][e]);
+            }
+            if constexpr (VE > 0) {
+#pragma unroll
+                for (int vi = 0; vi < VE; ++vi) vv[vi] = vn[vi];
             }
             cur = nxt;
             wave_lds_sync();   // p_lds / alpha_lds are rewritten by the next tile
