@@ -184,9 +184,11 @@ template <>
 struct KVLoad<uint16_t> {
     static constexpr int KS = 1;   // key splits
     struct Vec { u32x4 w; };
+    // Non-temporal: every K / V byte of a decode is read exactly once, and streaming it past the caches (instead of
+    // allocating it there) raised the split kernel's HBM rate at config 3 from 5.57 to 5.90 TB/s (same bits)
     __device__ static Vec load(const void* base, long long off) {
         Vec v;
-        v.w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
+        v.w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off));
         return v;
     }
     __device__ static void key_operands(const Vec& v, u32x4* ops) { ops[0] = v.w; }
