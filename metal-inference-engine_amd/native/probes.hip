@@ -2,13 +2,14 @@
 // arithmetic. They bound what the kernels can reach and are not on the path (no counterpart in the reference).
 //
 //   probe_block_stream: reads whole 16-position KV tiles (both pools) given as a list of pool tile offsets, in the
-//     list's order, with 16-byte loads, and keeps an xor of everything read. With the decode's own tiles in table
-//     order this is the paged decode's K/V traffic (scattered 16 KiB blocks) without the softmax or the merge; with
-//     the same tiles sorted by address it is a near-sequential stream of the same bytes. Either as persistent waves
-//     striding over the list, or as one-shot workgroups over consecutive runs of it.
+//     list's order, with 16-byte non-temporal loads (as the decode kernel reads them), and keeps an xor of everything
+//     read. With the decode's own tiles in table order this is the paged decode's K/V traffic (scattered 16 KiB
+//     blocks) without the softmax or the merge; with the same tiles sorted by address it is a near-sequential stream
+//     of the same bytes. Either as persistent waves striding over the list, or as one-shot workgroups over
+//     consecutive runs of it.
 //   probe_state_rmw: reads each selected (sequence, head) state block of the DeltaNet pool, scales it, and writes it
-//     back: the recurrent step's state traffic (one read and one write of 64 KiB per head) without the conv, norms
-//     or delta rule, with `split` workgroups per head.
+//     back with non-temporal loads and stores (as the step kernel does): the recurrent step's state traffic (one
+//     read and one write of 64 KiB per head) without the conv, norms or delta rule, with `split` workgroups per head.
 #include "rk_device.h"
 #include "rk_internal.h"
 
@@ -32,8 +33,8 @@ __global__ __launch_bounds__(64 * kProbeWaves) void probe_block_stream(const cha
         u32x4 x[2 * kVec];
 #pragma unroll
         for (int j = 0; j < kVec; ++j) {
-            x[j] = *reinterpret_cast<const u32x4*>(kp + off + 1024ll * j);
-            x[kVec + j] = *reinterpret_cast<const u32x4*>(vp + off + 1024ll * j);
+            x[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + off + 1024ll * j));
+            x[kVec + j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp + off + 1024ll * j));
         }
 #pragma unroll
         for (int j = 0; j < 2 * kVec; ++j) acc ^= x[j][0] ^ x[j][1] ^ x[j][2] ^ x[j][3];
@@ -57,8 +58,8 @@ __global__ __launch_bounds__(64 * kProbeWaves) void probe_block_oneshot(const ch
         u32x4 x[2 * kVec];
 #pragma unroll
         for (int j = 0; j < kVec; ++j) {
-            x[j] = *reinterpret_cast<const u32x4*>(kp + off + 1024ll * j);
-            x[kVec + j] = *reinterpret_cast<const u32x4*>(vp + off + 1024ll * j);
+            x[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + off + 1024ll * j));
+            x[kVec + j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp + off + 1024ll * j));
         }
 #pragma unroll
         for (int j = 0; j < 2 * kVec; ++j) acc ^= x[j][0] ^ x[j][1] ^ x[j][2] ^ x[j][3];
@@ -75,16 +76,15 @@ __global__ __launch_bounds__(256) void probe_state_rmw(float* S, const int32_t* 
     const int b = blockIdx.x / (split * H);
     const long long head = (((long long)seq_index[b] * n_linear + slot) * H + h) * dk * dv;
     const int n4 = dk * dv / 4 / split;
-    float4* p = reinterpret_cast<float4*>(S + head) + (long long)part * n4;
-    constexpr int kMax = 16;                    // float4 per thread held at once (64 KiB / 256 threads)
-    float4 x[kMax];
+    f32x4* p = reinterpret_cast<f32x4*>(S + head) + (long long)part * n4;
+    constexpr int kMax = 16;                    // f32x4 per thread held at once (64 KiB / 256 threads)
+    f32x4 x[kMax];
 #pragma unroll
     for (int i = 0; i < kMax; ++i)
-        if (threadIdx.x + 256 * i < n4) x[i] = p[threadIdx.x + 256 * i];
+        if (threadIdx.x + 256 * i < n4) x[i] = __builtin_nontemporal_load(p + threadIdx.x + 256 * i);
 #pragma unroll
     for (int i = 0; i < kMax; ++i)
-        if (threadIdx.x + 256 * i < n4)
-            p[threadIdx.x + 256 * i] = make_float4(x[i].x * scale, x[i].y * scale, x[i].z * scale, x[i].w * scale);
+        if (threadIdx.x + 256 * i < n4) __builtin_nontemporal_store(x[i] * scale, p + threadIdx.x + 256 * i);
 }
 
 }  // namespace
