@@ -688,12 +688,22 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         }
         for (int k = 0; k < cnt; ++k, ++j) {
             // the next entry's rows: from the lane arrays, refilled when the next entry starts a new 64-entry chunk
-            // (the refill's table load makes that one prefetch wait); the last entry re-requests its own rows,
-            // which hit in L2
+            // (the refill's table load makes that one prefetch wait). The last entry's prefetch is never used: it
+            // is aimed at position 0 of the pool's first block (one 512-byte row per kv-head that the last
+            // prefetch of every wave shares, so it stays cached), not at this tile again, whose bf16 rows were
+            // streamed past the caches and would be fetched a second time (32 MB per call at config 3)
             const TileRows<NVI, TPI, LPT, ALIGNED> cur_now = cur;
             TileRows<NVI, TPI, LPT, ALIGNED> nxt;
             if (j + 1 >= my_total) {
                 nxt = cur_now;
+                nxt.krow = (long long)kvh * D;
+                if constexpr (ALIGNED) {
+                    nxt.vbase = (long long)kvh * D + (lane % LPT) * 8;
+                    nxt.vstride = 0;
+                } else {
+#pragma unroll
+                    for (int vi = 0; vi < NVI; ++vi) nxt.vr[vi] = (long long)kvh * D + (lane % LPT) * 8;
+                }
             } else {
                 if (j + 1 - j0 == 64) {
                     j0 += 64;
