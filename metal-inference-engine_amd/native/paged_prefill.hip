@@ -65,6 +65,19 @@ struct PrefillArgs {
     uint32_t bs_recip;          // floor((2^32 - 1) / bs): mulhi(pos, bs_recip) is pos / bs or one less
 };
 
+// Workgroup -> (work entry, head chunk, kv-head). The grid is one-dimensional with the kv-head fastest, then the head
+// chunk, then the entry: the hardware dispatcher starts workgroups in index order, so every kv-head and chunk of an
+// entry starts before the next entry and the list's longest-first order holds across kv-heads. (With the kv-head
+// as a second grid dimension, the second kv-head's longest entries were dispatched only after every entry of the
+// first kv-head.)
+struct WorkSlot {
+    int entry, kvh, chunk;
+};
+__device__ __forceinline__ WorkSlot work_slot(int Hkv, int chunks) {
+    const int i = blockIdx.x;
+    return WorkSlot{i / (Hkv * chunks), i % Hkv, (i / Hkv) % chunks};
+}
+
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
@@ -181,8 +194,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.G;
     const bool producer = wave >= G;
-    const int kvh = blockIdx.y;
-    const int32_t* we = a.work + (long long)kWorkInts * blockIdx.x;
+    const WorkSlot ws = work_slot(a.Hkv, 1);
+    const int kvh = ws.kvh;
+    const int32_t* we = a.work + (long long)kWorkInts * ws.entry;
     const int item = we[0];
     const int seg = item >> 16, qblk = item & 0xffff;
     const int row0 = a.cu[seg] + qblk * kBQ;
@@ -559,7 +573,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // fp32 q or pool and for exact requests (any group size, D = 64 / 128 / 256). The reference computes
 // attention in fp32 on widened inputs (src/ops.py:84-87, 91-103), so the products here are fp32 products:
 // v_mfma_f32_16x16x4_f32, bf16 pool rows widened exactly when staged, the probabilities kept in fp32.
-// blockDim = 512: wave w takes query head (blockIdx.z * 4 + w % 4) of the group (none past the group's end: that
+// blockDim = 512: wave w takes query head (chunk * 4 + w % 4) of the group (none past the group's end: that
 // wave only helps stage) and queries 16 (w / 4) .. + 15 of the work item's 32. All 8 waves stage each tile of 32
 // keys into a 2-stage LDS ring, requested a whole tile ahead: K row-major ([32 keys][D + 4 floats]) and V transposed
 // ([D dims][32 + 4 floats]), both fp32. A staging unit is one 16-byte piece of 4 consecutive key rows (4 loads);
@@ -713,10 +727,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     int* tab = reinterpret_cast<int*>(smem + 2 * STAGE * sizeof(float));       // [kTabCache] block ids
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int kvh = blockIdx.y;
-    const int gh = blockIdx.z * kF32Heads + (wave & 3);      // head within the group
+    const WorkSlot ws = work_slot(a.Hkv, (a.G + kF32Heads - 1) / kF32Heads);
+    const int kvh = ws.kvh;
+    const int gh = ws.chunk * kF32Heads + (wave & 3);        // head within the group
     const int half = wave >> 2;
-    const int32_t* we = a.work + (long long)kWorkInts * blockIdx.x;
+    const int32_t* we = a.work + (long long)kWorkInts * ws.entry;
     const int item = we[0];
     const int seg = item >> 16, qblk = item & 0xffff;
     const int row0 = a.cu[seg] + qblk * kBQ;
@@ -955,7 +970,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // ---- 4. attention on bf16 operands, 16 queries per consumer wave, for bf16 q and pool (v_mfma_f32_16x16x32_bf16).
-// blockDim = 768, warp-specialised: waves 0 .. 7 are consumers (wave w: query head blockIdx.z * 4 + w % 4 of the
+// blockDim = 768, warp-specialised: waves 0 .. 7 are consumers (wave w: query head chunk * 4 + w % 4 of the
 // group, queries 16 (w / 4) .. + 15 of the work item: the fp32-operand kernel's split of the work, its work list,
 // masks, split records and epilogue), waves 8 .. 11 are producers. Three waves per SIMD: two consumers, so one's
 // softmax and LDS waits hide behind the other's MFMAs, and a producer, whose loads and LDS writes overlap both.
@@ -1001,10 +1016,11 @@ __global__ __launch_bounds__(kB16Threads) void prefill_attention_b16(PrefillArgs
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool producer = wave >= 8;
-    const int kvh = blockIdx.y;
-    const int gh = blockIdx.z * kF32Heads + (wave & 3);      // head within the group (consumers)
+    const WorkSlot ws = work_slot(a.Hkv, (a.G + kF32Heads - 1) / kF32Heads);
+    const int kvh = ws.kvh;
+    const int gh = ws.chunk * kF32Heads + (wave & 3);        // head within the group (consumers)
     const int half = (wave >> 2) & 1;
-    const int32_t* we = a.work + (long long)kWorkInts * blockIdx.x;
+    const int32_t* we = a.work + (long long)kWorkInts * ws.entry;
     const int item = we[0];
     const int seg = item >> 16, qblk = item & 0xffff;
     const int row0 = a.cu[seg] + qblk * kBQ;
@@ -1269,6 +1285,9 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
                     block_size);
     if (Hkv < 1 || Hq < Hkv || Hq % Hkv)
         return fail(RK_ERR_ARG, "rk_paged_prefill: %d query heads over %d kv heads", Hq, Hkv);
+    if ((unsigned long long)n_work * Hq * 768 >= (1ull << 32))   // workgroups (entry, chunk, kv-head) x threads
+        return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: %d work entries x %d query heads exceed one launch", n_work,
+                    Hq);
     if (D != 64 && D != 128 && D != 256)
         return fail(RK_ERR_UNSUPPORTED, "rk_paged_prefill: head_dim %d not in {64, 128, 256}", D);
     if ((unsigned long long)max_nb * block_size >= (1ull << 31))
@@ -1311,7 +1330,7 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
         if (D == 256) fn = tab_lds ? prefill_attention<256, true> : prefill_attention<256, false>;
         else fn = tab_lds ? prefill_attention<128, true> : prefill_attention<128, false>;
         if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
-        hipLaunchKernelGGL(fn, dim3(n_work, Hkv), dim3(2 * 64 * a.G), lds, s, a);
+        hipLaunchKernelGGL(fn, dim3(n_work * Hkv), dim3(2 * 64 * a.G), lds, s, a);
         return check_launch("prefill_attention");
     }
     if (bf16_ops) {
@@ -1321,7 +1340,7 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
         else if (D == 128) fn = tab_lds ? prefill_attention_b16<128, true> : prefill_attention_b16<128, false>;
         else fn = tab_lds ? prefill_attention_b16<64, true> : prefill_attention_b16<64, false>;
         if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
-        hipLaunchKernelGGL(fn, dim3(n_work, Hkv, chunks), dim3(kB16Threads), lds, s, a);
+        hipLaunchKernelGGL(fn, dim3(n_work * Hkv * chunks), dim3(kB16Threads), lds, s, a);
         return check_launch("prefill_attention_b16");
     }
     const size_t lds = (size_t)2 * (kBKP * (D + kF32Pad) + D * (kBKP + kF32Pad)) * sizeof(float) +
@@ -1335,7 +1354,7 @@ int rk_paged_prefill(float* out, const void* q, int q_dtype, const void* k_new, 
     else RK_F32_PICK(64);
 #undef RK_F32_PICK
     if (int rc2 = allow_dynamic_lds((const void*)fn, lds)) return rc2;
-    hipLaunchKernelGGL(fn, dim3(n_work, Hkv, chunks), dim3(512), lds, s, a);
+    hipLaunchKernelGGL(fn, dim3(n_work * Hkv * chunks), dim3(512), lds, s, a);
     return check_launch("prefill_attention_f32");
 }
 
