@@ -60,15 +60,27 @@ __device__ __forceinline__ void store_pieces4(uint16_t* dst, const float (&x)[4]
     for (int pi = 0; pi < kTP; ++pi) *reinterpret_cast<u32x2*>(dst + pi * kPieceElems) = pc[pi];
 }
 
+// The prep's LDS holds only the 10 lower-triangular 16 x 16 blocks of A0 and of T, each padded to 16 x 17 floats,
+// block (w, b) (b <= w) at index w (w + 1) / 2 + b; the chunk's K rows share the same bytes until the Gram products
+// are in registers. 21.8 KB per workgroup for bf16 inputs (38.4 KB with full 64 x 65 arrays and separate K rows), so
+// 7 workgroups fit a CU instead of 4: the prep's time is the latency of its dependent steps, hidden by occupancy.
+constexpr int kBlkF = 16 * 17;                             // floats of one padded block
+constexpr int kTriBlocks = 10;
+__device__ __forceinline__ int tri_blk(int w, int b) { return w * (w + 1) / 2 + b; }
+
 template <typename In>
 __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     using St = PrepStage<In>;
-    __shared__ float sA[kC][kC + 1];                       // A0 = -beta_i (K K^T)_ij D_ij below the diagonal
-    __shared__ __align__(16) char sKT[kC * St::kRow * sizeof(In) > kC * (kC + 1) * 4
-                                          ? kC * St::kRow * sizeof(In) : kC * (kC + 1) * 4];
-    __shared__ float sTmp[4][16][17];                      // per-wave 16 x 16 scratch
-    In* sK = reinterpret_cast<In*>(sKT);                   // K rows of the chunk, until the Gram products are done
-    float (*sT)[kC + 1] = reinterpret_cast<float (*)[kC + 1]>(sKT);   // then T
+    constexpr int kKBytes = kC * St::kRow * sizeof(In), kTriBytes = 2 * kTriBlocks * kBlkF * 4;
+    __shared__ __align__(16) char smem[kKBytes > kTriBytes ? kKBytes : kTriBytes];
+    In* sK = reinterpret_cast<In*>(smem);                  // K rows of the chunk, until the Gram products are done
+    float* const sAb = reinterpret_cast<float*>(smem);     // then A0 = -beta_i (K K^T)_ij D_ij below the diagonal
+    float* const sTb = sAb + kTriBlocks * kBlkF;           // and T
+    // element (i, m) of block (w, b): A0 / T rows 16 w + i, columns 16 b + m
+    auto sA = [&](int w, int b, int i, int m) -> float& { return sAb[tri_blk(w, b) * kBlkF + 17 * i + m]; };
+    auto sT = [&](int w, int b, int i, int m) -> float& { return sTb[tri_blk(w, b) * kBlkF + 17 * i + m]; };
+    // per-wave 16 x 16 scratch of the off-diagonal products: A0's diagonal block w, dead once T's is formed
+    auto sTmp = [&](int w, int i, int m) -> float& { return sAb[tri_blk(w, w) * kBlkF + 17 * i + m]; };
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, q = lane >> 4, r = lane & 15;
     const int gc = blockIdx.x, h = blockIdx.y, H = p.H;
@@ -127,7 +139,10 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
     uint16_t* ws16 = reinterpret_cast<uint16_t*>(rec);
     const float Gt = __shfl(G, 16 * w + r), bt = __shfl(bl, 16 * w + r);
     const int t = 16 * w + r;
-    for (int b = 0; b < (kLane ? w + 1 : 2 * ((w >> 1) + 1)); ++b) {
+    float av[4][4];                        // A0 entries of tiles b <= w, kept until every wave is done with sK
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        if (b >= (kLane ? w + 1 : 2 * ((w >> 1) + 1))) break;      // uniform per wave
         float pv[4] = {0.f, 0.f, 0.f, 0.f};
         if (b <= w) {
             f32x4 kk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
@@ -157,13 +172,19 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
                 // masked before exp; exp(x) as 2^(x log2 e) on v_exp_f32: within ~1e-6 relative for the
                 // |x| < 20 that carry weight (the rounding of x log2 e is |x| 2^-24)
                 const float d = tp <= t ? fast_exp2((Gt - Gp) * kLog2e) : 0.f;
-                sA[t][tp] = tp < t ? -(bt * kk[i]) * d : 0.f;
+                av[b][i] = tp < t ? -(bt * kk[i]) * d : 0.f;
                 pv[i] = pq[i] * d;
             }
         }
         if constexpr (!kLane) store_pieces4(ws16 + kPOff + rt_base(w) + r * rt_width(w) + 16 * b + 4 * q, pv);
     }
-    lds_barrier();                         // sK is dead from here: its space holds T
+    lds_barrier();                         // sK is dead from here: its bytes hold A0 and T
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+        if (b <= w)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sA(w, b, r, 4 * q + i) = av[b][i];
+    lds_barrier();
 
     // diagonal block w of T = (I - A0)^-1: lane r keeps column r, rows by forward substitution
     {
@@ -172,12 +193,12 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
         for (int i = 0; i < 16; ++i) {
             float a = i == r ? 1.f : 0.f;
 #pragma unroll
-            for (int m = 0; m < i; ++m) a = fmaf(sA[16 * w + i][16 * w + m], x[m], a);
+            for (int m = 0; m < i; ++m) a = fmaf(sA(w, w, i, m), x[m], a);
             x[i] = a;
         }
         if (q == 0)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sT[16 * w + i][16 * w + r] = x[i];
+            for (int i = 0; i < 16; ++i) sT(w, w, i, r) = x[i];
     }
     lds_barrier();
 
@@ -189,16 +210,16 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
             for (int kb = j; kb < w; ++kb)
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
-                    tt = mfma_f32(sA[16 * w + r][16 * kb + 4 * ks + q], sT[16 * kb + 4 * ks + q][16 * j + r], tt);
+                    tt = mfma_f32(sA(w, kb, r, 4 * ks + q), sT(kb, j, 4 * ks + q, r), tt);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sTmp[w][4 * q + i][r] = tt[i];
+            for (int i = 0; i < 4; ++i) sTmp(w, 4 * q + i, r) = tt[i];
             wave_lds_sync();
             f32x4 u = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
-                u = mfma_f32(sT[16 * w + r][16 * w + 4 * ks + q], sTmp[w][4 * ks + q][r], u);
+                u = mfma_f32(sT(w, w, r, 4 * ks + q), sTmp(w, 4 * ks + q, r), u);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sT[16 * w + 4 * q + i][16 * j + r] = u[i];
+            for (int i = 0; i < 4; ++i) sT(w, j, 4 * q + i, r) = u[i];
         }
         lds_barrier();
     }
@@ -211,7 +232,11 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
             if (col <= row) {
                 f32x4 x;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) x[e] = col + e <= row ? sT[row][col + e] : 0.f;
+                for (int e = 0; e < 4; ++e) {
+                    const int c = min(col + e, row);            // entries above the diagonal are not held
+                    const float v = sT(row >> 4, c >> 4, row & 15, c & 15);
+                    x[e] = col + e <= row ? v : 0.f;
+                }
                 *reinterpret_cast<f32x4*>(rec + tri_base(row) + col) = x;
             }
         }
@@ -224,7 +249,11 @@ __global__ __launch_bounds__(256) void delta_chunk_prep(DeltaArgs p) {
         const int row = 16 * a + rel / rt_width(a), col = rel % rt_width(a);
         float x[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = col + e <= row ? sT[row][col + e] : 0.f;
+        for (int e = 0; e < 4; ++e) {
+            const int c = min(col + e, row);
+            const float v = sT(row >> 4, c >> 4, row & 15, c & 15);
+            x[e] = col + e <= row ? v : 0.f;
+        }
         store_pieces4(ws16 + kTOff + off, x);
     }
     if (w == 0) {
