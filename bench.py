@@ -571,7 +571,8 @@ def bench_chunked_delta(args, backend):
     flops = case.flops()
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = case.hbm_bytes() / (ms * 1e-3) / 1e9
-    log(f"[bench] c4: graph replays {GRAPH_WALL_MS[-1] * 1e3:.1f} us per call by the host clock (both replays)")
+    if GRAPH_WALL_MS:                                # (graph_time times eager launches under --no-graph)
+        log(f"[bench] c4: graph replays {GRAPH_WALL_MS[-1] * 1e3:.1f} us per call by the host clock (both replays)")
     log(f"[bench] c4: {ms * 1e3:.1f} us per packed call (eager {eager * 1e3:.1f} us), {tflops:.1f} TFLOP/s "
         f"({tflops / 25:.1f}% of bf16 MFMA peak), {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
     cpu = None
