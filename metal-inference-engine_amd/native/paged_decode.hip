@@ -54,15 +54,15 @@ constexpr int kMaxBatch = 1024;
 constexpr int kMaxKvHeads = 4;     // one wave per kv head in a split workgroup of at most 256 threads
 constexpr int kTile = 16;
 constexpr int kStash = 2;   // segments per split workgroup whose records wait in LDS until the range is done
-// Waves of a split workgroup: 8 (two per SIMD, <= 256 VGPRs each) for up to 4 query heads per kv-head, 4 (one per
-// SIMD, up to 512 registers) for the register-heavier 8-head instances and for small grids (at most kSmallTiles
-// tiles at the tile count's upper bound: a few short sequences, where each wave streams about one tile and the
-// latency of its loads is the time; one wave per SIMD then holds a whole fp32 tile in flight instead of half of
-// one, a round trip less per half). It depends on the shape only, never on the pool dtype, so that a bf16 pool and
-// an fp32 pool holding the same (widened) values are cut and combined identically and give bit-equal outputs (the
-// 8-wave fp32-pool instance at D = 256 streams half tiles to fit).
-constexpr long long kSmallTiles = 512;
-constexpr int waves_per_group(int GP, long long upper) { return GP == 4 && upper > kSmallTiles ? 8 : 4; }
+// Waves of a split workgroup: 4, one per SIMD, with up to 512 registers each, so that every instance holds the
+// whole next tile in flight, the values included, while it computes this one. With the non-temporal K/V loads this
+// beats 8-wave workgroups (two waves per SIMD, 256 registers, at most half of the next tile's values early) at
+// every batch size measured: config 3's split kernel 88.5 -> 86.5 us, batch 128 169.6 -> 165.7 us, batch 256
+// 351.5 -> 344.9 us, batch 16 unchanged (with temporal loads the 8-wave form had been faster, 101 vs 104 us at
+// config 3). Two 4-wave workgroups per CU measured slower again (87.6-88.1 us at config 3). The count is the same
+// for both pool dtypes, so a bf16 pool and an fp32 pool holding the same (widened) values are cut and combined
+// identically and give bit-equal outputs.
+constexpr int kSplitWaves = 4;
 // the tile count's upper bound: every sequence at its table's full width
 inline long long tile_upper(int B, int block_size, int max_nb) {
     return (long long)B * (((long long)max_nb * block_size + kTile - 1) / kTile);
@@ -378,7 +378,7 @@ __device__ __forceinline__ TileEntry tile_entry(const DecodeArgs& a, const Group
     return x;
 }
 
-// One workgroup = NG groups of Hkv waves (NG = WPG / Hkv, WPG = waves_per_group()); wave g * Hkv + k serves
+// One workgroup = NG groups of Hkv waves (NG = WPG / Hkv, WPG = kSplitWaves); wave g * Hkv + k serves
 // kv-head k for group g. The Hkv waves of a group walk the same tiles, so both halves of every interleaved pool row ([bs][Hkv][D]) are
 // fetched together. Within each sequence segment of the workgroup's range, group g takes the segment's tiles
 // g, g + NG, g + 2 NG, ...; at the segment's end the groups' (m, l, acc) states are combined through LDS and one
@@ -394,12 +394,8 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
     constexpr int KS = LD::KS;
     constexpr int HB = GP / 4;               // head blocks of 4 in the score layout
     constexpr int QV = (GP * D / 4 + 63) / 64;   // float4 query pieces per lane when a sequence starts
-    // register sets for keys (KB of the NIT k-steps) and values (VB of the NVI steps): a whole tile, the next one
-    // in flight; for fp32 pools at D = 256 half a tile (the sets are refilled with the tile's second half, then
-    // the next tile's first half), which keeps the workgroup at two waves per SIMD without spilling. The
-    // arithmetic and its order do not change.
-    constexpr bool kHalf = sizeof(T) == 4 && D == 256 && WPG == 8;
-    constexpr int KB = kHalf ? NIT / 2 : NIT, VB = kHalf ? NVI / 2 : NVI;
+    // register sets for keys (KB = NIT k-steps) and values (VB = NVI steps): a whole tile, the next one in flight
+    constexpr int KB = NIT, VB = NVI;
     constexpr int REC = GP * D + 2 * GP;     // floats of one (acc, m, l) record
     static_assert(REC * 4 <= NT * NIT * 64 * 16, "a combine record must fit in the wave's query operand area");
 
@@ -431,11 +427,12 @@ __global__ __launch_bounds__(64 * WPG) void paged_decode_split(DecodeArgs a) {
         for (int i = 0; i < NT * NIT; ++i) qop[i * 64 + lane] = u32x4{0u, 0u, 0u, 0u};
     };
     typename LD::Vec kv[KB], vv[VB];
-    // With whole-tile sets, the next tile's first VE value steps are requested into vn right after its keys, before
-    // this tile's softmax, and the rest as this tile's values are used: more bytes in flight per wave through the
-    // scores and the softmax (half a tile's values is what the 256 registers of the 8-wave instance leave room for;
-    // the unaligned-table instance, one register short, keeps the later requests)
-    constexpr int VE = (kHalf || !ALIGNED) ? 0 : VB / 2;
+    // The next tile's values (bf16 pools; half of them for fp32 pools) are requested into vn right after its keys,
+    // before this tile's softmax, instead of one step at a time as this tile's values are used: more bytes in
+    // flight per wave through the scores and the softmax (config 3: 86.8 -> 86.5 us; all of an fp32 tile's values
+    // that early made config 1 slower, 11.1 -> 11.4 us; with the unaligned tables' per-step row offsets the
+    // instance keeps the later requests)
+    constexpr int VE = !ALIGNED ? 0 : (sizeof(T) == 2 ? VB : VB / 2);
     typename LD::Vec vn[VE > 0 ? VE : 1];
     TileRows<NVI, TPI, LPT, ALIGNED> cur;
     // issue order K then V, here and in the loop, so that waiting for a tile's keys never waits for its values
@@ -1030,30 +1027,26 @@ typedef void (*SplitFn)(DecodeArgs);
 typedef void (*MergeFn)(DecodeArgs);
 
 template <typename T, bool ALIGNED>
-SplitFn pick_split(int D, int GP, int wpg) {
-    if (GP == 4 && wpg == 8) {
-        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED, 8>;
-        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED, 8>;
-        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED, 8>;
-    } else if (GP == 4) {
-        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED, 4>;
-        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED, 4>;
-        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED, 4>;
+SplitFn pick_split(int D, int GP) {
+    constexpr int W = kSplitWaves;
+    if (GP == 4) {
+        if (D == 64) return paged_decode_split<T, 64, 4, ALIGNED, W>;
+        if (D == 128) return paged_decode_split<T, 128, 4, ALIGNED, W>;
+        if (D == 256) return paged_decode_split<T, 256, 4, ALIGNED, W>;
     } else {
-        if (D == 64) return paged_decode_split<T, 64, 8, ALIGNED, 4>;
-        if (D == 128) return paged_decode_split<T, 128, 8, ALIGNED, 4>;
-        if (D == 256) return paged_decode_split<T, 256, 8, ALIGNED, 4>;
+        if (D == 64) return paged_decode_split<T, 64, 8, ALIGNED, W>;
+        if (D == 128) return paged_decode_split<T, 128, 8, ALIGNED, W>;
+        if (D == 256) return paged_decode_split<T, 256, 8, ALIGNED, W>;
     }
     return nullptr;
 }
 
-SplitFn pick_split(int kv_dtype, bool aligned, int D, int GP, int wpg) {
-    if (kv_dtype == RK_BF16)
-        return aligned ? pick_split<uint16_t, true>(D, GP, wpg) : pick_split<uint16_t, false>(D, GP, wpg);
-    return aligned ? pick_split<float, true>(D, GP, wpg) : pick_split<float, false>(D, GP, wpg);
+SplitFn pick_split(int kv_dtype, bool aligned, int D, int GP) {
+    if (kv_dtype == RK_BF16) return aligned ? pick_split<uint16_t, true>(D, GP) : pick_split<uint16_t, false>(D, GP);
+    return aligned ? pick_split<float, true>(D, GP) : pick_split<float, false>(D, GP);
 }
 
-int groups_of(int Hkv, int wpg) { return wpg / Hkv > 0 ? wpg / Hkv : 1; }
+int groups_of(int Hkv) { return kSplitWaves / Hkv > 0 ? kSplitWaves / Hkv : 1; }
 
 int split_lds_bytes(int B, int Hkv, int D, int GP, int NG) {
     int per_wave = 0;
@@ -1076,16 +1069,13 @@ MergeFn pick_merge(int D, int GP) {
 }
 
 // Workgroups of the split phase (NG groups of Hkv waves): enough for about one tile per group at the tile count's
-// upper bound, capped at the waves per compute unit that stay resident all at once: 8 for 8-wave workgroups (two
-// per SIMD), 4 for 4-wave ones (their registers allow one per SIMD).
-int split_groups(int B, int Hkv, int block_size, int max_nb, int GP) {
+// upper bound, capped at one workgroup per compute unit (one wave per SIMD), all resident at once.
+int split_groups(int B, int Hkv, int block_size, int max_nb) {
     const long long upper = tile_upper(B, block_size, max_nb);
-    const int wpg = waves_per_group(GP, upper);
-    const int per_cu = wpg == 8 ? 8 : 4;
     int cus = device_cus();
     if (cus <= 0) cus = 256;
-    const int ng = groups_of(Hkv, wpg);
-    const long long cap = (long long)cus * per_cu / (ng * Hkv);
+    const int ng = groups_of(Hkv);
+    const long long cap = (long long)cus * kSplitWaves / (ng * Hkv);
     const long long want = (upper + ng - 1) / ng;
     long long nw = want < cap ? want : cap;
     return (int)(nw < 1 ? 1 : nw);
@@ -1122,14 +1112,13 @@ extern "C" {
 size_t rk_paged_decode_workspace_bytes(int B, int Hq, int Hkv, int D, int block_size, int max_nb) {
     if (B < 1 || Hkv < 1 || Hq < Hkv || block_size < 1 || max_nb < 1) return 0;
     const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
-    return workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb, GP));
+    return workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb));
 }
 
 size_t rk_paged_decode_plan_ints(int B, int Hq, int Hkv, int D, int block_size, int max_nb) {
     if (B < 1 || Hkv < 1 || Hq < Hkv || block_size < 1 || max_nb < 1) return 0;
     const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
-    const int wpg = waves_per_group(GP, tile_upper(B, block_size, max_nb));
-    return plan_ints(B, split_groups(B, Hkv, block_size, max_nb, GP), groups_of(Hkv, wpg));
+    return plan_ints(B, split_groups(B, Hkv, block_size, max_nb), groups_of(Hkv));
 }
 
 int rk_paged_decode_plan(int32_t* plan, size_t plan_ints_, const int32_t* tables, const int32_t* lens, int B, int Hq,
@@ -1148,8 +1137,8 @@ int rk_paged_decode_plan(int32_t* plan, size_t plan_ints_, const int32_t* tables
     a.lens = lens;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = Hq / Hkv; a.bs = block_size; a.max_nb = max_nb;
     a.num_blocks = num_blocks; a.window = window;
-    a.NW = split_groups(B, Hkv, block_size, max_nb, GP);
-    a.NG = groups_of(Hkv, waves_per_group(GP, tile_upper(B, block_size, max_nb)));
+    a.NW = split_groups(B, Hkv, block_size, max_nb);
+    a.NG = groups_of(Hkv);
     auto fn = block_size % kTile == 0 ? paged_decode_plan<true> : paged_decode_plan<false>;
     hipLaunchKernelGGL(fn, dim3(a.NW), dim3(64 * a.NG), seq_lds_bytes(B), static_cast<hipStream_t>(stream), a, plan);
     return check_launch("paged_decode_plan");
@@ -1175,7 +1164,7 @@ int decode_launch(int phase, float* out, const float* q, const void* k_pool, con
                     rk_paged_decode_plan_ints(B, Hq, Hkv, D, block_size, max_nb));
     const int G = Hq / Hkv;
     const int GP = G <= 4 ? 4 : 8;
-    const int NW = split_groups(B, Hkv, block_size, max_nb, GP);
+    const int NW = split_groups(B, Hkv, block_size, max_nb);
     const size_t need = workspace_bytes(B, Hkv, D, GP, NW);
     if (!workspace || workspace_bytes_ < need)
         return fail(RK_ERR_WORKSPACE, "rk_paged_decode: workspace %zu bytes < %zu needed", workspace_bytes_, need);
@@ -1192,12 +1181,11 @@ int decode_launch(int phase, float* out, const float* q, const void* k_pool, con
     a.gate = gate;
     a.gate_ld = gate_ld;
     a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.G = G; a.bs = block_size; a.max_nb = max_nb;
-    const int wpg = waves_per_group(GP, tile_upper(B, block_size, max_nb));
-    a.num_blocks = num_blocks; a.window = window; a.NW = NW; a.NG = groups_of(Hkv, wpg);
+    a.num_blocks = num_blocks; a.window = window; a.NW = NW; a.NG = groups_of(Hkv);
     a.qscale = kLog2e / sqrtf((float)D);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (phase == 0) {
-        SplitFn fn = pick_split(kv_dtype, block_size % kTile == 0, D, GP, wpg);
+        SplitFn fn = pick_split(kv_dtype, block_size % kTile == 0, D, GP);
         const int lds = split_lds_bytes(B, Hkv, D, GP, a.NG);
         rc = allow_dynamic_lds(reinterpret_cast<const void*>(fn), lds);
         if (rc) return rc;
@@ -1245,7 +1233,7 @@ int rk_paged_decode_noalloc(float* out, const float* q, const void* k_pool, cons
                       num_blocks, window);
     if (rc) return rc;
     const int GP = (Hq / Hkv) <= 4 ? 4 : 8;
-    const size_t need = workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb, GP));
+    const size_t need = workspace_bytes(B, Hkv, D, GP, split_groups(B, Hkv, block_size, max_nb));
     if (need > kScratchBytes)
         return fail(RK_ERR_WORKSPACE, "rk_paged_decode_noalloc: %zu bytes of partials for batch %d x %d kv-heads x "
                     "head_dim %d exceed its fixed %zu-byte scratch (use rk_paged_decode with a workspace)", need, B,
