@@ -6,9 +6,9 @@
 // (src/ops.py:120-124). The conv tail and S are updated in place at [seq_index[i], slot] (src/state.py:428-429;
 // the Metal pair conv_step + gdn_decode, src/kernels/deltanet.metal:9-92, indexes them the same way).
 //
-// One workgroup of 512 threads per (sequence, head). The head's 128 x 128 fp32 state is loaded once into registers
-// (thread = 8 rows x 4 columns, a row of 32 threads reads 512 contiguous bytes), decayed, rank-1 updated and written
-// back once: 2 x 64 KiB of HBM traffic per head, the algorithmic minimum. The S loads are issued first, so the
+// One workgroup of 256 threads per (sequence, head) (6.62 -> 6.33 us per config-2 step against 512 threads, A/B in
+// one process). The head's 128 x 128 fp32 state is loaded once into registers (thread = 16 rows x 4 columns, a row
+// of 32 threads reads 512 contiguous bytes), decayed, rank-1 updated and written back once: 2 x 64 KiB of HBM traffic per head, the algorithmic minimum. The S loads are issued first, so the
 // convolution of the head's 384 channels, the l2 norms and the gate parameters are computed while they are in
 // flight. Elementwise steps keep the reference's operation order (products rounded before sums, no contraction into
 // FMA) wherever the reference rounds them separately; only the lengths-128 sums are reordered (tree instead of
@@ -19,7 +19,8 @@
 namespace rk {
 namespace {
 
-constexpr int kDK = 128, kDV = 128, kTaps = 4, kThreads = 512;
+constexpr int kDK = 128, kDV = 128, kTaps = 4, kThreads = 256;
+constexpr int kRowGroups = kThreads / 32, kRowsPer = kDK / kRowGroups;   // 8 row groups of 16 state rows
 
 struct StepArgs {
     float* out;
@@ -42,20 +43,24 @@ struct StepArgs {
 __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     __shared__ float us[3 * kDK];        // conv + SiLU output of this head: q | k | v
     __shared__ float qn[kDK], kn[kDK], dl[kDV];
-    __shared__ float red[16][kDV];       // partial sums over row groups
-    __shared__ float wsum[16];
+    __shared__ float red[kRowGroups][kDV];   // partial sums over row groups
+    __shared__ float wsum[8];
 
     const int t = threadIdx.x;
     const int bi = blockIdx.x / p.H, h = blockIdx.x % p.H;
     const int H = p.H, C = p.C;
 
     // ---- 0. every small input first, the state after them: one in-order counter serves loads and stores, so a
-    // load issued after the state stores could only be waited for together with them
-    const int part = t / kDK, j = t % kDK;
-    const int c = part == 0 ? h * kDK + j : (part == 1 ? H * kDK + h * kDK + j : 2 * H * kDK + h * kDV + (j & (kDV - 1)));
-    const float x = t < 3 * kDK ? p.qkv[(long long)bi * p.qkv_ld + c] : 0.0f;
-    const float4 w = t < 3 * kDK ? *reinterpret_cast<const float4*>(p.conv_w + (long long)c * kTaps)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    // load issued after the state stores could only be waited for together with them. Thread t owns channel t of
+    // q | k (t < 128: q, else k) and, for t < 128, v channel t as well.
+    const int ca = t < kDK ? h * kDK + t : H * kDK + h * kDK + (t - kDK);
+    const int cb = 2 * H * kDK + h * kDV + (t & (kDV - 1));
+    const bool has_v = t < kDV;
+    const float xa = p.qkv[(long long)bi * p.qkv_ld + ca];
+    const float xb = has_v ? p.qkv[(long long)bi * p.qkv_ld + cb] : 0.0f;
+    const float4 wa = *reinterpret_cast<const float4*>(p.conv_w + (long long)ca * kTaps);
+    const float4 wb = has_v ? *reinterpret_cast<const float4*>(p.conv_w + (long long)cb * kTaps)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
     const float b_in = p.b[(long long)bi * p.ba_ld + h], a_in = p.a[(long long)bi * p.ba_ld + h];
     const float dtb = p.dt_bias[h], alog = p.A_log[h];
     const float zj = t < kDV ? p.z[(long long)bi * p.z_ld + h * kDV + t] : 0.0f;
@@ -63,39 +68,48 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     const long long seq = p.seq[bi];
     float* Sh = p.S + (((seq * p.n_linear + p.slot) * H + h) * kDK) * kDV;
     float* tail = p.conv + (seq * p.n_linear + p.slot) * (long long)(kTaps - 1) * C;
-    float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
-    if (t < 3 * kDK) {
-        h0 = tail[c];
-        h1 = tail[C + c];
-        h2 = tail[2 * C + c];
+    const float a0 = tail[ca], a1 = tail[C + ca], a2 = tail[2 * C + ca];
+    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;
+    if (has_v) {
+        b0 = tail[cb];
+        b1 = tail[C + cb];
+        b2 = tail[2 * C + cb];
     }
 
-    // ---- 1. state tile of this thread
-    const int cg = t & 31, rg = t >> 5;       // columns 4*cg .. 4*cg+3, rows 8*rg .. 8*rg+7
-    float4 s[8];
+    // ---- 1. state tile of this thread: columns 4 cg .. +3, rows kRowsPer rg .. +kRowsPer-1 (a row group of 32
+    // threads reads 512 contiguous bytes per row). Non-temporal: the head's state is read once and written once per
+    // step (streamed past the caches, same bits)
+    const int cg = t & 31, rg = t >> 5;
+    float4 s[kRowsPer];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        // non-temporal: the head's state is read once and written once per step (streamed past the caches; 7.9 ->
-        // 6.6 us per config-2 step together with the stores below, same bits)
-        const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(Sh + (8 * rg + r) * kDV + 4 * cg));
+    for (int r = 0; r < kRowsPer; ++r) {
+        const f32x4 v = __builtin_nontemporal_load(
+            reinterpret_cast<const f32x4*>(Sh + (kRowsPer * rg + r) * kDV + 4 * cg));
         s[r] = make_float4(v[0], v[1], v[2], v[3]);
     }
 
     // ---- 2. causal conv (taps 0..2 = tail, tap 3 = current token) + SiLU for the head's 384 channels
-    if (t < 3 * kDK) {
+    auto conv = [](float h0, float h1, float h2, float x, float4 w) {
         float y = __fmul_rn(h0, w.x);
         y = __fadd_rn(y, __fmul_rn(h1, w.y));
         y = __fadd_rn(y, __fmul_rn(h2, w.z));
         y = __fadd_rn(y, __fmul_rn(x, w.w));
-        us[t] = y / (1.0f + expf(-y));
-        tail[c] = h1;
-        tail[C + c] = h2;
-        tail[2 * C + c] = x;
+        return y / (1.0f + expf(-y));
+    };
+    us[t] = conv(a0, a1, a2, xa, wa);
+    tail[ca] = a1;
+    tail[C + ca] = a2;
+    tail[2 * C + ca] = xa;
+    if (has_v) {
+        us[2 * kDK + t] = conv(b0, b1, b2, xb, wb);
+        tail[cb] = b1;
+        tail[C + cb] = b2;
+        tail[2 * C + cb] = xb;
     }
     __syncthreads();
 
     // ---- 3. l2 norms of q and k (sum of squares + 1e-6), q scale 1/sqrt(dk); gate parameters
-    if (t < 2 * kDK) {
+    {
         const float x = us[t];
         const float sq = wave_sum(__fmul_rn(x, x));
         if ((t & 63) == 0) wsum[t >> 6] = sq;
@@ -117,8 +131,8 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     // ---- 4. decay, kv = k^T S (decayed), delta = beta * (v - kv)
     float kvp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        const float kr = kn[8 * rg + r];
+    for (int r = 0; r < kRowsPer; ++r) {
+        const float kr = kn[kRowsPer * rg + r];
         s[r].x = __fmul_rn(s[r].x, decay);
         s[r].y = __fmul_rn(s[r].y, decay);
         s[r].z = __fmul_rn(s[r].z, decay);
@@ -133,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     if (t < kDV) {
         float kv = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) kv += red[r][t];
+        for (int r = 0; r < kRowGroups; ++r) kv += red[r][t];
         dl[t] = __fmul_rn(us[2 * kDK + t] - kv, beta);
     }
     __syncthreads();
@@ -142,14 +156,14 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     const float4 d4 = *reinterpret_cast<const float4*>(&dl[4 * cg]);
     float op[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        const float kr = kn[8 * rg + r], qr = qn[8 * rg + r];
+    for (int r = 0; r < kRowsPer; ++r) {
+        const float kr = kn[kRowsPer * rg + r], qr = qn[kRowsPer * rg + r];
         s[r].x = __fadd_rn(s[r].x, __fmul_rn(kr, d4.x));
         s[r].y = __fadd_rn(s[r].y, __fmul_rn(kr, d4.y));
         s[r].z = __fadd_rn(s[r].z, __fmul_rn(kr, d4.z));
         s[r].w = __fadd_rn(s[r].w, __fmul_rn(kr, d4.w));
         __builtin_nontemporal_store((f32x4{s[r].x, s[r].y, s[r].z, s[r].w}),
-                                    reinterpret_cast<f32x4*>(Sh + (8 * rg + r) * kDV + 4 * cg));
+                                    reinterpret_cast<f32x4*>(Sh + (kRowsPer * rg + r) * kDV + 4 * cg));
         op[0] = fmaf(s[r].x, qr, op[0]);
         op[1] = fmaf(s[r].y, qr, op[1]);
         op[2] = fmaf(s[r].z, qr, op[2]);
@@ -162,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void deltanet_step_kernel(StepArgs p) {
     float o = 0.0f;
     if (t < kDV) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o += red[r][t];
+        for (int r = 0; r < kRowGroups; ++r) o += red[r][t];
         const float sq = wave_sum(__fmul_rn(o, o));
         if ((t & 63) == 0) wsum[4 + (t >> 6)] = sq;
     }
